@@ -1,0 +1,292 @@
+/* q27x.h -- C ABI of the MI355X (gfx950) chained-MTP speculative decode step.
+ *
+ * Two tiers, mirroring the reference engine's own boundary:
+ *   kernel tier  : stream-ordered launchers on caller-owned device buffers (reference:
+ *                  include/q27.h:208-477, include/q27_nr.h:6-79). They never allocate and never
+ *                  synchronise. Return Q27X_OK or a negative Q27X_E_* (the reference returns 1/0
+ *                  "ran / shape declined"; a declined shape here is Q27X_E_SHAPE, never a silent
+ *                  fallback).
+ *   engine tier  : a context that owns weights, KV cache, recurrent state and scratch, with the
+ *                  reference's load / decode / speculative-round entry points (reference:
+ *                  include/q27_load.h:146-243 for load, src/q27_main.cpp:1704 run_layer_tp for the
+ *                  plain step, src/q27_main.cpp:2702 spec_round for the speculative round).
+ *
+ * Plain C types only: pointers, sizes, ints, floats. Streams are hipStream_t passed as void*.
+ * bf16 values are uint16_t bit patterns (round-to-nearest-even, include/q27.h:133-139).
+ * Threading: one context per host thread; launchers are stream-ordered; calls that share a
+ * context or the module scratch of a launcher must not run concurrently on different streams
+ * (the same contract as the reference, include/q27_nr.h + src/q27_elem.hip:218-220).
+ */
+#ifndef Q27X_H
+#define Q27X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* q27x_stream_t; /* hipStream_t; NULL = the null stream */
+
+/* ---- status codes (the reference loader's Q27_OK / Q27_E_*, include/q27_load.h:70-78) ---- */
+#define Q27X_OK        0
+#define Q27X_E_ARG    -1   /* null pointer, bad count, bad flag                  */
+#define Q27X_E_SHAPE  -2   /* geometry this build has no kernel for              */
+#define Q27X_E_HIP    -3   /* a HIP runtime call failed                          */
+#define Q27X_E_NOMEM  -4   /* device or host allocation failed                   */
+#define Q27X_E_STATE  -5   /* call out of order (no weights, no prefill, ...)   */
+#define Q27X_E_RANGE  -6   /* position / context / row count out of range        */
+#define Q27X_E_DEVICE -7   /* a kernel raised its device-side error flag         */
+
+/* Last error message of the calling thread (never NULL). */
+const char* q27x_last_error(void);
+const char* q27x_version(void);
+
+/* ======================================================================================
+ * Device plumbing (no reference counterpart: the reference calls HIP directly). Lets tests and
+ * benches drive the kernel tier without any framework.
+ * ====================================================================================== */
+int q27x_device_count(int* n);
+int q27x_set_device(int dev);
+int q27x_device_name(int dev, char* buf, int len);
+int q27x_device_cus(int dev, int* n_cu);
+int q27x_malloc(void** p, size_t bytes);
+int q27x_free(void* p);
+int q27x_host_malloc(void** p, size_t bytes);   /* pinned host memory */
+int q27x_host_free(void* p);
+int q27x_memcpy_h2d(void* dst, const void* src, size_t bytes, q27x_stream_t s);
+int q27x_memcpy_d2h(void* dst, const void* src, size_t bytes, q27x_stream_t s);
+int q27x_memcpy_d2d(void* dst, const void* src, size_t bytes, q27x_stream_t s);
+int q27x_memset(void* p, int value, size_t bytes, q27x_stream_t s);
+int q27x_stream_create(q27x_stream_t* s);
+int q27x_stream_destroy(q27x_stream_t s);
+int q27x_stream_sync(q27x_stream_t s);
+int q27x_device_sync(void);
+int q27x_event_create(void** e);
+int q27x_event_destroy(void* e);
+int q27x_event_record(void* e, q27x_stream_t s);
+int q27x_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ======================================================================================
+ * Kernel tier
+ * ====================================================================================== */
+
+/* INT8 per-64-group weight handle. Replaces q27_i8g_t (include/q27.h:158-163); same fields,
+ * same meaning: w [rows][K] int8 natural K order, s [rows][K/64] fp32 group scales, alpha the
+ * per-tensor multiplier applied once per output. */
+typedef struct q27x_i8g {
+    const int8_t* w;
+    const float*  s;
+    float alpha;
+    int rows, K;
+} q27x_i8g_t;
+
+/* R5 activation quantizer, natural order, per-16 absmax (replaces q27_quant_fp8_b,
+ * include/q27_nr.h:73-74; math at src/q27_fp8.hip:373-425):
+ *   g = 1/in_scale; per 16: mx = max|x|; s = mx*g*(1/127); inv = s>0 ? g/s : 0;
+ *   q = clamp(rint(x*inv), -127, 127); xs = s.
+ * Row r of x starts at x + r*xstride (bf16 elements), of xq at xq + r*qstride, of xs at
+ * xs + r*sstride. n % 16 == 0. */
+int q27x_quant_rows(const uint16_t* x, int xstride, int8_t* xq, int qstride, float* xs,
+                    int sstride, int n, float in_scale, int nrows, q27x_stream_t s);
+
+/* R8 weight mirror rule, per 64 (replaces q27_fp8_to_i8g64_conv, include/q27.h:397; math at
+ * src/q27_nvfp4.hip:4259-4289): sc = mx*(1/127); inv = sc>0 ? 1/sc : 0; q = clamp(rint(v*inv)).
+ * w fp32 [rows][K] -> wq int8 [rows][K] + ws fp32 [rows][K/64]. K % 64 == 0. */
+int q27x_quant_weights_i8g64(const float* w, int rows, int K, int8_t* wq, float* ws,
+                             q27x_stream_t s);
+
+/* R7 W8A8 projection of nr rows (1..8) through one pass over the weights (replaces
+ * q27_proj_i8g_rows via q27_df2_gemm, include/q27_nr.h:57-58, and the NR launchers
+ * q27_proj_fp8_bf16_nr / q27_proj_fp8_res_nr, include/q27_nr.h:7-11; math at
+ * src/q27_fp8.hip:3814-3871):
+ *   y[n][r] = alpha * sum over 16-slabs s of (float)(int32 dot of the slab) * (ws64*xs16)
+ *             (+ rs * res[n][r])
+ * xq row n at xq + n*xstride, xs row n at xs + n*(xstride/16). out_bf16: 1 = bf16 (RNE) output,
+ * 0 = fp32 output. res may be NULL; res_bf16 selects its element type (bf16 / fp32); row n of res
+ * at res + n*rstride. K in {1024*k} or any K % 64 == 0 up to 20480. */
+int q27x_proj_rows(const q27x_i8g_t* w, const int8_t* xq, int xstride, const float* xs,
+                   void* y, int ystride, int out_bf16, const void* res, int res_bf16,
+                   int rstride, float rs, int nr, q27x_stream_t s);
+
+/* Debug export for the bit-exactness gate: the exact int32 dot of every 16-element slab,
+ * part[n][r][slab] (slab = k/16), for nr rows. */
+int q27x_proj_partials(const q27x_i8g_t* w, const int8_t* xq, int xstride, int32_t* part,
+                       int nr, q27x_stream_t s);
+
+/* R9 / lm_head bf16 GEMV of nr rows (replaces q27_bf16_gemv2_tile, include/q27_nr.h:75-76):
+ *   y[n][r] = sum_k bf16(W[r][k]) * bf16(x[n][k]) in fp32; out_bf16 selects bf16 / fp32 out.
+ * K % 8 == 0. */
+int q27x_bf16_gemv_rows(const uint16_t* w, int rows, int K, const uint16_t* x, int xstride,
+                        void* y, int ystride, int out_bf16, int nr, q27x_stream_t s);
+
+/* R22 + R5 RMSNorm + quantize of nr rows (replaces q27_rmsnorm_quant_fp8, include/q27.h:321-323,
+ * and q27_rmsnorm_hostss_fp8_b, include/q27_nr.h:33-35; math at src/q27_elem.hip:453-613,
+ * 835-910):
+ *   inv = 1/sqrt(sum x^2 / n + eps); nrm = x*inv*(plus + w)
+ *   hcopy = bf16(x) (optional), y = bf16(nrm) (optional), xq/xs = quantize(quant_bf16 ? y : nrm)
+ * x is fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1). n % 1024 == 0. */
+int q27x_rmsnorm_quant_rows(const void* x, int x_bf16, int xstride, const uint16_t* w,
+                            float plus, float eps, int n, uint16_t* hcopy, uint16_t* y,
+                            int ystride, int8_t* xq, float* xs, int quant_bf16,
+                            float in_scale, int nr, q27x_stream_t s);
+
+/* R16 SwiGLU + per-16 quantize (replaces q27_swiglu_quant_b, include/q27_nr.h:71-72; math at
+ * src/q27_nvfp4.hip:3984-4031, natural order):
+ *   v = (g/(1+e^-g)) * u * (1/in_scale); per 16: s = mx/127; q = clamp(rint(v/s)). */
+int q27x_swiglu_quant_rows(const float* gate, const float* up, int stride, int8_t* xq,
+                           float* xs, int n, float in_scale, int nr, q27x_stream_t s);
+
+/* R10 + R11 + R12 gated-delta-rule verify of nr rows for one layer (replaces
+ * q27_gdn_conv_tp_tile2 + q27_gdn_scan_tp_snap + the snapshot-bank restore, include/q27_nr.h:
+ * 77-83, src/q27_main.cpp:2933-2941; math at src/q27_gdn.hip:206-372, 411-592).
+ * Deferred commit replaces the snapshot banks: the state S in HBM is the state after the last
+ * COMMITTED position minus `npend` pending rows whose (k^, delta, decay) vectors and raw conv
+ * inputs the previous call left in `pend`. The call first applies those npend rows (the exact
+ * update the rows already received), writes the committed state back, then runs the nr new rows
+ * and leaves their update vectors in `pend` for the next call. Rolling back to an accepted prefix
+ * of a rows is therefore just calling again with npend = a.
+ *   qkv_raw  [nr][nqkv] bf16  projection output before conv (q | k | v, nqkv = (2*KH+VH)*D)
+ *   z        [nr][VH*D] bf16, a/b logits [nr][VH] fp32 (already a = in_proj_a.x, b = in_proj_b.x)
+ *   A_log, dt_bias [VH] bf16; norm_w [D] bf16 (raw weight, no +1); conv_w [nqkv][4] bf16
+ *   S [VH][D][D] fp32 key-major; conv_hist [nqkv][3] bf16 (oldest first)
+ *   pend: opaque buffer of q27x_gdn_pend_bytes(KH, VH, D, 8) bytes
+ *   out [nr][VH*D] bf16 gated-normed output, xq/xs its per-16 quantization (nullable). */
+size_t q27x_gdn_pend_bytes(int kh, int vh, int d, int max_rows);
+int q27x_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, int z_stride,
+                    const float* a, const float* b, int ab_stride, const uint16_t* A_log,
+                    const uint16_t* dt_bias, const uint16_t* norm_w, const uint16_t* conv_w,
+                    float* S, uint16_t* conv_hist, void* pend, int npend, int kh, int vh,
+                    int d, uint16_t* out, int out_stride, int8_t* xq, float* xs,
+                    int nr, q27x_stream_t s);
+
+/* R14 attention prep for nr consecutive positions pos0..pos0+nr-1 (replaces
+ * q27_attn_prep_tp_nr, include/q27_nr.h:84-86; math at src/q27_attn.hip:156-253):
+ * per head RMSNorm(1+w) over head_dim, rotate-half RoPE on the first rot dims using the
+ * [pos][rot/2] cos/sin tables, q -> bf16 qh [nr][nq*hd]; K (normed, roped) and V (raw) ->
+ * int8 KV cache [pos][nkv*hd] with fp32 per-`kv_group` scales [pos][nkv*hd/kv_group].
+ * qkv row layout: q block (nq heads x (gate ? 2*hd : hd), query dims first) | k | v. */
+int q27x_attn_prep_rows(const uint16_t* qkv, int qkv_stride, const uint16_t* q_norm_w,
+                        const uint16_t* k_norm_w, const float* rope_cos, const float* rope_sin,
+                        int rot, int8_t* kc, float* ks, int8_t* vc, float* vs, int kv_group,
+                        uint16_t* qh, int nq, int nkv, int hd, int gate, float eps, int pos0,
+                        int nr, q27x_stream_t s);
+
+/* R15 causal GQA attention of nr verify rows over the int8 KV cache (replaces
+ * q27_attn_decode_tp_nr, include/q27_nr.h:87-89; math at src/q27_attn.hip:258-463):
+ * row r attends keys 0..pos0+r; fixed 64-key splits; out = bf16(softmax(q.k/sqrt(hd)) v *
+ * sigmoid(gate)) [nr][nq*hd]; xq/xs its per-16 quantization (nullable). `work` is scratch of
+ * q27x_attn_work_bytes(nq, hd, ctx, nr) bytes. */
+size_t q27x_attn_work_bytes(int nq, int hd, int ctx, int nr);
+int q27x_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
+                   const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
+                   int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
+                   void* work, uint16_t* out, int8_t* xq, float* xs, q27x_stream_t s);
+
+/* R18 argmax of nr rows of n logits: non-finite filtered, ties -> lowest index, all non-finite
+ * -> index 0 / value -inf (replaces q27_argmax_val, include/q27.h:348; src/q27_elem.hip:216-322). */
+int q27x_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val,
+                     q27x_stream_t s);
+
+/* R20 greedy acceptance on the device: nacc = longest prefix with nx[j] == dt[j] (j < k),
+ * ncommit = nacc + 1, committed = nx[0..nacc] (src/q27_main.cpp:2811-2812, 2929-2932). */
+int q27x_accept(const int32_t* nx, const int32_t* dt, int k, int32_t* nacc_ncommit,
+                int32_t* committed, q27x_stream_t s);
+
+/* Test hook: the device's elementwise math (exp, exp2, log1p, sigmoid, SiLU, softplus) on n
+ * values, op = 0..5, so the bit-exact host restatement can be checked against it. */
+int q27x_math_test(const float* x, float* y, int n, int op, q27x_stream_t s);
+
+/* ======================================================================================
+ * Engine tier: the reference's load / decode / speculative-round entry points
+ * ====================================================================================== */
+
+/* Model geometry and semantic switches. All dimensions are runtime values. */
+typedef struct q27x_config {
+    int hidden;          /* 5120 */
+    int inter;           /* 17408 (SwiGLU intermediate) */
+    int vocab;           /* 62080 (untied bf16 lm_head rows) */
+    int n_layers;        /* 64 */
+    int attn_period;     /* 4: layer L is full attention when L % attn_period == attn_period-1 */
+    int gdn_kh, gdn_vh, gdn_d;      /* 16, 48, 128 */
+    int n_q, n_kv, head_dim;        /* 32, 8, 128 */
+    int attn_gate;       /* 1: q_proj emits an output gate per head (trunk semantics) */
+    int rot_dims;        /* rotary dims of a head (32 = partial factor 0.25 of 128) */
+    double rope_theta;   /* 1e7 */
+    int kv_group;        /* 32: fp32 scale per 32 KV elements */
+    float rms_eps;       /* 1e-6 */
+    int head_double_residual; /* 1: final-norm input bf16(bf16(r1)+r2) as the reference */
+    int mtp_swap;        /* Q27_MTP_SWAP (0: embedding half first) */
+    int mtp_plus_one;    /* Q27_MTP_PO (1) */
+    int spec;            /* Q27_SPEC: 1 = speculative decode */
+    int spec_k;          /* Q27_SPEC_K: drafts per round, [1, 7] */
+    int ctx;             /* context capacity in positions */
+} q27x_config;
+
+/* Statistics of a decode run (the reference's Q27_SPEC / Q27_SPEC_T lines,
+ * src/q27_main.cpp:6725-6733). */
+typedef struct q27x_stats {
+    long long rounds;
+    long long committed;
+    long long accepted;        /* sum of nacc */
+    long long acc_hist[9];     /* rounds with >= j accepted drafts, j = 0..8 */
+    double decode_ms;          /* wall clock of the decode loop (no load, no prefill) */
+    double prefill_ms;
+} q27x_stats;
+
+typedef struct q27x_ctx q27x_ctx;
+
+/* The BASELINE config-3 geometry (64 layers: 48 GDN + 16 attention). */
+int q27x_config_default(q27x_config* c);
+/* A tiny geometry with the same structure for CPU-checkable parity runs. */
+int q27x_config_tiny(q27x_config* c);
+/* Q27_SPEC (bool, default 1) / Q27_SPEC_K (int, default 1, clamped to [1,7]) with the reference's
+ * fail-closed parsing (include/q27.h:189-206, src/q27_main.cpp:3360-3361): an unparseable value
+ * prints FATAL and aborts. Host-only. */
+int q27x_spec_config_from_env(q27x_config* c);
+
+int q27x_ctx_create(int device, const q27x_config* c, q27x_ctx** out);
+int q27x_ctx_destroy(q27x_ctx* ctx);
+/* Seeded random-init weights (replaces q27_open + q27_upload_*, include/q27_load.h:146-243,
+ * for a synthetic checkpoint): int8 per-64 projections from N(0, 0.02) draws, bf16 lm_head,
+ * embeddings, norms and GDN parameters; deterministic in (seed, tensor, index). */
+int q27x_load_synthetic(q27x_ctx* ctx, uint64_t seed);
+/* Bytes of weights resident on the device. */
+int q27x_weight_bytes(q27x_ctx* ctx, size_t* bytes);
+/* Reset positions, KV, recurrent state and speculation state (a new request). */
+int q27x_reset(q27x_ctx* ctx);
+/* Ingest a prompt (positions 0..n-1), produce the first decode token, and prompt-condition the
+ * MTP layer (reference: prefill sweep + mtp_prompt_pass, src/q27_main.cpp:2649-2692, 5131-5136). */
+int q27x_prefill(q27x_ctx* ctx, const int32_t* ids, int n, int32_t* first_token);
+/* One plain greedy step (Q27_SPEC=0 semantics): consumes the current token, returns the next. */
+int q27x_decode_step(q27x_ctx* ctx, int32_t* out_token);
+/* One chained-MTP speculative round (spec_round, src/q27_main.cpp:2702-2958): K drafts, an
+ * NR = K+1 row verify, greedy acceptance, rollback and hand-off, all on the device. Returns the
+ * committed tokens (ncommit = nacc+1 <= K+1). */
+int q27x_spec_round(q27x_ctx* ctx, int32_t* out_tokens, int* ncommit);
+/* Forced-acceptance mode: drafts are taken from this token stream (the trunk's own greedy
+ * continuation, positions after the prompt) instead of the MTP argmax; the draft and verify work
+ * is unchanged. n = 0 switches it off. */
+int q27x_set_forced_drafts(q27x_ctx* ctx, const int32_t* toks, int n);
+/* Decode loop (src/q27_main.cpp:6382-6696): after q27x_prefill, generate until max_new tokens
+ * are committed (including the first token from prefill). spec = 1 runs speculative rounds
+ * (with the device-side graph and a one-round-lagged host mailbox), 0 plain steps. */
+int q27x_generate(q27x_ctx* ctx, int max_new, int spec, int32_t* out, int* n_out,
+                  q27x_stats* st);
+/* Exactly n speculative rounds (spec = 1) or plain steps (spec = 0) from the current state, launched
+ * back to back; stats cover those n. */
+int q27x_run_rounds(q27x_ctx* ctx, int n, int spec, q27x_stats* st);
+/* Time of one verify pass (64 layers + head, nr rows) averaged over iters, device events. */
+int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
+/* Time one projection launch of layer `layer` (which: 0 in_qkv|in_z, 1 gate|up, 2 down, 3 out_proj,
+ * 4 lm_head) over iters launches with device events; reports ms per launch and its algorithmic
+ * bytes (weights + scales + activations + outputs). */
+int q27x_bench_kernel(q27x_ctx* ctx, int layer, int which, int nr, int iters, float* ms, double* bytes);
+/* Raw access for tests: copy a device tensor of the context to the host by name. */
+int q27x_debug_read(q27x_ctx* ctx, const char* name, int layer, void* dst, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q27X_H */

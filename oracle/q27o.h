@@ -1,0 +1,134 @@
+/* q27o.h -- CPU oracle for the chained-MTP verify path. TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference engine's arithmetic for the speculative verify step
+ * (bespokeontology/qwen3.8-27b-mi50-cpp-engine; citations are file:line into that tree). It is
+ * the checker the GPU path is compared against, and the CPU baseline's integer loop. Nothing in
+ * the product links, loads or calls it: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg do.
+ *
+ * Fixed reduction orders. Every floating-point sum is restated in one fixed order so that the
+ * GPU kernels (which use the same order) match bit for bit:
+ *   lane-slab order (W8A8 projection, src/q27_fp8.hip:3826-3861): slab s of 16 elements belongs
+ *     to lane s%64 at step s/64; each lane accumulates its slabs in ascending step order with
+ *     fmaf((float)dot, ws*xs, acc); the 64 lane sums are combined by the shfl_down tree
+ *     (offsets 32,16,8,4,2,1).
+ *   bf16 GEMV: the same with chunks of 8 bf16 (lane c%64, step c/64), fmaf per element.
+ *   row sum of squares (hidden rows, n % 1024 == 0): thread t of 256 accumulates elements
+ *     1024i + 4t + e; four wave trees; ((w0 + w1) + w2) + w3.
+ *   head sums (128 dims): tree(elements 0..63) + tree(elements 64..127).
+ * Transcendentals (exp, exp2, log1p) are the portable routines below (range reduction + fixed
+ * polynomial, basic IEEE operations only), used identically on the device, so that greedy token
+ * sequences are reproducible bit for bit. Their accuracy against libm is pinned by tests.
+ *
+ * parity pinning: see tests/test_oracle_*.py (closed forms, fp64 brute force, invariants).
+ */
+#ifndef Q27O_H
+#define Q27O_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar helpers ---- */
+uint16_t q27o_f2bf(float f);            /* RNE, include/q27.h:136-139 */
+float    q27o_bf2f(uint16_t b);         /* include/q27.h:133-135 */
+float    q27o_exp(float x);
+float    q27o_exp2(float x);
+float    q27o_log1p(float x);
+float    q27o_sigmoid(float x);          /* 1/(1+e^-x), src/q27_gdn.hip:114-116 */
+float    q27o_silu(float x);             /* x/(1+e^-x), src/q27_gdn.hip:117-119 */
+float    q27o_softplus(float x);         /* x > 20 ? x : log1p(e^x), src/q27_gdn.hip:317 */
+void     q27o_math_vec(const float* x, float* y, int n, int op);
+
+/* ---- seeded synthetic generator (shared definition with the device generator) ---- */
+uint64_t q27o_hash(uint64_t seed, uint64_t tensor, uint64_t idx);
+float    q27o_normal(uint64_t seed, uint64_t tensor, uint64_t idx);   /* ~N(0,1), Irwin-Hall(4) */
+float    q27o_uniform(uint64_t seed, uint64_t tensor, uint64_t idx);  /* [0,1), 24-bit */
+
+/* ---- R5 / R8 / R16 quantizers ---- */
+void q27o_quant_rows(const uint16_t* x, int xstride, int8_t* xq, int qstride, float* xs,
+                     int sstride, int n, float in_scale, int nrows);
+void q27o_quant_f32(const float* v, int n, int group, int8_t* q, float* s);
+void q27o_quant_weights_i8g64(const float* w, int rows, int K, int8_t* wq, float* ws);
+void q27o_swiglu_quant_rows(const float* gate, const float* up, int stride, int8_t* xq,
+                            float* xs, int n, float in_scale, int nr);
+
+/* ---- R7 projection (pre-epilogue value acc*alpha) and its int32 slab partials ---- */
+void q27o_proj_rows(const int8_t* W, const float* WS, float alpha, int rows, int K,
+                    const int8_t* xq, int xstride, const float* xs, float* y, int ystride,
+                    int nr);
+void q27o_proj_partials(const int8_t* W, int rows, int K, const int8_t* xq, int xstride,
+                        int32_t* part, int nr);
+/* the kernel-tier epilogue of q27x_proj_rows */
+void q27o_proj_rows_epi(const int8_t* W, const float* WS, float alpha, int rows, int K,
+                        const int8_t* xq, int xstride, const float* xs, void* y, int ystride,
+                        int out_bf16, const void* res, int res_bf16, int rstride, float rs,
+                        int nr);
+
+/* ---- bf16 GEMV (R9, lm_head) ---- */
+void q27o_bf16_gemv_rows(const uint16_t* W, int rows, int K, const uint16_t* x, int xstride,
+                         float* y, int ystride, int nr);
+
+/* ---- R22 norms ---- */
+float q27o_rowsumsq(const float* x, int n);
+float q27o_headsum(const float* a, const float* b, int n);  /* sum a*b over n (n%64==0) */
+void  q27o_rmsnorm_quant_rows(const void* x, int x_bf16, int xstride, const uint16_t* w,
+                              float plus, float eps, int n, uint16_t* hcopy, uint16_t* y,
+                              int ystride, int8_t* xq, float* xs, int quant_bf16,
+                              float in_scale, int nr);
+
+/* ---- R10/R11/R12 GDN verify with deferred commit ---- */
+size_t q27o_gdn_pend_bytes(int kh, int vh, int d, int max_rows);
+void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, int z_stride,
+                     const float* a, const float* b, int ab_stride, const uint16_t* A_log,
+                     const uint16_t* dt_bias, const uint16_t* norm_w, const uint16_t* conv_w,
+                     float* S, uint16_t* conv_hist, void* pend, int npend, int kh, int vh,
+                     int d, float eps, uint16_t* out, int out_stride, int8_t* xq, float* xs,
+                     int nr);
+
+/* ---- R14/R15 attention ---- */
+void q27o_rope_table(int ctx, int rot, double theta, float* cosv, float* sinv);
+void q27o_attn_prep_rows(const uint16_t* qkv, int qkv_stride, const uint16_t* q_norm_w,
+                         const uint16_t* k_norm_w, const float* rope_cos,
+                         const float* rope_sin, int rot, int8_t* kc, float* ks, int8_t* vc,
+                         float* vs, int kv_group, uint16_t* qh, int nq, int nkv, int hd,
+                         int gate, float eps, int pos0, int nr);
+void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
+                    const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
+                    int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
+                    uint16_t* out, int8_t* xq, float* xs);
+
+/* ---- R18 / R20 ---- */
+void q27o_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val);
+int  q27o_accept(const int32_t* nx, const int32_t* dt, int k, int32_t* committed);
+
+/* ---- whole model (R1-R4, R17-R21) ---- */
+typedef struct q27o_cfg {
+    int hidden, inter, vocab, n_layers, attn_period;
+    int gdn_kh, gdn_vh, gdn_d;
+    int n_q, n_kv, head_dim, attn_gate, rot_dims;
+    double rope_theta;
+    int kv_group;
+    float rms_eps;
+    int head_double_residual, mtp_swap, mtp_plus_one;
+    int spec_k, ctx;
+} q27o_cfg;
+
+typedef struct q27o_model q27o_model;
+q27o_model* q27o_model_create(const q27o_cfg* c, uint64_t seed);   /* generates the weights */
+void q27o_model_destroy(q27o_model* m);
+void q27o_model_reset(q27o_model* m);
+int  q27o_model_prefill(q27o_model* m, const int32_t* ids, int n);          /* returns token */
+int  q27o_model_decode_step(q27o_model* m);                                 /* returns token */
+int  q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced); /* ncommit */
+int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx);
+double q27o_model_weight_bytes(const q27o_model* m);
+/* access to named tensors / buffers for the tests */
+void* q27o_model_tensor(q27o_model* m, const char* name, int layer, size_t* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

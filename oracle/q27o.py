@@ -1,0 +1,138 @@
+"""ctypes binding of the CPU oracle (libq27o.so). TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker; the
+product never loads it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq27o.so")
+VP, I, F, SZ, U64, D = (ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t,
+                        ctypes.c_uint64, ctypes.c_double)
+
+
+class Cfg(ctypes.Structure):
+    _fields_ = [
+        ("hidden", I), ("inter", I), ("vocab", I), ("n_layers", I), ("attn_period", I),
+        ("gdn_kh", I), ("gdn_vh", I), ("gdn_d", I),
+        ("n_q", I), ("n_kv", I), ("head_dim", I), ("attn_gate", I), ("rot_dims", I),
+        ("rope_theta", D), ("kv_group", I), ("rms_eps", F),
+        ("head_double_residual", I), ("mtp_swap", I), ("mtp_plus_one", I),
+        ("spec_k", I), ("ctx", I),
+    ]
+
+
+_SIGS = {
+    "q27o_f2bf": ([F], ctypes.c_uint16), "q27o_bf2f": ([ctypes.c_uint16], F),
+    "q27o_exp": ([F], F), "q27o_exp2": ([F], F), "q27o_log1p": ([F], F),
+    "q27o_math_vec": ([VP, VP, I, I], None),
+    "q27o_hash": ([U64, U64, U64], U64), "q27o_normal": ([U64, U64, U64], F),
+    "q27o_uniform": ([U64, U64, U64], F),
+    "q27o_quant_rows": ([VP, I, VP, I, VP, I, I, F, I], None),
+    "q27o_quant_f32": ([VP, I, I, VP, VP], None),
+    "q27o_quant_weights_i8g64": ([VP, I, I, VP, VP], None),
+    "q27o_swiglu_quant_rows": ([VP, VP, I, VP, VP, I, F, I], None),
+    "q27o_proj_rows": ([VP, VP, F, I, I, VP, I, VP, VP, I, I], None),
+    "q27o_proj_partials": ([VP, I, I, VP, I, VP, I], None),
+    "q27o_proj_rows_epi": ([VP, VP, F, I, I, VP, I, VP, VP, I, I, VP, I, I, F, I], None),
+    "q27o_bf16_gemv_rows": ([VP, I, I, VP, I, VP, I, I], None),
+    "q27o_rowsumsq": ([VP, I], F), "q27o_headsum": ([VP, VP, I], F),
+    "q27o_rmsnorm_quant_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, VP, I, F, I], None),
+    "q27o_gdn_pend_bytes": ([I, I, I, I], SZ),
+    "q27o_gdn_verify": ([VP, I, VP, I, VP, VP, I, VP, VP, VP, VP, VP, VP, VP, I, I, I, I, F, VP,
+                         I, VP, VP, I], None),
+    "q27o_rope_table": ([I, I, D, VP, VP], None),
+    "q27o_attn_prep_rows": ([VP, I, VP, VP, VP, VP, I, VP, VP, VP, VP, I, VP, I, I, I, I, F, I,
+                             I], None),
+    "q27o_attn_rows": ([VP, VP, I, VP, VP, VP, VP, I, I, I, I, I, I, I, VP, VP, VP], None),
+    "q27o_argmax_rows": ([VP, I, I, I, VP, VP], None),
+    "q27o_accept": ([VP, VP, I, VP], I),
+    "q27o_model_create": ([VP, U64], VP), "q27o_model_destroy": ([VP], None),
+    "q27o_model_reset": ([VP], None), "q27o_model_prefill": ([VP, VP, I], I),
+    "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
+    "q27o_model_verify_rows": ([VP, I, VP, VP], I),
+    "q27o_model_weight_bytes": ([VP], D),
+    "q27o_model_tensor": ([VP, ctypes.c_char_p, I, VP], VP),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def f2bf(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf2f(b):
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def cfg_from(c):
+    """A q27o config from a q27x Config (or a dict with the same fields)."""
+    d = c.as_dict() if hasattr(c, "as_dict") else dict(c)
+    o = Cfg()
+    for f, _ in Cfg._fields_:
+        setattr(o, f, d[f])
+    return o
+
+
+class Model:
+    def __init__(self, cfg, seed):
+        self.cfg = cfg_from(cfg)
+        self.m = lib().q27o_model_create(ctypes.byref(self.cfg), seed)
+        if not self.m:
+            raise RuntimeError("q27o_model_create failed")
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        return lib().q27o_model_prefill(self.m, ids.ctypes.data, len(ids))
+
+    def decode_step(self):
+        return lib().q27o_model_decode_step(self.m)
+
+    def spec_round(self, forced=None):
+        out = np.zeros(8, dtype=np.int32)
+        f = None if forced is None else np.ascontiguousarray(forced, dtype=np.int32)
+        n = lib().q27o_model_spec_round(self.m, out.ctypes.data, ptr(f))
+        return out[:n].tolist()
+
+    def tensor(self, name, layer, dtype):
+        nb = ctypes.c_size_t(0)
+        p = lib().q27o_model_tensor(self.m, name.encode(), layer, ctypes.byref(nb))
+        if not p:
+            raise KeyError(name)
+        n = nb.value // np.dtype(dtype).itemsize
+        return np.ctypeslib.as_array((ctypes.c_byte * nb.value).from_address(p)).view(dtype)[:n].copy()
+
+    def close(self):
+        if self.m:
+            lib().q27o_model_destroy(self.m)
+            self.m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

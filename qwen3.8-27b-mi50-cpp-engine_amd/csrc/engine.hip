@@ -1,0 +1,1124 @@
+// engine.hip -- the chained-MTP speculative decode step on one MI355X.
+//
+// Host side of the reference's spec_round (src/q27_main.cpp:2702-2958) and its verify layer
+// run_layer_tp_nr (2271-2489), re-planned for one GPU:
+//   * no tensor parallelism: every projection is unsharded and the residual share is 1;
+//   * the round never returns to the host: drafts, verify-row tokens, acceptance, rollback and
+//     hand-off live in a device control block (Dctl) that small control kernels update, so one
+//     round is a fixed kernel sequence captured once in a HIP graph and replayed;
+//   * rollback is the GDN kernel's deferred commit (no snapshot banks); KV needs none (R13);
+//   * only the round's (ncommit, tokens) reach the host, through a pinned mailbox.
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <chrono>
+#include <string>
+#include <vector>
+
+#include "q27x_dev.h"
+#include "q27x_int.h"
+
+namespace q27x {
+
+// tensor ids shared with the host restatement: ((layer code) << 8) | kind
+enum {
+    T_IN_NORM = 1, T_POST_NORM = 2,
+    T_IN_QKV = 10, T_IN_Z = 11, T_IN_A = 12, T_IN_B = 13, T_A_LOG = 14, T_DT_BIAS = 15,
+    T_GDN_NORM = 16, T_CONV_W = 17, T_OUT_PROJ = 18,
+    T_Q = 20, T_K = 21, T_V = 22, T_Q_NORM = 23, T_K_NORM = 24, T_O = 25,
+    T_GATE = 30, T_UP = 31, T_DOWN = 32,
+    T_EMB = 40, T_FINAL_NORM = 41, T_LM_HEAD = 42,
+    T_PRE_EMB = 50, T_PRE_HID = 51, T_FC0 = 52, T_FC1 = 53, T_MTP_NORM = 54
+};
+static uint64_t tid(int code, int kind) { return ((uint64_t)code << 8) | (uint64_t)kind; }
+
+struct Mat { int8_t* w = nullptr; float* s = nullptr; int rows = 0, K = 0; };
+
+struct LayerDev {
+    int is_attn = 0;
+    uint16_t *in_norm = nullptr, *post_norm = nullptr;
+    Mat qkvz; uint16_t *in_a = nullptr, *in_b = nullptr, *A_log = nullptr, *dt_bias = nullptr;
+    uint16_t *gdn_norm = nullptr, *conv_w = nullptr; Mat out_proj;
+    Mat qkv; uint16_t *q_norm = nullptr, *k_norm = nullptr; Mat o;
+    Mat gu, down;
+    int8_t *kc = nullptr, *vc = nullptr; float *ks = nullptr, *vs = nullptr;
+    float* S = nullptr; uint16_t* conv_hist = nullptr; void* pend = nullptr;
+};
+
+// device control block (the Dev NR fields of src/q27_main.cpp:360-379 plus the round's tokens)
+struct Dctl {
+    int pos, tok, ncatch, gdn_npend;
+    int catch_tok[8];
+    int dt[8], nx[8];
+    float nxval[8];
+    int vtok[8];
+    int mtp_nact, mtp_dpos0, mtp_head, mtp_out;
+    int mtp_tok[8];
+    int committed, max_new, stop, rounds;
+    int forced_on, forced_n, forced_base, ctx;
+    int nacc_last, ncommit_last, err, pad0;
+    long long acc_hist[9];
+    long long accepted;
+};
+
+struct Mailbox { volatile int round; volatile int committed; volatile int ncommit; volatile int stop; volatile int tok[8]; };
+
+}  // namespace q27x
+
+using namespace q27x;
+
+struct q27x_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    q27x_config c{};
+    int H = 0, I = 0, V = 0, D = 128, nqkv = 0, nz = 0, qr = 0, kvr = 0, att = 0;
+    char* warena = nullptr; size_t wcap = 0, woff = 0;
+    char* sarena = nullptr; size_t scap = 0, soff = 0;
+    std::vector<LayerDev> L;
+    LayerDev mtp;
+    uint16_t *pre_emb = nullptr, *pre_hid = nullptr, *mtp_norm = nullptr;
+    Mat fc0, fc1;
+    uint16_t *emb = nullptr, *final_norm = nullptr, *lm_head = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    size_t weight_bytes = 0;
+    // scratch
+    Dctl* dctl = nullptr;
+    uint16_t *hid = nullptr, *ynorm = nullptr, *hfinal = nullptr, *hall = nullptr;
+    float* xres = nullptr;
+    int8_t* xq = nullptr; float* xs = nullptr;
+    uint16_t *conv_out = nullptr, *zbuf = nullptr, *pb = nullptr, *qh = nullptr, *ao = nullptr, *gout = nullptr;
+    uint16_t *cat = nullptr, *mtp_hin = nullptr, *mtp_res = nullptr, *hprev = nullptr, *hcatch = nullptr;
+    float* attn_work = nullptr; int max_splits = 0;
+    float* pval = nullptr; uint32_t* pidx = nullptr; int pstride = 1024;
+    int32_t* out_ring = nullptr; int ring_cap = 0;
+    int32_t* forced = nullptr; int forced_cap = 0;
+    int32_t* prompt_dev = nullptr; int prompt_cap = 0;
+    Mailbox* mbox = nullptr;   // pinned host memory, mapped
+    Mailbox* mbox_dev = nullptr;
+    int loaded = 0, prefilled = 0, s_fail = 0;
+    int n_prompt = 0;
+    hipGraphExec_t g_spec = nullptr, g_plain = nullptr;
+    int g_spec_k = 0;
+    float sl2e = 0.0f;
+};
+
+namespace q27x {
+
+static void* walloc(q27x_ctx* x, size_t bytes) {
+    const size_t off = (x->woff + 255) & ~(size_t)255;
+    if (off + bytes > x->wcap) return nullptr;
+    x->woff = off + bytes;
+    return x->warena + off;
+}
+static void* salloc(q27x_ctx* x, size_t bytes) {
+    const size_t off = (x->soff + 255) & ~(size_t)255;
+    if (x->s_fail || off + bytes > x->scap) { x->s_fail = 1; return nullptr; }
+    x->soff = off + bytes;
+    return x->sarena + off;
+}
+static int is_attn_layer(const q27x_config& c, int L) { return (L % c.attn_period) == c.attn_period - 1; }
+
+// ---------------------------------------------------------------- control kernels
+// Small single-block kernels that move the round's bookkeeping on the device.
+__global__ void k_set_ints(int* base, int n, int o0, int v0, int o1, int v1, int o2, int v2, int o3, int v3) {
+    if (threadIdx.x != 0) return;
+    const int offs[4] = { o0, o1, o2, o3 }, vals[4] = { v0, v1, v2, v3 };
+    for (int i = 0; i < n && i < 4; ++i) base[offs[i]] = vals[i];
+}
+__device__ __forceinline__ void copy_row(uint16_t* dst, const uint16_t* src, int H) {
+    for (int i = threadIdx.x * 8; i < H; i += blockDim.x * 8) *(uint4*)(dst + i) = *(const uint4*)(src + i);
+}
+// draft 0 rows: the catch-up rows then (h_prev, tok) (src/q27_main.cpp:2737-2744)
+__global__ __launch_bounds__(256) void k_round_begin(Dctl* d, uint16_t* mtp_hin, const uint16_t* hcatch,
+                                                     const uint16_t* hprev, int H, int K) {
+    if (d->stop) return;
+    if (d->pos + K + 1 > d->ctx) {
+        if (threadIdx.x == 0) { d->err = 6; d->stop = 1; }
+        return;
+    }
+    const int nc = d->ncatch;
+    for (int r = 0; r < nc; ++r) copy_row(mtp_hin + (size_t)r * H, hcatch + (size_t)r * H, H);
+    copy_row(mtp_hin + (size_t)nc * H, hprev, H);
+    if (threadIdx.x == 0) {
+        for (int r = 0; r < nc; ++r) d->mtp_tok[r] = d->catch_tok[r];
+        d->mtp_tok[nc] = d->tok;
+        for (int r = nc + 1; r < 8; ++r) d->mtp_tok[r] = 0;
+        d->mtp_nact = nc + 1;
+        d->mtp_dpos0 = d->pos - 1 - nc;
+        d->mtp_head = nc;
+    }
+}
+// after draft j: record dt[j] (the MTP argmax, or the forced token), chain the layer's own
+// residual into the next draft (src/q27_main.cpp:2745-2750), or set the verify rows after the
+// last draft
+__global__ __launch_bounds__(256) void k_draft_post(Dctl* d, uint16_t* mtp_hin, const uint16_t* mtp_res,
+                                                    const int32_t* forced, int H, int j, int K) {
+    if (d->stop) return;
+    __shared__ int s_tok;
+    if (threadIdx.x == 0) {
+        int t = d->mtp_out;
+        if (d->forced_on) {
+            const int fi = d->pos - d->forced_base + 1 + j;
+            if (fi >= 0 && fi < d->forced_n) t = forced[fi];
+        }
+        d->dt[j] = t;
+        s_tok = t;
+    }
+    __syncthreads();
+    if (j + 1 < K) {
+        copy_row(mtp_hin, mtp_res + (size_t)d->mtp_head * H, H);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            d->mtp_tok[0] = s_tok;
+            d->mtp_nact = 1;
+            d->mtp_dpos0 = d->pos + j;      // pos - 1 + (j + 1)
+            d->mtp_head = 0;
+        }
+    } else if (threadIdx.x == 0) {
+        d->vtok[0] = d->tok;
+        for (int r = 1; r <= K; ++r) d->vtok[r] = d->dt[r - 1];
+        d->ncatch = 0;
+    }
+}
+// [3] greedy acceptance, [4] rollback (= how many rows the next GDN call commits) and hand-off
+// (src/q27_main.cpp:2811-2812, 2929-2950); one-round-lagged mailbox to the host
+__global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal, uint16_t* hcatch, uint16_t* hprev,
+                                                int32_t* ring, int ring_cap, Mailbox* mb, int H, int K) {
+    if (d->stop) return;
+    __shared__ int s_nacc;
+    if (threadIdx.x == 0) {
+        int nacc = 0;
+        while (nacc < K && d->nx[nacc] == d->dt[nacc]) ++nacc;
+        s_nacc = nacc;
+    }
+    __syncthreads();
+    const int nacc = s_nacc;
+    for (int j = 0; j < nacc; ++j) copy_row(hcatch + (size_t)j * H, hfinal + (size_t)j * H, H);
+    copy_row(hprev, hfinal + (size_t)nacc * H, H);
+    if (threadIdx.x == 0) {
+        const int ncommit = nacc + 1;
+        int c = d->committed;
+        int emitted = 0;
+        for (int j = 0; j < ncommit && c < d->max_new; ++j, ++emitted) {
+            if (c < ring_cap) ring[c] = d->nx[j];
+            ++c;
+        }
+        for (int j = 0; j < nacc; ++j) d->catch_tok[j] = d->nx[j];
+        d->ncatch = nacc;
+        d->tok = d->nx[nacc];
+        d->pos += ncommit;
+        d->gdn_npend = ncommit;
+        d->committed = c;
+        d->rounds += 1;
+        d->accepted += nacc;
+        for (int j = 0; j <= nacc && j < 9; ++j) d->acc_hist[j] += 1;
+        d->nacc_last = nacc;
+        d->ncommit_last = ncommit;
+        if (c >= d->max_new) d->stop = 1;
+        if (mb) {
+            for (int j = 0; j < 8; ++j) mb->tok[j] = j < ncommit ? d->nx[j] : -1;
+            mb->ncommit = ncommit;
+            mb->committed = c;
+            mb->stop = d->stop;
+            __threadfence_system();
+            mb->round = d->rounds;
+        }
+    }
+}
+// plain greedy step bookkeeping (src/q27_main.cpp:6462-6466, 6680-6695)
+__global__ void k_plain_pre(Dctl* d) {
+    if (d->stop || threadIdx.x) return;
+    if (d->pos + 1 > d->ctx) { d->err = 6; d->stop = 1; return; }
+    d->vtok[0] = d->tok;
+}
+__global__ __launch_bounds__(256) void k_plain_post(Dctl* d, const uint16_t* hfinal, uint16_t* hprev, int32_t* ring,
+                                                    int ring_cap, Mailbox* mb, int H) {
+    if (d->stop) return;
+    copy_row(hprev, hfinal, H);
+    if (threadIdx.x == 0) {
+        const int c = d->committed;
+        if (c < d->max_new && c < ring_cap) ring[c] = d->nx[0];
+        d->committed = c + 1;
+        d->tok = d->nx[0];
+        d->pos += 1;
+        d->gdn_npend = 1;
+        d->ncatch = 0;
+        d->rounds += 1;
+        if (d->committed >= d->max_new) d->stop = 1;
+        if (mb) {
+            mb->tok[0] = d->nx[0];
+            mb->ncommit = 1;
+            mb->committed = d->committed;
+            mb->stop = d->stop;
+            __threadfence_system();
+            mb->round = d->rounds;
+        }
+    }
+}
+__global__ void k_accept_rows(const int32_t* nx, const int32_t* dt, int k, int32_t* out2, int32_t* committed) {
+    if (threadIdx.x) return;
+    int nacc = 0;
+    while (nacc < k && nx[nacc] == dt[nacc]) ++nacc;
+    for (int j = 0; j <= nacc; ++j) committed[j] = nx[j];
+    out2[0] = nacc;
+    out2[1] = nacc + 1;
+}
+
+// ---------------------------------------------------------------- the verify pass
+// run_layer_tp_nr on one card for nr rows: tokens d->vtok, positions d->pos.., GDN commits
+// d->gdn_npend pending rows. head: 0 = final residual rows only, 1 = + final norm, lm_head and
+// argmax into d->nx. hout: where the final residual rows go (default ctx->hfinal).
+static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
+    const q27x_config& c = x->c;
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    const int H = x->H, I = x->I;
+    int rc;
+    for (int l = 0; l < c.n_layers; ++l) {
+        LayerDev& Y = x->L[l];
+        NormArgs na{};
+        na.w = Y.in_norm; na.plus = 1.0f; na.eps = c.rms_eps; na.n = H; na.in_scale = 1.0f;
+        na.y = x->ynorm; na.ystride = H; na.xq = x->xq; na.xs = x->xs; na.stop = &d->stop;
+        if (l == 0) { na.emb = x->emb; na.tok = d->vtok; na.hcopy = x->hid; na.quant_bf16 = 1; }
+        else { na.x = x->xres; na.x_bf16 = 0; na.xstride = H; na.hcopy = x->hid; na.quant_bf16 = 0; }
+        if ((rc = launch_norm(na, nr, s))) return rc;
+        ProjArgs p{};
+        p.alpha = 1.0f; p.xq = x->xq; p.xst = H; p.xs = x->xs; p.stop = &d->stop;
+        if (Y.is_attn) {
+            p.W = Y.qkv.w; p.WS = Y.qkv.s; p.rows = Y.qkv.rows; p.K = H;
+            p.y = x->pb; p.ystride = Y.qkv.rows; p.out_bf16 = 1;
+            if ((rc = launch_proj(p, EPI_STORE, nr, s))) return rc;
+            AttnArgs a{};
+            a.qkv = x->pb; a.qkv_stride = Y.qkv.rows; a.q_norm_w = Y.q_norm; a.k_norm_w = Y.k_norm;
+            a.rope_cos = x->rope_cos; a.rope_sin = x->rope_sin; a.rot = c.rot_dims;
+            a.kc = Y.kc; a.ks = Y.ks; a.vc = Y.vc; a.vs = Y.vs; a.kv_group = c.kv_group; a.qh = x->qh;
+            a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
+            a.pos0_ptr = &d->pos; a.work = x->attn_work; a.max_splits = x->max_splits; a.sl2e = x->sl2e;
+            a.out = x->ao; a.xq = x->xq; a.xs = x->xs; a.stop = &d->stop;
+            if ((rc = launch_attn_prep(a, nr, s))) return rc;
+            if ((rc = launch_attn(a, nr, s))) return rc;
+            ProjArgs o{};
+            o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.alpha = 1.0f;
+            o.xq = x->xq; o.xst = x->att; o.xs = x->xs;
+            o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
+            o.res = x->hid; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f; o.stop = &d->stop;
+            if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
+        } else {
+            p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H;
+            p.nconv = x->nqkv; p.conv_out = x->conv_out; p.conv_stride = x->nqkv;
+            p.z_out = x->zbuf; p.z_stride = x->nz;
+            p.conv_w = Y.conv_w; p.conv_hist = Y.conv_hist;
+            p.pend_raw = (uint16_t*)((char*)Y.pend + gdn_pend_raw_offset(c.gdn_kh, c.gdn_vh, x->D));
+            p.npend_ptr = &d->gdn_npend;
+            if ((rc = launch_proj(p, EPI_GDN_IN, nr, s))) return rc;
+            GdnArgs g{};
+            g.qkv = x->conv_out; g.qkv_stride = x->nqkv; g.z = x->zbuf; g.z_stride = x->nz;
+            g.in_a = Y.in_a; g.in_b = Y.in_b; g.ynorm = x->ynorm; g.ystride = H; g.H = H;
+            g.A_log = Y.A_log; g.dt_bias = Y.dt_bias; g.norm_w = Y.gdn_norm;
+            g.S = Y.S; g.pend = Y.pend; g.npend_ptr = &d->gdn_npend;
+            g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
+            g.out = x->gout; g.out_stride = x->nz; g.xq = x->xq; g.xs = x->xs; g.stop = &d->stop;
+            if ((rc = launch_gdn(g, nr, s))) return rc;
+            ProjArgs o{};
+            o.W = Y.out_proj.w; o.WS = Y.out_proj.s; o.rows = H; o.K = x->nz; o.alpha = 1.0f;
+            o.xq = x->xq; o.xst = x->nz; o.xs = x->xs;
+            o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
+            o.res = x->hid; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f; o.stop = &d->stop;
+            if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
+        }
+        // post norm: h = bf16(r1), quantize the fp32 normed rows
+        NormArgs pn{};
+        pn.x = x->xres; pn.x_bf16 = 0; pn.xstride = H; pn.w = Y.post_norm; pn.plus = 1.0f; pn.eps = c.rms_eps;
+        pn.n = H; pn.hcopy = x->hid; pn.xq = x->xq; pn.xs = x->xs; pn.quant_bf16 = 0; pn.in_scale = 1.0f;
+        pn.stop = &d->stop;
+        if ((rc = launch_norm(pn, nr, s))) return rc;
+        ProjArgs gu{};
+        gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
+        gu.xq = x->xq; gu.xst = H; gu.xs = x->xs;
+        gu.act_q = x->xq + (size_t)kMaxRows * H; gu.act_s = x->xs + (size_t)kMaxRows * H / 16; gu.act_stride = I;
+        gu.gscale = 1.0f; gu.stop = &d->stop;
+        if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
+        ProjArgs dn{};
+        dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f;
+        dn.xq = gu.act_q; dn.xst = I; dn.xs = gu.act_s;
+        dn.y = x->xres; dn.ystride = H; dn.out_bf16 = 0;
+        dn.res = x->hid; dn.res_bf16 = 1; dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
+        if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
+    }
+    // head (src/q27_main.cpp:2457-2481): final residual rows, final norm, lm_head, argmax
+    NormArgs hn{};
+    hn.x = x->xres; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->hid : nullptr;
+    hn.hout = hout ? hout : x->hfinal; hn.w = x->final_norm; hn.plus = 1.0f; hn.eps = c.rms_eps; hn.n = H;
+    hn.y = head ? x->ynorm : nullptr; hn.ystride = H; hn.in_scale = 1.0f; hn.stop = &d->stop;
+    if ((rc = launch_norm(hn, nr, s))) return rc;
+    if (head) {
+        GemvArgs ga{};
+        ga.W = x->lm_head; ga.rows = x->V; ga.K = H; ga.x = x->ynorm; ga.xst = H;
+        ga.pval = x->pval; ga.pidx = x->pidx; ga.pstride = x->pstride; ga.stop = &d->stop;
+        int nb = 0;
+        if ((rc = launch_gemv(ga, 1, nr, &nb, s))) return rc;
+        if ((rc = launch_argmax_final(x->pval, x->pidx, x->pstride, nb, nr, d->nx, d->nxval, &d->stop, s))) return rc;
+    }
+    return Q27X_OK;
+}
+
+// ---------------------------------------------------------------- the MTP pass
+// mtp_pass_nr (src/q27_main.cpp:2551-2618) over nr row slots (d->mtp_nact active): hidden rows
+// ctx->mtp_hin, tokens d->mtp_tok, draft positions d->mtp_dpos0.. on the layer's own KV cache.
+// kv_only stops after the K/V write (prompt conditioning, 2649-2692). head: mtp.norm + lm_head +
+// argmax of row d->mtp_head into d->mtp_out.
+static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
+    const q27x_config& c = x->c;
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    LayerDev& Y = x->mtp;
+    const int H = x->H, I = x->I;
+    const float po = c.mtp_plus_one ? 1.0f : 0.0f;
+    const int eoff = c.mtp_swap ? 0 : H, hoff = c.mtp_swap ? H : 0;   // src/q27_mtp_defs.h:108-109
+    int rc;
+    NormArgs ne{};
+    ne.emb = x->emb; ne.tok = d->mtp_tok; ne.w = x->pre_emb; ne.plus = po; ne.eps = c.rms_eps; ne.n = H;
+    ne.y = x->cat + eoff; ne.ystride = 2 * H; ne.in_scale = 1.0f; ne.stop = &d->stop;
+    if ((rc = launch_norm(ne, nr, s))) return rc;
+    NormArgs nh{};
+    nh.x = x->mtp_hin; nh.x_bf16 = 1; nh.xstride = H; nh.w = x->pre_hid; nh.plus = po; nh.eps = c.rms_eps; nh.n = H;
+    nh.y = x->cat + hoff; nh.ystride = 2 * H; nh.in_scale = 1.0f; nh.stop = &d->stop;
+    if ((rc = launch_norm(nh, nr, s))) return rc;
+    if ((rc = launch_quant_rows(x->cat, 2 * H, x->xq, 2 * H, x->xs, 2 * H / 16, 2 * H, 1.0f, nr, s))) return rc;
+    ProjArgs f{};
+    f.W = x->fc0.w; f.WS = x->fc0.s; f.rows = H; f.K = H; f.alpha = 1.0f;
+    f.xq = x->xq; f.xst = 2 * H; f.xs = x->xs; f.y = x->mtp_res; f.ystride = H; f.out_bf16 = 1; f.stop = &d->stop;
+    if ((rc = launch_proj(f, EPI_STORE, nr, s))) return rc;
+    f.W = x->fc1.w; f.WS = x->fc1.s; f.xq = x->xq + H; f.xs = x->xs + H / 16;
+    f.res = x->mtp_res; f.res_bf16 = 1; f.rstride = H; f.rs = 1.0f;
+    if ((rc = launch_proj(f, EPI_STORE, nr, s))) return rc;
+    NormArgs ni{};
+    ni.x = x->mtp_res; ni.x_bf16 = 1; ni.xstride = H; ni.w = Y.in_norm; ni.plus = po; ni.eps = c.rms_eps; ni.n = H;
+    ni.y = x->ynorm; ni.ystride = H; ni.xq = x->xq; ni.xs = x->xs; ni.quant_bf16 = 1; ni.in_scale = 1.0f;
+    ni.stop = &d->stop;
+    if ((rc = launch_norm(ni, nr, s))) return rc;
+    ProjArgs q{};
+    q.W = Y.qkv.w; q.WS = Y.qkv.s; q.rows = Y.qkv.rows; q.K = H; q.alpha = 1.0f; q.xq = x->xq; q.xst = H; q.xs = x->xs;
+    q.y = x->pb; q.ystride = Y.qkv.rows; q.out_bf16 = 1; q.stop = &d->stop;
+    if ((rc = launch_proj(q, EPI_STORE, nr, s))) return rc;
+    AttnArgs a{};
+    a.qkv = x->pb; a.qkv_stride = Y.qkv.rows; a.q_norm_w = Y.q_norm; a.k_norm_w = Y.k_norm;
+    a.rope_cos = x->rope_cos; a.rope_sin = x->rope_sin; a.rot = c.rot_dims;
+    a.kc = Y.kc; a.ks = Y.ks; a.vc = Y.vc; a.vs = Y.vs; a.kv_group = c.kv_group; a.qh = x->qh;
+    a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
+    a.pos0_ptr = &d->mtp_dpos0; a.nact_ptr = &d->mtp_nact; a.work = x->attn_work; a.max_splits = x->max_splits;
+    a.sl2e = x->sl2e; a.out = x->ao; a.xq = x->xq; a.xs = x->xs; a.stop = &d->stop;
+    if ((rc = launch_attn_prep(a, nr, s))) return rc;
+    if (kv_only) return Q27X_OK;
+    if ((rc = launch_attn(a, nr, s))) return rc;
+    ProjArgs o{};
+    o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.alpha = 1.0f; o.xq = x->xq; o.xst = x->att; o.xs = x->xs;
+    o.y = x->mtp_res; o.ystride = H; o.out_bf16 = 1; o.res = x->mtp_res; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f;
+    o.res_round = 1; o.stop = &d->stop;
+    if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
+    NormArgs pn{};
+    pn.x = x->mtp_res; pn.x_bf16 = 1; pn.xstride = H; pn.w = Y.post_norm; pn.plus = po; pn.eps = c.rms_eps; pn.n = H;
+    pn.xq = x->xq; pn.xs = x->xs; pn.quant_bf16 = 1; pn.in_scale = 1.0f; pn.stop = &d->stop;
+    pn.y = x->ynorm; pn.ystride = H;
+    if ((rc = launch_norm(pn, nr, s))) return rc;
+    ProjArgs gu{};
+    gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f; gu.xq = x->xq; gu.xst = H; gu.xs = x->xs;
+    gu.act_q = x->xq + (size_t)kMaxRows * 2 * H; gu.act_s = x->xs + (size_t)kMaxRows * 2 * H / 16; gu.act_stride = I;
+    gu.gscale = 1.0f; gu.stop = &d->stop;
+    if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
+    ProjArgs dn{};
+    dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f; dn.xq = gu.act_q; dn.xst = I;
+    dn.xs = gu.act_s; dn.y = x->mtp_res; dn.ystride = H; dn.out_bf16 = 1; dn.res = x->mtp_res; dn.res_bf16 = 1;
+    dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
+    if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
+    if (head) {
+        NormArgs hn{};
+        hn.x = x->mtp_res; hn.x_bf16 = 1; hn.xstride = H; hn.w = x->mtp_norm; hn.plus = 1.0f; hn.eps = c.rms_eps;
+        hn.n = H; hn.y = x->ynorm; hn.ystride = H; hn.in_scale = 1.0f; hn.row_sel = &d->mtp_head; hn.stop = &d->stop;
+        if ((rc = launch_norm(hn, 1, s))) return rc;
+        GemvArgs ga{};
+        ga.W = x->lm_head; ga.rows = x->V; ga.K = H; ga.x = x->ynorm; ga.xst = H;
+        ga.pval = x->pval; ga.pidx = x->pidx; ga.pstride = x->pstride; ga.stop = &d->stop;
+        int nb = 0;
+        if ((rc = launch_gemv(ga, 1, 1, &nb, s))) return rc;
+        if ((rc = launch_argmax_final(x->pval, x->pidx, x->pstride, nb, 1, &d->mtp_out, nullptr, &d->stop, s))) return rc;
+    }
+    return Q27X_OK;
+}
+
+static int set_ints(q27x_ctx* x, int n, int o0, int v0, int o1 = 0, int v1 = 0, int o2 = 0, int v2 = 0, int o3 = 0,
+                    int v3 = 0) {
+    hipLaunchKernelGGL(k_set_ints, dim3(1), dim3(64), 0, x->stream, (int*)x->dctl, n, o0, v0, o1, v1, o2, v2, o3, v3);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+#define DOFF(f) ((int)(offsetof(Dctl, f) / sizeof(int)))
+
+// one speculative round as a fixed kernel sequence (captured into a graph)
+static int enqueue_spec_round(q27x_ctx* x) {
+    const int K = x->c.spec_k, H = x->H;
+    Dctl* d = x->dctl;
+    int rc;
+    hipLaunchKernelGGL(k_round_begin, dim3(1), dim3(256), 0, x->stream, d, x->mtp_hin, x->hcatch, x->hprev, H, K);
+    Q27X_HIP(hipGetLastError());
+    for (int j = 0; j < K; ++j) {
+        if ((rc = mtp_pass(x, j == 0 ? K + 1 : 1, 1, 0))) return rc;
+        hipLaunchKernelGGL(k_draft_post, dim3(1), dim3(256), 0, x->stream, d, x->mtp_hin, x->mtp_res, x->forced, H, j, K);
+        Q27X_HIP(hipGetLastError());
+    }
+    if ((rc = verify_pass(x, K + 1, 1, nullptr))) return rc;
+    hipLaunchKernelGGL(k_accept, dim3(1), dim3(256), 0, x->stream, d, x->hfinal, x->hcatch, x->hprev, x->out_ring,
+                       x->ring_cap, x->mbox_dev, H, K);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+static int enqueue_plain_step(q27x_ctx* x) {
+    hipLaunchKernelGGL(k_plain_pre, dim3(1), dim3(64), 0, x->stream, x->dctl);
+    Q27X_HIP(hipGetLastError());
+    int rc = verify_pass(x, 1, 1, nullptr);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_plain_post, dim3(1), dim3(256), 0, x->stream, x->dctl, x->hfinal, x->hprev, x->out_ring,
+                       x->ring_cap, x->mbox_dev, x->H);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+static int build_graph(q27x_ctx* x, int spec, hipGraphExec_t* out) {
+    hipGraph_t g = nullptr;
+    Q27X_HIP(hipStreamBeginCapture(x->stream, hipStreamCaptureModeThreadLocal));
+    int rc = spec ? enqueue_spec_round(x) : enqueue_plain_step(x);
+    hipError_t e = hipStreamEndCapture(x->stream, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    return Q27X_OK;
+}
+static int use_graphs() {
+    const char* v = getenv("Q27X_GRAPH");
+    return !(v && v[0] == '0');
+}
+static int check_device_err(q27x_ctx* x) {
+    int err = 0;
+    Q27X_HIP(hipMemcpy(&err, &x->dctl->err, 4, hipMemcpyDeviceToHost));
+    if (err == 6) { set_error("context capacity exhausted (ctx=%d)", x->c.ctx); return Q27X_E_RANGE; }
+    if (err) { set_error("device error flag %d", err); return Q27X_E_DEVICE; }
+    return Q27X_OK;
+}
+
+}  // namespace q27x
+
+// ================================================================ C ABI: engine tier
+extern "C" {
+
+int q27x_config_default(q27x_config* c) {
+    if (!c) return Q27X_E_ARG;
+    memset(c, 0, sizeof *c);
+    c->hidden = 5120; c->inter = 17408; c->vocab = 62080; c->n_layers = 64; c->attn_period = 4;
+    c->gdn_kh = 16; c->gdn_vh = 48; c->gdn_d = 128;
+    c->n_q = 32; c->n_kv = 8; c->head_dim = 128; c->attn_gate = 1; c->rot_dims = 32; c->rope_theta = 1e7;
+    c->kv_group = 32; c->rms_eps = 1e-6f; c->head_double_residual = 1; c->mtp_swap = 1; c->mtp_plus_one = 1;
+    c->spec = 1; c->spec_k = 2; c->ctx = 2048;
+    return Q27X_OK;
+}
+int q27x_config_tiny(q27x_config* c) {
+    if (!c) return Q27X_E_ARG;
+    q27x_config_default(c);
+    c->hidden = 1024; c->inter = 2048; c->vocab = 4096; c->n_layers = 8;
+    c->gdn_kh = 2; c->gdn_vh = 6; c->n_q = 4; c->n_kv = 1; c->ctx = 512;
+    return Q27X_OK;
+}
+
+// fail-closed parsing (include/q27.h:189-206)
+static int env_flag(const char* name, int def) {
+    const char* v = getenv(name);
+    if (!v || !*v) return def;
+    if (!strcmp(v, "0") || !strcmp(v, "false") || !strcmp(v, "no") || !strcmp(v, "off")) return 0;
+    if (!strcmp(v, "1") || !strcmp(v, "true") || !strcmp(v, "yes") || !strcmp(v, "on")) return 1;
+    fprintf(stderr, "FATAL %s=\"%s\" is not a boolean (use 0/1, false/true, no/yes, off/on). "
+                    "Refusing to guess which arm you meant.\n", name, v);
+    abort();
+}
+static int env_int(const char* name, int def) {
+    const char* v = getenv(name);
+    if (!v || !*v) return def;
+    char* end = nullptr;
+    const long x = strtol(v, &end, 10);
+    if (end == v || *end) { fprintf(stderr, "FATAL %s=\"%s\" is not an integer.\n", name, v); abort(); }
+    return (int)x;
+}
+// src/q27_main.cpp:3360-3361: Q27_SPEC default on; Q27_SPEC_K default 1, clamped to [1, 7]
+int q27x_spec_config_from_env(q27x_config* c) {
+    if (!c) return Q27X_E_ARG;
+    c->spec = env_flag("Q27_SPEC", 1);
+    int k = env_int("Q27_SPEC_K", 1);
+    if (k < 1) k = 1;
+    if (k > 7) k = 7;
+    c->spec_k = k;
+    c->mtp_swap = env_flag("Q27_MTP_SWAP", c->mtp_swap);
+    c->mtp_plus_one = env_int("Q27_MTP_PO", c->mtp_plus_one);
+    return Q27X_OK;
+}
+
+int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
+    if (!cfg || !out) { set_error("q27x_ctx_create: null argument"); return Q27X_E_ARG; }
+    *out = nullptr;
+    const q27x_config& c = *cfg;
+    if (c.hidden % 1024 || c.hidden > 8192 || c.inter % 1024 || c.gdn_d != 128 || c.head_dim != 128 ||
+        c.n_layers < 1 || c.attn_period < 1 || c.spec_k < 1 || c.spec_k > 7 || c.ctx < 16 || c.vocab < 16 ||
+        c.gdn_vh % c.gdn_kh || c.n_q % c.n_kv || (c.n_q / c.n_kv) * 8 > 64 || c.kv_group < 16) {
+        set_error("q27x_ctx_create: unsupported geometry");
+        return Q27X_E_SHAPE;
+    }
+    q27x_ctx* x = new q27x_ctx();
+    x->device = device; x->c = c;
+    x->H = c.hidden; x->I = c.inter; x->V = c.vocab; x->D = c.gdn_d;
+    x->nqkv = (2 * c.gdn_kh + c.gdn_vh) * c.gdn_d; x->nz = c.gdn_vh * c.gdn_d;
+    x->qr = c.n_q * (c.attn_gate ? 2 * c.head_dim : c.head_dim); x->kvr = c.n_kv * c.head_dim;
+    x->att = c.n_q * c.head_dim;
+    x->sl2e = (float)((1.0 / sqrt((double)c.head_dim)) * 1.4426950408889634);
+    auto fail = [&](int rc) { q27x_ctx_destroy(x); return rc; };
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(hip_fail(e, "hipSetDevice"));
+    if ((e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking)) != hipSuccess) return fail(hip_fail(e, "hipStreamCreate"));
+    // weight arena
+    const size_t H = x->H, I = x->I, V = x->V;
+    auto i8b = [](size_t r, size_t k) { return r * k + r * (k / 64) * 4 + 512; };
+    size_t wb = 0;
+    int n_attn = 0;
+    for (int l = 0; l < c.n_layers; ++l) {
+        wb += 2 * H * 2 + 512 + i8b(2 * I, H) + i8b(H, I);
+        if (is_attn_layer(c, l)) { wb += i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 2 * 128 * 2 + 512; ++n_attn; }
+        else wb += i8b(x->nqkv + x->nz, H) + 2 * (size_t)c.gdn_vh * H * 2 + (size_t)x->nqkv * 4 * 2 + i8b(H, x->nz) + 4096;
+    }
+    wb += 2 * H * 2 + i8b(2 * I, H) + i8b(H, I) + i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 1024;   // MTP
+    wb += 3 * H * 2 + 2 * i8b(H, H) + 2 * V * H * 2 + H * 2 + 8192;
+    x->wcap = wb;
+    if ((e = hipMalloc((void**)&x->warena, wb)) != hipSuccess) return fail(hip_fail(e, "hipMalloc(weights)"));
+    // state + scratch arena
+    const size_t kvn = (size_t)c.ctx * x->kvr;
+    const size_t n_gdn = (size_t)(c.n_layers - n_attn);
+    x->max_splits = (c.ctx + kSplit - 1) / kSplit;
+    size_t sb = (n_attn + 1) * (2 * kvn + 2 * kvn / c.kv_group * 4 + 1024);
+    sb += n_gdn * ((size_t)c.gdn_vh * 128 * 128 * 4 + (size_t)x->nqkv * 3 * 2 + gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128) + 1024);
+    const size_t R = kMaxRows;
+    const size_t xqn = R * (2 * H + I + (size_t)x->nz + 2 * H);
+    sb += sizeof(Dctl) + R * H * 2 * 4 + R * H * 4 + xqn + xqn / 16 * 4 + R * (size_t)x->nqkv * 2 + R * (size_t)x->nz * 2 * 2;
+    sb += R * (size_t)(x->qr + 2 * x->kvr) * 2 + 2 * R * (size_t)x->att * 2 + R * 2 * H * 2 + R * H * 2 * 3 + H * 2;
+    sb += attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4 + R * (size_t)x->pstride * 8;
+    x->ring_cap = c.ctx + 64; x->forced_cap = c.ctx + 64; x->prompt_cap = c.ctx + 64;
+    sb += (size_t)(x->ring_cap + x->forced_cap + x->prompt_cap) * 4 + (size_t)c.ctx * H * 2;
+    sb += (size_t)c.ctx * (c.rot_dims / 2) * 4 * 2 + 64 * 256;
+    x->scap = sb;
+    if ((e = hipMalloc((void**)&x->sarena, sb)) != hipSuccess) return fail(hip_fail(e, "hipMalloc(state)"));
+    if ((e = hipMemset(x->sarena, 0, sb)) != hipSuccess) return fail(hip_fail(e, "hipMemset(state)"));
+    x->L.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        LayerDev& Y = x->L[l];
+        Y.is_attn = is_attn_layer(c, l);
+        if (Y.is_attn) {
+            Y.kc = (int8_t*)salloc(x, kvn); Y.vc = (int8_t*)salloc(x, kvn);
+            Y.ks = (float*)salloc(x, kvn / c.kv_group * 4); Y.vs = (float*)salloc(x, kvn / c.kv_group * 4);
+        } else {
+            Y.S = (float*)salloc(x, (size_t)c.gdn_vh * 128 * 128 * 4);
+            Y.conv_hist = (uint16_t*)salloc(x, (size_t)x->nqkv * 3 * 2);
+            Y.pend = salloc(x, gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128));
+        }
+    }
+    x->mtp.is_attn = 1;
+    x->mtp.kc = (int8_t*)salloc(x, kvn); x->mtp.vc = (int8_t*)salloc(x, kvn);
+    x->mtp.ks = (float*)salloc(x, kvn / c.kv_group * 4); x->mtp.vs = (float*)salloc(x, kvn / c.kv_group * 4);
+    x->dctl = (Dctl*)salloc(x, sizeof(Dctl));
+    x->hid = (uint16_t*)salloc(x, R * H * 2);
+    x->ynorm = (uint16_t*)salloc(x, R * H * 2);
+    x->hfinal = (uint16_t*)salloc(x, R * H * 2);
+    x->xres = (float*)salloc(x, R * H * 4);
+    x->xq = (int8_t*)salloc(x, xqn);
+    x->xs = (float*)salloc(x, xqn / 16 * 4);
+    x->conv_out = (uint16_t*)salloc(x, R * (size_t)x->nqkv * 2);
+    x->zbuf = (uint16_t*)salloc(x, R * (size_t)x->nz * 2);
+    x->gout = (uint16_t*)salloc(x, R * (size_t)x->nz * 2);
+    x->pb = (uint16_t*)salloc(x, R * (size_t)(x->qr + 2 * x->kvr) * 2);
+    x->qh = (uint16_t*)salloc(x, R * (size_t)x->att * 2);
+    x->ao = (uint16_t*)salloc(x, R * (size_t)x->att * 2);
+    x->cat = (uint16_t*)salloc(x, R * 2 * H * 2);
+    x->mtp_hin = (uint16_t*)salloc(x, R * H * 2);
+    x->mtp_res = (uint16_t*)salloc(x, R * H * 2);
+    x->hcatch = (uint16_t*)salloc(x, R * H * 2);
+    x->hprev = (uint16_t*)salloc(x, H * 2);
+    x->attn_work = (float*)salloc(x, attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4);
+    x->pval = (float*)salloc(x, R * (size_t)x->pstride * 4);
+    x->pidx = (uint32_t*)salloc(x, R * (size_t)x->pstride * 4);
+    x->out_ring = (int32_t*)salloc(x, (size_t)x->ring_cap * 4);
+    x->forced = (int32_t*)salloc(x, (size_t)x->forced_cap * 4);
+    x->prompt_dev = (int32_t*)salloc(x, (size_t)x->prompt_cap * 4);
+    x->hall = (uint16_t*)salloc(x, (size_t)c.ctx * H * 2);
+    x->rope_cos = (float*)salloc(x, (size_t)c.ctx * (c.rot_dims / 2) * 4);
+    x->rope_sin = (float*)salloc(x, (size_t)c.ctx * (c.rot_dims / 2) * 4);
+    if (x->s_fail || !x->rope_sin) { set_error("q27x_ctx_create: state arena sizing"); return fail(Q27X_E_NOMEM); }
+    // RoPE tables (src/q27_attn.hip:239-247): double inv_freq and angle, rounded to float
+    {
+        const int half = c.rot_dims / 2;
+        std::vector<float> cs((size_t)c.ctx * half), sn((size_t)c.ctx * half);
+        const double l2t = log2(c.rope_theta);
+        for (int p = 0; p < c.ctx; ++p)
+            for (int f = 0; f < half; ++f) {
+                const double ifq = exp2(-((double)(2 * f) / (double)c.rot_dims) * l2t);
+                const double ang = (double)p * ifq;
+                cs[(size_t)p * half + f] = (float)cos(ang);
+                sn[(size_t)p * half + f] = (float)sin(ang);
+            }
+        if ((e = hipMemcpy(x->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) return fail(hip_fail(e, "rope"));
+        if ((e = hipMemcpy(x->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) return fail(hip_fail(e, "rope"));
+    }
+    if ((e = hipHostMalloc((void**)&x->mbox, sizeof(Mailbox), hipHostMallocMapped)) != hipSuccess) return fail(hip_fail(e, "hipHostMalloc"));
+    memset((void*)x->mbox, 0, sizeof(Mailbox));
+    if ((e = hipHostGetDevicePointer((void**)&x->mbox_dev, (void*)x->mbox, 0)) != hipSuccess) return fail(hip_fail(e, "hipHostGetDevicePointer"));
+    *out = x;
+    return Q27X_OK;
+}
+
+int q27x_ctx_destroy(q27x_ctx* x) {
+    if (!x) return Q27X_OK;
+    (void)hipSetDevice(x->device);
+    if (x->stream) (void)hipStreamSynchronize(x->stream);
+    if (x->g_spec) (void)hipGraphExecDestroy(x->g_spec);
+    if (x->g_plain) (void)hipGraphExecDestroy(x->g_plain);
+    if (x->mbox) (void)hipHostFree((void*)x->mbox);
+    if (x->warena) (void)hipFree(x->warena);
+    if (x->sarena) (void)hipFree(x->sarena);
+    if (x->stream) (void)hipStreamDestroy(x->stream);
+    delete x;
+    return Q27X_OK;
+}
+
+static int gen_i8m(q27x_ctx* x, Mat& m, int rows, int K) {
+    m.rows = rows; m.K = K;
+    m.w = (int8_t*)walloc(x, (size_t)rows * K);
+    m.s = (float*)walloc(x, (size_t)rows * (K / 64) * 4);
+    if (!m.s) { set_error("weight arena sizing"); return Q27X_E_NOMEM; }
+    x->weight_bytes += (size_t)rows * K + (size_t)rows * (K / 64) * 4;
+    return Q27X_OK;
+}
+static uint16_t* gen_vec(q27x_ctx* x, uint64_t seed, uint64_t t, size_t n, float stdv, float mean, int uni) {
+    uint16_t* p = (uint16_t*)walloc(x, n * 2);
+    if (!p) return nullptr;
+    x->weight_bytes += n * 2;
+    if (launch_gen_bf16(p, n, tensor_key(seed, t), stdv, mean, uni, x->stream)) return nullptr;
+    return p;
+}
+
+int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
+    if (!x) return Q27X_E_ARG;
+    const q27x_config& c = x->c;
+    const int H = x->H, I = x->I;
+    hipStream_t s = x->stream;
+    x->woff = 0; x->weight_bytes = 0;
+    int rc;
+#define GEN(m, rows, K) if ((rc = gen_i8m(x, m, rows, K))) return rc
+#define VEC(dst, t, n, sd, mn, uni) if (!((dst) = gen_vec(x, seed, t, n, sd, mn, uni))) { set_error("weight generation"); return Q27X_E_NOMEM; }
+    auto mlp = [&](LayerDev& Y, int code) -> int {
+        int r2;
+        VEC(Y.in_norm, tid(code, T_IN_NORM), H, 0.02f, 0.0f, 0);
+        VEC(Y.post_norm, tid(code, T_POST_NORM), H, 0.02f, 0.0f, 0);
+        if ((r2 = gen_i8m(x, Y.gu, 2 * I, H))) return r2;
+        if ((r2 = launch_gen_i8(Y.gu.w, Y.gu.s, I, H, tensor_key(seed, tid(code, T_GATE)), 1, 0, s))) return r2;
+        if ((r2 = launch_gen_i8(Y.gu.w, Y.gu.s, I, H, tensor_key(seed, tid(code, T_UP)), 1, 1, s))) return r2;
+        if ((r2 = gen_i8m(x, Y.down, H, I))) return r2;
+        if ((r2 = launch_gen_i8(Y.down.w, Y.down.s, H, I, tensor_key(seed, tid(code, T_DOWN)), 0, 0, s))) return r2;
+        return Q27X_OK;
+    };
+    auto attn = [&](LayerDev& Y, int code) -> int {
+        int r2;
+        if ((r2 = gen_i8m(x, Y.qkv, x->qr + 2 * x->kvr, H))) return r2;
+        if ((r2 = launch_gen_i8(Y.qkv.w, Y.qkv.s, x->qr, H, tensor_key(seed, tid(code, T_Q)), 0, 0, s))) return r2;
+        if ((r2 = launch_gen_i8(Y.qkv.w + (size_t)x->qr * H, Y.qkv.s + (size_t)x->qr * (H / 64), x->kvr, H,
+                                tensor_key(seed, tid(code, T_K)), 0, 0, s))) return r2;
+        if ((r2 = launch_gen_i8(Y.qkv.w + (size_t)(x->qr + x->kvr) * H, Y.qkv.s + (size_t)(x->qr + x->kvr) * (H / 64),
+                                x->kvr, H, tensor_key(seed, tid(code, T_V)), 0, 0, s))) return r2;
+        VEC(Y.q_norm, tid(code, T_Q_NORM), 128, 0.02f, 0.0f, 0);
+        VEC(Y.k_norm, tid(code, T_K_NORM), 128, 0.02f, 0.0f, 0);
+        if ((r2 = gen_i8m(x, Y.o, H, x->att))) return r2;
+        if ((r2 = launch_gen_i8(Y.o.w, Y.o.s, H, x->att, tensor_key(seed, tid(code, T_O)), 0, 0, s))) return r2;
+        return Q27X_OK;
+    };
+    for (int l = 0; l < c.n_layers; ++l) {
+        LayerDev& Y = x->L[l];
+        const int code = l + 1;
+        if ((rc = mlp(Y, code))) return rc;
+        if (Y.is_attn) { if ((rc = attn(Y, code))) return rc; continue; }
+        GEN(Y.qkvz, x->nqkv + x->nz, H);
+        if ((rc = launch_gen_i8(Y.qkvz.w, Y.qkvz.s, x->nqkv, H, tensor_key(seed, tid(code, T_IN_QKV)), 0, 0, s))) return rc;
+        if ((rc = launch_gen_i8(Y.qkvz.w + (size_t)x->nqkv * H, Y.qkvz.s + (size_t)x->nqkv * (H / 64), x->nz, H,
+                                tensor_key(seed, tid(code, T_IN_Z)), 0, 0, s))) return rc;
+        VEC(Y.in_a, tid(code, T_IN_A), (size_t)c.gdn_vh * H, 0.02f, 0.0f, 0);
+        VEC(Y.in_b, tid(code, T_IN_B), (size_t)c.gdn_vh * H, 0.02f, 0.0f, 0);
+        VEC(Y.A_log, tid(code, T_A_LOG), c.gdn_vh, 2.7f, 0.0f, 1);
+        VEC(Y.dt_bias, tid(code, T_DT_BIAS), c.gdn_vh, 0.1f, 0.0f, 0);
+        VEC(Y.gdn_norm, tid(code, T_GDN_NORM), 128, 0.02f, 1.0f, 0);
+        VEC(Y.conv_w, tid(code, T_CONV_W), (size_t)x->nqkv * 4, 0.3f, 0.0f, 0);
+        GEN(Y.out_proj, H, x->nz);
+        if ((rc = launch_gen_i8(Y.out_proj.w, Y.out_proj.s, H, x->nz, tensor_key(seed, tid(code, T_OUT_PROJ)), 0, 0, s))) return rc;
+    }
+    if ((rc = mlp(x->mtp, 1000))) return rc;
+    if ((rc = attn(x->mtp, 1000))) return rc;
+    VEC(x->pre_emb, tid(1000, T_PRE_EMB), H, 0.02f, 0.0f, 0);
+    VEC(x->pre_hid, tid(1000, T_PRE_HID), H, 0.02f, 0.0f, 0);
+    VEC(x->mtp_norm, tid(1000, T_MTP_NORM), H, 0.02f, 0.0f, 0);
+    GEN(x->fc0, H, H);
+    if ((rc = launch_gen_i8(x->fc0.w, x->fc0.s, H, H, tensor_key(seed, tid(1000, T_FC0)), 0, 0, s))) return rc;
+    GEN(x->fc1, H, H);
+    if ((rc = launch_gen_i8(x->fc1.w, x->fc1.s, H, H, tensor_key(seed, tid(1000, T_FC1)), 0, 0, s))) return rc;
+    VEC(x->emb, tid(0, T_EMB), (size_t)x->V * H, 1.0f, 0.0f, 0);
+    VEC(x->final_norm, tid(0, T_FINAL_NORM), H, 0.02f, 0.0f, 0);
+    VEC(x->lm_head, tid(0, T_LM_HEAD), (size_t)x->V * H, 0.02f, 0.0f, 0);
+#undef GEN
+#undef VEC
+    Q27X_HIP(hipStreamSynchronize(s));
+    x->loaded = 1;
+    return q27x_reset(x);
+}
+
+int q27x_weight_bytes(q27x_ctx* x, size_t* bytes) {
+    if (!x || !bytes) return Q27X_E_ARG;
+    *bytes = x->weight_bytes;
+    return Q27X_OK;
+}
+
+int q27x_reset(q27x_ctx* x) {
+    if (!x) return Q27X_E_ARG;
+    const q27x_config& c = x->c;
+    const size_t kvn = (size_t)c.ctx * x->kvr;
+    hipStream_t s = x->stream;
+    for (auto* Y : { (LayerDev*)nullptr }) (void)Y;
+    for (int l = 0; l < c.n_layers; ++l) {
+        LayerDev& Y = x->L[l];
+        if (Y.is_attn) {
+            Q27X_HIP(hipMemsetAsync(Y.kc, 0, kvn, s)); Q27X_HIP(hipMemsetAsync(Y.vc, 0, kvn, s));
+            Q27X_HIP(hipMemsetAsync(Y.ks, 0, kvn / c.kv_group * 4, s)); Q27X_HIP(hipMemsetAsync(Y.vs, 0, kvn / c.kv_group * 4, s));
+        } else {
+            Q27X_HIP(hipMemsetAsync(Y.S, 0, (size_t)c.gdn_vh * 128 * 128 * 4, s));
+            Q27X_HIP(hipMemsetAsync(Y.conv_hist, 0, (size_t)x->nqkv * 3 * 2, s));
+            Q27X_HIP(hipMemsetAsync(Y.pend, 0, gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128), s));
+        }
+    }
+    Q27X_HIP(hipMemsetAsync(x->mtp.kc, 0, kvn, s)); Q27X_HIP(hipMemsetAsync(x->mtp.vc, 0, kvn, s));
+    Q27X_HIP(hipMemsetAsync(x->mtp.ks, 0, kvn / c.kv_group * 4, s)); Q27X_HIP(hipMemsetAsync(x->mtp.vs, 0, kvn / c.kv_group * 4, s));
+    Dctl h{};
+    h.ctx = c.ctx;
+    h.max_new = 0x7fffffff;
+    Q27X_HIP(hipMemcpyAsync(x->dctl, &h, sizeof h, hipMemcpyHostToDevice, s));
+    Q27X_HIP(hipStreamSynchronize(s));
+    memset((void*)x->mbox, 0, sizeof(Mailbox));
+    x->prefilled = 0;
+    return Q27X_OK;
+}
+
+// Prompt ingest through the verify path in chunks of 8 rows, then the MTP prompt conditioning.
+int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
+    if (!x || !ids || n < 1) { set_error("q27x_prefill: bad arguments"); return Q27X_E_ARG; }
+    if (!x->loaded) { set_error("q27x_prefill: no weights"); return Q27X_E_STATE; }
+    if (n + x->c.spec_k + 2 > x->c.ctx || n > x->prompt_cap) { set_error("q27x_prefill: prompt of %d exceeds ctx %d", n, x->c.ctx); return Q27X_E_RANGE; }
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= x->V) { set_error("q27x_prefill: token %d out of range", ids[i]); return Q27X_E_RANGE; }
+    int rc = q27x_reset(x);
+    if (rc) return rc;
+    const auto t0 = std::chrono::steady_clock::now();
+    hipStream_t s = x->stream;
+    const int H = x->H;
+    Q27X_HIP(hipMemcpyAsync(x->prompt_dev, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    int npend = 0;
+    for (int c0 = 0; c0 < n; c0 += kMaxRows) {
+        const int cn = (n - c0 < kMaxRows) ? n - c0 : kMaxRows;
+        const int last = (c0 + cn == n);
+        Q27X_HIP(hipMemcpyAsync(x->dctl->vtok, x->prompt_dev + c0, (size_t)cn * 4, hipMemcpyDeviceToDevice, s));
+        if ((rc = set_ints(x, 2, DOFF(pos), c0, DOFF(gdn_npend), npend))) return rc;
+        if ((rc = verify_pass(x, cn, last, x->hall + (size_t)c0 * H))) return rc;
+        npend = cn;
+    }
+    int32_t first = 0;
+    Q27X_HIP(hipMemcpyAsync(&first, &x->dctl->nx[(n - 1) % kMaxRows], 4, hipMemcpyDeviceToHost, s));
+    // prompt conditioning: MTP position p pairs the final residual at p with token p+1
+    for (int p0 = 0; p0 + 1 < n; p0 += kMaxRows) {
+        const int cn = (n - 1 - p0 < kMaxRows) ? n - 1 - p0 : kMaxRows;
+        Q27X_HIP(hipMemcpyAsync(x->dctl->mtp_tok, x->prompt_dev + p0 + 1, (size_t)cn * 4, hipMemcpyDeviceToDevice, s));
+        Q27X_HIP(hipMemcpyAsync(x->mtp_hin, x->hall + (size_t)p0 * H, (size_t)cn * H * 2, hipMemcpyDeviceToDevice, s));
+        if ((rc = set_ints(x, 2, DOFF(mtp_nact), cn, DOFF(mtp_dpos0), p0))) return rc;
+        if ((rc = mtp_pass(x, cn, 0, 1))) return rc;
+    }
+    Q27X_HIP(hipMemcpyAsync(x->hprev, x->hall + (size_t)(n - 1) * H, (size_t)H * 2, hipMemcpyDeviceToDevice, s));
+    Q27X_HIP(hipStreamSynchronize(s));
+    if ((rc = set_ints(x, 4, DOFF(pos), n, DOFF(tok), first, DOFF(ncatch), 0, DOFF(gdn_npend), npend))) return rc;
+    if ((rc = set_ints(x, 4, DOFF(committed), 1, DOFF(rounds), 0, DOFF(stop), 0, DOFF(max_new), 0x7fffffff))) return rc;
+    Q27X_HIP(hipMemcpyAsync(x->out_ring, &first, 4, hipMemcpyHostToDevice, s));
+    Q27X_HIP(hipStreamSynchronize(s));
+    if ((rc = check_device_err(x))) return rc;
+    x->prefilled = 1;
+    x->n_prompt = n;
+    if (first_token) *first_token = first;
+    (void)t0;
+    return Q27X_OK;
+}
+
+static int run_step(q27x_ctx* x, int spec) {
+    if (use_graphs()) {
+        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
+        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
+        if (!*g) {
+            int rc = build_graph(x, spec, g);
+            if (rc) return rc;
+            if (spec) x->g_spec_k = x->c.spec_k;
+        }
+        Q27X_HIP(hipGraphLaunch(*g, x->stream));
+        return Q27X_OK;
+    }
+    return spec ? enqueue_spec_round(x) : enqueue_plain_step(x);
+}
+
+int q27x_decode_step(q27x_ctx* x, int32_t* out_token) {
+    if (!x || !x->prefilled) { set_error("q27x_decode_step: no prefill"); return Q27X_E_STATE; }
+    int rc = run_step(x, 0);
+    if (rc) return rc;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    if ((rc = check_device_err(x))) return rc;
+    int32_t t = 0;
+    Q27X_HIP(hipMemcpy(&t, &x->dctl->nx[0], 4, hipMemcpyDeviceToHost));
+    if (out_token) *out_token = t;
+    return Q27X_OK;
+}
+
+int q27x_spec_round(q27x_ctx* x, int32_t* out_tokens, int* ncommit) {
+    if (!x || !x->prefilled) { set_error("q27x_spec_round: no prefill"); return Q27X_E_STATE; }
+    int rc = run_step(x, 1);
+    if (rc) return rc;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    if ((rc = check_device_err(x))) return rc;
+    Dctl h;
+    Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
+    if (ncommit) *ncommit = h.ncommit_last;
+    if (out_tokens) for (int j = 0; j < h.ncommit_last; ++j) out_tokens[j] = h.nx[j];
+    return Q27X_OK;
+}
+
+int q27x_set_forced_drafts(q27x_ctx* x, const int32_t* toks, int n) {
+    if (!x || n < 0 || (n > 0 && !toks) || n > x->forced_cap) { set_error("q27x_set_forced_drafts: bad arguments"); return Q27X_E_ARG; }
+    for (int i = 0; i < n; ++i)
+        if (toks[i] < 0 || toks[i] >= x->V) { set_error("q27x_set_forced_drafts: token %d out of range", toks[i]); return Q27X_E_RANGE; }
+    if (n) Q27X_HIP(hipMemcpy(x->forced, toks, (size_t)n * 4, hipMemcpyHostToDevice));
+    const int base = x->n_prompt;
+    int rc = set_ints(x, 3, DOFF(forced_on), n > 0 ? 1 : 0, DOFF(forced_n), n, DOFF(forced_base), base);
+    if (rc) return rc;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    return Q27X_OK;
+}
+
+int q27x_generate(q27x_ctx* x, int max_new, int spec, int32_t* out, int* n_out, q27x_stats* st) {
+    if (!x || !x->prefilled || max_new < 1 || !out) { set_error("q27x_generate: bad arguments"); return Q27X_E_ARG; }
+    if (max_new > x->ring_cap) { set_error("q27x_generate: max_new exceeds capacity"); return Q27X_E_RANGE; }
+    int rc = set_ints(x, 1, DOFF(max_new), max_new);
+    if (rc) return rc;
+    Dctl h0;
+    Q27X_HIP(hipMemcpyAsync(&h0, x->dctl, sizeof h0, hipMemcpyDeviceToHost, x->stream));
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    if (h0.committed >= max_new) rc = set_ints(x, 1, DOFF(stop), 1);
+    if (rc) return rc;
+    // build the graph outside the timed loop
+    if (use_graphs()) {
+        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
+        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
+        if (!*g) { if ((rc = build_graph(x, spec, g))) return rc; if (spec) x->g_spec_k = x->c.spec_k; }
+    }
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    const auto t0 = std::chrono::steady_clock::now();
+    // two rounds in flight: a round is launched once the one before the previous has landed
+    std::vector<hipEvent_t> ev(2, nullptr);
+    for (auto& e : ev) Q27X_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    long long launched = 0;
+    const int max_rounds = x->c.ctx;
+    while (launched < max_rounds) {
+        if (launched >= 2) {
+            Q27X_HIP(hipEventSynchronize(ev[launched & 1]));
+            if (x->mbox->stop || x->mbox->committed >= max_new) break;
+        }
+        if ((rc = run_step(x, spec))) break;
+        Q27X_HIP(hipEventRecord(ev[launched & 1], x->stream));
+        ++launched;
+    }
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    const auto t1 = std::chrono::steady_clock::now();
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    if (rc) return rc;
+    if ((rc = check_device_err(x))) return rc;
+    Dctl h;
+    Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
+    const int n = h.committed < max_new ? h.committed : max_new;
+    Q27X_HIP(hipMemcpy(out, x->out_ring, (size_t)n * 4, hipMemcpyDeviceToHost));
+    if (n_out) *n_out = n;
+    if (st) {
+        memset(st, 0, sizeof *st);
+        st->rounds = h.rounds - h0.rounds;
+        st->committed = n - h0.committed;
+        st->accepted = h.accepted - h0.accepted;
+        for (int j = 0; j < 9; ++j) st->acc_hist[j] = h.acc_hist[j] - h0.acc_hist[j];
+        st->decode_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    }
+    return Q27X_OK;
+}
+
+// Exactly n rounds (spec) or plain steps back to back from the current state, one graph launch
+// each, no host synchronisation in between; stats over those rounds (wall clock around the launches
+// and the final synchronisation).
+int q27x_run_rounds(q27x_ctx* x, int n, int spec, q27x_stats* st) {
+    if (!x || !x->prefilled || n < 1) { set_error("q27x_run_rounds: bad arguments"); return Q27X_E_ARG; }
+    int rc = set_ints(x, 1, DOFF(max_new), 0x7fffffff);
+    if (rc) return rc;
+    if (use_graphs()) {
+        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
+        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
+        if (!*g) { if ((rc = build_graph(x, spec, g))) return rc; if (spec) x->g_spec_k = x->c.spec_k; }
+    }
+    Dctl h0;
+    Q27X_HIP(hipMemcpyAsync(&h0, x->dctl, sizeof h0, hipMemcpyDeviceToHost, x->stream));
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < n && !rc; ++i) rc = run_step(x, spec);
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    const auto t1 = std::chrono::steady_clock::now();
+    if (rc) return rc;
+    if ((rc = check_device_err(x))) return rc;
+    Dctl h;
+    Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
+    if (st) {
+        memset(st, 0, sizeof *st);
+        st->rounds = h.rounds - h0.rounds;
+        st->committed = h.committed - h0.committed;
+        st->accepted = h.accepted - h0.accepted;
+        for (int j = 0; j < 9; ++j) st->acc_hist[j] = h.acc_hist[j] - h0.acc_hist[j];
+        st->decode_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    }
+    return Q27X_OK;
+}
+
+int q27x_bench_verify(q27x_ctx* x, int nr, int iters, float* ms) {
+    if (!x || !x->loaded || nr < 1 || nr > kMaxRows || iters < 1 || !ms) return Q27X_E_ARG;
+    hipEvent_t a, b;
+    Q27X_HIP(hipEventCreate(&a));
+    Q27X_HIP(hipEventCreate(&b));
+    int rc = verify_pass(x, nr, 1, nullptr);
+    if (rc) return rc;
+    Q27X_HIP(hipEventRecord(a, x->stream));
+    for (int i = 0; i < iters && !rc; ++i) rc = verify_pass(x, nr, 1, nullptr);
+    Q27X_HIP(hipEventRecord(b, x->stream));
+    Q27X_HIP(hipEventSynchronize(b));
+    float t = 0.0f;
+    Q27X_HIP(hipEventElapsedTime(&t, a, b));
+    *ms = t / (float)iters;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return rc;
+}
+
+// Time one projection launch of the verify path (hipEvents on the engine's stream) and report its
+// algorithmic bytes (weights + scales + activations + outputs). which: 0 in_qkv|in_z (GDN epilogue),
+// 1 gate|up (SwiGLU epilogue), 2 down (+residual), 3 out_proj (+residual), 4 lm_head (bf16 +
+// argmax partials).
+int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, float* ms, double* bytes) {
+    if (!x || !x->loaded || nr < 1 || nr > kMaxRows || iters < 1 || !ms || !bytes) return Q27X_E_ARG;
+    const q27x_config& c = x->c;
+    if (layer < 0 || layer >= c.n_layers) return Q27X_E_ARG;
+    LayerDev& Y = x->L[layer];
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    const int H = x->H, I = x->I;
+    ProjArgs p{};
+    p.alpha = 1.0f; p.stop = &d->stop;
+    int epi = EPI_STORE;
+    GemvArgs ga{};
+    double b = 0;
+    if (which == 0) {
+        if (Y.is_attn) return Q27X_E_ARG;
+        p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+        p.nconv = x->nqkv; p.conv_out = x->conv_out; p.conv_stride = x->nqkv; p.z_out = x->zbuf; p.z_stride = x->nz;
+        p.conv_w = Y.conv_w; p.conv_hist = Y.conv_hist; p.npend_imm = 0;
+        p.pend_raw = (uint16_t*)((char*)Y.pend + gdn_pend_raw_offset(c.gdn_kh, c.gdn_vh, x->D));
+        epi = EPI_GDN_IN;
+        b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * p.rows * 2 +
+            (double)x->nqkv * (4 + 3 + nr) * 2;
+    } else if (which == 1) {
+        p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+        p.act_q = x->xq + (size_t)kMaxRows * H; p.act_s = x->xs + (size_t)kMaxRows * H / 16; p.act_stride = I;
+        p.gscale = 1.0f;
+        epi = EPI_SWIGLU;
+        b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * I * (1 + 4.0 / 16);
+    } else if (which == 2 || which == 3) {
+        const Mat& m = (which == 2) ? Y.down : Y.out_proj;
+        if (which == 3 && Y.is_attn) return Q27X_E_ARG;
+        p.W = m.w; p.WS = m.s; p.rows = H; p.K = m.K; p.xq = x->xq; p.xst = m.K; p.xs = x->xs;
+        p.y = x->xres; p.ystride = H; p.res = x->hid; p.res_bf16 = 1; p.rstride = H; p.rs = 1.0f;
+        b = (double)H * m.K * (1 + 4.0 / 64) + (double)nr * m.K * (1 + 4.0 / 16) + (double)nr * H * (2 + 4);
+    } else if (which == 4) {
+        ga.W = x->lm_head; ga.rows = x->V; ga.K = H; ga.x = x->ynorm; ga.xst = H;
+        ga.pval = x->pval; ga.pidx = x->pidx; ga.pstride = x->pstride; ga.stop = &d->stop;
+        b = (double)x->V * H * 2 + (double)nr * H * 2;
+    } else return Q27X_E_ARG;
+    hipEvent_t e0, e1;
+    Q27X_HIP(hipEventCreate(&e0));
+    Q27X_HIP(hipEventCreate(&e1));
+    int rc = Q27X_OK, nb = 0;
+    auto launch = [&]() { return which == 4 ? launch_gemv(ga, 1, nr, &nb, s) : launch_proj(p, epi, nr, s); };
+    for (int i = 0; i < 3 && !rc; ++i) rc = launch();
+    Q27X_HIP(hipEventRecord(e0, s));
+    for (int i = 0; i < iters && !rc; ++i) rc = launch();
+    Q27X_HIP(hipEventRecord(e1, s));
+    Q27X_HIP(hipEventSynchronize(e1));
+    float t = 0.0f;
+    Q27X_HIP(hipEventElapsedTime(&t, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *ms = t / (float)iters;
+    *bytes = b;
+    return rc;
+}
+
+int q27x_debug_read(q27x_ctx* x, const char* name, int layer, void* dst, size_t bytes) {
+    if (!x || !name || !dst) return Q27X_E_ARG;
+    const void* src = nullptr;
+    size_t n = 0;
+    const LayerDev* Y = (layer >= 0 && layer < x->c.n_layers) ? &x->L[layer] : &x->mtp;
+    const size_t kvn = (size_t)x->c.ctx * x->kvr;
+    if (!strcmp(name, "S") && Y->S) { src = Y->S; n = (size_t)x->c.gdn_vh * 128 * 128 * 4; }
+    else if (!strcmp(name, "conv_hist") && Y->conv_hist) { src = Y->conv_hist; n = (size_t)x->nqkv * 3 * 2; }
+    else if (!strcmp(name, "kc") && Y->kc) { src = Y->kc; n = kvn; }
+    else if (!strcmp(name, "hprev")) { src = x->hprev; n = (size_t)x->H * 2; }
+    else if (!strcmp(name, "hfinal")) { src = x->hfinal; n = (size_t)kMaxRows * x->H * 2; }
+    else if (!strcmp(name, "emb")) { src = x->emb; n = (size_t)x->V * x->H * 2; }
+    else if (!strcmp(name, "lm_head")) { src = x->lm_head; n = (size_t)x->V * x->H * 2; }
+    else if (!strcmp(name, "gu_w")) { src = Y->gu.w; n = (size_t)2 * x->I * x->H; }
+    else if (!strcmp(name, "gu_s")) { src = Y->gu.s; n = (size_t)2 * x->I * (x->H / 64) * 4; }
+    else if (!strcmp(name, "conv_w") && Y->conv_w) { src = Y->conv_w; n = (size_t)x->nqkv * 4 * 2; }
+    else if (!strcmp(name, "dctl")) { src = x->dctl; n = sizeof(Dctl); }
+    if (!src) { set_error("q27x_debug_read: unknown tensor %s", name); return Q27X_E_ARG; }
+    if (bytes < n) n = bytes;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    Q27X_HIP(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+    return Q27X_OK;
+}
+
+int q27x_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val, q27x_stream_t s) {
+    if (!logits || !idx || n < 1 || ld < n || nr < 1 || nr > kMaxRows) { set_error("q27x_argmax_rows: bad arguments"); return Q27X_E_ARG; }
+    float* pv = nullptr; uint32_t* pi = nullptr;
+    int rc = argmax_scratch(&pv, &pi);
+    if (rc) return rc;
+    return launch_argmax_rows(logits, n, ld, nr, idx, val, pv, pi, (hipStream_t)s);
+}
+
+int q27x_accept(const int32_t* nx, const int32_t* dt, int k, int32_t* nacc_ncommit, int32_t* committed, q27x_stream_t s) {
+    if (!nx || !dt || !nacc_ncommit || !committed || k < 0 || k > 7) { set_error("q27x_accept: bad arguments"); return Q27X_E_ARG; }
+    hipLaunchKernelGGL(k_accept_rows, dim3(1), dim3(64), 0, (hipStream_t)s, nx, dt, k, nacc_ncommit, committed);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+}  // extern "C"

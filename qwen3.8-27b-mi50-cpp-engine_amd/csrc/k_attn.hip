@@ -1,0 +1,279 @@
+// k_attn.hip -- full attention of NR verify rows over the int8 KV cache (R14, R15).
+//
+// prep (src/q27_attn.hip:177-253): one wave per (head, row): RMSNorm over the head (1+w), lane l
+//   holds dims l and l+64; rotate-half RoPE on the first `rot` dims from the host's cos/sin
+//   tables; q -> bf16; K (normed, roped) and V (raw) -> int8 with one fp32 scale per kv_group.
+// attention (src/q27_attn.hip:258-463 semantics): GQA, row r attends keys 0..pos0+r. Keys are cut
+//   into FIXED 64-key splits, so a row's result depends only on its own keys and never on how
+//   many rows share the launch (the verify row and the plain step agree bit for bit). A block
+//   owns (split, kv head) for all rows and all GQA heads: K/V tile dequantised into LDS once,
+//   scores by 16-lane dot products, two-pass softmax in base 2, p.V in key order; the combine
+//   merges splits in order, applies sigmoid(gate) and quantises for o_proj.
+#include "q27x_dev.h"
+#include "q27x_int.h"
+
+namespace q27x {
+
+constexpr int kHD = 128;
+constexpr int kMaxQ = kMaxRows * 8;   // rows x GQA heads per kv head held by one block
+
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    if (a.stop && *a.stop) return;
+    const int r = blockIdx.y;
+    if (a.nact_ptr && r >= *a.nact_ptr) return;
+    const int pos = (a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm) + r;
+    const int l = threadIdx.x;
+    const int u = blockIdx.x;
+    const bool isq = u < a.nq;
+    const int head = isq ? u : u - a.nq;
+    const int qw = a.gate ? 2 * kHD : kHD;
+    const int qrows = a.nq * qw, kvrows = a.nkv * kHD;
+    const uint16_t* row = a.qkv + (size_t)r * a.qkv_stride;
+    const uint16_t* src = isq ? row + (size_t)head * qw : row + qrows + (size_t)head * kHD;
+    const uint16_t* wgt = isq ? a.q_norm_w : a.k_norm_w;
+    const float x0 = bf2f(src[l]), x1 = bf2f(src[l + 64]);
+    const float w0 = tree64(x0 * x0), w1 = tree64(x1 * x1);
+    const float ss = __shfl(w0, 0, 64) + __shfl(w1, 0, 64);
+    const float inv = rsqrt_cr(ss * (1.0f / (float)kHD) + a.eps);
+    float y0 = x0 * inv * (1.0f + bf2f(wgt[l]));
+    float y1 = x1 * inv * (1.0f + bf2f(wgt[l + 64]));
+    const int half = a.rot >> 1;
+    const float* cs = a.rope_cos + (size_t)pos * half;
+    const float* sn = a.rope_sin + (size_t)pos * half;
+    if (a.rot <= 64) {
+        const float pv = __shfl_xor(y0, half, 64);
+        if (l < a.rot) {
+            const float rv = (l < half) ? -pv : pv;
+            const int f = l & (half - 1);
+            y0 = y0 * cs[f] + rv * sn[f];
+        }
+    } else {   // rot == 128: dims l and l+64 are partners
+        const float c = cs[l], s = sn[l];
+        const float n0 = y0 * c + (-y1) * s;
+        const float n1 = y1 * c + y0 * s;
+        y0 = n0; y1 = n1;
+    }
+    if (isq) {
+        uint16_t* dst = a.qh + (size_t)r * a.nq * kHD + (size_t)head * kHD;
+        dst[l] = f2bf(y0);
+        dst[l + 64] = f2bf(y1);
+        return;
+    }
+    const uint16_t* vsrc = row + qrows + kvrows + (size_t)head * kHD;
+    const float v0 = bf2f(vsrc[l]), v1 = bf2f(vsrc[l + 64]);
+    const size_t off = (size_t)pos * kvrows + (size_t)head * kHD;
+    const int G = a.kv_group;
+    const float vals[4] = { y0, y1, v0, v1 };
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float v = vals[q];
+        const float mx = max_xor(fabsf(v), G);
+        const float sc = mx * (1.0f / 127.0f);
+        const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        const int dd = l + ((q & 1) ? 64 : 0);
+        int8_t* c8 = (q < 2) ? a.kc : a.vc;
+        float* cs8 = (q < 2) ? a.ks : a.vs;
+        c8[off + dd] = qcode(v, qi);
+        if ((dd % G) == 0) cs8[(off + dd) / G] = sc;
+    }
+}
+
+size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
+    return (size_t)nr * nq * max_splits * (size_t)(hd + 2);
+}
+
+// work layout: o [nr][nq][ms][hd] | m [nr][nq][ms] | l [nr][nq][ms]
+__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
+    if (a.stop && *a.stop) return;
+    const int kvh = blockIdx.y;
+    const int G = a.nq / a.nkv;
+    const int nact = a.nact_ptr ? *a.nact_ptr : nr;
+    const int pos0 = a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm;
+    const int Lmax = pos0 + nact;
+    const int nqr = nact * G;                       // query vectors of this kv head
+    const int kvrows = a.nkv * kHD;
+    const int ms = a.max_splits;
+    __shared__ float qf[kMaxQ][kHD];
+    __shared__ float kd[kSplit][kHD + 4];
+    __shared__ float vd[kSplit][kHD];
+    __shared__ float sc[kMaxQ][kSplit];
+    const int t = threadIdx.x;
+    for (int i = t; i < nqr * kHD; i += 256) {
+        const int qi = i / kHD, dd = i - qi * kHD;
+        const int r = qi / G, g = qi - r * G;
+        qf[qi][dd] = bf2f(a.qh[(size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + dd]);
+    }
+    float* wo = a.work;
+    float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
+    float* wl = wm + (size_t)nr * a.nq * ms;
+    for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
+        const int k0 = s * kSplit;
+        const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
+        __syncthreads();   // previous split's tiles and the query stage are complete
+        for (int i = t; i < nk * kHD; i += 256) {
+            const int k = i / kHD, dd = i - k * kHD;
+            const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + dd;
+            kd[k][dd] = (float)a.kc[off] * a.ks[off / a.kv_group];
+            vd[k][dd] = (float)a.vc[off] * a.vs[off / a.kv_group];
+        }
+        __syncthreads();
+        // scores: 16 lanes per key, lane c holds dims 8c..8c+7 (fmaf chain), xor butterfly 8,4,2,1
+        {
+            const int c = t & 15, kl = t >> 4;
+            for (int kb = 0; kb < nk; kb += 16) {
+                const int k = kb + kl;
+                const int kk = k < nk ? k : nk - 1;
+                for (int qi = 0; qi < nqr; ++qi) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qf[qi][8 * c + e], kd[kk][8 * c + e], acc);
+                    acc = acc + __shfl_xor(acc, 8, 64);
+                    acc = acc + __shfl_xor(acc, 4, 64);
+                    acc = acc + __shfl_xor(acc, 2, 64);
+                    acc = acc + __shfl_xor(acc, 1, 64);
+                    if (c == 0 && k < nk) sc[qi][k] = acc * a.sl2e;
+                }
+            }
+        }
+        __syncthreads();
+        // per query: max over the split's valid keys, p = 2^(x - m) in place, l = sum in key order
+        if (t < nqr) {
+            const int qi = t, r = qi / G, g = qi - r * G;
+            const int L = pos0 + r + 1;
+            const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
+            if (nv > 0) {
+                float m = -__builtin_huge_valf();
+                for (int k = 0; k < nv; ++k) m = fmaxf(m, sc[qi][k]);
+                float l = 0.0f;
+                for (int k = 0; k < nv; ++k) { const float p = qexp2(sc[qi][k] - m); sc[qi][k] = p; l = l + p; }
+                const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
+                wm[mi] = m;
+                wl[mi] = l;
+            }
+        }
+        __syncthreads();
+        // o = sum_k p_k v_k in key order, one output per thread per pass
+        for (int i = t; i < nqr * kHD; i += 256) {
+            const int qi = i / kHD, dd = i - qi * kHD;
+            const int r = qi / G, g = qi - r * G;
+            const int L = pos0 + r + 1;
+            const int nv = (L - k0 < nk) ? (L - k0) : nk;
+            if (nv <= 0) continue;
+            float o = 0.0f;
+            for (int k = 0; k < nv; ++k) o = __builtin_fmaf(sc[qi][k], vd[k][dd], o);
+            wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + dd] = o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
+    if (a.stop && *a.stop) return;
+    const int hq = blockIdx.x, r = blockIdx.y;
+    if (a.nact_ptr && r >= *a.nact_ptr) return;
+    const int pos0 = a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm;
+    const int L = pos0 + r + 1;
+    const int ns = (L + kSplit - 1) / kSplit;
+    const int ms = a.max_splits;
+    const int t = threadIdx.x;
+    const float* wo = a.work;
+    const float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
+    const float* wl = wm + (size_t)nr * a.nq * ms;
+    const size_t base = ((size_t)r * a.nq + hq) * ms;
+    float M = -__builtin_huge_valf();
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, wm[base + s]);
+    float den = 0.0f, o = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+        const float w = qexp2(wm[base + s] - M);
+        den = __builtin_fmaf(wl[base + s], w, den);
+        o = __builtin_fmaf(wo[(base + s) * kHD + t], w, o);
+    }
+    const float inv = 1.0f / den;
+    float v = o * inv;
+    const int qw = a.gate ? 2 * kHD : kHD;
+    if (a.gate) v = v * qsigmoid(bf2f(a.qkv[(size_t)r * a.qkv_stride + (size_t)hq * qw + kHD + t]));
+    const uint16_t vb = f2bf(v);
+    const size_t k = (size_t)r * a.nq * kHD + (size_t)hq * kHD + t;
+    a.out[k] = vb;
+    if (a.xq) {
+        const float yv = bf2f(vb);
+        const float m16 = max_xor(fabsf(yv), 16);
+        const float sc = m16 * (1.0f / 127.0f);
+        const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        a.xq[k] = qcode(yv, qi);
+        if ((t & 15) == 0) a.xs[k >> 4] = sc;
+    }
+}
+
+static int attn_check(const AttnArgs& a, int nr) {
+    if (a.hd != kHD || a.nkv < 1 || a.nq % a.nkv || nr < 1 || nr > kMaxRows || nr * (a.nq / a.nkv) > kMaxQ ||
+        (a.kv_group != 16 && a.kv_group != 32 && a.kv_group != 64) || a.rot < 2 || a.rot > kHD || (a.rot & (a.rot - 1))) {
+        set_error("attn: unsupported shape (nq=%d nkv=%d hd=%d nr=%d kv_group=%d rot=%d)", a.nq, a.nkv, a.hd, nr,
+                  a.kv_group, a.rot);
+        return Q27X_E_SHAPE;
+    }
+    return Q27X_OK;
+}
+
+int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
+    if (int rc = attn_check(a, nr)) return rc;
+    if (a.rot == kHD || a.rot <= 64) {
+        hipLaunchKernelGGL(k_attn_prep, dim3(a.nq + a.nkv, nr), dim3(64), 0, s, a);
+        Q27X_HIP(hipGetLastError());
+        return Q27X_OK;
+    }
+    set_error("attn: rot=%d unsupported", a.rot);
+    return Q27X_E_SHAPE;
+}
+
+int launch_attn(const AttnArgs& a, int nr, hipStream_t s) {
+    if (int rc = attn_check(a, nr)) return rc;
+    if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
+    int gx = a.max_splits < 64 ? a.max_splits : 64;
+    hipLaunchKernelGGL(k_attn_split, dim3(gx, a.nkv), dim3(256), 0, s, a, nr);
+    Q27X_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr), dim3(kHD), 0, s, a, nr);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+}  // namespace q27x
+
+using namespace q27x;
+extern "C" size_t q27x_attn_work_bytes(int nq, int hd, int ctx, int nr) {
+    return attn_work_floats(nq, hd, (ctx + kSplit - 1) / kSplit, nr) * 4;
+}
+
+extern "C" int q27x_attn_prep_rows(const uint16_t* qkv, int qkv_stride, const uint16_t* q_norm_w,
+                                   const uint16_t* k_norm_w, const float* rope_cos, const float* rope_sin, int rot,
+                                   int8_t* kc, float* ks, int8_t* vc, float* vs, int kv_group, uint16_t* qh, int nq,
+                                   int nkv, int hd, int gate, float eps, int pos0, int nr, q27x_stream_t s) {
+    if (!qkv || !q_norm_w || !k_norm_w || !rope_cos || !rope_sin || !kc || !ks || !vc || !vs || !qh || pos0 < 0) {
+        set_error("q27x_attn_prep_rows: null argument");
+        return Q27X_E_ARG;
+    }
+    AttnArgs a{};
+    a.qkv = qkv; a.qkv_stride = qkv_stride; a.q_norm_w = q_norm_w; a.k_norm_w = k_norm_w;
+    a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.rot = rot;
+    a.kc = kc; a.ks = ks; a.vc = vc; a.vs = vs; a.kv_group = kv_group; a.qh = qh;
+    a.nq = nq; a.nkv = nkv; a.hd = hd; a.gate = gate; a.eps = eps; a.pos0_imm = pos0;
+    return launch_attn_prep(a, nr, (hipStream_t)s);
+}
+
+extern "C" int q27x_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride, const int8_t* kc,
+                              const float* ks, const int8_t* vc, const float* vs, int kv_group, int nq, int nkv,
+                              int hd, int gate, int pos0, int nr, void* work, uint16_t* out, int8_t* xq, float* xs,
+                              q27x_stream_t s) {
+    if (!qh || (gate && !qkv_gate) || !kc || !ks || !vc || !vs || !work || !out || pos0 < 0) {
+        set_error("q27x_attn_rows: null argument");
+        return Q27X_E_ARG;
+    }
+    AttnArgs a{};
+    a.qh = const_cast<uint16_t*>(qh); a.qkv = qkv_gate; a.qkv_stride = qkv_stride;
+    a.kc = const_cast<int8_t*>(kc); a.ks = const_cast<float*>(ks);
+    a.vc = const_cast<int8_t*>(vc); a.vs = const_cast<float*>(vs);
+    a.kv_group = kv_group; a.nq = nq; a.nkv = nkv; a.hd = hd; a.gate = gate; a.rot = 2;
+    a.pos0_imm = pos0; a.work = (float*)work; a.max_splits = (pos0 + nr + kSplit - 1) / kSplit;
+    a.sl2e = (float)((1.0 / sqrt((double)hd)) * 1.4426950408889634);
+    a.out = out; a.xq = xq; a.xs = xs;
+    return launch_attn(a, nr, (hipStream_t)s);
+}

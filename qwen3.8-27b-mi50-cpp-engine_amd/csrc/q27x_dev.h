@@ -1,0 +1,149 @@
+// q27x_dev.h -- device helpers shared by the gfx950 kernels.
+//
+// Numerics contract: every kernel computes its floating-point results in one fixed order with
+// correctly rounded IEEE operations (no FMA contraction, correctly rounded divide and sqrt,
+// explicit fmaf), and the transcendentals below are built from those operations only, so the
+// results are reproducible bit for bit by a host restatement of the same order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q27x {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 (include/q27.h:133-139)
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bfr(float f) { return bf2f(f2bf(f)); }   // round through bf16
+
+// ---------------------------------------------------------------- transcendentals
+// p * 2^n for p in [0.5, 2), n in [-152, 130]; one rounding at the final product.
+__device__ __forceinline__ float scale2(float p, int n) {
+    if (n > 127) { p = p * 0x1p127f; n -= 127; }
+    if (n < -126) { p = p * 0x1p-64f; n += 64; }
+    return p * __uint_as_float((uint32_t)(n + 127) << 23);
+}
+// e^x: Cody-Waite reduction with ln2 split in hi/lo, degree-7 Taylor polynomial (Horner, fmaf).
+__device__ __forceinline__ float qexp(float x) {
+    if (x != x) return x;
+    if (x > 88.7228393555f) return __builtin_huge_valf();
+    if (x < -103.972084045f) return 0.0f;
+    const float kf = rintf(x * 1.44269502163f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.42860682e-06f, r);
+    float p = 1.98412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333377e-3f);
+    p = __builtin_fmaf(p, r, 4.16666679e-2f);
+    p = __builtin_fmaf(p, r, 1.66666672e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return scale2(p, (int)kf);
+}
+// 2^x = 2^k * e^(r ln2), x = k + r exactly.
+__device__ __forceinline__ float qexp2(float x) {
+    if (x != x) return x;
+    if (x >= 128.0f) return __builtin_huge_valf();
+    if (x < -150.0f) return 0.0f;
+    const float kf = rintf(x);
+    const float r = x - kf;
+    float p = 1.52527336e-5f;
+    p = __builtin_fmaf(p, r, 1.54035304e-4f);
+    p = __builtin_fmaf(p, r, 1.33335581e-3f);
+    p = __builtin_fmaf(p, r, 9.61812911e-3f);
+    p = __builtin_fmaf(p, r, 5.55041087e-2f);
+    p = __builtin_fmaf(p, r, 2.40226507e-1f);
+    p = __builtin_fmaf(p, r, 6.93147182e-1f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return scale2(p, (int)kf);
+}
+// log(u), finite normal u > 0: u = m 2^e, s = (m-1)/(m+1), log m = 2 atanh(s) to s^9.
+__device__ __forceinline__ float qlog_pos(float u) {
+    const uint32_t b = __float_as_uint(u);
+    int e = (int)((b >> 23) & 0xffu) - 127;
+    float m = __uint_as_float((b & 0x7fffffu) | 0x3f800000u);
+    if (m > 1.41421354f) { m = m * 0.5f; e += 1; }
+    const float f = m - 1.0f;
+    const float s = f / (2.0f + f);
+    const float s2 = s * s;
+    float p = 0.222222224f;
+    p = __builtin_fmaf(p, s2, 0.285714298f);
+    p = __builtin_fmaf(p, s2, 0.400000006f);
+    p = __builtin_fmaf(p, s2, 0.666666687f);
+    p = p * s2;
+    const float lm = __builtin_fmaf(s, p, s + s);
+    const float ef = (float)e;
+    return __builtin_fmaf(ef, 0.693145751953125f, __builtin_fmaf(ef, 1.42860682e-06f, lm));
+}
+__device__ __forceinline__ float qlog1p(float y) {
+    if (y != y) return y;
+    if (y == __builtin_huge_valf()) return y;
+    const float u = 1.0f + y;
+    if (u == 1.0f) return y;
+    return qlog_pos(u) * (y / (u - 1.0f));
+}
+__device__ __forceinline__ float qsigmoid(float x) { return 1.0f / (1.0f + qexp(-x)); }
+__device__ __forceinline__ float qsilu(float x) { return x / (1.0f + qexp(-x)); }
+__device__ __forceinline__ float qsoftplus(float x) { return (x > 20.0f) ? x : qlog1p(qexp(x)); }
+__device__ __forceinline__ float rsqrt_cr(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+// ---------------------------------------------------------------- reductions
+// shfl_down tree over the 64 lanes (offsets 32..1); the result is valid in lane 0.
+__device__ __forceinline__ float tree64(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = x + __shfl_down(x, o, 64);
+    return x;
+}
+__device__ __forceinline__ float max_xor(float x, int width) {   // exact max over `width` lanes
+#pragma unroll
+    for (int o = width >> 1; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+// ---------------------------------------------------------------- int8
+__device__ __forceinline__ int dot16(const uint4 w, const uint4 x) {
+    int d = __builtin_amdgcn_sdot4((int)w.x, (int)x.x, 0, false);
+    d = __builtin_amdgcn_sdot4((int)w.y, (int)x.y, d, false);
+    d = __builtin_amdgcn_sdot4((int)w.z, (int)x.z, d, false);
+    d = __builtin_amdgcn_sdot4((int)w.w, (int)x.w, d, false);
+    return d;
+}
+__device__ __forceinline__ int8_t qcode(float v, float inv) {
+    int c = (int)rintf(v * inv);
+    c = c < -127 ? -127 : (c > 127 ? 127 : c);
+    return (int8_t)c;
+}
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---------------------------------------------------------------- synthetic generator
+__host__ __device__ __forceinline__ uint64_t sm64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+__host__ __device__ __forceinline__ uint64_t tensor_key(uint64_t seed, uint64_t tensor) {
+    return sm64(seed ^ (tensor * 0xD6E8FEB86659FD93ull));
+}
+// Irwin-Hall(4) normal: sum of four 16-bit fields (exact), one subtraction (exact), one multiply.
+__device__ __forceinline__ float normal_k(uint64_t key, uint64_t idx) {
+    const uint64_t h = sm64(key + idx);
+    const uint32_t s = (uint32_t)(h & 0xffffu) + (uint32_t)((h >> 16) & 0xffffu) +
+                       (uint32_t)((h >> 32) & 0xffffu) + (uint32_t)(h >> 48);
+    return ((float)s - 131070.0f) * 2.64289800e-05f;
+}
+__device__ __forceinline__ float uniform_k(uint64_t key, uint64_t idx) {
+    const uint64_t h = sm64(key + idx);
+    return (float)(uint32_t)(h >> 40) * 0x1p-24f;
+}
+
+}  // namespace q27x

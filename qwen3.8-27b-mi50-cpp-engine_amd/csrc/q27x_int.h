@@ -1,0 +1,124 @@
+// q27x_int.h -- internal launcher interface between the kernel files and the engine.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/q27x.h"
+
+namespace q27x {
+
+// thread-local error text behind q27x_last_error()
+void set_error(const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+#define Q27X_HIP(call)                                                   \
+    do {                                                                 \
+        hipError_t e_ = (call);                                          \
+        if (e_ != hipSuccess) return ::q27x::hip_fail(e_, #call);        \
+    } while (0)
+
+constexpr int kMaxRows = 8;      // verify rows (K <= 7) and prefill chunk
+constexpr int kSplit = 64;       // attention keys per split (fixed: results independent of NR)
+
+// ---------------------------------------------------------------- projection
+enum ProjEpi { EPI_STORE = 0, EPI_GDN_IN = 1, EPI_SWIGLU = 2 };
+struct ProjArgs {
+    const int8_t* W; const float* WS; int rows; int K; float alpha;
+    const int8_t* xq; int xst; const float* xs;
+    // EPI_STORE: y = v (+ rs*res); res_round rounds v through bf16 before the add
+    void* y; int ystride; int out_bf16;
+    const void* res; int res_bf16; int rstride; float rs; int res_round;
+    // EPI_GDN_IN: rows [0, nconv) are conv channels (conv + SiLU with deferred commit of the
+    // shift register), rows [nconv, rows) are z; outputs bf16
+    int nconv; uint16_t* conv_out; int conv_stride; uint16_t* z_out; int z_stride;
+    const uint16_t* conv_w; uint16_t* conv_hist; uint16_t* pend_raw;
+    const int* npend_ptr; int npend_imm;
+    // EPI_SWIGLU: the weight rows interleave 16 gate rows and 16 up rows per block of 32
+    int8_t* act_q; float* act_s; int act_stride; float gscale;
+    const int* stop;             // early exit when *stop != 0
+};
+int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
+
+// bf16 GEMV: y = W x (fp32 / bf16 out) or, argmax mode, per-block (val, idx) partials
+struct GemvArgs {
+    const uint16_t* W; int rows; int K;
+    const uint16_t* x; int xst;
+    void* y; int ystride; int out_bf16;
+    float* pval; uint32_t* pidx; int pstride;   // argmax partials [n][pstride]
+    const int* stop;
+};
+int launch_gemv(const GemvArgs& a, int argmax_mode, int nr, int* nblocks_out, hipStream_t s);
+int launch_argmax_final(const float* pval, const uint32_t* pidx, int pstride, int nblocks,
+                        int nr, int32_t* idx, float* val, const int* stop, hipStream_t s);
+int argmax_scratch(float** pv, uint32_t** pi);
+int launch_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val,
+                       float* pval, uint32_t* pidx, hipStream_t s);
+
+// ---------------------------------------------------------------- norms / elementwise
+struct NormArgs {
+    const void* x; int x_bf16; int xstride;      // input rows
+    const uint16_t* emb; const int* tok;          // embedding mode: x = emb[tok[r]]
+    const uint16_t* hadd;                         // head mode: x = bf16(bf16(hadd) + x) (fp32 x)
+    uint16_t* hout;                               // head mode: writes the combined bf16 rows
+    const uint16_t* w; float plus; float eps; int n;
+    uint16_t* hcopy;                              // bf16(x)
+    uint16_t* y; int ystride;                     // bf16 normed
+    int8_t* xq; float* xs; int quant_bf16; float in_scale;
+    const int* stop;
+    const int* row_sel;                           // optional: process only row *row_sel (into row 0)
+};
+int launch_norm(const NormArgs& a, int nr, hipStream_t s);
+int launch_quant_rows(const uint16_t* x, int xstride, int8_t* xq, int qstride, float* xs,
+                      int sstride, int n, float in_scale, int nrows, hipStream_t s);
+int launch_swiglu(const float* g, const float* u, int stride, int8_t* xq, float* xs, int n,
+                  float in_scale, int nr, hipStream_t s);
+
+// ---------------------------------------------------------------- GDN
+struct GdnArgs {
+    const uint16_t* qkv; int qkv_stride;          // conv'd q|k|v rows (bf16)
+    const uint16_t* z; int z_stride;
+    const float* a; const float* b; int ab_stride; // precomputed a/b (fp32), or
+    const uint16_t* in_a; const uint16_t* in_b;  // bf16 weights [vh][H] with
+    const uint16_t* ynorm; int ystride; int H;    // the bf16 normed rows (a/b fused)
+    const uint16_t* A_log; const uint16_t* dt_bias; const uint16_t* norm_w;
+    float* S; void* pend; const int* npend_ptr; int npend_imm;
+    int kh, vh, d; float eps;
+    uint16_t* out; int out_stride; int8_t* xq; float* xs;
+    const int* stop;
+};
+int launch_gdn(const GdnArgs& a, int nr, hipStream_t s);
+// conv + SiLU with deferred commit as a standalone kernel (kernel-tier entry)
+int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_stride,
+                    int nconv, const uint16_t* conv_w, uint16_t* conv_hist, uint16_t* pend_raw,
+                    const int* npend_ptr, int npend_imm, int nr, hipStream_t s);
+size_t gdn_pend_bytes(int kh, int vh, int d);
+size_t gdn_pend_raw_offset(int kh, int vh, int d);
+
+// ---------------------------------------------------------------- attention
+struct AttnArgs {
+    const uint16_t* qkv; int qkv_stride;          // projection rows q(+gate) | k | v
+    const uint16_t* q_norm_w; const uint16_t* k_norm_w;
+    const float* rope_cos; const float* rope_sin; int rot;
+    int8_t* kc; float* ks; int8_t* vc; float* vs; int kv_group;
+    uint16_t* qh;                                 // [nr][nq*hd]
+    int nq, nkv, hd, gate; float eps;
+    const int* pos0_ptr; int pos0_imm;
+    const int* nact_ptr;                          // active rows (MTP), null = nr
+    float* work; int max_splits;                  // split partials
+    float sl2e;                                   // (float)(log2(e) / sqrt(hd))
+    uint16_t* out; int8_t* xq; float* xs;
+    const int* stop;
+};
+int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s);
+int launch_attn(const AttnArgs& a, int nr, hipStream_t s);
+size_t attn_work_floats(int nq, int hd, int max_splits, int nr);
+
+// ---------------------------------------------------------------- synthetic weights
+int launch_gen_i8(int8_t* W, float* WS, int rows, int K, uint64_t key, int layout_gu, int is_up,
+                  hipStream_t s);
+int launch_gen_bf16(uint16_t* p, size_t n, uint64_t key, float stdv, float mean, int uniform,
+                    hipStream_t s);
+int launch_quant_w(const float* w, int rows, int K, int8_t* wq, float* ws, hipStream_t s);
+int launch_math_test(const float* x, float* y, int n, int op, hipStream_t s);
+
+}  // namespace q27x
