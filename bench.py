@@ -192,7 +192,7 @@ def main():
         "plain_decode_tok_s": round(plain_tps, 2),
         "verify_step": {"ms": round(vms, 4), "bytes": vbytes, "GB_s": round(v_gbs, 1),
                         "frac_of_hbm_peak": round(v_gbs / HBM_PEAK_GBS, 4), "rows": K + 1},
-        "roofline": {"bound": "hbm", "kernel": "k_proj<3,5,4,8,EPI_SWIGLU> (gate|up + SwiGLU + quantize)",
+        "roofline": {"bound": "hbm", "kernel": "k_proj<NR=3, NSTEP=5, RPW=1, EPI_SWIGLU> (gate|up + SwiGLU + quantize)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": kbytes,
                      "us_per_launch": round(kms * 1e3, 2)},

@@ -554,28 +554,18 @@ void q27o_attn_prep_rows(const uint16_t* qkv, int qkv_stride, const uint16_t* q_
     }
 }
 
-/* 16-lane score: lane c holds dims 8c..8c+7 (fmaf chain), xor butterfly 8,4,2,1. */
-static float score16(const float* q, const float* k, int hd) {
-    float p[16];
-    const int lanes = hd / 8;
-    for (int c = 0; c < 16; ++c) {
-        float a = 0.0f;
-        if (c < lanes)
-            for (int e = 0; e < 8; ++e) a = fmaf(q[8 * c + e], k[8 * c + e], a);
-        p[c] = a;
-    }
-    float t[16];
-    for (int o = 8; o > 0; o >>= 1) {
-        for (int c = 0; c < 16; ++c) t[c] = p[c] + p[c ^ o];
-        memcpy(p, t, sizeof p);
-    }
-    return p[0];
+/* score: fmaf over the head dims in order */
+static float score_seq(const float* q, const float* k, int hd) {
+    float a = 0.0f;
+    for (int i = 0; i < hd; ++i) a = fmaf(q[i], k[i], a);
+    return a;
 }
 
 #define Q27O_SPLIT 64
 /* src/q27_attn.hip:258-463 semantics (GQA, causal over pos0+r, log2-domain softmax, split
- * combine, sigmoid output gate); this build's order: fixed 64-key splits, two-pass softmax per
- * split with keys in ascending order, splits combined in ascending order. */
+ * combine, sigmoid output gate); this build's order: fixed 64-key splits, scores summed over the
+ * head dims in order, two-pass softmax per split with keys in ascending order, splits combined in
+ * ascending order. */
 void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
                     const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
                     int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
@@ -604,7 +594,7 @@ void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride
                 for (int k = k0; k < k1; ++k) {
                     const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
                     for (int i = 0; i < hd; ++i) kd[i] = (float)kc[off + i] * ks[(off + i) / kv_group];
-                    const float x = score16(q, kd, hd) * sl2e;
+                    const float x = score_seq(q, kd, hd) * sl2e;
                     xsc[k - k0] = x;
                     m = fmaxf(m, x);
                 }

@@ -83,6 +83,10 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
 }
 
 // work layout: o [nr][nq][ms][hd] | m [nr][nq][ms] | l [nr][nq][ms]
+// Block = (split of 64 keys, kv head), all rows and all GQA heads of the kv head. Scores are
+// register-tiled (one query x 4 keys per thread, fmaf over the 128 dims in order), the softmax of a
+// split is two-pass in base 2 with keys in order, P.V is register-tiled (4 queries x 4 dims per
+// thread, keys in order).
 __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
     if (a.stop && *a.stop) return;
     const int kvh = blockIdx.y;
@@ -93,15 +97,20 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
     const int nqr = nact * G;                       // query vectors of this kv head
     const int kvrows = a.nkv * kHD;
     const int ms = a.max_splits;
-    __shared__ float qf[kMaxQ][kHD];
+    __shared__ float qf[kMaxQ][kHD + 4];
     __shared__ float kd[kSplit][kHD + 4];
-    __shared__ float vd[kSplit][kHD];
-    __shared__ float sc[kMaxQ][kSplit];
+    __shared__ float vd[kSplit][kHD + 4];
+    __shared__ float sc[kMaxQ][kSplit + 4];
     const int t = threadIdx.x;
-    for (int i = t; i < nqr * kHD; i += 256) {
-        const int qi = i / kHD, dd = i - qi * kHD;
+    for (int i = t; i < nqr * (kHD / 8); i += 256) {
+        const int qi = i / (kHD / 8), c = i - qi * (kHD / 8);
         const int r = qi / G, g = qi - r * G;
-        qf[qi][dd] = bf2f(a.qh[(size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + dd]);
+        const uint4 u = *(const uint4*)(a.qh + (size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + 8 * c);
+        float* dst = &qf[qi][8 * c];
+        dst[0] = __uint_as_float(u.x << 16); dst[1] = __uint_as_float(u.x & 0xFFFF0000u);
+        dst[2] = __uint_as_float(u.y << 16); dst[3] = __uint_as_float(u.y & 0xFFFF0000u);
+        dst[4] = __uint_as_float(u.z << 16); dst[5] = __uint_as_float(u.z & 0xFFFF0000u);
+        dst[6] = __uint_as_float(u.w << 16); dst[7] = __uint_as_float(u.w & 0xFFFF0000u);
     }
     float* wo = a.work;
     float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
@@ -109,31 +118,39 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
     for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
         const int k0 = s * kSplit;
         const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
-        __syncthreads();   // previous split's tiles and the query stage are complete
-        for (int i = t; i < nk * kHD; i += 256) {
-            const int k = i / kHD, dd = i - k * kHD;
-            const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + dd;
-            kd[k][dd] = (float)a.kc[off] * a.ks[off / a.kv_group];
-            vd[k][dd] = (float)a.vc[off] * a.vs[off / a.kv_group];
+        __syncthreads();   // previous split's tiles (and the query stage) are complete
+        // K/V tiles: 16 int8 per thread-load, dequantised (k8 * scale) into LDS
+        for (int i = t; i < 2 * nk * (kHD / 16); i += 256) {
+            const int isv = i >= nk * (kHD / 16);
+            const int j = isv ? i - nk * (kHD / 16) : i;
+            const int k = j / (kHD / 16), c = j - k * (kHD / 16);
+            const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + 16 * c;
+            const uint4 u = *(const uint4*)((isv ? a.vc : a.kc) + off);
+            const float scl = (isv ? a.vs : a.ks)[off / a.kv_group];
+            float* dst = isv ? &vd[k][16 * c] : &kd[k][16 * c];
+            const uint32_t w4[4] = { u.x, u.y, u.z, u.w };
+#pragma unroll
+            for (int e = 0; e < 16; ++e) dst[e] = (float)(int8_t)(w4[e >> 2] >> (8 * (e & 3))) * scl;
         }
         __syncthreads();
-        // scores: 16 lanes per key, lane c holds dims 8c..8c+7 (fmaf chain), xor butterfly 8,4,2,1
-        {
-            const int c = t & 15, kl = t >> 4;
-            for (int kb = 0; kb < nk; kb += 16) {
-                const int k = kb + kl;
-                const int kk = k < nk ? k : nk - 1;
-                for (int qi = 0; qi < nqr; ++qi) {
-                    float acc = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qf[qi][8 * c + e], kd[kk][8 * c + e], acc);
-                    acc = acc + __shfl_xor(acc, 8, 64);
-                    acc = acc + __shfl_xor(acc, 4, 64);
-                    acc = acc + __shfl_xor(acc, 2, 64);
-                    acc = acc + __shfl_xor(acc, 1, 64);
-                    if (c == 0 && k < nk) sc[qi][k] = acc * a.sl2e;
-                }
+        // scores: thread = (query, 4 consecutive keys); sum over dims in order
+        for (int i = t; i < nqr * (kSplit / 4); i += 256) {
+            const int qi = i / (kSplit / 4), kb = (i - qi * (kSplit / 4)) * 4;
+            if (kb >= nk) continue;
+            float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+            const int kk1 = kb + 1 < nk ? kb + 1 : kb, kk2 = kb + 2 < nk ? kb + 2 : kb, kk3 = kb + 3 < nk ? kb + 3 : kb;
+#pragma unroll 8
+            for (int dd = 0; dd < kHD; ++dd) {
+                const float qv = qf[qi][dd];
+                acc0 = __builtin_fmaf(qv, kd[kb][dd], acc0);
+                acc1 = __builtin_fmaf(qv, kd[kk1][dd], acc1);
+                acc2 = __builtin_fmaf(qv, kd[kk2][dd], acc2);
+                acc3 = __builtin_fmaf(qv, kd[kk3][dd], acc3);
             }
+            sc[qi][kb] = acc0 * a.sl2e;
+            if (kb + 1 < nk) sc[qi][kb + 1] = acc1 * a.sl2e;
+            if (kb + 2 < nk) sc[qi][kb + 2] = acc2 * a.sl2e;
+            if (kb + 3 < nk) sc[qi][kb + 3] = acc3 * a.sl2e;
         }
         __syncthreads();
         // per query: max over the split's valid keys, p = 2^(x - m) in place, l = sum in key order
@@ -152,20 +169,48 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
             }
         }
         __syncthreads();
-        // o = sum_k p_k v_k in key order, one output per thread per pass
-        for (int i = t; i < nqr * kHD; i += 256) {
-            const int qi = i / kHD, dd = i - qi * kHD;
-            const int r = qi / G, g = qi - r * G;
-            const int L = pos0 + r + 1;
-            const int nv = (L - k0 < nk) ? (L - k0) : nk;
-            if (nv <= 0) continue;
-            float o = 0.0f;
-            for (int k = 0; k < nv; ++k) o = __builtin_fmaf(sc[qi][k], vd[k][dd], o);
-            wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + dd] = o;
+        // o = sum_k p_k v_k in key order: thread = (4 queries, 4 dims)
+        for (int i = t; i < ((nqr + 3) / 4) * (kHD / 4); i += 256) {
+            const int qb = (i / (kHD / 4)) * 4, db = (i % (kHD / 4)) * 4;
+            float o[4][4];
+            int nvq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int qi = qb + u;
+                const int L = pos0 + qi / G + 1;
+                nvq[u] = (qi < nqr) ? ((L - k0 < nk) ? (L - k0) : nk) : 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = 0.0f;
+            }
+            const int kmax = nvq[0] > nvq[3] ? (nvq[0] > nvq[1] ? nvq[0] : nvq[1]) : (nvq[3] > nvq[2] ? nvq[3] : nvq[2]);
+            for (int k = 0; k < kmax; ++k) {
+                const float4 v4 = *(const float4*)&vd[k][db];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (k < nvq[u]) {
+                        const float p = sc[qb + u][k];
+                        o[u][0] = __builtin_fmaf(p, v4.x, o[u][0]);
+                        o[u][1] = __builtin_fmaf(p, v4.y, o[u][1]);
+                        o[u][2] = __builtin_fmaf(p, v4.z, o[u][2]);
+                        o[u][3] = __builtin_fmaf(p, v4.w, o[u][3]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (nvq[u] <= 0) continue;
+                const int qi = qb + u, r = qi / G, g = qi - r * G;
+                float* dst = &wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + db];
+                *(float4*)dst = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+            }
         }
     }
 }
 
+// Merge the splits of one (row, query head): M = max m_s; w_s = 2^(m_s - M) computed once per
+// split in LDS; den and o accumulated over splits in order (fmaf), o's split values staged 32 at a
+// time with coalesced loads; x sigmoid(gate) -> bf16 -> per-16 quantize.
+constexpr int kCombChunk = 32;
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     if (a.stop && *a.stop) return;
     const int hq = blockIdx.x, r = blockIdx.y;
@@ -174,18 +219,31 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     const int L = pos0 + r + 1;
     const int ns = (L + kSplit - 1) / kSplit;
     const int ms = a.max_splits;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63;
     const float* wo = a.work;
     const float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
     const float* wl = wm + (size_t)nr * a.nq * ms;
     const size_t base = ((size_t)r * a.nq + hq) * ms;
+    __shared__ float smax[2];
+    __shared__ float sw[kCombChunk], sl[kCombChunk];
+    __shared__ float so[kCombChunk][kHD];
     float M = -__builtin_huge_valf();
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, wm[base + s]);
+    for (int s = t; s < ns; s += kHD) M = fmaxf(M, wm[base + s]);
+    M = max_xor(M, 64);
+    if (lane == 0) smax[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(smax[0], smax[1]);
     float den = 0.0f, o = 0.0f;
-    for (int s = 0; s < ns; ++s) {
-        const float w = qexp2(wm[base + s] - M);
-        den = __builtin_fmaf(wl[base + s], w, den);
-        o = __builtin_fmaf(wo[(base + s) * kHD + t], w, o);
+    for (int s0 = 0; s0 < ns; s0 += kCombChunk) {
+        const int cn = (ns - s0 < kCombChunk) ? ns - s0 : kCombChunk;
+        __syncthreads();
+        if (t < cn) { sw[t] = qexp2(wm[base + s0 + t] - M); sl[t] = wl[base + s0 + t]; }
+        for (int j = 0; j < cn; ++j) so[j][t] = wo[(base + s0 + j) * kHD + t];
+        __syncthreads();
+        for (int j = 0; j < cn; ++j) {
+            den = __builtin_fmaf(sl[j], sw[j], den);
+            o = __builtin_fmaf(so[j][t], sw[j], o);
+        }
     }
     const float inv = 1.0f / den;
     float v = o * inv;
@@ -228,7 +286,7 @@ int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
-    int gx = a.max_splits < 64 ? a.max_splits : 64;
+    int gx = a.max_splits < 256 ? a.max_splits : 256;
     hipLaunchKernelGGL(k_attn_split, dim3(gx, a.nkv), dim3(256), 0, s, a, nr);
     Q27X_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr), dim3(kHD), 0, s, a, nr);

@@ -6,6 +6,7 @@
 
 #include "q27x_dev.h"
 #include "q27x_int.h"
+#include "q27x_norm.h"
 
 namespace q27x {
 
@@ -23,104 +24,29 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 // ---------------------------------------------------------------- RMSNorm + quantize
-// One 256-thread block per row. Thread t owns elements 1024i + 4t + e (sum of squares in that
-// order, four wave trees, ((w0+w1)+w2)+w3); nrm = x*inv*(plus+w); a group of 16 is 4 threads.
+// One 256-thread block per row, in the canonical order of norm_rows (q27x_norm.h).
 constexpr int kNormMaxChunks = 8;   // n <= 8192
+template <int NCH>
 __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
     if (a.stop && *a.stop) return;
-    const int r = blockIdx.x;
-    const int rs = a.row_sel ? *a.row_sel : r;      // source row
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int n = a.n, nch = n >> 10;
-    float xv[kNormMaxChunks][4];
-#pragma unroll
-    for (int i = 0; i < kNormMaxChunks; ++i) {
-        if (i >= nch) break;
-        const int k = i * 1024 + 4 * t;
-        float v[4];
-        if (a.emb) {
-            const uint2 u = *(const uint2*)(a.emb + (size_t)a.tok[rs] * n + k);
-            v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
-            v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
-        } else if (a.x_bf16) {
-            const uint2 u = *(const uint2*)((const uint16_t*)a.x + (size_t)rs * a.xstride + k);
-            v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
-            v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
-        } else {
-            const float4 f = *(const float4*)((const float*)a.x + (size_t)rs * a.xstride + k);
-            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        }
-        if (a.hout) {   // head: the final residual row, bf16(bf16(r1) + r2) or bf16(r2)
-            uint16_t hb[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float s = a.hadd ? bf2f(a.hadd[(size_t)rs * n + k + e]) + v[e] : v[e];
-                hb[e] = f2bf(s);
-                v[e] = bf2f(hb[e]);
-            }
-            *(uint2*)(a.hout + (size_t)r * n + k) = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
-                                                              (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
-        }
-        if (a.hcopy) {
-            *(uint2*)(a.hcopy + (size_t)r * n + k) =
-                make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
-                           (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xv[i][e] = v[e];
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kNormMaxChunks; ++i) {
-        if (i >= nch) break;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(xv[i][e], xv[i][e], acc);
-    }
-    __shared__ float wsum[4];
-    acc = tree64(acc);
-    if (lane == 0) wsum[wv] = acc;
-    __syncthreads();
-    const float ss = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    const float inv = rsqrt_cr(ss * (1.0f / (float)n) + a.eps);
-    const float g = 1.0f / a.in_scale;
-#pragma unroll
-    for (int i = 0; i < kNormMaxChunks; ++i) {
-        if (i >= nch) break;
-        const int k = i * 1024 + 4 * t;
-        const uint2 wu = *(const uint2*)(a.w + k);
-        const float wf[4] = { __uint_as_float(wu.x << 16), __uint_as_float(wu.x & 0xFFFF0000u),
-                              __uint_as_float(wu.y << 16), __uint_as_float(wu.y & 0xFFFF0000u) };
-        float nm[4];
-        uint16_t yb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            nm[e] = xv[i][e] * inv * (a.plus + wf[e]);
-            yb[e] = f2bf(nm[e]);
-        }
-        if (a.y)
-            *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
-                                                                   (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
-        if (a.xq) {
-            float q[4], mx = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { q[e] = a.quant_bf16 ? bf2f(yb[e]) : nm[e]; mx = fmaxf(mx, fabsf(q[e])); }
-            mx = max_xor(mx, 4);
-            const float s = mx * g * (1.0f / 127.0f);
-            const float qi = (s > 0.0f) ? (g / s) : 0.0f;
-            uint32_t pk = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(q[e], qi)) << (8 * e);
-            *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
-            if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
-        }
-    }
+    __shared__ float wsum[1][4];
+    norm_rows<NCH, 1>(a, blockIdx.x, 1, wsum);
 }
 int launch_norm(const NormArgs& a, int nr, hipStream_t s) {
     if (a.n < 1024 || (a.n & 1023) || (a.n >> 10) > kNormMaxChunks || !a.w || nr < 1) {
         set_error("norm: n=%d must be a multiple of 1024 up to 8192", a.n);
         return Q27X_E_SHAPE;
     }
-    hipLaunchKernelGGL(k_norm, dim3(nr), dim3(256), 0, s, a);
+    switch (a.n >> 10) {
+        case 1: hipLaunchKernelGGL(k_norm<1>, dim3(nr), dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(k_norm<2>, dim3(nr), dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(k_norm<3>, dim3(nr), dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(k_norm<4>, dim3(nr), dim3(256), 0, s, a); break;
+        case 5: hipLaunchKernelGGL(k_norm<5>, dim3(nr), dim3(256), 0, s, a); break;
+        case 6: hipLaunchKernelGGL(k_norm<6>, dim3(nr), dim3(256), 0, s, a); break;
+        case 7: hipLaunchKernelGGL(k_norm<7>, dim3(nr), dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(k_norm<8>, dim3(nr), dim3(256), 0, s, a); break;
+    }
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

@@ -6,100 +6,229 @@
 //   A = S^T k^, B = S^T q^, delta = (v - decay A) beta, mixed = decay B + delta (k^.q^)
 //   S <- decay S + k^ (x) delta
 //   out = mixed rsqrt(mean(mixed^2) + eps) norm_w SiLU(z)  -> bf16 -> per-16 int8
-// Layout: S [VH][D=128][D] fp32 key-major. Four blocks per head, each owning 32 value dims of
-// all 128 key rows (16 KiB of state, 32 floats per thread, VGPR-resident for every row of the
-// verify); the four blocks of a head are placed on one XCD so they share an L2.
+// Layout: S [VH][D=128][D] fp32 key-major. One 512-thread block per value head: thread (g, d)
+// holds key rows 32g..32g+31 of value column d (64 KiB of state per block in VGPRs). Every
+// global load of the block is issued before the first wait, so a call costs one memory round
+// trip plus on-chip work; the rows then run with one barrier each.
 // Rollback: instead of the reference's per-row snapshot banks (src/q27_main.cpp:2933-2941) the
 // state in HBM stays at the last committed position; each row's (k^, delta, decay) goes to
 // `pend`, and the next call first applies the rows that were accepted (npend), writes that state
 // back once, then continues. The commit uses exactly the update the row already received, so the
 // committed state is bit-identical to stepping the accepted rows one at a time.
+// Conv (CONV = 1, the engine path; k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439): the raw
+// projection rows are convolved here. The committed shift register lives in `pend` in two parity
+// areas (read `par`, write `1 - par`), because the q and k channels of a key head are read by all
+// the value heads that share it and written by one of them.
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
 namespace q27x {
 
 constexpr int kD = 128;
-constexpr int kDSplit = 4;            // blocks per value head
-constexpr int kDB = kD / kDSplit;     // value dims per block (32)
-constexpr int kNT = 4 * kDB;          // threads: 4 key groups x 32 value dims
+constexpr int kNT = 512;              // threads per block: 4 key groups x 128 value dims
 constexpr int kJ = kD / 4;            // key rows per thread (32)
+constexpr int kStg = 8;               // staging loads per thread per batch
 
-// pend buffer: header (parity, global counter, per-head counters) | two parity areas of
-// khat [R][KH][D] | delta [R][VH][D] | decay [R][VH] | mixed [R][VH][D] | raw [R][NQKV] bf16 |
-// work [R][NQKV] bf16 (conv output of the kernel-tier entry). A call reads the pending rows from
-// area `par` and writes its own rows to area 1-par; the last block of the grid flips par, so no
-// block can overwrite a vector a sibling block has still to read.
-__host__ __device__ static inline size_t hdr_bytes(int vh) { return (((size_t)(2 + vh) * 4) + 255) & ~(size_t)255; }
+// pend buffer: header (parity, grid counter) | two parity areas of khat [R][KH][D] |
+// delta [R][VH][D] | decay [R][VH] (fp32) | raw [2][R][NQKV] bf16 | hist [2][NQKV][4] bf16 |
+// work [R][NQKV] bf16 (conv output of the kernel-tier entry). A call reads area `par` and writes
+// area 1-par; the last block of the grid flips par.
+__host__ __device__ static inline size_t hdr_bytes() { return 256; }
 __host__ __device__ static inline size_t area_floats(int kh, int vh) {
     return (size_t)kMaxRows * ((size_t)kh * kD + (size_t)vh * kD + vh);
 }
 size_t gdn_pend_raw_offset(int kh, int vh, int d) {
     (void)d;
-    return hdr_bytes(vh) + (2 * area_floats(kh, vh) + (size_t)kMaxRows * vh * kD) * 4;
+    return hdr_bytes() + 2 * area_floats(kh, vh) * 4;
 }
-size_t gdn_pend_bytes(int kh, int vh, int d) {
+static size_t gdn_hist_offset(int kh, int vh, int d) {
     const size_t nqkv = (size_t)(2 * kh + vh) * d;
     return gdn_pend_raw_offset(kh, vh, d) + 2 * (size_t)kMaxRows * nqkv * 2;
 }
-struct PendHdr { unsigned par; unsigned gcnt; unsigned hcnt[1]; };
+size_t gdn_pend_bytes(int kh, int vh, int d) {
+    const size_t nqkv = (size_t)(2 * kh + vh) * d;
+    return gdn_hist_offset(kh, vh, d) + 2 * nqkv * 4 * 2 + (size_t)kMaxRows * nqkv * 2;
+}
+static size_t gdn_work_offset(int kh, int vh, int d) {
+    const size_t nqkv = (size_t)(2 * kh + vh) * d;
+    return gdn_hist_offset(kh, vh, d) + 2 * nqkv * 4 * 2;
+}
+struct PendHdr { unsigned par; unsigned gcnt; };
 struct PendArea { float* khat; float* delta; float* decay; };
 __device__ __forceinline__ PendArea pend_area(void* p, int kh, int vh, int which) {
-    float* b = (float*)((char*)p + hdr_bytes(vh)) + (size_t)which * area_floats(kh, vh);
+    float* b = (float*)((char*)p + hdr_bytes()) + (size_t)which * area_floats(kh, vh);
     PendArea v;
     v.khat = b;  b += (size_t)kMaxRows * kh * kD;
     v.delta = b; b += (size_t)kMaxRows * vh * kD;
     v.decay = b;
     return v;
 }
-__device__ __forceinline__ float* pend_mixed(void* p, int kh, int vh) {
-    return (float*)((char*)p + hdr_bytes(vh)) + 2 * area_floats(kh, vh);
-}
 
-template <int FUSE_AB>
-__global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
+template <int CONV, int FUSE_AB>
+__global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, size_t hist_off) {
     if (a.stop && *a.stop) return;
-    // XCD-aware placement: block b runs on XCD b%8; the 4 blocks of a head share one XCD.
-    const int nb = gridDim.x;                       // vh * 4
-    const int b = blockIdx.x;
-    int h, dq;
-    if ((nb & 7) == 0 && ((nb >> 3) % kDSplit) == 0) {
-        const int x = b & 7, i = b >> 3;            // XCD, index within the XCD
-        const int hx = (nb >> 3) / kDSplit;         // heads per XCD
-        h = x * hx + i / kDSplit;
-        dq = i % kDSplit;
-    } else { h = b / kDSplit; dq = b % kDSplit; }
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int dl = t & (kDB - 1), g = t / kDB;      // local value dim, key group
-    const int d = dq * kDB + dl;
+    const int h = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int d = t & (kD - 1), g = t >> 7;
     const int ratio = a.vh / a.kh, kk = h / ratio;
-    const int KD = a.kh * kD;
+    const bool owner = (h % ratio) == 0;           // writes the shared q/k channels
+    const int KD = a.kh * kD, nqkv = 2 * KD + a.vh * kD;
     PendHdr* hdr = (PendHdr*)a.pend;
     const unsigned par = hdr->par & 1u;
-    const PendArea P = pend_area(a.pend, a.kh, a.vh, (int)par);       // pending rows (read)
-    const PendArea Q = pend_area(a.pend, a.kh, a.vh, (int)(par ^ 1u)); // this call's rows (write)
-    float* mixed_g = pend_mixed(a.pend, a.kh, a.vh);
-    __shared__ float sq[kD], sk[kD];
-    __shared__ float pA[4][kDB], pB[4][kDB];
-    __shared__ float red[2][3];
-    __shared__ float sab[2][kMaxRows];
-    __shared__ float skp[kMaxRows][kD];
-    __shared__ float sdp[kMaxRows][kDB];
-    __shared__ float sdc[kMaxRows];
-    __shared__ unsigned s_last;
+    const PendArea P = pend_area(a.pend, a.kh, a.vh, (int)par);        // pending rows (read)
+    const PendArea Q = pend_area(a.pend, a.kh, a.vh, (int)(par ^ 1u));  // this call's rows (write)
     const int npend = a.npend_ptr ? *a.npend_ptr : a.npend_imm;
 
-    // ---- a / b logits: bf16 GEMV of in_a / in_b row h on the bf16 normed rows (lane-chunk
-    //      order; bf16 rounding of the result as k_bf16_gemv2_tile, src/q27_util.hip:158-162)
+    __shared__ float skp[kMaxRows][kD], sdp[kMaxRows][kD], sdc[kMaxRows];
+    __shared__ float scv[kMaxRows][3 * kD];        // conv'd q | k | v of this head (bf16 values)
+    __shared__ float sz[kMaxRows][kD];
+    __shared__ float sq[kMaxRows][kD], sk[kMaxRows][kD];
+    __shared__ float pA[2][4][kD], pB[2][4][kD];
+    __shared__ float smix[kMaxRows][kD];
+    __shared__ float red[kMaxRows][2][3];
+    __shared__ float sab[2][kMaxRows];
+    extern __shared__ uint4 sy[];                  // FUSE_AB: in_a row | in_b row | nr ynorm rows
+
+    // ================= phase A: every global load of the block =================
+    // (a) committed state slice
+    const float* Sp = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
+    float st[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
+    // (b) pending update vectors: thread t covers rows p = t/128 and p + 4
+    float pk[2], pd[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int p = g + 4 * u;
+        pk[u] = (p < npend) ? P.khat[((size_t)p * a.kh + kk) * kD + d] : 0.0f;
+        pd[u] = (p < npend) ? P.delta[((size_t)p * a.vh + h) * kD + d] : 0.0f;
+    }
+    const float pdc = (t < npend) ? P.decay[(size_t)t * a.vh + h] : 0.0f;
+    // (c) channel t < 384 of this head: q (key head kk), k (kk), v (h)
+    const int cl = (t < 3 * kD) ? t : 0;
+    const int ch = (cl < kD) ? kk * kD + cl : (cl < 2 * kD) ? KD + kk * kD + (cl - kD) : 2 * KD + h * kD + (cl - 2 * kD);
+    uint16_t xr[kMaxRows];
+#pragma unroll
+    for (int n = 0; n < kMaxRows; ++n) xr[n] = (t < 3 * kD && n < nr) ? a.qkv[(size_t)n * a.qkv_stride + ch] : (uint16_t)0;
+    uint2 cw = make_uint2(0u, 0u), hs = make_uint2(0u, 0u);
+    uint16_t pr[kMaxRows];
+    const uint16_t* raw_r = (const uint16_t*)((const char*)a.pend + raw_off) + (size_t)par * kMaxRows * nqkv;
+    uint16_t* raw_w = (uint16_t*)((char*)a.pend + raw_off) + (size_t)(par ^ 1u) * kMaxRows * nqkv;
+    const uint16_t* hist_r = (const uint16_t*)((const char*)a.pend + hist_off) + (size_t)par * nqkv * 4;
+    uint16_t* hist_w = (uint16_t*)((char*)a.pend + hist_off) + (size_t)(par ^ 1u) * nqkv * 4;
+    if (CONV) {
+        if (t < 3 * kD) {
+            cw = *(const uint2*)(a.conv_w + (size_t)ch * 4);
+            hs = *(const uint2*)(hist_r + (size_t)ch * 4);
+        }
+#pragma unroll
+        for (int p = 0; p < kMaxRows; ++p) pr[p] = (t < 3 * kD && p < npend) ? raw_r[(size_t)p * nqkv + ch] : (uint16_t)0;
+    }
+    // (d) gate rows z: threads 384..511
+    uint16_t zr[kMaxRows];
+#pragma unroll
+    for (int n = 0; n < kMaxRows; ++n)
+        zr[n] = (t >= 3 * kD && n < nr) ? a.z[(size_t)n * a.z_stride + (size_t)h * kD + d] : (uint16_t)0;
+    // (e) a/b: the two weight rows and the nr normed input rows, staged through LDS
+    const int hc = a.H >> 3;                       // 8-element chunks per row
+    const int nstg = FUSE_AB ? (2 + nr) * hc : 0;
+    float ab_a = 0.0f, ab_b = 0.0f;
+    if (!FUSE_AB && t < nr) {
+        ab_a = a.a[(size_t)t * a.ab_stride + h];
+        ab_b = a.b[(size_t)t * a.ab_stride + h];
+    }
+    const float Aexp = qexp(bf2f(a.A_log[h]));
+    const float dtb = bf2f(a.dt_bias[h]);
+    const float nw = bf2f(a.norm_w[(t & 63) + 64 * (wv & 1)]);
+    for (int base = 0; base < nstg; base += kStg * kNT) {
+        uint4 v[kStg];
+#pragma unroll
+        for (int u = 0; u < kStg; ++u) {
+            const int i = base + u * kNT + t;
+            v[u] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nstg) {
+                const int r = i / hc, c = i - r * hc;
+                const uint16_t* src = (r == 0) ? a.in_a + (size_t)h * a.H : (r == 1) ? a.in_b + (size_t)h * a.H
+                                                                                       : a.ynorm + (size_t)(r - 2) * a.ystride;
+                v[u] = *(const uint4*)(src + 8 * c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kStg; ++u) {
+            const int i = base + u * kNT + t;
+            if (i < nstg) sy[i] = v[u];
+        }
+    }
+
+    // ================= phase B: on-chip work =================
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int p = g + 4 * u;
+        if (p < npend) { skp[p][d] = pk[u]; sdp[p][d] = pd[u]; }
+    }
+    if (t < npend) sdc[t] = pdc;
+    if (!FUSE_AB && t < nr) { sab[0][t] = ab_a; sab[1][t] = ab_b; }
+    if (t < 3 * kD) {
+        if (CONV) {
+            uint16_t h0 = (uint16_t)(hs.x & 0xFFFFu), h1 = (uint16_t)(hs.x >> 16), h2 = (uint16_t)(hs.y & 0xFFFFu);
+#pragma unroll
+            for (int p = 0; p < kMaxRows; ++p)
+                if (p < npend) { h0 = h1; h1 = h2; h2 = pr[p]; }
+            const bool own = (cl >= 2 * kD) || owner;
+            if (own) {
+                *(uint2*)(hist_w + (size_t)ch * 4) = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2);
+                if (a.conv_hist) {
+                    a.conv_hist[(size_t)ch * 3] = h0; a.conv_hist[(size_t)ch * 3 + 1] = h1;
+                    a.conv_hist[(size_t)ch * 3 + 2] = h2;
+                }
+            }
+            const float w0 = __uint_as_float(cw.x << 16), w1 = __uint_as_float(cw.x & 0xFFFF0000u);
+            const float w2 = __uint_as_float(cw.y << 16), w3 = __uint_as_float(cw.y & 0xFFFF0000u);
+#pragma unroll
+            for (int n = 0; n < kMaxRows; ++n) {
+                if (n >= nr) break;
+                const uint16_t x = xr[n];
+                float acc = bf2f(h0) * w0;
+                acc = __builtin_fmaf(bf2f(h1), w1, acc);
+                acc = __builtin_fmaf(bf2f(h2), w2, acc);
+                acc = __builtin_fmaf(bf2f(x), w3, acc);
+                h0 = h1; h1 = h2; h2 = x;
+                if (own) raw_w[(size_t)n * nqkv + ch] = x;
+                scv[n][cl] = bf2f(f2bf(qsilu(acc)));
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < kMaxRows; ++n)
+                if (n < nr) scv[n][cl] = bf2f(xr[n]);
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < kMaxRows; ++n)
+            if (n < nr) sz[n][d] = bf2f(zr[n]);
+    }
+    __syncthreads();
+
+    // commit the accepted rows of the previous call, write the committed state back once
+    for (int p = 0; p < npend; ++p) {
+        const float dp = sdp[p][d], dc = sdc[p];
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(skp[p][g * kJ + j], dp, dc * st[j]);
+    }
+    if (npend > 0) {
+        float* Sw = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) Sw[(size_t)j * kD] = st[j];
+    }
+    // a/b logits: pair (which, n) per wave, lane-chunk order (chunk c on lane c%64, fmaf per
+    // element), shfl tree, bf16 rounding as k_bf16_gemv2_tile (src/q27_util.hip:158-162)
     if (FUSE_AB) {
-        for (int q = wv; q < 2 * nr; q += kNT / 64) {
-            const int which = q & 1, n = q >> 1;
-            const uint16_t* wr = (which ? a.in_b : a.in_a) + (size_t)h * a.H;
-            const uint16_t* yr = a.ynorm + (size_t)n * a.ystride;
+        for (int pi = wv; pi < 2 * nr; pi += 8) {
+            const int which = pi & 1, n = pi >> 1;
+            const uint4* wrow = sy + (size_t)which * hc;
+            const uint4* yrow = sy + (size_t)(2 + n) * hc;
             float acc = 0.0f;
-            for (int c = lane; c < (a.H >> 3); c += 64) {
-                const uint4 w = *(const uint4*)(wr + 8 * c);
-                const uint4 y = *(const uint4*)(yr + 8 * c);
+            for (int c = lane; c < hc; c += 64) {
+                const uint4 w = wrow[c], y = yrow[c];
                 acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(y.x << 16), acc);
                 acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(y.x & 0xFFFF0000u), acc);
                 acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(y.y << 16), acc);
@@ -112,145 +241,122 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
             acc = tree64(acc);
             if (lane == 0) sab[which][n] = bfr(acc);
         }
-    } else if (t < 2 * nr) {
-        const int which = t & 1, n = t >> 1;
-        sab[which][n] = (which ? a.b : a.a)[(size_t)n * a.ab_stride + h];
     }
-
-    // ---- the committed state of this block's slice, plus the pending rows
-    float* Sp = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
-    float st[kJ];
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
-    for (int i = t; i < npend * kD; i += kNT) {
-        const int p = i / kD, j = i - p * kD;
-        skp[p][j] = P.khat[((size_t)p * a.kh + kk) * kD + j];
+    // q/k L2 norms and k^.q^ of row n on the wave pair (2m, 2m+1), element e = 64 (w&1) + lane
+    const int e = 64 * (wv & 1) + lane;
+    for (int n = wv >> 1; n < nr; n += 4) {
+        const float qv = scv[n][e], kv = scv[n][kD + e];
+        const float r0 = tree64(qv * qv), r1 = tree64(kv * kv), r2 = tree64(qv * kv);
+        if (lane == 0) { red[n][wv & 1][0] = r0; red[n][wv & 1][1] = r1; red[n][wv & 1][2] = r2; }
     }
-    for (int i = t; i < npend * kDB; i += kNT) {
-        const int p = i / kDB, e = i - p * kDB;
-        sdp[p][e] = P.delta[((size_t)p * a.vh + h) * kD + dq * kDB + e];
-    }
-    if (t < npend) sdc[t] = P.decay[(size_t)t * a.vh + h];
     __syncthreads();
-    for (int p = 0; p < npend; ++p) {
-        const float dp = sdp[p][dl], dc = sdc[p];
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(skp[p][g * kJ + j], dp, dc * st[j]);
+    for (int n = wv >> 1; n < nr; n += 4) {
+        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
+        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
+        const float skv = scv[n][kD + e] * invk;
+        sq[n][e] = scv[n][e] * invq;
+        sk[n][e] = skv;
+        if (owner) Q.khat[((size_t)n * a.kh + kk) * kD + e] = skv;
     }
-    if (npend > 0) {
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) Sp[(size_t)j * kD] = st[j];
-    }
+    __syncthreads();
 
-    const float Aexp = qexp(bf2f(a.A_log[h]));
-    const float dtb = bf2f(a.dt_bias[h]);
+    // the rows, in order: one barrier each (pA / pB alternate between two buffers)
     for (int n = 0; n < nr; ++n) {
-        const uint16_t* row = a.qkv + (size_t)n * a.qkv_stride;
-        // q/k L2 norms and k^.q^: two waves, one element per lane (redundant in every block)
-        {
-            const float qv = bf2f(row[kk * kD + t]);
-            const float kv = bf2f(row[KD + kk * kD + t]);
-            const float r0 = tree64(qv * qv), r1 = tree64(kv * kv), r2 = tree64(qv * kv);
-            if (lane == 0) { red[wv][0] = r0; red[wv][1] = r1; red[wv][2] = r2; }
-        }
-        __syncthreads();
-        const float sumq2 = red[0][0] + red[1][0];
-        const float sumk2 = red[0][1] + red[1][1];
-        const float sumqk = red[0][2] + red[1][2];
-        const float invq = rsqrt_cr(sumq2 + 1e-6f) * 0.0883883476f;
-        const float invk = rsqrt_cr(sumk2 + 1e-6f);
-        const float kq = sumqk * invq * invk;
-        sq[t] = bf2f(row[kk * kD + t]) * invq;
-        sk[t] = bf2f(row[KD + kk * kD + t]) * invk;
+        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
+        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
+        const float kq = ((red[n][0][2] + red[n][1][2]) * invq) * invk;
         const float beta = qsigmoid(sab[1][n]);
         const float sp = qsoftplus(sab[0][n] + dtb);
         const float decay = qexp(-(Aexp * sp));
-        const float vv = bf2f(row[2 * KD + h * kD + d]);
-        __syncthreads();
+        const float vv = scv[n][2 * kD + d];
         float accA = 0.0f, accB = 0.0f;
 #pragma unroll
         for (int j = 0; j < kJ; ++j) {
-            accA = __builtin_fmaf(st[j], sk[g * kJ + j], accA);
-            accB = __builtin_fmaf(st[j], sq[g * kJ + j], accB);
+            accA = __builtin_fmaf(st[j], sk[n][g * kJ + j], accA);
+            accB = __builtin_fmaf(st[j], sq[n][g * kJ + j], accB);
         }
-        pA[g][dl] = accA;
-        pB[g][dl] = accB;
+        pA[n & 1][g][d] = accA;
+        pB[n & 1][g][d] = accB;
         __syncthreads();
-        const float A = ((pA[0][dl] + pA[1][dl]) + pA[2][dl]) + pA[3][dl];
-        const float B = ((pB[0][dl] + pB[1][dl]) + pB[2][dl]) + pB[3][dl];
+        const float A = ((pA[n & 1][0][d] + pA[n & 1][1][d]) + pA[n & 1][2][d]) + pA[n & 1][3][d];
+        const float B = ((pB[n & 1][0][d] + pB[n & 1][1][d]) + pB[n & 1][2][d]) + pB[n & 1][3][d];
         const float delta = (vv - decay * A) * beta;
         const float mixed = __builtin_fmaf(delta, kq, decay * B);
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(sk[g * kJ + j], delta, decay * st[j]);
+        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(sk[n][g * kJ + j], delta, decay * st[j]);
         if (g == 0) {
             Q.delta[((size_t)n * a.vh + h) * kD + d] = delta;
-            mixed_g[((size_t)n * a.vh + h) * kD + d] = mixed;
+            smix[n][d] = mixed;
         }
-        if (dq == 0 && t == 0) Q.decay[(size_t)n * a.vh + h] = decay;
-        if (dq == 0 && (h % ratio) == 0) Q.khat[((size_t)n * a.kh + kk) * kD + t] = sk[t];
-        __syncthreads();   // sq / sk / red reused by the next row
+        if (t == 0) Q.decay[(size_t)n * a.vh + h] = decay;
     }
+    __syncthreads();
 
-    // ---- output norm + gate + quantize: the last of the head's four blocks does all rows
-    __threadfence();
-    __syncthreads();
-    if (t == 0) s_last = (atomicAdd(&hdr->hcnt[h], 1u) == (unsigned)(kDSplit - 1)) ? 1u : 0u;
-    __syncthreads();
-    if (s_last) {
-        __threadfence();
-        const float nw = bf2f(a.norm_w[t]);
-        for (int n = 0; n < nr; ++n) {
-            const float mx = __builtin_nontemporal_load(&mixed_g[((size_t)n * a.vh + h) * kD + t]);
-            const float r3 = tree64(mx * mx);
-            if (lane == 0) red[wv][0] = r3;
-            __syncthreads();
-            const float summ = red[0][0] + red[1][0];
-            const float inv = rsqrt_cr(summ * (1.0f / (float)kD) + a.eps);
-            const float z = bf2f(a.z[(size_t)n * a.z_stride + (size_t)h * kD + t]);
-            const float y = mx * inv * nw * qsilu(z);
-            const uint16_t yb = f2bf(y);
-            a.out[(size_t)n * a.out_stride + (size_t)h * kD + t] = yb;
-            if (a.xq) {
-                const float yv = bf2f(yb);
-                const float m16 = max_xor(fabsf(yv), 16);
-                const float sc = m16 * (1.0f / 127.0f);
-                const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
-                const size_t k = (size_t)n * a.out_stride + (size_t)h * kD + t;
-                a.xq[k] = qcode(yv, qi);
-                if ((t & 15) == 0) a.xs[k >> 4] = sc;
-            }
-            __syncthreads();
-        }
-        if (t == 0) hdr->hcnt[h] = 0u;
+    // output norm + gate + quantize, row n on the wave pair (2m, 2m+1)
+    for (int n = wv >> 1; n < nr; n += 4) {
+        const float mx = smix[n][e];
+        const float r3 = tree64(mx * mx);
+        if (lane == 0) red[n][wv & 1][0] = r3;
     }
-    // ---- the last block of the grid flips the parity (every block has read it by now)
-    if (t == 0) {
-        __threadfence();
-        if (atomicAdd(&hdr->gcnt, 1u) == (unsigned)(nb - 1)) {
-            hdr->gcnt = 0u;
-            hdr->par = par ^ 1u;
-            __threadfence();
+    __syncthreads();
+    for (int n = wv >> 1; n < nr; n += 4) {
+        const float mx = smix[n][e];
+        const float inv = rsqrt_cr((red[n][0][0] + red[n][1][0]) * (1.0f / (float)kD) + a.eps);
+        const float y = mx * inv * nw * qsilu(sz[n][e]);
+        const uint16_t yb = f2bf(y);
+        const size_t k = (size_t)n * a.out_stride + (size_t)h * kD + e;
+        a.out[k] = yb;
+        if (a.xq) {
+            const float yv = bf2f(yb);
+            const float m16 = max_xor(fabsf(yv), 16);
+            const float sc = m16 * (1.0f / 127.0f);
+            const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+            a.xq[k] = qcode(yv, qi);
+            if ((e & 15) == 0) a.xs[k >> 4] = sc;
         }
+    }
+    // the last block of the grid flips the parity (every block read it at its start; what this
+    // call wrote is read by the next call, after the kernel boundary)
+    if (t == 0 &&
+        __hip_atomic_fetch_add(&hdr->gcnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(gridDim.x - 1)) {
+        st_agent(&hdr->gcnt, 0u);
+        st_agent(&hdr->par, par ^ 1u);
     }
 }
 
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s) {
-    if (a.d != kD || a.kh < 1 || a.vh % a.kh || nr < 1 || nr > kMaxRows || !a.qkv || !a.z || !a.S || !a.pend || !a.out) {
+    if (a.d != kD || a.kh < 1 || a.vh % a.kh || nr < 1 || nr > kMaxRows || !a.qkv || !a.z || !a.S || !a.pend ||
+        !a.out || !a.A_log || !a.dt_bias || !a.norm_w) {
         set_error("gdn: unsupported shape or null argument (d=%d kh=%d vh=%d nr=%d)", a.d, a.kh, a.vh, nr);
         return Q27X_E_SHAPE;
     }
     if (a.xq && a.out_stride % 16) { set_error("gdn: out_stride must be a multiple of 16"); return Q27X_E_ARG; }
     const int fuse = (a.in_a && a.in_b && a.ynorm) ? 1 : 0;
     if (!fuse && (!a.a || !a.b)) { set_error("gdn: a/b logits or in_a/in_b weights required"); return Q27X_E_ARG; }
-    const int grid = a.vh * kDSplit;
-    if (fuse) hipLaunchKernelGGL(k_gdn<1>, dim3(grid), dim3(kNT), 0, s, a, nr);
-    else hipLaunchKernelGGL(k_gdn<0>, dim3(grid), dim3(kNT), 0, s, a, nr);
+    if (fuse && (a.H < 8 || (a.H & 7) || a.H > 8192)) { set_error("gdn: H=%d unsupported for the fused a/b", a.H); return Q27X_E_SHAPE; }
+    if (a.conv_w && ((size_t)a.conv_w & 7)) { set_error("gdn: conv_w must be 8-byte aligned"); return Q27X_E_ARG; }
+    const size_t lds = fuse ? (size_t)(2 + nr) * a.H * 2 : 0;
+    const size_t ro = gdn_pend_raw_offset(a.kh, a.vh, a.d), ho = gdn_hist_offset(a.kh, a.vh, a.d);
+    if (a.conv_w) {
+        if (fuse) hipLaunchKernelGGL((k_gdn<1, 1>), dim3(a.vh), dim3(kNT), lds, s, a, nr, ro, ho);
+        else hipLaunchKernelGGL((k_gdn<1, 0>), dim3(a.vh), dim3(kNT), 0, s, a, nr, ro, ho);
+    } else {
+        if (fuse) hipLaunchKernelGGL((k_gdn<0, 1>), dim3(a.vh), dim3(kNT), lds, s, a, nr, ro, ho);
+        else hipLaunchKernelGGL((k_gdn<0, 0>), dim3(a.vh), dim3(kNT), 0, s, a, nr, ro, ho);
+    }
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
+int gdn_set_lds_limit() {
+    // the fused a/b stage of 8 rows at H = 8192 needs 160 KiB of dynamic LDS at most
+    const int mx = 160 * 1024 - 48 * 1024;
+    Q27X_HIP(hipFuncSetAttribute((const void*)k_gdn<1, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+    Q27X_HIP(hipFuncSetAttribute((const void*)k_gdn<0, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+    return Q27X_OK;
+}
 
-// conv + SiLU with the deferred shift-register commit as a standalone kernel (the engine fuses
-// it into the in_qkv projection epilogue; this form serves the kernel-tier entry and its tests)
+// conv + SiLU with the deferred shift-register commit as a standalone kernel (the kernel-tier
+// entry; the engine convolves inside k_gdn)
 __global__ __launch_bounds__(256) void k_gdn_conv(const uint16_t* __restrict__ raw, int raw_stride,
                                                   uint16_t* __restrict__ out, int out_stride, int nconv,
                                                   const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ hist,
@@ -292,8 +398,8 @@ extern "C" size_t q27x_gdn_pend_bytes(int kh, int vh, int d, int max_rows) {
     return gdn_pend_bytes(kh, vh, d);
 }
 
-// Kernel-tier entry: conv (deferred commit) then the recurrence. The conv'd rows go to the work
-// area at the end of `pend`, so the call allocates nothing.
+// Kernel-tier entry: conv (deferred commit, in place on conv_hist) then the recurrence. The
+// conv'd rows go to the work area at the end of `pend`, so the call allocates nothing.
 extern "C" int q27x_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, int z_stride,
                                const float* a, const float* b, int ab_stride, const uint16_t* A_log,
                                const uint16_t* dt_bias, const uint16_t* norm_w, const uint16_t* conv_w, float* S,
@@ -306,7 +412,7 @@ extern "C" int q27x_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const ui
     }
     const int nconv = (2 * kh + vh) * d;
     uint16_t* pend_raw = (uint16_t*)((char*)pend + gdn_pend_raw_offset(kh, vh, d));
-    uint16_t* conv_buf = pend_raw + (size_t)kMaxRows * nconv;
+    uint16_t* conv_buf = (uint16_t*)((char*)pend + gdn_work_offset(kh, vh, d));
     int rc = launch_gdn_conv(qkv_raw, qkv_stride, conv_buf, nconv, nconv, conv_w, conv_hist, pend_raw, nullptr,
                              npend, nr, (hipStream_t)s);
     if (rc) return rc;

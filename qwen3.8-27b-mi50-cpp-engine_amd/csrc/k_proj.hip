@@ -7,164 +7,208 @@
 //   int d = sdot4 x 4 (exact int32), acc = fmaf((float)d, ws64 * xs16, acc)
 // then the 64 lane sums meet in the shfl_down tree -- the reference's order
 // (src/q27_fp8.hip:3814-3871), kept so results match its host restatement bit for bit.
-// The grid is persistent-ish (grid-stride over row tiles) with the next tile's weights
-// prefetched into registers while the current tile is reduced and stored.
+// Pipelining: each weight register is refilled with the next row group's slab as soon as its
+// dot products have issued, so a full group of loads stays in flight through the reduction and
+// the epilogue; epilogue inputs are requested before those refills (vector-memory counters
+// retire in order, so a later load would make its wait drain the prefetch).
+#include <type_traits>
+
 #include "q27x_dev.h"
 #include "q27x_int.h"
+#include "q27x_norm.h"
 
 namespace q27x {
 
-template <int NR, int NSTEP, int RPW, int NW, int EPI>
-__global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
-    constexpr int NT = NW * 64;
-    constexpr int TILE = NW * RPW;
-    constexpr int SL = NSTEP * 64;                  // slabs per staged activation row
+constexpr int kPW = 4;              // waves per block
+
+template <int V> struct Pow2 {
+    static constexpr int value = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : V <= 32 ? 32 : 64;
+};
+
+// Transposed shfl tree: P values per lane, each reduced over the 64 lanes with exactly the pairs
+// of the shfl_down tree (offsets 32..1; a + b and b + a are the same float); value v ends in lane
+// v * (64 / P). The halving levels exchange half of the values per step, so P values cost
+// P - 1 + log2(64 / P) shuffles instead of 6 P.
+template <int P>
+__device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
+#pragma unroll
+    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
+        // bitwise selects: a select between two array elements would become a select of
+        // addresses and push the array out of registers
+        const uint32_t up = (lane & o) ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+        for (int v = 0; v < h; ++v) {
+            const uint32_t lo = __float_as_uint(x[v]), hi = __float_as_uint(x[v + h]);
+            const float send = __uint_as_float((lo & up) | (hi & ~up));
+            const float keep = __uint_as_float((hi & up) | (lo & ~up));
+            x[v] = keep + __shfl_xor(send, o, 64);
+        }
+    }
+    float y = x[0];
+#pragma unroll
+    for (int o = 32 / P; o > 0; o >>= 1) y = y + __shfl_down(y, o, 64);
+    return y;
+}
+
+// Norm tail of a residual projection: the last block of the grid normalizes the rows the grid
+// has just written (row count nr, n = NCH * 1024), three rows per pass.
+__device__ __forceinline__ void proj_tail(const ProjArgs& a, int nr, float (*wsum)[4], unsigned* s_last) {
+    if (!arrive_last(a.tail_cnt, gridDim.x, s_last)) return;
+    switch (a.tail.n >> 10) {
+        case 1: norm_rows<1, 3>(a.tail, 0, nr, wsum); break;
+        case 5: norm_rows<5, 3>(a.tail, 0, nr, wsum); break;
+        default: break;                                // rejected by the launcher
+    }
+}
+
+// One row group = RPW consecutive weight rows; a wave owns `upw` consecutive units of `urows`
+// rows (urows = RPW, or 32 for the SwiGLU epilogue whose unit is one 16-output quantization
+// group: 16 gate rows | 16 up rows), so every wave streams the same number of bytes.
+// FULL: K == 1024 * NSTEP (no slab bounds checks).
+template <int NR, int NSTEP, int RPW, int EPI, bool FULL>
+__global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urows) {
+    constexpr int SL = NSTEP * 64;
+    constexpr int NT = kPW * 64;
+    constexpr int NSTG = (NR * SL + NT - 1) / NT;      // staging loads per thread
+    constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
     __shared__ uint4 sx[NR * SL];
     __shared__ float ssc[NR * SL];
-    __shared__ float tout[NR][TILE];
+    __shared__ float sacc[(EPI == EPI_SWIGLU) ? kPW * 32 * NR : 1];
+    __shared__ float wsum[3][4];
+    __shared__ unsigned s_last;
     if (a.stop && *a.stop) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
-    for (int i = threadIdx.x; i < NR * SL; i += NT) {
-        const int n = i / SL, s = i - n * SL;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        float sc = 0.0f;
-        if (s < nslab) {
-            v = *(const uint4*)(a.xq + (size_t)n * a.xst + 16 * s);
-            sc = a.xs[(size_t)n * (a.xst >> 4) + s];
+    const int gpu = urows / RPW;                       // groups per unit
+    const int nunits = (a.rows + urows - 1) / urows;
+    const int gw = blockIdx.x * kPW + wave;
+    const int u0 = gw * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
+    const int g0 = u0 * gpu, g1 = u1 * gpu;
+    // activation stage: every load issued before any LDS write (one round trip)
+    {
+        uint4 tv[NSTG];
+        float ts[NSTG];
+#pragma unroll
+        for (int j = 0; j < NSTG; ++j) {
+            const int i = threadIdx.x + j * NT;
+            const int n = i / SL, s = i - n * SL;
+            tv[j] = make_uint4(0u, 0u, 0u, 0u);
+            ts[j] = 0.0f;
+            if (i < NR * SL && (FULL || s < nslab)) {
+                tv[j] = *(const uint4*)(a.xq + (size_t)n * a.xst + 16 * s);
+                ts[j] = a.xs[(size_t)n * (a.xst >> 4) + s];
+            }
         }
-        sx[i] = v;
-        ssc[i] = sc;
+#pragma unroll
+        for (int j = 0; j < NSTG; ++j) {
+            const int i = threadIdx.x + j * NT;
+            if (i < NR * SL) { sx[i] = tv[j]; ssc[i] = ts[j]; }
+        }
+    }
+    uint4 W[RPW][NSTEP];
+    float S[RPW][NSTEP];
+    auto ld = [&](int g, int r, int t) __attribute__((always_inline)) {
+        int row = g * RPW + r;
+        row = row < a.rows ? row : a.rows - 1;
+        const int s = t * 64 + lane;
+        if (FULL || s < nslab) {
+            W[r][t] = ld_nt16(a.W + (size_t)row * K + 16 * s);
+            S[r][t] = a.WS[(size_t)row * ng64 + (s >> 2)];
+        } else {
+            W[r][t] = make_uint4(0u, 0u, 0u, 0u);
+            S[r][t] = 0.0f;
+        }
+    };
+    if (g0 < g1) {
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) ld(g0, r, t);
     }
     __syncthreads();
-    const int ntiles = (a.rows + TILE - 1) / TILE;
-    uint4 wv[RPW][NSTEP];
-    float wsv[RPW][NSTEP];
-    auto load = [&](int tl, uint4 (&W_)[RPW][NSTEP], float (&S_)[RPW][NSTEP]) {
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            int row = tl * TILE + wave * RPW + r;
+    const int vi = lane / LPV;                         // the value this lane holds after the tree
+    const bool holder = (lane % LPV) == 0 && vi < V;
+    const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
+    const uint32_t* resw = (const uint32_t*)a.res;
+    for (int g = g0; g < g1; ++g) {
+        // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use
+        uint32_t rw = 0u;
+        size_t ridx = 0;
+        if (EPI == EPI_STORE && resw) {
+            int row = g * RPW + hr;
             row = row < a.rows ? row : a.rows - 1;
-            const int8_t* wp = a.W + (size_t)row * K;
-            const float* sp = a.WS + (size_t)row * ng64;
+            ridx = (size_t)hn * a.rstride + row;
+            rw = a.res_bf16 ? resw[ridx >> 1] : resw[ridx];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[P];
+#pragma unroll
+        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
+        auto body = [&](auto reload) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < NSTEP; ++t) {
                 const int s = t * 64 + lane;
-                if (s < nslab) { W_[r][t] = ld_nt16(wp + 16 * s); S_[r][t] = sp[s >> 2]; }
-                else { W_[r][t] = make_uint4(0u, 0u, 0u, 0u); S_[r][t] = 0.0f; }
-            }
-        }
-    };
-    int tile = blockIdx.x;
-    if (tile < ntiles) load(tile, wv, wsv);
-    for (; tile < ntiles; tile += gridDim.x) {
-        uint4 wn[RPW][NSTEP];
-        float wsn[RPW][NSTEP];
-        const int next = tile + gridDim.x;
-        if (next < ntiles) load(next, wn, wsn);
-        float acc[RPW][NR];
-#pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int n = 0; n < NR; ++n) acc[r][n] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NSTEP; ++t) {
-            const int s = t * 64 + lane;
-            if (s < nslab) {
 #pragma unroll
                 for (int n = 0; n < NR; ++n) {
                     const uint4 xa = sx[n * SL + s];
                     const float sa = ssc[n * SL + s];
 #pragma unroll
                     for (int r = 0; r < RPW; ++r) {
-                        const int d = dot16(wv[r][t], xa);
-                        acc[r][n] = __builtin_fmaf((float)d, wsv[r][t] * sa, acc[r][n]);
+                        const int d = dot16(W[r][t], xa);
+                        acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
                     }
                 }
+                if constexpr (decltype(reload)::value) {
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) ld(g + 1, r, t);
+                }
             }
-        }
-#pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int n = 0; n < NR; ++n) acc[r][n] = tree64(acc[r][n]);
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < RPW; ++r)
-#pragma unroll
-                for (int n = 0; n < NR; ++n) tout[n][wave * RPW + r] = acc[r][n] * a.alpha;
-        }
-        __syncthreads();
-        const int row0 = tile * TILE;
+        };
+        if (g + 1 < g1) body(std::true_type{});
+        else body(std::false_type{});
+        const float tv = tree_t<P>(acc, lane) * a.alpha;
         if (EPI == EPI_STORE) {
-            for (int i = threadIdx.x; i < NR * TILE; i += NT) {
-                const int n = i / TILE, j = i - n * TILE, row = row0 + j;
-                if (row >= a.rows) continue;
-                float v = tout[n][j];
-                if (a.res) {
-                    const float rv = a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)n * a.rstride + row])
-                                                : ((const float*)a.res)[(size_t)n * a.rstride + row];
+            const int row = g * RPW + hr;
+            if (holder && row < a.rows) {
+                float v = tv;
+                if (resw) {
+                    const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
+                                                : __uint_as_float(rw);
                     if (a.res_round) v = bfr(v);
                     v = v + a.rs * rv;
                 }
-                if (a.out_bf16) ((uint16_t*)a.y)[(size_t)n * a.ystride + row] = f2bf(v);
-                else ((float*)a.y)[(size_t)n * a.ystride + row] = v;
+                const size_t yi = (size_t)hn * a.ystride + row;
+                if (a.has_tail) {                      // read back by the tail block
+                    if (a.out_bf16) st_agent((uint16_t*)a.y + yi, f2bf(v));
+                    else st_agent((float*)a.y + yi, v);
+                } else if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
+                else ((float*)a.y)[yi] = v;
             }
-        } else if (EPI == EPI_GDN_IN) {
-            const int j = threadIdx.x;
-            const int row = row0 + j;
-            if (j < TILE && row < a.rows) {
-                if (row < a.nconv) {
-                    // k_gdn_conv_tp_tile (src/q27_gdn.hip:411-439): raw bf16 shift register,
-                    // first tap a plain product, fmaf for taps 1..3, SiLU, bf16. The pending rows
-                    // of the previous call are shifted in first (deferred commit).
-                    const int c = row;
-                    const int npend = a.npend_ptr ? *a.npend_ptr : a.npend_imm;
-                    uint16_t h0 = a.conv_hist[3 * c], h1 = a.conv_hist[3 * c + 1], h2 = a.conv_hist[3 * c + 2];
-                    for (int p = 0; p < npend; ++p) {
-                        h0 = h1; h1 = h2; h2 = a.pend_raw[(size_t)p * a.nconv + c];
-                    }
-                    a.conv_hist[3 * c] = h0; a.conv_hist[3 * c + 1] = h1; a.conv_hist[3 * c + 2] = h2;
-                    const float w0 = bf2f(a.conv_w[4 * c]), w1 = bf2f(a.conv_w[4 * c + 1]);
-                    const float w2 = bf2f(a.conv_w[4 * c + 2]), w3 = bf2f(a.conv_w[4 * c + 3]);
+        } else {   // EPI_SWIGLU: 32 rows [16 gate | 16 up] -> 16 outputs, one quantization group
+            const int gi = g % gpu;
+            float* sw = sacc + wave * 32 * NR;
+            if (holder) sw[(gi * RPW + hr) * NR + hn] = tv;
+            if (gi == gpu - 1) {
+                __builtin_amdgcn_wave_barrier();
+                const int unit = g / gpu, j = lane & 15;
 #pragma unroll
-                    for (int n = 0; n < NR; ++n) {
-                        const uint16_t x = f2bf(tout[n][j]);
-                        float acc = bf2f(h0) * w0;
-                        acc = __builtin_fmaf(bf2f(h1), w1, acc);
-                        acc = __builtin_fmaf(bf2f(h2), w2, acc);
-                        acc = __builtin_fmaf(bf2f(x), w3, acc);
-                        h0 = h1; h1 = h2; h2 = x;
-                        a.pend_raw[(size_t)n * a.nconv + c] = x;
-                        a.conv_out[(size_t)n * a.conv_stride + c] = f2bf(qsilu(acc));
+                for (int nn = 0; nn < NR; ++nn) {
+                    const float gv = sw[j * NR + nn], uv = sw[(16 + j) * NR + nn];
+                    const float swv = gv / (1.0f + qexp(-gv));
+                    const float v = swv * uv * a.gscale;
+                    const float mx = max_xor(fabsf(v), 16);
+                    const float sc = mx * (1.0f / 127.0f);
+                    const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+                    if (lane < 16) {
+                        a.act_q[(size_t)nn * a.act_stride + unit * 16 + j] = qcode(v, inv);
+                        if (j == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
                     }
-                } else {
-#pragma unroll
-                    for (int n = 0; n < NR; ++n)
-                        a.z_out[(size_t)n * a.z_stride + (row - a.nconv)] = f2bf(tout[n][j]);
                 }
+                __builtin_amdgcn_wave_barrier();
             }
-        } else {   // EPI_SWIGLU: tile = [16 gate rows | 16 up rows] -> 16 outputs, one group
-            const int i = threadIdx.x;
-            if (i < NR * 16) {
-                const int n = i >> 4, j = i & 15;
-                const float g = tout[n][j], u = tout[n][16 + j];
-                const float sw = g / (1.0f + qexp(-g));
-                const float v = sw * u * a.gscale;
-                const float mx = max_xor(fabsf(v), 16);
-                const float sc = mx * (1.0f / 127.0f);
-                const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
-                a.act_q[(size_t)n * a.act_stride + tile * 16 + j] = qcode(v, inv);
-                if (j == 0) a.act_s[(size_t)n * (a.act_stride >> 4) + tile] = sc;
-            }
-        }
-        __syncthreads();
-        if (next < ntiles) {
-#pragma unroll
-            for (int r = 0; r < RPW; ++r)
-#pragma unroll
-                for (int t = 0; t < NSTEP; ++t) { wv[r][t] = wn[r][t]; wsv[r][t] = wsn[r][t]; }
         }
     }
+    if (EPI == EPI_STORE && a.has_tail) proj_tail(a, a.tail_rows, wsum, &s_last);
 }
 
 static int g_ncu = 0;
@@ -179,84 +223,103 @@ static int num_cus() {
     return g_ncu;
 }
 
-template <int NR, int NSTEP, int RPW, int NW, int EPI>
-static int run_proj(const ProjArgs& a, hipStream_t s, int blocks_per_cu) {
-    constexpr int TILE = NW * RPW;
-    const int ntiles = (a.rows + TILE - 1) / TILE;
-    int grid = num_cus() * blocks_per_cu;
-    if (grid > ntiles) grid = ntiles;
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, NW, EPI>), dim3(grid), dim3(NW * 64), 0, s, a);
+// Launch shape: units spread over num_cus() * wpc waves (wpc measured on MI355X: 16 for the
+// K <= 6144 shapes, 8 for K = 17408 whose 17 KiB-per-row prefetch holds ~250 VGPRs).
+template <int NR, int NSTEP, int EPI, bool FULL>
+static int run_proj(const ProjArgs& a, hipStream_t s) {
+    constexpr int RPW = 1;
+    const int urows = (EPI == EPI_SWIGLU) ? 32 : RPW;
+    const int nunits = (a.rows + urows - 1) / urows;
+    const int wpc = (NSTEP >= 17) ? 8 : 16;
+    const int wmax = num_cus() * wpc;
+    const int upw = (nunits + wmax - 1) / wmax;
+    const int waves = (nunits + upw - 1) / upw;
+    const int grid = (waves + kPW - 1) / kPW;
+    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL>), dim3(grid), dim3(kPW * 64), 0, s, a, upw, urows);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
 
-// Shape router. NSTEP = ceil(K/1024). The LDS stage is NR*NSTEP*1280 B; K = 17408 at NR = 8
-// (174 KB) is split by the caller into two launches of 4 rows.
-template <int NR, int EPI>
+// Shape router. NSTEP = ceil(K/1024); the LDS stage is NR*NSTEP*1280 B, so K = 17408 at NR > 4
+// (174 KB at NR = 8) is split by the caller into launches of <= 4 rows.
+template <int NR, int EPI, bool FULL>
 static int route_k(const ProjArgs& a, hipStream_t s) {
     const int ns = (a.K + 1023) / 1024;
     if constexpr (EPI == EPI_SWIGLU) {
-        if (ns == 1) return run_proj<NR, 1, 4, 8, EPI>(a, s, 2);
-        if (ns == 2) return run_proj<NR, 2, 4, 8, EPI>(a, s, 2);
-        if (ns == 5) return run_proj<NR, 5, 4, 8, EPI>(a, s, 2);
-        return -2;
-    }
-    else if constexpr (EPI == EPI_GDN_IN) {
-        if (ns == 1) return run_proj<NR, 1, 2, 4, EPI>(a, s, 4);
-        if (ns == 2) return run_proj<NR, 2, 2, 4, EPI>(a, s, 4);
-        if (ns == 5) return run_proj<NR, 5, 2, 4, EPI>(a, s, 4);
+        if (ns == 1) return run_proj<NR, 1, EPI, FULL>(a, s);
+        if (ns == 5) return run_proj<NR, 5, EPI, FULL>(a, s);
         return -2;
     } else {
-    switch (ns) {
-        case 1: return run_proj<NR, 1, 2, 4, EPI>(a, s, 4);
-        case 2: return run_proj<NR, 2, 2, 4, EPI>(a, s, 4);
-        case 4: return run_proj<NR, 4, 2, 4, EPI>(a, s, 4);
-        case 5: return run_proj<NR, 5, 2, 4, EPI>(a, s, 4);
-        case 6: return run_proj<NR, 6, 2, 4, EPI>(a, s, 4);
-        case 17:
-            if constexpr (NR <= 4) return run_proj<NR, 17, 1, 4, EPI>(a, s, 2);
-            return -2;
-        default: return -2;
-    }
+        switch (ns) {
+            case 1: return run_proj<NR, 1, EPI, FULL>(a, s);
+            case 2: return run_proj<NR, 2, EPI, FULL>(a, s);
+            case 4: return run_proj<NR, 4, EPI, FULL>(a, s);
+            case 5: return run_proj<NR, 5, EPI, FULL>(a, s);
+            case 6: return run_proj<NR, 6, EPI, FULL>(a, s);
+            case 17:
+                if constexpr (NR <= 4) return run_proj<NR, 17, EPI, FULL>(a, s);
+                return -2;
+            default: return -2;
+        }
     }
 }
 
-template <int EPI>
+template <int EPI, bool FULL>
 static int route_nr(const ProjArgs& a, int nr, hipStream_t s) {
     switch (nr) {
-        case 1: return route_k<1, EPI>(a, s);
-        case 2: return route_k<2, EPI>(a, s);
-        case 3: return route_k<3, EPI>(a, s);
-        case 4: return route_k<4, EPI>(a, s);
-        case 5: return route_k<5, EPI>(a, s);
-        case 6: return route_k<6, EPI>(a, s);
-        case 7: return route_k<7, EPI>(a, s);
-        case 8: return route_k<8, EPI>(a, s);
+        case 1: return route_k<1, EPI, FULL>(a, s);
+        case 2: return route_k<2, EPI, FULL>(a, s);
+        case 3: return route_k<3, EPI, FULL>(a, s);
+        case 4: return route_k<4, EPI, FULL>(a, s);
+        case 5: return route_k<5, EPI, FULL>(a, s);
+        case 6: return route_k<6, EPI, FULL>(a, s);
+        case 7: return route_k<7, EPI, FULL>(a, s);
+        case 8: return route_k<8, EPI, FULL>(a, s);
         default: return -2;
     }
+}
+
+static int route(const ProjArgs& a, int epi, int nr, hipStream_t s) {
+    const bool full = (a.K & 1023) == 0;
+    if (epi == EPI_SWIGLU) return full ? route_nr<EPI_SWIGLU, true>(a, nr, s) : route_nr<EPI_SWIGLU, false>(a, nr, s);
+    return full ? route_nr<EPI_STORE, true>(a, nr, s) : route_nr<EPI_STORE, false>(a, nr, s);
 }
 
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
-    if (!a.W || !a.WS || !a.xq || !a.xs || a.rows < 1 || a.K < 64 || (a.K & 63) || nr < 1 || nr > kMaxRows) {
+    if (!a.W || !a.WS || a.rows < 1 || a.K < 64 || (a.K & 63) || nr < 1 || nr > kMaxRows) {
         set_error("proj: bad arguments (rows=%d K=%d nr=%d)", a.rows, a.K, nr);
         return Q27X_E_ARG;
     }
+    if (!a.xq || !a.xs) { set_error("proj: no activations"); return Q27X_E_ARG; }
     if ((a.xst & 15) || a.xst < a.K) { set_error("proj: activation stride %d must be >= K and a multiple of 16", a.xst); return Q27X_E_ARG; }
+    if (a.res && ((size_t)a.res & 3)) { set_error("proj: residual must be 4-byte aligned"); return Q27X_E_ARG; }
+    if (epi == EPI_SWIGLU && (a.rows & 31)) { set_error("proj: SwiGLU rows %d not a multiple of 32", a.rows); return Q27X_E_SHAPE; }
+    if (a.has_tail) {
+        if (epi != EPI_STORE || !a.tail_cnt || !a.tail.w || !(a.tail.n == 1024 || a.tail.n == 5120) || a.tail.emb ||
+            a.tail.hout || a.tail.row_sel) {
+            set_error("proj: unsupported norm tail (n=%d)", a.tail.n);
+            return Q27X_E_SHAPE;
+        }
+    }
     int rc;
     if (epi == EPI_STORE && a.K > 8192 && nr > 4) {   // LDS stage limit: two launches of <= 4 rows
         ProjArgs b = a;
-        rc = route_nr<EPI_STORE>(b, 4, s);
-        if (rc) return rc;
+        b.has_tail = 0;                               // the tail runs once, after the second
+        rc = route(b, EPI_STORE, 4, s);
+        if (rc) return rc == -2 ? (set_error("proj: no kernel for K=%d", a.K), Q27X_E_SHAPE) : rc;
         b.xq = a.xq + (size_t)4 * a.xst;
         b.xs = a.xs + (size_t)4 * (a.xst >> 4);
         const size_t esz = a.out_bf16 ? 2 : 4;
         b.y = (char*)a.y + (size_t)4 * a.ystride * esz;
         if (a.res) b.res = (const char*)a.res + (size_t)4 * a.rstride * (a.res_bf16 ? 2 : 4);
-        rc = route_nr<EPI_STORE>(b, nr - 4, s);
-    } else if (epi == EPI_STORE) rc = route_nr<EPI_STORE>(a, nr, s);
-    else if (epi == EPI_GDN_IN) rc = route_nr<EPI_GDN_IN>(a, nr, s);
-    else rc = route_nr<EPI_SWIGLU>(a, nr, s);
+        b.has_tail = a.has_tail;
+        b.tail_rows = nr;
+        rc = route(b, EPI_STORE, nr - 4, s);
+    } else {
+        ProjArgs b = a;
+        b.tail_rows = nr;
+        rc = route(b, epi, nr, s);
+    }
     if (rc == -2) { set_error("proj: no kernel for K=%d nr=%d epi=%d", a.K, nr, epi); return Q27X_E_SHAPE; }
     return rc;
 }
@@ -290,30 +353,20 @@ __device__ __forceinline__ void am_merge(float& bv, uint32_t& bi, float v, uint3
 __device__ __forceinline__ bool finitef(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
 
 template <int NR, int NSTEP, int RPW, int MODE>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-    constexpr int NW = 4, NT = 256, TILE = NW * RPW, CH = NSTEP * 64;
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a, int upw) {
+    constexpr int CH = NSTEP * 64;
     __shared__ float sxf[NR * CH * 8];
-    __shared__ float tout[NR][TILE];
-    __shared__ float bvs[NR][NW];
-    __shared__ uint32_t bis[NR][NW];
     if (a.stop && *a.stop) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nch = K >> 3;
-    for (int i = threadIdx.x; i < NR * CH * 8; i += NT) {
-        const int n = i / (CH * 8), k = i - n * (CH * 8);
-        sxf[i] = (k < K) ? bf2f(a.x[(size_t)n * a.xst + k]) : 0.0f;
-    }
-    __syncthreads();
-    float bv[NR];
-    uint32_t bi[NR];
-#pragma unroll
-    for (int n = 0; n < NR; ++n) { bv[n] = -__builtin_huge_valf(); bi[n] = 0xFFFFFFFFu; }
-    const int ntiles = (a.rows + TILE - 1) / TILE;
+    const int ngroups = (a.rows + RPW - 1) / RPW;
+    const int gw = blockIdx.x * 4 + wave;
+    const int g0 = gw * upw, g1 = (g0 + upw < ngroups) ? g0 + upw : ngroups;
     uint4 wv[RPW][NSTEP];
-    auto load = [&](int tl, uint4 (&W_)[RPW][NSTEP]) {
+    auto load = [&](int g, uint4 (&W_)[RPW][NSTEP]) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            int row = tl * TILE + wave * RPW + r;
+            int row = g * RPW + r;
             row = row < a.rows ? row : a.rows - 1;
             const uint16_t* wp = a.W + (size_t)row * K;
 #pragma unroll
@@ -323,12 +376,17 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             }
         }
     };
-    int tile = blockIdx.x;
-    if (tile < ntiles) load(tile, wv);
-    for (; tile < ntiles; tile += gridDim.x) {
+    if (g0 < g1) load(g0, wv);
+    for (int i = threadIdx.x; i < NR * CH * 8; i += 256) {
+        const int n = i / (CH * 8), k = i - n * (CH * 8);
+        sxf[i] = (k < K) ? bf2f(a.x[(size_t)n * a.xst + k]) : 0.0f;
+    }
+    __syncthreads();
+    float bv = -__builtin_huge_valf();                  // MODE 1: lane n < NR keeps row n's best
+    uint32_t bi = 0xFFFFFFFFu;
+    for (int g = g0; g < g1; ++g) {
         uint4 wn[RPW][NSTEP];
-        const int next = tile + gridDim.x;
-        if (next < ntiles) load(next, wn);
+        if (g + 1 < g1) load(g + 1, wn);
         float acc[RPW][NR];
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
@@ -363,56 +421,57 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int n = 0; n < NR; ++n) acc[r][n] = tree64(acc[r][n]);
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < RPW; ++r)
-#pragma unroll
-                for (int n = 0; n < NR; ++n) tout[n][wave * RPW + r] = acc[r][n];
-        }
-        __syncthreads();
-        const int row0 = tile * TILE;
+            for (int n = 0; n < NR; ++n) acc[r][n] = __shfl(tree64(acc[r][n]), 0, 64);
+        const int row0 = g * RPW;
         if (MODE == 0) {
-            for (int i = threadIdx.x; i < NR * TILE; i += NT) {
-                const int n = i / TILE, j = i - n * TILE, row = row0 + j;
-                if (row >= a.rows) continue;
-                if (a.out_bf16) ((uint16_t*)a.y)[(size_t)n * a.ystride + row] = f2bf(tout[n][j]);
-                else ((float*)a.y)[(size_t)n * a.ystride + row] = tout[n][j];
+            if (lane < RPW * NR) {
+                const int r = lane % RPW, n = lane / RPW, row = row0 + r;
+                float v = 0.0f;
+#pragma unroll
+                for (int rr = 0; rr < RPW; ++rr)
+#pragma unroll
+                    for (int nn = 0; nn < NR; ++nn) if (rr == r && nn == n) v = acc[rr][nn];
+                if (row < a.rows) {
+                    if (a.out_bf16) ((uint16_t*)a.y)[(size_t)n * a.ystride + row] = f2bf(v);
+                    else ((float*)a.y)[(size_t)n * a.ystride + row] = v;
+                }
             }
-        } else if (threadIdx.x < NR) {
-            const int n = threadIdx.x;
-            for (int j = 0; j < TILE; ++j) {
-                const int row = row0 + j;
-                const float v = tout[n][j];
-                if (row < a.rows && finitef(v)) am_merge(bv[0], bi[0], v, (uint32_t)row);
+        } else if (lane < NR) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const int row = row0 + r;
+                float v = 0.0f;
+#pragma unroll
+                for (int nn = 0; nn < NR; ++nn) if (nn == lane) v = acc[r][nn];
+                if (row < a.rows && finitef(v)) am_merge(bv, bi, v, (uint32_t)row);
             }
         }
-        __syncthreads();
-        if (next < ntiles) {
+        if (g + 1 < g1) {
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
 #pragma unroll
                 for (int t = 0; t < NSTEP; ++t) wv[r][t] = wn[r][t];
         }
     }
-    if (MODE == 1 && threadIdx.x < NR) {
-        a.pval[(size_t)threadIdx.x * a.pstride + blockIdx.x] = bv[0];
-        a.pidx[(size_t)threadIdx.x * a.pstride + blockIdx.x] = bi[0];
+    if (MODE == 1 && lane < NR) {
+        a.pval[(size_t)lane * a.pstride + gw] = bv;
+        a.pidx[(size_t)lane * a.pstride + gw] = bi;
     }
-    (void)bvs; (void)bis;
 }
 
 template <int NR, int MODE>
 static int gemv_k(const GemvArgs& a, hipStream_t s, int* nb) {
     const int ns = (a.K + 511) / 512;
-    constexpr int RPW = 2, TILE = 4 * RPW;
-    const int ntiles = (a.rows + TILE - 1) / TILE;
-    int grid = num_cus() * 4;
-    if (MODE == 1 && grid > a.pstride) grid = a.pstride;
-    if (grid > ntiles) grid = ntiles;
-    if (grid < 1) grid = 1;
-    if (nb) *nb = grid;
-#define Q27X_G(NS) hipLaunchKernelGGL((k_gemv<NR, NS, RPW, MODE>), dim3(grid), dim3(256), 0, s, a)
+    constexpr int RPW = 2;
+    const int ngroups = (a.rows + RPW - 1) / RPW;
+    int wmax = num_cus() * 8;
+    if (MODE == 1 && wmax > a.pstride) wmax = a.pstride & ~3;
+    const int upw = (ngroups + wmax - 1) / wmax;
+    const int waves = (ngroups + upw - 1) / upw;
+    const int grid = (waves + 3) / 4;
+    if (nb) *nb = grid * 4;
+    if (MODE == 1 && grid * 4 > a.pstride) return -2;
+#define Q27X_G(NS) hipLaunchKernelGGL((k_gemv<NR, NS, RPW, MODE>), dim3(grid), dim3(256), 0, s, a, upw)
     switch (ns) {
         case 1: Q27X_G(1); break;
         case 2: Q27X_G(2); break;

@@ -124,6 +124,55 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---------------------------------------------------------------- grid-wide hand-off
+// MI355X's L2 is private to each XCD and not coherent across XCDs; an agent-scope release fence
+// (__threadfence) writes back and then invalidates the issuing XCD's whole L2, which costs tens
+// of microseconds when every block of a large grid does it. Instead the values that another
+// block must read inside the same kernel are written with agent-scope stores (sc1: written
+// through to the coherence point), every thread waits for its stores to be acknowledged before
+// the block's arrival is counted, and only the reader block invalidates its L2 (acquire fence,
+// one buffer_inv) before plain loads.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint16_t* p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Arrival counting over 16 sub-counters (one 256-B line each, cnt[64 (1 + j)]) and a top counter
+// cnt[0]: same-address atomics serialize (~11 ns each on MI355X), so a flat counter over 1000+
+// blocks would cost more than the work it guards. Every counter is reset by its last arrival.
+// Returns true in every thread of the block that arrives last; that block has passed an
+// agent-scope acquire. Called by all threads of the block after their agent-scope stores.
+constexpr int kArriveLines = 17;                   // counter lines of 256 B
+__device__ __forceinline__ bool arrive_last(unsigned* cnt, unsigned nblocks, unsigned* s_flag) {
+    __builtin_amdgcn_s_waitcnt(0);                   // this thread's stores acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned ns = nblocks < 16u ? nblocks : 16u;
+        const unsigned j = blockIdx.x % ns;
+        const unsigned nj = (nblocks - j + ns - 1) / ns;   // blocks counted on sub-counter j
+        unsigned last = 0u;
+        if (add_agent(cnt + 64 * (1 + j), 1u) == nj - 1) {
+            st_agent(cnt + 64 * (1 + j), 0u);
+            if (add_agent(cnt, 1u) == ns - 1) {
+                st_agent(cnt, 0u);
+                last = 1u;
+            }
+        }
+        *s_flag = last;
+    }
+    __syncthreads();
+    if (*s_flag == 0u) return false;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return true;
+}
+
 // ---------------------------------------------------------------- synthetic generator
 __host__ __device__ __forceinline__ uint64_t sm64(uint64_t x) {
     x += 0x9E3779B97F4A7C15ull;

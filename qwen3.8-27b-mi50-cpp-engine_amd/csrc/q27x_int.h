@@ -20,22 +20,33 @@ int hip_fail(hipError_t e, const char* what);
 constexpr int kMaxRows = 8;      // verify rows (K <= 7) and prefill chunk
 constexpr int kSplit = 64;       // attention keys per split (fixed: results independent of NR)
 
+// ---------------------------------------------------------------- norms
+struct NormArgs {
+    const void* x; int x_bf16; int xstride;      // input rows
+    const uint16_t* emb; const int* tok;          // embedding mode: x = emb[tok[r]]
+    const uint16_t* hadd;                         // head mode: x = bf16(bf16(hadd) + x) (fp32 x)
+    uint16_t* hout;                               // head mode: writes the combined bf16 rows
+    const uint16_t* w; float plus; float eps; int n;
+    uint16_t* hcopy;                              // bf16(x)
+    uint16_t* y; int ystride;                     // bf16 normed
+    int8_t* xq; float* xs; int quant_bf16; float in_scale;
+    const int* stop;
+    const int* row_sel;                           // optional: process only row *row_sel (into row 0)
+};
 // ---------------------------------------------------------------- projection
-enum ProjEpi { EPI_STORE = 0, EPI_GDN_IN = 1, EPI_SWIGLU = 2 };
+enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2 };
 struct ProjArgs {
     const int8_t* W; const float* WS; int rows; int K; float alpha;
     const int8_t* xq; int xst; const float* xs;
     // EPI_STORE: y = v (+ rs*res); res_round rounds v through bf16 before the add
     void* y; int ystride; int out_bf16;
     const void* res; int res_bf16; int rstride; float rs; int res_round;
-    // EPI_GDN_IN: rows [0, nconv) are conv channels (conv + SiLU with deferred commit of the
-    // shift register), rows [nconv, rows) are z; outputs bf16
-    int nconv; uint16_t* conv_out; int conv_stride; uint16_t* z_out; int z_stride;
-    const uint16_t* conv_w; uint16_t* conv_hist; uint16_t* pend_raw;
-    const int* npend_ptr; int npend_imm;
     // EPI_SWIGLU: the weight rows interleave 16 gate rows and 16 up rows per block of 32
     int8_t* act_q; float* act_s; int act_stride; float gscale;
     const int* stop;             // early exit when *stop != 0
+    // EPI_STORE tail: the last block of the grid runs `tail` (RMSNorm + quantize of the rows just
+    // written) once every block's stores are visible; tail_cnt is a zeroed counter it resets
+    int has_tail; unsigned* tail_cnt; int tail_rows; NormArgs tail;
 };
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
 
@@ -54,19 +65,6 @@ int argmax_scratch(float** pv, uint32_t** pi);
 int launch_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val,
                        float* pval, uint32_t* pidx, hipStream_t s);
 
-// ---------------------------------------------------------------- norms / elementwise
-struct NormArgs {
-    const void* x; int x_bf16; int xstride;      // input rows
-    const uint16_t* emb; const int* tok;          // embedding mode: x = emb[tok[r]]
-    const uint16_t* hadd;                         // head mode: x = bf16(bf16(hadd) + x) (fp32 x)
-    uint16_t* hout;                               // head mode: writes the combined bf16 rows
-    const uint16_t* w; float plus; float eps; int n;
-    uint16_t* hcopy;                              // bf16(x)
-    uint16_t* y; int ystride;                     // bf16 normed
-    int8_t* xq; float* xs; int quant_bf16; float in_scale;
-    const int* stop;
-    const int* row_sel;                           // optional: process only row *row_sel (into row 0)
-};
 int launch_norm(const NormArgs& a, int nr, hipStream_t s);
 int launch_quant_rows(const uint16_t* x, int xstride, int8_t* xq, int qstride, float* xs,
                       int sstride, int n, float in_scale, int nrows, hipStream_t s);
@@ -75,18 +73,20 @@ int launch_swiglu(const float* g, const float* u, int stride, int8_t* xq, float*
 
 // ---------------------------------------------------------------- GDN
 struct GdnArgs {
-    const uint16_t* qkv; int qkv_stride;          // conv'd q|k|v rows (bf16)
+    const uint16_t* qkv; int qkv_stride;          // raw (conv_w set) or conv'd q|k|v rows (bf16)
     const uint16_t* z; int z_stride;
     const float* a; const float* b; int ab_stride; // precomputed a/b (fp32), or
     const uint16_t* in_a; const uint16_t* in_b;  // bf16 weights [vh][H] with
     const uint16_t* ynorm; int ystride; int H;    // the bf16 normed rows (a/b fused)
     const uint16_t* A_log; const uint16_t* dt_bias; const uint16_t* norm_w;
+    const uint16_t* conv_w; uint16_t* conv_hist;  // conv in the kernel: weights, committed-history mirror
     float* S; void* pend; const int* npend_ptr; int npend_imm;
     int kh, vh, d; float eps;
     uint16_t* out; int out_stride; int8_t* xq; float* xs;
     const int* stop;
 };
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s);
+int gdn_set_lds_limit();
 // conv + SiLU with deferred commit as a standalone kernel (kernel-tier entry)
 int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_stride,
                     int nconv, const uint16_t* conv_w, uint16_t* conv_hist, uint16_t* pend_raw,

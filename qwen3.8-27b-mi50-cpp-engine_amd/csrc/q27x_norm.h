@@ -1,0 +1,124 @@
+// q27x_norm.h -- the RMSNorm + per-16 quantize of activation rows, as one 256-thread block.
+//
+// Canonical order (q27_rmsnorm_quant_fp8 / q27_rmsnorm_hostss_fp8_b, src/q27_fp8.hip): thread t
+// owns elements 1024 i + 4 t + e; its squares are accumulated with fmaf in (i, e) order, the four
+// waves reduce with the shfl_down tree and meet as ((w0 + w1) + w2) + w3; inv = 1/sqrt(ss/n + eps);
+// nrm = x * inv * (plus + w); a group of 16 is 4 adjacent threads (exact max, s = mx/127 * 1/in_scale).
+// Used by the standalone norm kernel (one block per row) and by the last block of a residual
+// projection (all rows of the step), so both write the same bits.
+#pragma once
+#include "q27x_dev.h"
+#include "q27x_int.h"
+
+namespace q27x {
+
+// Rows [r0, r0 + nrows) of `a` (source row index rs = row_sel ? *row_sel : r), RB rows per pass.
+// NCH = n / 1024. wsum: __shared__ float[RB][4]. Every thread of the 256-thread block calls it.
+template <int NCH, int RB>
+__device__ __forceinline__ void norm_rows(const NormArgs& a, int r0, int nrows, float (*wsum)[4]) {
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    constexpr int n = NCH * 1024;
+    float wf[NCH][4];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const uint2 wu = *(const uint2*)(a.w + i * 1024 + 4 * t);
+        wf[i][0] = __uint_as_float(wu.x << 16); wf[i][1] = __uint_as_float(wu.x & 0xFFFF0000u);
+        wf[i][2] = __uint_as_float(wu.y << 16); wf[i][3] = __uint_as_float(wu.y & 0xFFFF0000u);
+    }
+    const float g = 1.0f / a.in_scale;
+    for (int rb = 0; rb < nrows; rb += RB) {
+        float xv[RB][NCH][4];
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + rb + j;
+            if (rb + j >= nrows) break;
+            const int rs = a.row_sel ? *a.row_sel : r;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int k = i * 1024 + 4 * t;
+                float* v = xv[j][i];
+                if (a.emb) {
+                    const uint2 u = *(const uint2*)(a.emb + (size_t)a.tok[rs] * n + k);
+                    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
+                    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
+                } else if (a.x_bf16) {
+                    const uint2 u = *(const uint2*)((const uint16_t*)a.x + (size_t)rs * a.xstride + k);
+                    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
+                    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
+                } else {
+                    const float4 f = *(const float4*)((const float*)a.x + (size_t)rs * a.xstride + k);
+                    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + rb + j;
+            if (rb + j >= nrows) break;
+            const int rs = a.row_sel ? *a.row_sel : r;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int k = i * 1024 + 4 * t;
+                float* v = xv[j][i];
+                if (a.hout) {   // head: the final residual row, bf16(bf16(r1) + r2) or bf16(r2)
+                    uint16_t hb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float s = a.hadd ? bf2f(a.hadd[(size_t)rs * n + k + e]) + v[e] : v[e];
+                        hb[e] = f2bf(s);
+                        v[e] = bf2f(hb[e]);
+                    }
+                    *(uint2*)(a.hout + (size_t)r * n + k) = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
+                                                                      (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+                }
+                if (a.hcopy)
+                    *(uint2*)(a.hcopy + (size_t)r * n + k) =
+                        make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                                   (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(v[e], v[e], acc);
+            }
+            acc = tree64(acc);
+            if (lane == 0) wsum[j][wv] = acc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + rb + j;
+            if (rb + j >= nrows) break;
+            const float ss = ((wsum[j][0] + wsum[j][1]) + wsum[j][2]) + wsum[j][3];
+            const float inv = rsqrt_cr(ss * (1.0f / (float)n) + a.eps);
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int k = i * 1024 + 4 * t;
+                float nm[4];
+                uint16_t yb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    nm[e] = xv[j][i][e] * inv * (a.plus + wf[i][e]);
+                    yb[e] = f2bf(nm[e]);
+                }
+                if (a.y)
+                    *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                           (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                if (a.xq) {
+                    float q[4], mx = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { q[e] = a.quant_bf16 ? bf2f(yb[e]) : nm[e]; mx = fmaxf(mx, fabsf(q[e])); }
+                    mx = max_xor(mx, 4);
+                    const float s = mx * g * (1.0f / 127.0f);
+                    const float qi = (s > 0.0f) ? (g / s) : 0.0f;
+                    uint32_t pk = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(q[e], qi)) << (8 * e);
+                    *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
+                    if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
+                }
+            }
+        }
+        __syncthreads();   // wsum reused by the next pass
+    }
+}
+
+}  // namespace q27x
