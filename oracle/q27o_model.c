@@ -312,7 +312,7 @@ static int mtp_pass(q27o_model* m, int nr, const uint16_t* const* hrows, const i
     const int H = c->hidden, I = c->inter;
     const int qr = qrows_of(c), kvr = c->n_kv * c->head_dim, att = c->n_q * c->head_dim;
     const float po = c->mtp_plus_one ? 1.0f : 0.0f;
-    uint16_t* cat = (uint16_t*)malloc((size_t)nr * 2 * H * 2);
+    uint16_t* cat = (uint16_t*)calloc((size_t)nr * 2 * H, 2);
     uint16_t* t1 = (uint16_t*)malloc((size_t)nr * H * 2);
     int8_t* xa = (int8_t*)malloc((size_t)nr * (I > 2 * H ? I : 2 * H));
     float* sa = (float*)malloc((size_t)nr * (I > 2 * H ? I : 2 * H) / 16 * 4);
@@ -384,7 +384,7 @@ int q27o_model_prefill(q27o_model* m, const int32_t* ids, int n) {
     uint16_t* hall = (uint16_t*)malloc((size_t)n * H * 2);
     int32_t nx[8];
     int first = 0;
-    m->pos = 0;
+    q27o_model_reset(m);                       /* a prompt starts a new request */
     for (int c0 = 0; c0 < n; c0 += 8) {
         const int cn = (n - c0 < 8) ? n - c0 : 8;
         const int last = (c0 + cn == n);

@@ -1,0 +1,147 @@
+"""Float64 textbook forms of the verify-path operators, written from the mathematics (not from
+the oracle's code): the independent side of the oracle-pinning tests and of the golden fixtures.
+Nothing here mirrors a reduction order; agreement is asserted within stated tolerances."""
+import numpy as np
+
+
+def bf2f(b):
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_rne(x):
+    """Round float32 values to the nearest bf16 (ties to even mantissa), by comparing the two
+    neighbouring bf16 values in float64 -- no bit trick."""
+    x = np.asarray(x, np.float32)
+    u = x.view(np.uint32)
+    lo = (u >> 16).astype(np.uint32)                 # truncation (toward zero in magnitude)
+    hi = lo + 1
+    flo = (lo << 16).view(np.float32).astype(np.float64)
+    fhi = (hi << 16).view(np.float32).astype(np.float64)
+    xd = x.astype(np.float64)
+    dlo, dhi = np.abs(xd - flo), np.abs(fhi - xd)
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ((lo & 1) == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def quant_ideal(v, group):
+    """Symmetric absmax int8 quantization in float64: s = max|v|/127, q = round-half-even(v/s)."""
+    v = np.asarray(v, np.float64).reshape(-1, group)
+    mx = np.abs(v).max(axis=1, keepdims=True)
+    s = mx / 127.0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(s > 0, np.rint(v / np.where(s > 0, s, 1)), 0)
+    return np.clip(q, -127, 127).astype(np.int64).ravel(), s.ravel(), (v / np.where(s > 0, s, 1)).ravel()
+
+
+def assert_codes_match_ideal(codes, v, group, tie_tol=1e-4):
+    """int8 codes equal the float64 ideal except where v/s sits within tie_tol of a half-integer
+    (there float32 rounding may legitimately go either way, by one code)."""
+    q, s, t = quant_ideal(v, group)
+    codes = np.asarray(codes).astype(np.int64).ravel()
+    diff = codes != q
+    if diff.any():
+        near_tie = np.abs(np.abs(t - np.floor(t)) - 0.5) < tie_tol
+        bad = diff & ~(near_tie & (np.abs(codes - q) == 1))
+        assert not bad.any(), f"{bad.sum()} codes off the float64 ideal (first at {np.flatnonzero(bad)[:5]})"
+
+
+def silu(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))
+
+
+def softplus(x):
+    x = np.asarray(x, np.float64)
+    return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20))))
+
+
+def rmsnorm(x, w, plus, eps):
+    x = np.asarray(x, np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return x * inv * (plus + np.asarray(w, np.float64))
+
+
+def proj(Wq, Ws, xq, xs, alpha):
+    """y[n][r] = alpha * sum_k W[r][k] x[n][k] * ws[r][k/64] * xs[n][k/16] in float64."""
+    rows, K = Wq.shape
+    wd = Wq.astype(np.float64) * np.repeat(Ws.astype(np.float64), 64, axis=1)
+    xd = xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 16, axis=1)
+    return alpha * (xd @ wd.T)
+
+
+def gdn_rows(qkv_raw, z, a, b, A_log, dt_bias, norm_w, conv_w, S, hist, kh, vh, d, eps=1e-6):
+    """Gated delta rule, two-pass textbook form in float64 over nr rows.
+    Conv: causal depthwise over [h0, h1, h2, x] then SiLU (rounded to bf16, as the stored
+    activations are). Per value head h with key head h // (vh/kh):
+      q = q / ||q|| / sqrt(d), k = k / ||k||, beta = sigmoid(b), g = exp(-exp(A_log) softplus(a + dt))
+      S <- g S + k (beta (v - g S^T k))^T ;  o = S^T q  (state updated first, then read)
+      y = o / rms(o) * norm_w * silu(z).
+    S is key-major [h][key j][value e]. Returns y [nr][vh*d], new S, new history."""
+    S = np.array(S, np.float64, copy=True)
+    hist = np.array(bf2f(hist), np.float64).reshape(-1, 3)
+    cw = bf2f(conv_w).astype(np.float64).reshape(-1, 4)
+    nr = qkv_raw.shape[0]
+    ratio = vh // kh
+    ys = np.zeros((nr, vh * d))
+    for n in range(nr):
+        x = bf2f(qkv_raw[n]).astype(np.float64)
+        win = np.concatenate([hist, x[:, None]], axis=1)
+        acc = (win * cw).sum(axis=1)
+        cv = bf2f(bf16_rne(silu(acc).astype(np.float32))).astype(np.float64)
+        hist = win[:, 1:]
+        for h in range(vh):
+            kk = h // ratio
+            q = cv[kk * d:(kk + 1) * d]
+            k = cv[kh * d + kk * d: kh * d + (kk + 1) * d]
+            v = cv[2 * kh * d + h * d: 2 * kh * d + (h + 1) * d]
+            qh = q / np.sqrt((q * q).sum() + 1e-6) / np.sqrt(d)
+            khat = k / np.sqrt((k * k).sum() + 1e-6)
+            beta = sigmoid(b[n, h])
+            g = np.exp(-np.exp(float(bf2f(A_log)[h])) * softplus(a[n, h] + float(bf2f(dt_bias)[h])))
+            Sh = S[h]
+            delta = beta * (v - g * (Sh.T @ khat))
+            Sh = g * Sh + np.outer(khat, delta)
+            S[h] = Sh
+            o = Sh.T @ qh
+            zz = bf2f(z[n, h * d:(h + 1) * d]).astype(np.float64)
+            y = o / np.sqrt((o * o).mean() + eps) * bf2f(norm_w).astype(np.float64) * silu(zz)
+            ys[n, h * d:(h + 1) * d] = y
+    return ys, S, hist
+
+
+def rope_rotate(y, pos, rot, theta):
+    """Rotate-half RoPE on the first `rot` dims of y at position pos, float64."""
+    y = np.asarray(y, np.float64).copy()
+    half = rot // 2
+    f = np.arange(half)
+    ang = pos * theta ** (-(2.0 * f) / rot)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = y[:half].copy(), y[half:rot].copy()
+    y[:half] = a * c - b * s
+    y[half:rot] = b * c + a * s
+    return y
+
+
+def attention_rows(qh, gate_vals, Kd, Vd, nq, nkv, hd, pos0, nr):
+    """Causal GQA softmax attention in float64: row r attends keys 0..pos0+r; output times
+    sigmoid(gate) when gate_vals is given. qh [nr][nq*hd]; Kd/Vd dequantized [ctx][nkv*hd]."""
+    G = nq // nkv
+    out = np.zeros((nr, nq * hd))
+    for r in range(nr):
+        L = pos0 + r + 1
+        for h in range(nq):
+            kv = h // G
+            q = qh[r, h * hd:(h + 1) * hd].astype(np.float64)
+            K = Kd[:L, kv * hd:(kv + 1) * hd].astype(np.float64)
+            V = Vd[:L, kv * hd:(kv + 1) * hd].astype(np.float64)
+            sc = K @ q / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            o = (p @ V) / p.sum()
+            if gate_vals is not None:
+                o = o * sigmoid(gate_vals[r, h * hd:(h + 1) * hd])
+            out[r, h * hd:(h + 1) * hd] = o
+    return out
