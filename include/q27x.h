@@ -279,10 +279,19 @@ int q27x_generate(q27x_ctx* ctx, int max_new, int spec, int32_t* out, int* n_out
 int q27x_run_rounds(q27x_ctx* ctx, int n, int spec, q27x_stats* st);
 /* Time of one verify pass (64 layers + head, nr rows) averaged over iters, device events. */
 int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
-/* Time one projection launch of layer `layer` (which: 0 in_qkv|in_z, 1 gate|up, 2 down, 3 out_proj,
- * 4 lm_head) over iters launches with device events; reports ms per launch and its algorithmic
- * bytes (weights + scales + activations + outputs). */
+/* Time one projection launch of layer `layer` as the verify pass runs it (which: 0 in_qkv|in_z with
+ * its input-norm prologue, 1 gate|up with its post-norm prologue and SwiGLU epilogue, 2 down +
+ * residual, 3 out_proj + residual, 4 lm_head + argmax partials) over iters launches with device
+ * events on the context's stream, cycling through the layers so no launch finds its weights in the
+ * Infinity Cache; reports ms per launch and its algorithmic bytes (weights + scales + input rows +
+ * outputs). Overwrites the context's activation scratch. */
 int q27x_bench_kernel(q27x_ctx* ctx, int layer, int which, int nr, int iters, float* ms, double* bytes);
+/* HBM calibration (no reference counterpart): a streaming read (mode 0) or plain copy (mode 1) of
+ * `bytes` per launch, cycling through 1 GiB so no launch hits the 256 MB Infinity Cache; grid =
+ * CUs x blocks_per_cu blocks of 256 threads, `unroll` (1, 2, 4, 8) 16-byte loads in flight per
+ * thread. Reports ms per launch over iters launches (device events, null stream). Allocates and
+ * frees its own buffers. */
+int q27x_bench_stream(int mode, size_t bytes, int blocks_per_cu, int unroll, int iters, float* ms);
 /* Raw access for tests: copy a device tensor of the context to the host by name. */
 int q27x_debug_read(q27x_ctx* ctx, const char* name, int layer, void* dst, size_t bytes);
 

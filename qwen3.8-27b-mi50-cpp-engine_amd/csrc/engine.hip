@@ -91,7 +91,6 @@ struct q27x_ctx {
     // ACT (SwiGLU output), each kMaxRows rows; offsets in elements
     int8_t* xq = nullptr; float* xs = nullptr;
     size_t xb_off = 0, act_off = 0;
-    unsigned* tail_cnt = nullptr;                 // norm-tail counter of the residual projections
     uint16_t *pb = nullptr, *qh = nullptr, *ao = nullptr, *gout = nullptr;
     uint16_t *cat = nullptr, *mtp_hin = nullptr, *mtp_res = nullptr, *hprev = nullptr, *hcatch = nullptr;
     float* attn_work = nullptr; int max_splits = 0;
@@ -271,21 +270,18 @@ __global__ void k_accept_rows(const int32_t* nx, const int32_t* dt, int k, int32
 }
 
 // ---------------------------------------------------------------- the verify pass
-// Norms: each RMSNorm + quantize of the step's rows runs as the tail of the projection that
-// produces its input (the last block of that grid), so no norm is a launch of its own except the
-// first (from the embedding rows) and the head. norm_into() fills such a tail.
-static NormArgs norm_into(q27x_ctx* x, const void* src, int src_bf16, const uint16_t* w, float plus, int quant_bf16,
-                          uint16_t* hcopy, uint16_t* y, int8_t* xq, float* xs) {
+// Norms: each RMSNorm + quantize of the step's rows runs as the prologue of the projection that
+// consumes it (every block normalizes the rows into its own LDS stage; block 0 writes the bf16
+// side outputs), so no norm is a launch of its own except the head's. norm_of() describes one.
+static NormArgs norm_of(q27x_ctx* x, const void* src, int src_bf16, const uint16_t* w, float plus, int quant_bf16,
+                        uint16_t* hcopy, uint16_t* y) {
     NormArgs n{};
     n.x = src; n.x_bf16 = src_bf16; n.xstride = x->H; n.w = w; n.plus = plus; n.eps = x->c.rms_eps; n.n = x->H;
-    n.hcopy = hcopy; n.y = y; n.ystride = x->H; n.xq = xq; n.xs = xs; n.quant_bf16 = quant_bf16; n.in_scale = 1.0f;
+    n.hcopy = hcopy; n.y = y; n.ystride = x->H; n.quant_bf16 = quant_bf16; n.in_scale = 1.0f;
     n.stop = &x->dctl->stop;
     return n;
 }
-static void set_tail(q27x_ctx* x, ProjArgs& p, const NormArgs& n) {
-    p.has_tail = 1; p.tail_cnt = x->tail_cnt; p.tail = n;
-}
-static int tail_ok(const q27x_ctx* x) { return x->H == 1024 || x->H == 5120; }
+static void set_pre(ProjArgs& p, const NormArgs& n) { p.has_pre = 1; p.pre = n; }
 
 // run_layer_tp_nr on one card for nr rows: tokens d->vtok, positions d->pos.., GDN commits
 // d->gdn_npend pending rows. head: 0 = final residual rows only, 1 = + final norm, lm_head and
@@ -297,28 +293,28 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
     const int H = x->H, I = x->I;
     int8_t* xa = x->xq;  float* sa = x->xs;
     int8_t* xact = x->xq + x->act_off;  float* sact = x->xs + x->act_off / 16;
-    const int tails = tail_ok(x);
     int rc;
-    // layer 0 input norm from the bf16 embedding rows (quantize the bf16 normed rows,
-    // q27_rmsnorm_quant_fp8); h = bf16(x) and y = bf16(normed) for the GDN a/b GEMVs
-    {
-        NormArgs n = norm_into(x, nullptr, 1, x->L[0].in_norm, 1.0f, 1, x->hid, x->ynorm, xa, sa);
-        n.emb = x->emb; n.tok = d->vtok;
-        if ((rc = launch_norm(n, nr, s))) return rc;
-    }
     for (int l = 0; l < c.n_layers; ++l) {
         LayerDev& Y = x->L[l];
-        // post norm of r1 (fp32, quantize the fp32 normed rows): tail of the mixer's output projection
-        const NormArgs post = norm_into(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr, xa, sa);
+        // input norm. Layer 0: the bf16 embedding rows, quantizing the bf16 normed rows
+        // (q27_rmsnorm_quant_fp8); later layers: the fp32 residual r2, quantizing the fp32 normed
+        // rows (q27_rmsnorm_hostss_fp8_b). Side outputs h = bf16(x), y = bf16(normed) (GDN a/b).
+        NormArgs nin;
+        if (l == 0) {
+            nin = norm_of(x, nullptr, 1, Y.in_norm, 1.0f, 1, x->hid, x->ynorm);
+            nin.emb = x->emb; nin.tok = d->vtok;
+        } else {
+            nin = norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, x->ynorm);
+        }
         ProjArgs o{};
         o.alpha = 1.0f; o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
         o.res = x->hid; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f; o.stop = &d->stop;
-        if (tails) set_tail(x, o, post);
         if (Y.is_attn) {
             ProjArgs p{};
-            p.alpha = 1.0f; p.stop = &d->stop; p.xq = xa; p.xst = H; p.xs = sa;
+            p.alpha = 1.0f; p.stop = &d->stop;
             p.W = Y.qkv.w; p.WS = Y.qkv.s; p.rows = Y.qkv.rows; p.K = H;
             p.y = x->pb; p.ystride = Y.qkv.rows; p.out_bf16 = 1;
+            set_pre(p, nin);
             if ((rc = launch_proj(p, EPI_STORE, nr, s))) return rc;
             AttnArgs a{};
             a.qkv = x->pb; a.qkv_stride = Y.qkv.rows; a.q_norm_w = Y.q_norm; a.k_norm_w = Y.k_norm;
@@ -334,9 +330,10 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
             // in_qkv | in_z (raw bf16 rows; the conv runs inside the GDN kernel)
             const int rows = Y.qkvz.rows;
             ProjArgs p{};
-            p.alpha = 1.0f; p.stop = &d->stop; p.xq = xa; p.xst = H; p.xs = sa;
+            p.alpha = 1.0f; p.stop = &d->stop;
             p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = rows; p.K = H;
             p.y = x->pb; p.ystride = rows; p.out_bf16 = 1;
+            set_pre(p, nin);
             if ((rc = launch_proj(p, EPI_STORE, nr, s))) return rc;
             GdnArgs g{};
             g.qkv = x->pb; g.qkv_stride = rows; g.z = x->pb + x->nqkv; g.z_stride = rows;
@@ -350,26 +347,18 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
             o.W = Y.out_proj.w; o.WS = Y.out_proj.s; o.rows = H; o.K = x->nz; o.xq = xa; o.xst = x->nz; o.xs = sa;
         }
         if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
-        if (!tails && (rc = launch_norm(post, nr, s))) return rc;
+        // post norm of r1 (fp32, quantize the fp32 normed rows, h = bf16(r1)): gate|up prologue
         ProjArgs gu{};
         gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
-        gu.xq = xa; gu.xst = H; gu.xs = sa;
         gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f; gu.stop = &d->stop;
+        set_pre(gu, norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr));
         if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
         ProjArgs dn{};
         dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f;
         dn.xq = xact; dn.xst = I; dn.xs = sact;
         dn.y = x->xres; dn.ystride = H; dn.out_bf16 = 0;
         dn.res = x->hid; dn.res_bf16 = 1; dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
-        // next layer's input norm of r2 (fp32, quantize the fp32 normed rows,
-        // q27_rmsnorm_hostss_fp8_b): tail of the down projection
-        NormArgs nin{};
-        if (l + 1 < c.n_layers) {
-            nin = norm_into(x, x->xres, 0, x->L[l + 1].in_norm, 1.0f, 0, x->hid, x->ynorm, xa, sa);
-            if (tails) set_tail(x, dn, nin);
-        }
         if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
-        if (l + 1 < c.n_layers && !tails && (rc = launch_norm(nin, nr, s))) return rc;
     }
     // head (src/q27_main.cpp:2457-2481): final residual rows, final norm, lm_head, argmax
     NormArgs hn{};
@@ -401,36 +390,32 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     const int H = x->H, I = x->I;
     const float po = c.mtp_plus_one ? 1.0f : 0.0f;
     int8_t* xa = x->xq;  float* sa = x->xs;
-    int8_t* xb = x->xq + x->xb_off;  float* sb = x->xs + x->xb_off / 16;
     int8_t* xact = x->xq + x->act_off;  float* sact = x->xs + x->act_off / 16;
-    const int tails = tail_ok(x);
     int rc;
     // fc over [norm(emb) | norm(h)] (order by mtp_swap, src/q27_mtp_defs.h:108-109) as two K = H
-    // halves (per-16 groups never straddle halves); both halves quantize their bf16 normed rows
-    NormArgs ne = norm_into(x, nullptr, 1, x->pre_emb, po, 1, nullptr, nullptr, nullptr, nullptr);
+    // halves (per-16 groups never straddle halves); each half's norm (quantizing the bf16 normed
+    // rows) is the prologue of its fc projection
+    NormArgs ne = norm_of(x, nullptr, 1, x->pre_emb, po, 1, nullptr, nullptr);
     ne.emb = x->emb; ne.tok = d->mtp_tok;
-    NormArgs nh = norm_into(x, x->mtp_hin, 1, x->pre_hid, po, 1, nullptr, nullptr, nullptr, nullptr);
-    NormArgs& n0 = c.mtp_swap ? ne : nh;
-    NormArgs& n1 = c.mtp_swap ? nh : ne;
-    n0.xq = xa; n0.xs = sa; n1.xq = xb; n1.xs = sb;
-    if ((rc = launch_norm(n0, nr, s))) return rc;
-    if ((rc = launch_norm(n1, nr, s))) return rc;
+    NormArgs nh = norm_of(x, x->mtp_hin, 1, x->pre_hid, po, 1, nullptr, nullptr);
+    const NormArgs& n0 = c.mtp_swap ? ne : nh;
+    const NormArgs& n1 = c.mtp_swap ? nh : ne;
     ProjArgs f0{};
-    f0.W = x->fc0.w; f0.WS = x->fc0.s; f0.rows = H; f0.K = H; f0.alpha = 1.0f; f0.xq = xa; f0.xst = H; f0.xs = sa;
+    f0.W = x->fc0.w; f0.WS = x->fc0.s; f0.rows = H; f0.K = H; f0.alpha = 1.0f;
     f0.y = x->mtp_res; f0.ystride = H; f0.out_bf16 = 1; f0.stop = &d->stop;
+    set_pre(f0, n0);
     if ((rc = launch_proj(f0, EPI_STORE, nr, s))) return rc;
-    // input norm (bf16 residual, quantize the bf16 normed rows): tail of the second fc half
-    const NormArgs nin = norm_into(x, x->mtp_res, 1, Y.in_norm, po, 1, nullptr, nullptr, xa, sa);
     ProjArgs f1{};
-    f1.W = x->fc1.w; f1.WS = x->fc1.s; f1.rows = H; f1.K = H; f1.alpha = 1.0f; f1.xq = xb; f1.xst = H; f1.xs = sb;
+    f1.W = x->fc1.w; f1.WS = x->fc1.s; f1.rows = H; f1.K = H; f1.alpha = 1.0f;
     f1.y = x->mtp_res; f1.ystride = H; f1.out_bf16 = 1; f1.res = x->mtp_res; f1.res_bf16 = 1; f1.rstride = H;
     f1.rs = 1.0f; f1.stop = &d->stop;
-    if (tails) set_tail(x, f1, nin);
+    set_pre(f1, n1);
     if ((rc = launch_proj(f1, EPI_STORE, nr, s))) return rc;
-    if (!tails && (rc = launch_norm(nin, nr, s))) return rc;
+    // input norm (bf16 residual, quantize the bf16 normed rows): q|k|v prologue
     ProjArgs q{};
-    q.W = Y.qkv.w; q.WS = Y.qkv.s; q.rows = Y.qkv.rows; q.K = H; q.alpha = 1.0f; q.xq = xa; q.xst = H; q.xs = sa;
+    q.W = Y.qkv.w; q.WS = Y.qkv.s; q.rows = Y.qkv.rows; q.K = H; q.alpha = 1.0f;
     q.y = x->pb; q.ystride = Y.qkv.rows; q.out_bf16 = 1; q.stop = &d->stop;
+    set_pre(q, norm_of(x, x->mtp_res, 1, Y.in_norm, po, 1, nullptr, nullptr));
     if ((rc = launch_proj(q, EPI_STORE, nr, s))) return rc;
     AttnArgs a{};
     a.qkv = x->pb; a.qkv_stride = Y.qkv.rows; a.q_norm_w = Y.q_norm; a.k_norm_w = Y.k_norm;
@@ -442,19 +427,17 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     if ((rc = launch_attn_prep(a, nr, s))) return rc;
     if (kv_only) return Q27X_OK;
     if ((rc = launch_attn(a, nr, s))) return rc;
-    // o-proj rounded to bf16 before the residual add; post norm (bf16 residual, quantize the bf16
-    // normed rows) as its tail
-    const NormArgs npost = norm_into(x, x->mtp_res, 1, Y.post_norm, po, 1, nullptr, nullptr, xa, sa);
+    // o-proj rounded to bf16 before the residual add
     ProjArgs o{};
     o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.alpha = 1.0f; o.xq = xa; o.xst = x->att; o.xs = sa;
     o.y = x->mtp_res; o.ystride = H; o.out_bf16 = 1; o.res = x->mtp_res; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f;
     o.res_round = 1; o.stop = &d->stop;
-    if (tails) set_tail(x, o, npost);
     if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
-    if (!tails && (rc = launch_norm(npost, nr, s))) return rc;
+    // post norm (bf16 residual, quantize the bf16 normed rows): gate|up prologue
     ProjArgs gu{};
-    gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f; gu.xq = xa; gu.xst = H; gu.xs = sa;
+    gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
     gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f; gu.stop = &d->stop;
+    set_pre(gu, norm_of(x, x->mtp_res, 1, Y.post_norm, po, 1, nullptr, nullptr));
     if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
     ProjArgs dn{};
     dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f; dn.xq = xact; dn.xst = I;
@@ -594,7 +577,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     if (!cfg || !out) { set_error("q27x_ctx_create: null argument"); return Q27X_E_ARG; }
     *out = nullptr;
     const q27x_config& c = *cfg;
-    if (c.hidden % 1024 || c.hidden > 8192 || c.inter % 1024 || c.gdn_d != 128 || c.head_dim != 128 ||
+    if ((c.hidden != 1024 && c.hidden != 5120) || c.inter % 1024 || c.gdn_d != 128 || c.head_dim != 128 ||
         c.n_layers < 1 || c.attn_period < 1 || c.spec_k < 1 || c.spec_k > 7 || c.ctx < 16 || c.vocab < 16 ||
         c.gdn_vh % c.gdn_kh || c.n_q % c.n_kv || (c.n_q / c.n_kv) * 8 > 64 || c.kv_group < 16) {
         set_error("q27x_ctx_create: unsupported geometry");
@@ -672,7 +655,6 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     x->xs = (float*)salloc(x, xqn / 16 * 4);
     x->xb_off = R * maxk;
     x->act_off = 2 * R * maxk;
-    x->tail_cnt = (unsigned*)salloc(x, kArriveLines * 256);
     x->gout = (uint16_t*)salloc(x, R * (size_t)x->nz * 2);
     x->pb = (uint16_t*)salloc(x, pbn * 2);
     x->qh = (uint16_t*)salloc(x, R * (size_t)x->att * 2);
@@ -1082,16 +1064,18 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
         LayerDev& Y = x->L[l];
         ProjArgs p{};
         p.alpha = 1.0f; p.stop = &d->stop;
-        if (which == 0) {
-            p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+        if (which == 0) {   // as in the verify pass: input-norm prologue over the fp32 residual rows
+            p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H;
             p.y = x->pb; p.ystride = Y.qkvz.rows; p.out_bf16 = 1;
-            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * p.rows * 2;
-        } else if (which == 1) {
-            p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+            set_pre(p, norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, x->ynorm));
+            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * p.rows * 2;
+        } else if (which == 1) {   // post-norm prologue, SwiGLU + quantize epilogue
+            p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H;
             p.act_q = x->xq + x->act_off; p.act_s = x->xs + x->act_off / 16; p.act_stride = I;
             p.gscale = 1.0f;
+            set_pre(p, norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr));
             epi = EPI_SWIGLU;
-            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * I * (1 + 4.0 / 16);
+            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * I * (1 + 4.0 / 16);
         } else {
             const Mat& m = (which == 2) ? Y.down : Y.out_proj;
             p.W = m.w; p.WS = m.s; p.rows = H; p.K = m.K; p.xq = x->xq; p.xst = m.K; p.xs = x->xs;

@@ -11,6 +11,8 @@
 // dot products have issued, so a full group of loads stays in flight through the reduction and
 // the epilogue; epilogue inputs are requested before those refills (vector-memory counters
 // retire in order, so a later load would make its wait drain the prefetch).
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "q27x_dev.h"
@@ -50,22 +52,12 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
     return y;
 }
 
-// Norm tail of a residual projection: the last block of the grid normalizes the rows the grid
-// has just written (row count nr, n = NCH * 1024), three rows per pass.
-__device__ __forceinline__ void proj_tail(const ProjArgs& a, int nr, float (*wsum)[4], unsigned* s_last) {
-    if (!arrive_last(a.tail_cnt, gridDim.x, s_last)) return;
-    switch (a.tail.n >> 10) {
-        case 1: norm_rows<1, 3>(a.tail, 0, nr, wsum); break;
-        case 5: norm_rows<5, 3>(a.tail, 0, nr, wsum); break;
-        default: break;                                // rejected by the launcher
-    }
-}
-
 // One row group = RPW consecutive weight rows; a wave owns `upw` consecutive units of `urows`
 // rows (urows = RPW, or 32 for the SwiGLU epilogue whose unit is one 16-output quantization
 // group: 16 gate rows | 16 up rows), so every wave streams the same number of bytes.
-// FULL: K == 1024 * NSTEP (no slab bounds checks).
-template <int NR, int NSTEP, int RPW, int EPI, bool FULL>
+// FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
+// quantize of the raw input rows (a.pre), computed by every block (K = NSTEP * 1024).
+template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE>
 __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urows) {
     constexpr int SL = NSTEP * 64;
     constexpr int NT = kPW * 64;
@@ -73,19 +65,66 @@ __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urow
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
     __shared__ uint4 sx[NR * SL];
     __shared__ float ssc[NR * SL];
-    __shared__ float sacc[(EPI == EPI_SWIGLU) ? kPW * 32 * NR : 1];
-    __shared__ float wsum[3][4];
-    __shared__ unsigned s_last;
+    __shared__ float sacc[(EPI == EPI_SWIGLU) ? 2 * 32 * NR : 1];
+    __shared__ float wsum[PreNorm<NSTEP, NR>::RB][4];
     if (a.stop && *a.stop) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
-    const int gpu = urows / RPW;                       // groups per unit
     const int nunits = (a.rows + urows - 1) / urows;
-    const int gw = blockIdx.x * kPW + wave;
-    const int u0 = gw * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
-    const int g0 = u0 * gpu, g1 = u1 * gpu;
-    // activation stage: every load issued before any LDS write (one round trip)
-    {
+    // EPI_STORE: a wave owns `upw` units of RPW rows, group g = rows g*RPW ..;
+    // EPI_SWIGLU (RPW = 1): a block owns `upw` 32-row units and wave w streams rows 8w..8w+7 of
+    // each, group g = row 8w + (g & 7) of unit g >> 3
+    int g0, g1;
+    if constexpr (EPI == EPI_SWIGLU) {
+        static_assert(RPW == 1 && kPW == 4, "SwiGLU units are 4 waves x 8 rows");
+        const int u0 = blockIdx.x * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
+        g0 = u0 * 8; g1 = u1 * 8;
+    } else {
+        const int gpu = urows / RPW;
+        const int gw = blockIdx.x * kPW + wave;
+        const int u0 = gw * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
+        g0 = u0 * gpu; g1 = u1 * gpu;
+    }
+    uint4 W[RPW][NSTEP];
+    float S[RPW][NSTEP];
+    auto ld = [&](int g, int r, int t) __attribute__((always_inline)) {
+        int row = (EPI == EPI_SWIGLU) ? (g >> 3) * 32 + 8 * wave + (g & 7) : g * RPW + r;
+        row = row < a.rows ? row : a.rows - 1;
+        const int s = t * 64 + lane;
+        if (FULL || s < nslab) {
+            W[r][t] = ld_nt16(a.W + (size_t)row * K + 16 * s);
+            S[r][t] = a.WS[(size_t)row * ng64 + (s >> 2)];
+        } else {
+            W[r][t] = make_uint4(0u, 0u, 0u, 0u);
+            S[r][t] = 0.0f;
+        }
+    };
+    auto prefetch = [&]() __attribute__((always_inline)) {
+        if (g0 < g1) {
+#pragma unroll
+            for (int t = 0; t < NSTEP; ++t)
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) ld(g0, r, t);
+        }
+    };
+    if constexpr (PRE) {
+        // input rows first, then the weights, so waiting for the rows leaves the weights in flight
+        PreNorm<NSTEP, NR> pn;
+        constexpr int RB = PreNorm<NSTEP, NR>::RB;
+        pn.load_w(a.pre);
+        pn.load_x(a.pre, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch();
+        __builtin_amdgcn_sched_barrier(0);
+        const bool writer = blockIdx.x == 0;
+        pn.finish(a.pre, 0, (uint32_t*)sx, ssc, SL, wsum, writer);
+#pragma unroll
+        for (int r0 = RB; r0 < NR; r0 += RB) {
+            pn.load_x(a.pre, r0);
+            pn.finish(a.pre, r0, (uint32_t*)sx, ssc, SL, wsum, writer);
+        }
+    } else {
+        // activation stage: every load issued before any LDS write (one round trip)
         uint4 tv[NSTG];
         float ts[NSTG];
 #pragma unroll
@@ -104,26 +143,7 @@ __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urow
             const int i = threadIdx.x + j * NT;
             if (i < NR * SL) { sx[i] = tv[j]; ssc[i] = ts[j]; }
         }
-    }
-    uint4 W[RPW][NSTEP];
-    float S[RPW][NSTEP];
-    auto ld = [&](int g, int r, int t) __attribute__((always_inline)) {
-        int row = g * RPW + r;
-        row = row < a.rows ? row : a.rows - 1;
-        const int s = t * 64 + lane;
-        if (FULL || s < nslab) {
-            W[r][t] = ld_nt16(a.W + (size_t)row * K + 16 * s);
-            S[r][t] = a.WS[(size_t)row * ng64 + (s >> 2)];
-        } else {
-            W[r][t] = make_uint4(0u, 0u, 0u, 0u);
-            S[r][t] = 0.0f;
-        }
-    };
-    if (g0 < g1) {
-#pragma unroll
-        for (int t = 0; t < NSTEP; ++t)
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) ld(g0, r, t);
+        prefetch();
     }
     __syncthreads();
     const int vi = lane / LPV;                         // the value this lane holds after the tree
@@ -178,37 +198,33 @@ __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urow
                     v = v + a.rs * rv;
                 }
                 const size_t yi = (size_t)hn * a.ystride + row;
-                if (a.has_tail) {                      // read back by the tail block
-                    if (a.out_bf16) st_agent((uint16_t*)a.y + yi, f2bf(v));
-                    else st_agent((float*)a.y + yi, v);
-                } else if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
+                if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
                 else ((float*)a.y)[yi] = v;
             }
         } else {   // EPI_SWIGLU: 32 rows [16 gate | 16 up] -> 16 outputs, one quantization group
-            const int gi = g % gpu;
-            float* sw = sacc + wave * 32 * NR;
-            if (holder) sw[(gi * RPW + hr) * NR + hn] = tv;
-            if (gi == gpu - 1) {
-                __builtin_amdgcn_wave_barrier();
-                const int unit = g / gpu, j = lane & 15;
+            float* sw = sacc + ((g >> 3) & 1) * 32 * NR;   // double buffer: one barrier per unit
+            if (holder) sw[(8 * wave + (g & 7)) * NR + hn] = tv;
+            if ((g & 7) == 7) {
+                __syncthreads();
+                if (wave == 0) {
+                    const int unit = g >> 3, j = lane & 15;
 #pragma unroll
-                for (int nn = 0; nn < NR; ++nn) {
-                    const float gv = sw[j * NR + nn], uv = sw[(16 + j) * NR + nn];
-                    const float swv = gv / (1.0f + qexp(-gv));
-                    const float v = swv * uv * a.gscale;
-                    const float mx = max_xor(fabsf(v), 16);
-                    const float sc = mx * (1.0f / 127.0f);
-                    const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
-                    if (lane < 16) {
-                        a.act_q[(size_t)nn * a.act_stride + unit * 16 + j] = qcode(v, inv);
-                        if (j == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
+                    for (int nn = 0; nn < NR; ++nn) {
+                        const float gv = sw[j * NR + nn], uv = sw[(16 + j) * NR + nn];
+                        const float swv = gv / (1.0f + qexp(-gv));
+                        const float v = swv * uv * a.gscale;
+                        const float mx = max_xor(fabsf(v), 16);
+                        const float sc = mx * (1.0f / 127.0f);
+                        const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+                        if (lane < 16) {
+                            a.act_q[(size_t)nn * a.act_stride + unit * 16 + j] = qcode(v, inv);
+                            if (j == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
+                        }
                     }
                 }
-                __builtin_amdgcn_wave_barrier();
             }
         }
     }
-    if (EPI == EPI_STORE && a.has_tail) proj_tail(a, a.tail_rows, wsum, &s_last);
 }
 
 static int g_ncu = 0;
@@ -223,41 +239,68 @@ static int num_cus() {
     return g_ncu;
 }
 
-// Launch shape: units spread over num_cus() * wpc waves (wpc measured on MI355X: 16 for the
+// Launch shape. EPI_STORE: units spread over num_cus() * wpc waves (16 waves per CU for the
 // K <= 6144 shapes, 8 for K = 17408 whose 17 KiB-per-row prefetch holds ~250 VGPRs).
-template <int NR, int NSTEP, int EPI, bool FULL>
+// EPI_SWIGLU: 32-row units spread over num_cus() * bpc blocks of 4 waves. Both knobs can be
+// overridden for launch-shape sweeps (Q27X_WPC5, Q27X_WPC17, Q27X_GU_BPC).
+static int env_knob(const char* name, int def, int lo, int hi) {
+    const char* v = getenv(name);
+    if (!v || !*v) return def;
+    const int x = atoi(v);
+    return (x < lo) ? lo : (x > hi ? hi : x);
+}
+static int knob_wpc5() { static const int v = env_knob("Q27X_WPC5", 16, 4, 32); return v; }
+static int knob_wpc17() { static const int v = env_knob("Q27X_WPC17", 8, 4, 16); return v; }
+static int knob_gu_bpc() { static const int v = env_knob("Q27X_GU_BPC", 2, 1, 8); return v; }
+
+template <int NR, int NSTEP, int EPI, bool FULL, bool PRE>
 static int run_proj(const ProjArgs& a, hipStream_t s) {
     constexpr int RPW = 1;
     const int urows = (EPI == EPI_SWIGLU) ? 32 : RPW;
     const int nunits = (a.rows + urows - 1) / urows;
-    const int wpc = (NSTEP >= 17) ? 8 : 16;
-    const int wmax = num_cus() * wpc;
-    const int upw = (nunits + wmax - 1) / wmax;
-    const int waves = (nunits + upw - 1) / upw;
-    const int grid = (waves + kPW - 1) / kPW;
-    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL>), dim3(grid), dim3(kPW * 64), 0, s, a, upw, urows);
+    int upw, grid;
+    if (EPI == EPI_SWIGLU) {
+        const int bmax = num_cus() * knob_gu_bpc();
+        upw = (nunits + bmax - 1) / bmax;
+        grid = (nunits + upw - 1) / upw;
+    } else {
+        const int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
+        const int wmax = num_cus() * wpc;
+        upw = (nunits + wmax - 1) / wmax;
+        const int waves = (nunits + upw - 1) / upw;
+        grid = (waves + kPW - 1) / kPW;
+    }
+    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL, PRE>), dim3(grid), dim3(kPW * 64), 0, s, a, upw, urows);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
 
 // Shape router. NSTEP = ceil(K/1024); the LDS stage is NR*NSTEP*1280 B, so K = 17408 at NR > 4
-// (174 KB at NR = 8) is split by the caller into launches of <= 4 rows.
+// (174 KB at NR = 8) is split by the caller into launches of <= 4 rows. The norm prologue (PRE)
+// exists for the hidden sizes K = 1024 and 5120, the inputs of the layers' first projections.
 template <int NR, int EPI, bool FULL>
 static int route_k(const ProjArgs& a, hipStream_t s) {
     const int ns = (a.K + 1023) / 1024;
+    if (a.has_pre) {
+        if constexpr (FULL) {
+            if (ns == 1) return run_proj<NR, 1, EPI, true, true>(a, s);
+            if (ns == 5) return run_proj<NR, 5, EPI, true, true>(a, s);
+        }
+        return -2;
+    }
     if constexpr (EPI == EPI_SWIGLU) {
-        if (ns == 1) return run_proj<NR, 1, EPI, FULL>(a, s);
-        if (ns == 5) return run_proj<NR, 5, EPI, FULL>(a, s);
+        if (ns == 1) return run_proj<NR, 1, EPI, FULL, false>(a, s);
+        if (ns == 5) return run_proj<NR, 5, EPI, FULL, false>(a, s);
         return -2;
     } else {
         switch (ns) {
-            case 1: return run_proj<NR, 1, EPI, FULL>(a, s);
-            case 2: return run_proj<NR, 2, EPI, FULL>(a, s);
-            case 4: return run_proj<NR, 4, EPI, FULL>(a, s);
-            case 5: return run_proj<NR, 5, EPI, FULL>(a, s);
-            case 6: return run_proj<NR, 6, EPI, FULL>(a, s);
+            case 1: return run_proj<NR, 1, EPI, FULL, false>(a, s);
+            case 2: return run_proj<NR, 2, EPI, FULL, false>(a, s);
+            case 4: return run_proj<NR, 4, EPI, FULL, false>(a, s);
+            case 5: return run_proj<NR, 5, EPI, FULL, false>(a, s);
+            case 6: return run_proj<NR, 6, EPI, FULL, false>(a, s);
             case 17:
-                if constexpr (NR <= 4) return run_proj<NR, 17, EPI, FULL>(a, s);
+                if constexpr (NR <= 4) return run_proj<NR, 17, EPI, FULL, false>(a, s);
                 return -2;
             default: return -2;
         }
@@ -290,21 +333,23 @@ int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
         set_error("proj: bad arguments (rows=%d K=%d nr=%d)", a.rows, a.K, nr);
         return Q27X_E_ARG;
     }
-    if (!a.xq || !a.xs) { set_error("proj: no activations"); return Q27X_E_ARG; }
-    if ((a.xst & 15) || a.xst < a.K) { set_error("proj: activation stride %d must be >= K and a multiple of 16", a.xst); return Q27X_E_ARG; }
-    if (a.res && ((size_t)a.res & 3)) { set_error("proj: residual must be 4-byte aligned"); return Q27X_E_ARG; }
-    if (epi == EPI_SWIGLU && (a.rows & 31)) { set_error("proj: SwiGLU rows %d not a multiple of 32", a.rows); return Q27X_E_SHAPE; }
-    if (a.has_tail) {
-        if (epi != EPI_STORE || !a.tail_cnt || !a.tail.w || !(a.tail.n == 1024 || a.tail.n == 5120) || a.tail.emb ||
-            a.tail.hout || a.tail.row_sel) {
-            set_error("proj: unsupported norm tail (n=%d)", a.tail.n);
+    if (a.has_pre) {
+        const NormArgs& n = a.pre;
+        if (n.n != a.K || !(a.K == 1024 || a.K == 5120) || !n.w || (!n.x && !(n.emb && n.tok)) || n.hout ||
+            n.hadd || n.row_sel || (!n.x_bf16 && !n.emb && (n.xstride & 3)) || (n.xstride & 3) ||
+            (n.xq && !n.xs) || (n.y && (n.ystride & 3))) {
+            set_error("proj: unsupported norm prologue (n=%d K=%d)", n.n, a.K);
             return Q27X_E_SHAPE;
         }
+    } else {
+        if (!a.xq || !a.xs) { set_error("proj: no activations"); return Q27X_E_ARG; }
+        if ((a.xst & 15) || a.xst < a.K) { set_error("proj: activation stride %d must be >= K and a multiple of 16", a.xst); return Q27X_E_ARG; }
     }
+    if (a.res && ((size_t)a.res & 3)) { set_error("proj: residual must be 4-byte aligned"); return Q27X_E_ARG; }
+    if (epi == EPI_SWIGLU && (a.rows & 31)) { set_error("proj: SwiGLU rows %d not a multiple of 32", a.rows); return Q27X_E_SHAPE; }
     int rc;
     if (epi == EPI_STORE && a.K > 8192 && nr > 4) {   // LDS stage limit: two launches of <= 4 rows
         ProjArgs b = a;
-        b.has_tail = 0;                               // the tail runs once, after the second
         rc = route(b, EPI_STORE, 4, s);
         if (rc) return rc == -2 ? (set_error("proj: no kernel for K=%d", a.K), Q27X_E_SHAPE) : rc;
         b.xq = a.xq + (size_t)4 * a.xst;
@@ -312,13 +357,9 @@ int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
         const size_t esz = a.out_bf16 ? 2 : 4;
         b.y = (char*)a.y + (size_t)4 * a.ystride * esz;
         if (a.res) b.res = (const char*)a.res + (size_t)4 * a.rstride * (a.res_bf16 ? 2 : 4);
-        b.has_tail = a.has_tail;
-        b.tail_rows = nr;
         rc = route(b, EPI_STORE, nr - 4, s);
     } else {
-        ProjArgs b = a;
-        b.tail_rows = nr;
-        rc = route(b, epi, nr, s);
+        rc = route(a, epi, nr, s);
     }
     if (rc == -2) { set_error("proj: no kernel for K=%d nr=%d epi=%d", a.K, nr, epi); return Q27X_E_SHAPE; }
     return rc;

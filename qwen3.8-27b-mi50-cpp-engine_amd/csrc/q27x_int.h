@@ -44,9 +44,9 @@ struct ProjArgs {
     // EPI_SWIGLU: the weight rows interleave 16 gate rows and 16 up rows per block of 32
     int8_t* act_q; float* act_s; int act_stride; float gscale;
     const int* stop;             // early exit when *stop != 0
-    // EPI_STORE tail: the last block of the grid runs `tail` (RMSNorm + quantize of the rows just
-    // written) once every block's stores are visible; tail_cnt is a zeroed counter it resets
-    int has_tail; unsigned* tail_cnt; int tail_rows; NormArgs tail;
+    // norm prologue: instead of xq/xs, every block stages the RMSNorm + quantize of the raw rows
+    // described by `pre` (K = pre.n); block 0 also writes pre's side outputs (hcopy, y, xq/xs)
+    int has_pre; NormArgs pre;
 };
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
 

@@ -122,3 +122,116 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int r0, int nrows, 
 }
 
 }  // namespace q27x
+
+namespace q27x {
+
+// Prologue form of the same RMSNorm + quantize: every 256-thread block of a consumer projection
+// normalizes the NR input rows itself (n = NCH * 1024 = the projection's K) and writes the codes
+// and scales straight into its LDS activation stage, in the slab layout of k_proj: element
+// k = 1024 i + 4 t + e lands in slab 64 i + t/4 at byte 4 (t % 4). The order of every operation
+// is the canonical one above, so all blocks hold the same bits as a standalone norm would write.
+// Block 0 also stores the side outputs (hcopy, y, xq/xs) for later kernels. Loads are split from
+// the arithmetic so the caller can issue its weight prefetch in between (vector-memory counters
+// retire in order: the input rows must be requested before the weights to be waited on alone).
+template <int NCH, int NR>
+struct PreNorm {
+    static constexpr int RB = NR <= 4 ? NR : 4;   // rows held in registers per pass
+    uint2 wb[NCH];                                // 4 bf16 norm weights per chunk
+    float xv[RB][NCH][4];
+
+    __device__ __forceinline__ void load_w(const NormArgs& a) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) wb[i] = *(const uint2*)(a.w + i * 1024 + 4 * t);
+    }
+    __device__ __forceinline__ void load_x(const NormArgs& a, int r0) {
+        const int t = threadIdx.x;
+        constexpr int n = NCH * 1024;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + j;
+            if (r >= NR) break;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int k = i * 1024 + 4 * t;
+                float* v = xv[j][i];
+                if (a.emb || a.x_bf16) {
+                    const uint16_t* src = a.emb ? a.emb + (size_t)a.tok[r] * n : (const uint16_t*)a.x + (size_t)r * a.xstride;
+                    const uint2 u = *(const uint2*)(src + k);
+                    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
+                    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
+                } else {
+                    const float4 f = *(const float4*)((const float*)a.x + (size_t)r * a.xstride + k);
+                    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+                }
+            }
+        }
+    }
+    // sxw: the LDS code stage as 32-bit words ([NR][SL] slabs of 4 words); ssc: [NR][SL] scales
+    __device__ __forceinline__ void finish(const NormArgs& a, int r0, uint32_t* sxw, float* ssc, int SL,
+                                           float (*wsum)[4], bool writer) {
+        const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+        constexpr int n = NCH * 1024;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + j;
+            if (r >= NR) break;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const float* v = xv[j][i];
+                if (writer && a.hcopy)
+                    *(uint2*)(a.hcopy + (size_t)r * n + i * 1024 + 4 * t) =
+                        make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                                   (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(v[e], v[e], acc);
+            }
+            acc = tree64(acc);
+            if (lane == 0) wsum[j][wv] = acc;
+        }
+        __syncthreads();
+        const float g = 1.0f / a.in_scale;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + j;
+            if (r >= NR) break;
+            const float ss = ((wsum[j][0] + wsum[j][1]) + wsum[j][2]) + wsum[j][3];
+            const float inv = rsqrt_cr(ss * (1.0f / (float)n) + a.eps);
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int k = i * 1024 + 4 * t;
+                const float wf[4] = {__uint_as_float(wb[i].x << 16), __uint_as_float(wb[i].x & 0xFFFF0000u),
+                                     __uint_as_float(wb[i].y << 16), __uint_as_float(wb[i].y & 0xFFFF0000u)};
+                float nm[4], q[4], mx = 0.0f;
+                uint16_t yb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    nm[e] = xv[j][i][e] * inv * (a.plus + wf[e]);
+                    yb[e] = f2bf(nm[e]);
+                    q[e] = a.quant_bf16 ? bf2f(yb[e]) : nm[e];
+                    mx = fmaxf(mx, fabsf(q[e]));
+                }
+                if (writer && a.y)
+                    *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                           (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                mx = max_xor(mx, 4);
+                const float s = mx * g * (1.0f / 127.0f);
+                const float qi = (s > 0.0f) ? (g / s) : 0.0f;
+                uint32_t pk = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(q[e], qi)) << (8 * e);
+                const int slab = 64 * i + (t >> 2);
+                sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
+                if ((t & 3) == 0) ssc[r * SL + slab] = s;
+                if (writer && a.xq) {
+                    *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
+                    if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
+                }
+            }
+        }
+        __syncthreads();   // wsum is reused by the next pass
+    }
+};
+
+}  // namespace q27x

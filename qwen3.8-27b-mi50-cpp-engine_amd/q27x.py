@@ -97,6 +97,7 @@ _SIGS = {
     "q27x_run_rounds": ([VP, I, I, VP], I),
     "q27x_bench_kernel": ([VP, I, I, I, I, VP, VP], I),
     "q27x_debug_read": ([VP, ctypes.c_char_p, I, VP, SZ], I),
+    "q27x_bench_stream": ([I, SZ, I, I, I, VP], I),
 }
 
 
