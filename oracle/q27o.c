@@ -564,8 +564,8 @@ static float score_seq(const float* q, const float* k, int hd) {
 #define Q27O_SPLIT 64
 /* src/q27_attn.hip:258-463 semantics (GQA, causal over pos0+r, log2-domain softmax, split
  * combine, sigmoid output gate); this build's order: fixed 64-key splits, scores summed over the
- * head dims in order, two-pass softmax per split with keys in ascending order, splits combined in
- * ascending order. */
+ * head dims in order, per split m = max, p = 2^(x - m), l = shfl_down tree over the split's 64
+ * lanes, o = fmaf over the keys in ascending order; splits combined in ascending order. */
 void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
                     const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
                     int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
@@ -598,14 +598,17 @@ void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride
                     xsc[k - k0] = x;
                     m = fmaxf(m, x);
                 }
-                float l = 0.0f;
+                /* l: the 64 keys' p (0 past the valid ones) summed by the shfl_down tree */
+                float pl[Q27O_SPLIT];
+                for (int i = 0; i < Q27O_SPLIT; ++i) pl[i] = 0.0f;
                 for (int i = 0; i < hd; ++i) os[i] = 0.0f;
                 for (int k = k0; k < k1; ++k) {
                     const float p = q27o_exp2(xsc[k - k0] - m);
-                    l = l + p;
+                    pl[k - k0] = p;
                     const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
                     for (int i = 0; i < hd; ++i) os[i] = fmaf(p, (float)vc[off + i] * vs[(off + i) / kv_group], os[i]);
                 }
+                const float l = tree64(pl);
                 ms[s] = m; ls[s] = l;
                 memcpy(ob + (size_t)s * hd, os, (size_t)hd * sizeof(float));
                 M = fmaxf(M, m);

@@ -83,11 +83,21 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
 }
 
 // work layout: o [nr][nq][ms][hd] | m [nr][nq][ms] | l [nr][nq][ms]
-// Block = (split of 64 keys, kv head), all rows and all GQA heads of the kv head. Scores are
-// register-tiled (one query x 4 keys per thread, fmaf over the 128 dims in order), the softmax of a
-// split is two-pass in base 2 with keys in order, P.V is register-tiled (4 queries x 4 dims per
-// thread, keys in order).
-__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
+// Block = (split of 64 keys, kv head), all rows and all GQA heads of the kv head (nqr query
+// vectors), 8 waves. The block requests its int8 K and V tiles, their scales and the queries up
+// front, dequantizes K and V once into LDS as fp32 (k8 * ks, v8 * vs: the host restatement's
+// values), K rows padded to 132 floats so 16 lanes reading 16 different keys hit distinct banks.
+//   scores: lane = key, wave w = queries w + 8 i (i < NQW); x = sl2e * (fmaf over the 128 dims in
+//           order of q[d] * k[d]);
+//   softmax of the split: m = wave max over the valid keys, p = 2^(x - m), l = shfl_down tree of
+//           the 64 lanes' p (0 for invalid keys);
+//   P.V: thread = (4 dims, queries t/32 + 16 u, u < QPT), o = fmaf(p_k, v_k, o) over the valid keys
+//        in order.
+// Dynamic LDS: queries [nqr][128] fp32 | p [nqr][65] fp32.
+constexpr int kKStride = kHD + 4;
+constexpr int kAttnThreads = 512;
+template <int NQW, int QPT>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
     if (a.stop && *a.stop) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
@@ -97,110 +107,159 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a, int nr) {
     const int nqr = nact * G;                       // query vectors of this kv head
     const int kvrows = a.nkv * kHD;
     const int ms = a.max_splits;
-    __shared__ float qf[kMaxQ][kHD + 4];
-    __shared__ float kd[kSplit][kHD + 4];
-    __shared__ float vd[kSplit][kHD + 4];
-    __shared__ float sc[kMaxQ][kSplit + 4];
-    const int t = threadIdx.x;
-    for (int i = t; i < nqr * (kHD / 8); i += 256) {
-        const int qi = i / (kHD / 8), c = i - qi * (kHD / 8);
-        const int r = qi / G, g = qi - r * G;
-        const uint4 u = *(const uint4*)(a.qh + (size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + 8 * c);
-        float* dst = &qf[qi][8 * c];
-        dst[0] = __uint_as_float(u.x << 16); dst[1] = __uint_as_float(u.x & 0xFFFF0000u);
-        dst[2] = __uint_as_float(u.y << 16); dst[3] = __uint_as_float(u.y & 0xFFFF0000u);
-        dst[4] = __uint_as_float(u.z << 16); dst[5] = __uint_as_float(u.z & 0xFFFF0000u);
-        dst[6] = __uint_as_float(u.w << 16); dst[7] = __uint_as_float(u.w & 0xFFFF0000u);
-    }
+    const int gpr = kHD / a.kv_group;               // scale groups per head row
+    const int gsh = __builtin_ctz(a.kv_group);      // kv_group is a power of two
+    __shared__ float kd[kSplit * kKStride];
+    __shared__ float vd[kSplit * kHD];
+    extern __shared__ float dyn[];
+    float* qf = dyn;                                // [nqr_max][kHD]
+    float* sp = dyn + (size_t)nr * G * kHD;         // [nqr_max][kSplit + 1]
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     float* wo = a.work;
     float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
     float* wl = wm + (size_t)nr * a.nq * ms;
+    bool staged_q = false;
     for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
         const int k0 = s * kSplit;
         const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
-        __syncthreads();   // previous split's tiles (and the query stage) are complete
-        // K/V tiles: 16 int8 per thread-load, dequantised (k8 * scale) into LDS
-        for (int i = t; i < 2 * nk * (kHD / 16); i += 256) {
-            const int isv = i >= nk * (kHD / 16);
-            const int j = isv ? i - nk * (kHD / 16) : i;
-            const int k = j / (kHD / 16), c = j - k * (kHD / 16);
-            const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + 16 * c;
-            const uint4 u = *(const uint4*)((isv ? a.vc : a.kc) + off);
-            const float scl = (isv ? a.vs : a.ks)[off / a.kv_group];
-            float* dst = isv ? &vd[k][16 * c] : &kd[k][16 * c];
-            const uint32_t w4[4] = { u.x, u.y, u.z, u.w };
+        // ---- loads: thread covers 16-byte words i = t and t + 512 (K words 0..511, V 512..1023)
+        uint4 kv4[2];
+        float scl[2];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) dst[e] = (float)(int8_t)(w4[e >> 2] >> (8 * (e & 3))) * scl;
-        }
-        __syncthreads();
-        // scores: thread = (query, 4 consecutive keys); sum over dims in order
-        for (int i = t; i < nqr * (kSplit / 4); i += 256) {
-            const int qi = i / (kSplit / 4), kb = (i - qi * (kSplit / 4)) * 4;
-            if (kb >= nk) continue;
-            float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
-            const int kk1 = kb + 1 < nk ? kb + 1 : kb, kk2 = kb + 2 < nk ? kb + 2 : kb, kk3 = kb + 3 < nk ? kb + 3 : kb;
-#pragma unroll 8
-            for (int dd = 0; dd < kHD; ++dd) {
-                const float qv = qf[qi][dd];
-                acc0 = __builtin_fmaf(qv, kd[kb][dd], acc0);
-                acc1 = __builtin_fmaf(qv, kd[kk1][dd], acc1);
-                acc2 = __builtin_fmaf(qv, kd[kk2][dd], acc2);
-                acc3 = __builtin_fmaf(qv, kd[kk3][dd], acc3);
-            }
-            sc[qi][kb] = acc0 * a.sl2e;
-            if (kb + 1 < nk) sc[qi][kb + 1] = acc1 * a.sl2e;
-            if (kb + 2 < nk) sc[qi][kb + 2] = acc2 * a.sl2e;
-            if (kb + 3 < nk) sc[qi][kb + 3] = acc3 * a.sl2e;
-        }
-        __syncthreads();
-        // per query: max over the split's valid keys, p = 2^(x - m) in place, l = sum in key order
-        if (t < nqr) {
-            const int qi = t, r = qi / G, g = qi - r * G;
-            const int L = pos0 + r + 1;
-            const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
-            if (nv > 0) {
-                float m = -__builtin_huge_valf();
-                for (int k = 0; k < nv; ++k) m = fmaxf(m, sc[qi][k]);
-                float l = 0.0f;
-                for (int k = 0; k < nv; ++k) { const float p = qexp2(sc[qi][k] - m); sc[qi][k] = p; l = l + p; }
-                const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
-                wm[mi] = m;
-                wl[mi] = l;
+        for (int u = 0; u < 2; ++u) {
+            const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
+            kv4[u] = make_uint4(0u, 0u, 0u, 0u);
+            scl[u] = 0.0f;
+            if (k < nk) {
+                const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + 16 * c;
+                kv4[u] = *(const uint4*)((isv ? a.vc : a.kc) + off);
+                scl[u] = (isv ? a.vs : a.ks)[off >> gsh];
             }
         }
-        __syncthreads();
-        // o = sum_k p_k v_k in key order: thread = (4 queries, 4 dims)
-        for (int i = t; i < ((nqr + 3) / 4) * (kHD / 4); i += 256) {
-            const int qb = (i / (kHD / 4)) * 4, db = (i % (kHD / 4)) * 4;
-            float o[4][4];
-            int nvq[4];
+        uint4 q4[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+        if (!staged_q) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int qi = qb + u;
-                const int L = pos0 + qi / G + 1;
-                nvq[u] = (qi < nqr) ? ((L - k0 < nk) ? (L - k0) : nk) : 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[u][e] = 0.0f;
+            for (int u = 0; u < 2; ++u) {
+                const int i = t + kAttnThreads * u;   // query vector i/16, 8 dims (i%16)*8
+                const int qi = i >> 4, c = i & 15;
+                if (qi < nqr) {
+                    const int r = qi / G, g = qi - r * G;
+                    q4[u] = *(const uint4*)(a.qh + (size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + 8 * c);
+                }
             }
-            const int kmax = nvq[0] > nvq[3] ? (nvq[0] > nvq[1] ? nvq[0] : nvq[1]) : (nvq[3] > nvq[2] ? nvq[3] : nvq[2]);
-            for (int k = 0; k < kmax; ++k) {
-                const float4 v4 = *(const float4*)&vd[k][db];
+        }
+        __syncthreads();                           // the previous split's tiles are consumed
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if (k < nvq[u]) {
-                        const float p = sc[qb + u][k];
-                        o[u][0] = __builtin_fmaf(p, v4.x, o[u][0]);
-                        o[u][1] = __builtin_fmaf(p, v4.y, o[u][1]);
-                        o[u][2] = __builtin_fmaf(p, v4.z, o[u][2]);
-                        o[u][3] = __builtin_fmaf(p, v4.w, o[u][3]);
+        for (int u = 0; u < 2; ++u) {
+            const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
+            const uint32_t w4[4] = {kv4[u].x, kv4[u].y, kv4[u].z, kv4[u].w};
+            float* dst = isv ? &vd[k * kHD + 16 * c] : &kd[k * kKStride + 16 * c];
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                float4 f;
+                f.x = (float)(int8_t)(w4[e4] & 0xFFu) * scl[u];
+                f.y = (float)(int8_t)((w4[e4] >> 8) & 0xFFu) * scl[u];
+                f.z = (float)(int8_t)((w4[e4] >> 16) & 0xFFu) * scl[u];
+                f.w = (float)(int8_t)(w4[e4] >> 24) * scl[u];
+                *(float4*)(dst + 4 * e4) = f;
+            }
+        }
+        if (!staged_q) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int i = t + kAttnThreads * u;
+                const int qi = i >> 4, c = i & 15;
+                if (qi < nqr) {
+                    float4* d = (float4*)&qf[qi * kHD + 8 * c];
+                    d[0] = make_float4(__uint_as_float(q4[u].x << 16), __uint_as_float(q4[u].x & 0xFFFF0000u),
+                                       __uint_as_float(q4[u].y << 16), __uint_as_float(q4[u].y & 0xFFFF0000u));
+                    d[1] = make_float4(__uint_as_float(q4[u].z << 16), __uint_as_float(q4[u].z & 0xFFFF0000u),
+                                       __uint_as_float(q4[u].w << 16), __uint_as_float(q4[u].w & 0xFFFF0000u));
+                }
+            }
+            staged_q = true;
+        }
+        __syncthreads();
+        // ---- scores + split softmax: lane = key, this wave's queries wv + 8 i
+        {
+            const int k = lane;
+            float acc[NQW];
+#pragma unroll
+            for (int i = 0; i < NQW; ++i) acc[i] = 0.0f;
+            const float* kr = &kd[k * kKStride];
+#pragma unroll 4
+            for (int c = 0; c < kHD / 4; ++c) {
+                const float4 kv = *(const float4*)(kr + 4 * c);
+#pragma unroll
+                for (int i = 0; i < NQW; ++i) {
+                    const int qi = wv + 8 * i;
+                    if (qi < nqr) {               // wave-uniform
+                        const float4 q = *(const float4*)&qf[qi * kHD + 4 * c];
+                        float v = acc[i];
+                        v = __builtin_fmaf(q.x, kv.x, v);
+                        v = __builtin_fmaf(q.y, kv.y, v);
+                        v = __builtin_fmaf(q.z, kv.z, v);
+                        v = __builtin_fmaf(q.w, kv.w, v);
+                        acc[i] = v;
                     }
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int i = 0; i < NQW; ++i) {
+                const int qi = wv + 8 * i;
+                if (qi >= nqr) break;             // wave-uniform
+                const int r = qi / G, g = qi - r * G;
+                const int L = pos0 + r + 1;
+                const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
+                const bool valid = k < nv;
+                const float x = acc[i] * a.sl2e;
+                float m = valid ? x : -__builtin_huge_valf();
+                m = max_xor(m, 64);
+                const float p = valid ? qexp2(x - m) : 0.0f;
+                sp[qi * (kSplit + 1) + k] = p;
+                const float l = tree64(p);
+                if (lane == 0 && nv > 0) {
+                    const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
+                    wm[mi] = m;
+                    wl[mi] = l;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- o = sum_k p_k v_k in key order
+        {
+            const int d4 = 4 * (t & 31), qs = t >> 5;
+            float o[QPT][4];
+            int nvq[QPT];
+            int kmax = 0;
+#pragma unroll
+            for (int u = 0; u < QPT; ++u) {
+                const int qi = qs + 16 * u;
+                const int L = pos0 + qi / G + 1;
+                nvq[u] = (qi < nqr) ? ((L - k0 < nk) ? (L - k0) : nk) : 0;
+                kmax = nvq[u] > kmax ? nvq[u] : kmax;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = 0.0f;
+            }
+            for (int k = 0; k < kmax; ++k) {
+                const float4 v = *(const float4*)&vd[k * kHD + d4];
+#pragma unroll
+                for (int u = 0; u < QPT; ++u) {
+                    if (k < nvq[u]) {
+                        const float p = sp[(qs + 16 * u) * (kSplit + 1) + k];
+                        o[u][0] = __builtin_fmaf(p, v.x, o[u][0]);
+                        o[u][1] = __builtin_fmaf(p, v.y, o[u][1]);
+                        o[u][2] = __builtin_fmaf(p, v.z, o[u][2]);
+                        o[u][3] = __builtin_fmaf(p, v.w, o[u][3]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < QPT; ++u) {
                 if (nvq[u] <= 0) continue;
-                const int qi = qb + u, r = qi / G, g = qi - r * G;
-                float* dst = &wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + db];
+                const int qi = qs + 16 * u, r = qi / G, g = qi - r * G;
+                float* dst = &wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + d4];
                 *(float4*)dst = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
             }
         }
@@ -286,8 +345,26 @@ int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
-    int gx = a.max_splits < 256 ? a.max_splits : 256;
-    hipLaunchKernelGGL(k_attn_split, dim3(gx, a.nkv), dim3(256), 0, s, a, nr);
+    const int nqr = nr * (a.nq / a.nkv);
+    const size_t lds = (size_t)nqr * (kHD + kSplit + 1) * 4;
+    static bool lds_set = false;                  // queries + p of up to 64 query vectors: 49 KiB
+    if (!lds_set) {
+        const int mx = 64 * (kHD + kSplit + 1) * 4;
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<1, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<2, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<3, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<6, 3>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<8, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        lds_set = true;
+    }
+    const dim3 grid(a.max_splits, a.nkv);
+    if (nqr <= 8) hipLaunchKernelGGL((k_attn_split<1, 1>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 16) hipLaunchKernelGGL((k_attn_split<2, 1>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 24) hipLaunchKernelGGL((k_attn_split<3, 2>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 32) hipLaunchKernelGGL((k_attn_split<4, 2>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 48) hipLaunchKernelGGL((k_attn_split<6, 3>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else hipLaunchKernelGGL((k_attn_split<8, 4>), grid, dim3(kAttnThreads), lds, s, a, nr);
     Q27X_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr), dim3(kHD), 0, s, a, nr);
     Q27X_HIP(hipGetLastError());
