@@ -281,7 +281,8 @@ int q27x_run_rounds(q27x_ctx* ctx, int n, int spec, q27x_stats* st);
 int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
 /* Time one projection launch of layer `layer` as the verify pass runs it (which: 0 in_qkv|in_z with
  * its input-norm prologue, 1 gate|up with its post-norm prologue and SwiGLU epilogue, 2 down +
- * residual, 3 out_proj + residual, 4 lm_head + argmax partials) over iters launches with device
+ * residual, 3 out_proj + residual, 4 lm_head + argmax partials; 5 and 6 are 0 and 1 fed with
+ * already-quantized rows, no prologue, for comparison) over iters launches with device
  * events on the context's stream, cycling through the layers so no launch finds its weights in the
  * Infinity Cache; reports ms per launch and its algorithmic bytes (weights + scales + input rows +
  * outputs). Overwrites the context's activation scratch. */

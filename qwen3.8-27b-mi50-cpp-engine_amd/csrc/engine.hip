@@ -1051,7 +1051,7 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
     hipStream_t s = x->stream;
     Dctl* d = x->dctl;
     const int H = x->H, I = x->I;
-    const bool need_gdn = (which == 0 || which == 3);
+    const bool need_gdn = (which == 0 || which == 3 || which == 5);
     std::vector<int> ls;
     for (int k = 0; k < c.n_layers; ++k) {
         const int l = (layer + k) % c.n_layers;
@@ -1069,6 +1069,16 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
             p.y = x->pb; p.ystride = Y.qkvz.rows; p.out_bf16 = 1;
             set_pre(p, norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, x->ynorm));
             b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * p.rows * 2;
+        } else if (which == 5) {   // in_qkv|in_z from pre-quantized rows (no prologue), for comparison
+            p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+            p.y = x->pb; p.ystride = Y.qkvz.rows; p.out_bf16 = 1;
+            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * p.rows * 2;
+        } else if (which == 6) {   // gate|up from pre-quantized rows (no prologue), for comparison
+            p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
+            p.act_q = x->xq + x->act_off; p.act_s = x->xs + x->act_off / 16; p.act_stride = I;
+            p.gscale = 1.0f;
+            epi = EPI_SWIGLU;
+            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * I * (1 + 4.0 / 16);
         } else if (which == 1) {   // post-norm prologue, SwiGLU + quantize epilogue
             p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H;
             p.act_q = x->xq + x->act_off; p.act_s = x->xs + x->act_off / 16; p.act_stride = I;
@@ -1086,7 +1096,7 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
     };
     std::vector<ProjArgs> ps;
     GemvArgs ga{};
-    if (which >= 0 && which <= 3) {
+    if ((which >= 0 && which <= 3) || which == 5 || which == 6) {
         for (int l : ls) ps.push_back(make(l));
     } else if (which == 4) {
         ga.W = x->lm_head; ga.rows = x->V; ga.K = H; ga.x = x->ynorm; ga.xst = H;

@@ -21,7 +21,6 @@
 
 namespace q27x {
 
-constexpr int kPW = 4;              // waves per block
 
 template <int V> struct Pow2 {
     static constexpr int value = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : V <= 32 ? 32 : 64;
@@ -52,43 +51,67 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
     return y;
 }
 
-// One row group = RPW consecutive weight rows; a wave owns `upw` consecutive units of `urows`
-// rows (urows = RPW, or 32 for the SwiGLU epilogue whose unit is one 16-output quantization
-// group: 16 gate rows | 16 up rows), so every wave streams the same number of bytes.
+// Work assignment. A row group is RPW consecutive weight rows.
+//   EPI_STORE: the grid's waves deal the groups round-robin: wave gw (of nw = gridDim.x * NW)
+//     takes groups gw, gw + nw, ..., so every wave streams within one group of the same number
+//     of bytes and the NW waves of a block read adjacent rows at the same time.
+//   EPI_SWIGLU: the 32-row units (16 gate rows | 16 up rows = one 16-output quantization group)
+//     are dealt round-robin to the blocks' UPB unit slots (unit u: block u % gridDim.x, slot and
+//     round from u / gridDim.x); the WPU waves of a slot stream 32 / WPU rows of its unit each, a
+//     barrier closes every round and the slot's first wave applies SwiGLU + quantize.
 // FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
-// quantize of the raw input rows (a.pre), computed by every block (K = NSTEP * 1024).
-template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE>
-__global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urows) {
+// quantize of the raw input rows (a.pre), computed by every block (K = NSTEP * 1024, NW = 16).
+template <int NW> struct SwigluShape {
+    static constexpr int WPU = (NW >= 8) ? 2 : 4;     // waves per unit
+    static constexpr int UPB = NW / WPU;               // unit slots per block
+    static constexpr int RW = 32 / WPU;                // rows per wave per unit
+};
+template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE, int NW>
+__global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr int SL = NSTEP * 64;
-    constexpr int NT = kPW * 64;
+    constexpr int NT = NW * 64;
     constexpr int NSTG = (NR * SL + NT - 1) / NT;      // staging loads per thread
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
+    using SW = SwigluShape<NW>;
+    constexpr int GPU_ = SW::RW / RPW;                 // SwiGLU: groups per wave per unit
+    static_assert(EPI != EPI_SWIGLU || (SW::RW % RPW == 0 && NW % SW::WPU == 0), "SwiGLU shape");
+    static_assert(!PRE || NW == 16, "the norm prologue runs on 16-wave blocks");
     __shared__ uint4 sx[NR * SL];
     __shared__ float ssc[NR * SL];
-    __shared__ float sacc[(EPI == EPI_SWIGLU) ? 2 * 32 * NR : 1];
-    __shared__ float wsum[PreNorm<NSTEP, NR>::RB][4];
+    __shared__ float sacc[(EPI == EPI_SWIGLU) ? 2 * SW::UPB * 32 * NR : 1];
+    __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
     if (a.stop && *a.stop) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
-    const int nunits = (a.rows + urows - 1) / urows;
-    // EPI_STORE: a wave owns `upw` units of RPW rows, group g = rows g*RPW ..;
-    // EPI_SWIGLU (RPW = 1): a block owns `upw` 32-row units and wave w streams rows 8w..8w+7 of
-    // each, group g = row 8w + (g & 7) of unit g >> 3
-    int g0, g1;
+    const int nb = gridDim.x;
+    // group sequence of this wave: index i = 0 .. niter-1
+    const int slot = wave / SW::WPU, sub = wave % SW::WPU;
+    const int nunits = (a.rows + 31) >> 5;
+    const int ngroups = (a.rows + RPW - 1) / RPW;
+    const int gw = blockIdx.x * NW + wave, nw = nb * NW;
+    int niter;
     if constexpr (EPI == EPI_SWIGLU) {
-        static_assert(RPW == 1 && kPW == 4, "SwiGLU units are 4 waves x 8 rows");
-        const int u0 = blockIdx.x * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
-        g0 = u0 * 8; g1 = u1 * 8;
+        const int per_round = nb * SW::UPB;
+        const int rounds = (nunits - (int)blockIdx.x + per_round - 1) / per_round;   // slot 0's
+        niter = rounds * GPU_;                         // the same for every wave of the block
     } else {
-        const int gpu = urows / RPW;
-        const int gw = blockIdx.x * kPW + wave;
-        const int u0 = gw * upw, u1 = (u0 + upw < nunits) ? u0 + upw : nunits;
-        g0 = u0 * gpu; g1 = u1 * gpu;
+        niter = (gw < ngroups) ? (ngroups - 1 - gw) / nw + 1 : 0;
     }
+    auto unit_of = [&](int i) __attribute__((always_inline)) {
+        return (int)blockIdx.x + nb * (slot + SW::UPB * (i / GPU_));
+    };
+    auto valid = [&](int i) __attribute__((always_inline)) {
+        if constexpr (EPI == EPI_SWIGLU) return i < niter && unit_of(i) < nunits;
+        else return i < niter;
+    };
+    auto row_of = [&](int i, int r) __attribute__((always_inline)) {
+        if constexpr (EPI == EPI_SWIGLU) return unit_of(i) * 32 + sub * SW::RW + RPW * (i % GPU_) + r;
+        else return (gw + i * nw) * RPW + r;
+    };
     uint4 W[RPW][NSTEP];
     float S[RPW][NSTEP];
-    auto ld = [&](int g, int r, int t) __attribute__((always_inline)) {
-        int row = (EPI == EPI_SWIGLU) ? (g >> 3) * 32 + 8 * wave + (g & 7) : g * RPW + r;
+    auto ld = [&](int i, int r, int t) __attribute__((always_inline)) {
+        int row = row_of(i, r);
         row = row < a.rows ? row : a.rows - 1;
         const int s = t * 64 + lane;
         if (FULL || s < nslab) {
@@ -100,29 +123,21 @@ __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urow
         }
     };
     auto prefetch = [&]() __attribute__((always_inline)) {
-        if (g0 < g1) {
+        if (valid(0)) {
 #pragma unroll
             for (int t = 0; t < NSTEP; ++t)
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) ld(g0, r, t);
+                for (int r = 0; r < RPW; ++r) ld(0, r, t);
         }
     };
     if constexpr (PRE) {
         // input rows first, then the weights, so waiting for the rows leaves the weights in flight
         PreNorm<NSTEP, NR> pn;
-        constexpr int RB = PreNorm<NSTEP, NR>::RB;
-        pn.load_w(a.pre);
-        pn.load_x(a.pre, 0);
+        pn.load(a.pre);
         __builtin_amdgcn_sched_barrier(0);
         prefetch();
         __builtin_amdgcn_sched_barrier(0);
-        const bool writer = blockIdx.x == 0;
-        pn.finish(a.pre, 0, (uint32_t*)sx, ssc, SL, wsum, writer);
-#pragma unroll
-        for (int r0 = RB; r0 < NR; r0 += RB) {
-            pn.load_x(a.pre, r0);
-            pn.finish(a.pre, r0, (uint32_t*)sx, ssc, SL, wsum, writer);
-        }
+        pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
     } else {
         // activation stage: every load issued before any LDS write (one round trip)
         uint4 tv[NSTG];
@@ -150,64 +165,72 @@ __global__ __launch_bounds__(kPW * 64) void k_proj(ProjArgs a, int upw, int urow
     const bool holder = (lane % LPV) == 0 && vi < V;
     const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
     const uint32_t* resw = (const uint32_t*)a.res;
-    for (int g = g0; g < g1; ++g) {
-        // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use
-        uint32_t rw = 0u;
-        size_t ridx = 0;
-        if (EPI == EPI_STORE && resw) {
-            int row = g * RPW + hr;
-            row = row < a.rows ? row : a.rows - 1;
-            ridx = (size_t)hn * a.rstride + row;
-            rw = a.res_bf16 ? resw[ridx >> 1] : resw[ridx];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        float acc[P];
+    for (int i = 0; i < niter; ++i) {
+        const bool vnow = valid(i);
+        if (vnow) {
+            // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use
+            uint32_t rw = 0u;
+            size_t ridx = 0;
+            if (EPI == EPI_STORE && resw) {
+                int row = row_of(i, hr);
+                row = row < a.rows ? row : a.rows - 1;
+                ridx = (size_t)hn * a.rstride + row;
+                rw = a.res_bf16 ? resw[ridx >> 1] : resw[ridx];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            float acc[P];
 #pragma unroll
-        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
-        auto body = [&](auto reload) __attribute__((always_inline)) {
+            for (int v = 0; v < P; ++v) acc[v] = 0.0f;
+            auto body = [&](auto reload) __attribute__((always_inline)) {
 #pragma unroll
-            for (int t = 0; t < NSTEP; ++t) {
-                const int s = t * 64 + lane;
+                for (int t = 0; t < NSTEP; ++t) {
+                    const int s = t * 64 + lane;
 #pragma unroll
-                for (int n = 0; n < NR; ++n) {
-                    const uint4 xa = sx[n * SL + s];
-                    const float sa = ssc[n * SL + s];
+                    for (int n = 0; n < NR; ++n) {
+                        const uint4 xa = sx[n * SL + s];
+                        const float sa = ssc[n * SL + s];
 #pragma unroll
-                    for (int r = 0; r < RPW; ++r) {
-                        const int d = dot16(W[r][t], xa);
-                        acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
+                        for (int r = 0; r < RPW; ++r) {
+                            const int d = dot16(W[r][t], xa);
+                            acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
+                        }
+                    }
+                    if constexpr (decltype(reload)::value) {
+#pragma unroll
+                        for (int r = 0; r < RPW; ++r) ld(i + 1, r, t);
                     }
                 }
-                if constexpr (decltype(reload)::value) {
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) ld(g + 1, r, t);
+            };
+            if (valid(i + 1)) body(std::true_type{});
+            else body(std::false_type{});
+            const float tv = tree_t<P>(acc, lane) * a.alpha;
+            if constexpr (EPI == EPI_STORE) {
+                const int row = row_of(i, hr);
+                if (holder && row < a.rows) {
+                    float v = tv;
+                    if (resw) {
+                        const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
+                                                    : __uint_as_float(rw);
+                        if (a.res_round) v = bfr(v);
+                        v = v + a.rs * rv;
+                    }
+                    const size_t yi = (size_t)hn * a.ystride + row;
+                    if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
+                    else ((float*)a.y)[yi] = v;
                 }
+            } else {
+                float* sw = sacc + (((i / GPU_) & 1) * SW::UPB + slot) * 32 * NR;
+                if (holder) sw[(sub * SW::RW + RPW * (i % GPU_) + hr) * NR + hn] = tv;
             }
-        };
-        if (g + 1 < g1) body(std::true_type{});
-        else body(std::false_type{});
-        const float tv = tree_t<P>(acc, lane) * a.alpha;
-        if (EPI == EPI_STORE) {
-            const int row = g * RPW + hr;
-            if (holder && row < a.rows) {
-                float v = tv;
-                if (resw) {
-                    const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
-                                                : __uint_as_float(rw);
-                    if (a.res_round) v = bfr(v);
-                    v = v + a.rs * rv;
-                }
-                const size_t yi = (size_t)hn * a.ystride + row;
-                if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
-                else ((float*)a.y)[yi] = v;
-            }
-        } else {   // EPI_SWIGLU: 32 rows [16 gate | 16 up] -> 16 outputs, one quantization group
-            float* sw = sacc + ((g >> 3) & 1) * 32 * NR;   // double buffer: one barrier per unit
-            if (holder) sw[(8 * wave + (g & 7)) * NR + hn] = tv;
-            if ((g & 7) == 7) {
+        }
+        if constexpr (EPI == EPI_SWIGLU) {
+            // end of a round: 32 rows [16 gate | 16 up] -> 16 outputs, one quantization group;
+            // double-buffered partials, one barrier per round
+            if (i % GPU_ == GPU_ - 1) {
                 __syncthreads();
-                if (wave == 0) {
-                    const int unit = g >> 3, j = lane & 15;
+                if (sub == 0 && vnow) {
+                    const float* sw = sacc + (((i / GPU_) & 1) * SW::UPB + slot) * 32 * NR;
+                    const int unit = unit_of(i), j = lane & 15;
 #pragma unroll
                     for (int nn = 0; nn < NR; ++nn) {
                         const float gv = sw[j * NR + nn], uv = sw[(16 + j) * NR + nn];
@@ -239,10 +262,11 @@ static int num_cus() {
     return g_ncu;
 }
 
-// Launch shape. EPI_STORE: units spread over num_cus() * wpc waves (16 waves per CU for the
-// K <= 6144 shapes, 8 for K = 17408 whose 17 KiB-per-row prefetch holds ~250 VGPRs).
-// EPI_SWIGLU: 32-row units spread over num_cus() * bpc blocks of 4 waves. Both knobs can be
-// overridden for launch-shape sweeps (Q27X_WPC5, Q27X_WPC17, Q27X_GU_BPC).
+// Launch shape. The norm-prologue and SwiGLU kernels run one 16-wave block per CU (the prologue
+// is then computed once per CU; SwiGLU deals its units over 8 slots per block). The plain store
+// kernels run 4-wave blocks, wpc waves per CU (16 for the K <= 6144 shapes, 8 for K = 17408 whose
+// 17 KiB-per-row prefetch holds ~250 VGPRs). Overridable for launch-shape sweeps (Q27X_WPC5,
+// Q27X_WPC17).
 static int env_knob(const char* name, int def, int lo, int hi) {
     const char* v = getenv(name);
     if (!v || !*v) return def;
@@ -251,28 +275,34 @@ static int env_knob(const char* name, int def, int lo, int hi) {
 }
 static int knob_wpc5() { static const int v = env_knob("Q27X_WPC5", 16, 4, 32); return v; }
 static int knob_wpc17() { static const int v = env_knob("Q27X_WPC17", 8, 4, 16); return v; }
-static int knob_gu_bpc() { static const int v = env_knob("Q27X_GU_BPC", 2, 1, 8); return v; }
 
-template <int NR, int NSTEP, int EPI, bool FULL, bool PRE>
-static int run_proj(const ProjArgs& a, hipStream_t s) {
-    constexpr int RPW = 1;
-    const int urows = (EPI == EPI_SWIGLU) ? 32 : RPW;
-    const int nunits = (a.rows + urows - 1) / urows;
-    int upw, grid;
+template <int NR, int NSTEP, int EPI, bool FULL, bool PRE, int RPW>
+static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
+    constexpr int NW = (PRE || EPI == EPI_SWIGLU) ? 16 : 4;
+    int grid;
     if (EPI == EPI_SWIGLU) {
-        const int bmax = num_cus() * knob_gu_bpc();
-        upw = (nunits + bmax - 1) / bmax;
-        grid = (nunits + upw - 1) / upw;
+        const int nunits = (a.rows + 31) >> 5;
+        grid = nunits < num_cus() ? nunits : num_cus();
+    } else if (NW == 16) {
+        const int ngroups = (a.rows + RPW - 1) / RPW;
+        const int nb = (ngroups + NW - 1) / NW;
+        grid = nb < num_cus() ? nb : num_cus();
     } else {
+        const int ngroups = (a.rows + RPW - 1) / RPW;
         const int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
         const int wmax = num_cus() * wpc;
-        upw = (nunits + wmax - 1) / wmax;
-        const int waves = (nunits + upw - 1) / upw;
-        grid = (waves + kPW - 1) / kPW;
+        const int nwv = ngroups < wmax ? ngroups : wmax;
+        grid = (nwv + NW - 1) / NW;
     }
-    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL, PRE>), dim3(grid), dim3(kPW * 64), 0, s, a, upw, urows);
+    hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL, PRE, NW>), dim3(grid), dim3(NW * 64), 0, s, a);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
+}
+// One weight row per wave step (two rows per step measured slower on MI355X, with and without
+// the prologue).
+template <int NR, int NSTEP, int EPI, bool FULL, bool PRE>
+static int run_proj(const ProjArgs& a, hipStream_t s) {
+    return run_proj_rpw<NR, NSTEP, EPI, FULL, PRE, 1>(a, s);
 }
 
 // Shape router. NSTEP = ceil(K/1024); the LDS stage is NR*NSTEP*1280 B, so K = 17408 at NR > 4

@@ -125,31 +125,30 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int r0, int nrows, 
 
 namespace q27x {
 
-// Prologue form of the same RMSNorm + quantize: every 256-thread block of a consumer projection
-// normalizes the NR input rows itself (n = NCH * 1024 = the projection's K) and writes the codes
-// and scales straight into its LDS activation stage, in the slab layout of k_proj: element
-// k = 1024 i + 4 t + e lands in slab 64 i + t/4 at byte 4 (t % 4). The order of every operation
-// is the canonical one above, so all blocks hold the same bits as a standalone norm would write.
-// Block 0 also stores the side outputs (hcopy, y, xq/xs) for later kernels. Loads are split from
-// the arithmetic so the caller can issue its weight prefetch in between (vector-memory counters
-// retire in order: the input rows must be requested before the weights to be waited on alone).
+// Prologue form of the same RMSNorm + quantize for a 1024-thread block: every block of a consumer
+// projection normalizes the NR input rows itself (n = NCH * 1024 = the projection's K) and writes
+// the codes and scales straight into its LDS activation stage, in the slab layout of k_proj:
+// element k = 1024 i + 4 t + e lands in slab 64 i + t/4 at byte 4 (t % 4). The four 256-thread
+// groups take rows tg, tg + 4, ... (tg = thread / 256), each in the canonical order above, so all
+// blocks hold the bits a standalone norm writes. Block 0 also stores the side outputs (hcopy, y,
+// xq/xs) for later kernels. Loads are split from the arithmetic so the caller can issue its
+// weight prefetch in between (vector-memory counters retire in order: the input rows must be
+// requested before the weights to be waited on alone).
 template <int NCH, int NR>
 struct PreNorm {
-    static constexpr int RB = NR <= 4 ? NR : 4;   // rows held in registers per pass
-    uint2 wb[NCH];                                // 4 bf16 norm weights per chunk
-    float xv[RB][NCH][4];
+    static constexpr int GR = 4;                          // 256-thread groups
+    static constexpr int RPG = (NR + GR - 1) / GR;        // rows per group
+    uint2 wb[NCH];                                        // 4 bf16 norm weights per chunk
+    float xv[RPG][NCH][4];
 
-    __device__ __forceinline__ void load_w(const NormArgs& a) {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) wb[i] = *(const uint2*)(a.w + i * 1024 + 4 * t);
-    }
-    __device__ __forceinline__ void load_x(const NormArgs& a, int r0) {
-        const int t = threadIdx.x;
+    __device__ __forceinline__ void load(const NormArgs& a) {
+        const int t = threadIdx.x & 255, tg = threadIdx.x >> 8;
         constexpr int n = NCH * 1024;
 #pragma unroll
-        for (int j = 0; j < RB; ++j) {
-            const int r = r0 + j;
+        for (int i = 0; i < NCH; ++i) wb[i] = *(const uint2*)(a.w + i * 1024 + 4 * t);
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) {
+            const int r = tg + GR * j;
             if (r >= NR) break;
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
@@ -167,14 +166,15 @@ struct PreNorm {
             }
         }
     }
-    // sxw: the LDS code stage as 32-bit words ([NR][SL] slabs of 4 words); ssc: [NR][SL] scales
-    __device__ __forceinline__ void finish(const NormArgs& a, int r0, uint32_t* sxw, float* ssc, int SL,
-                                           float (*wsum)[4], bool writer) {
-        const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    // sxw: the LDS code stage as 32-bit words ([NR][SL] slabs of 4 words); ssc: [NR][SL] scales;
+    // wsum: __shared__ float[RPG][GR][4]
+    __device__ __forceinline__ void finish(const NormArgs& a, uint32_t* sxw, float* ssc, int SL,
+                                           float (*wsum)[GR][4], bool writer) {
+        const int t = threadIdx.x & 255, tg = threadIdx.x >> 8, lane = t & 63, wv = t >> 6;
         constexpr int n = NCH * 1024;
 #pragma unroll
-        for (int j = 0; j < RB; ++j) {
-            const int r = r0 + j;
+        for (int j = 0; j < RPG; ++j) {
+            const int r = tg + GR * j;
             if (r >= NR) break;
             float acc = 0.0f;
 #pragma unroll
@@ -188,15 +188,15 @@ struct PreNorm {
                 for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(v[e], v[e], acc);
             }
             acc = tree64(acc);
-            if (lane == 0) wsum[j][wv] = acc;
+            if (lane == 0) wsum[j][tg][wv] = acc;
         }
         __syncthreads();
         const float g = 1.0f / a.in_scale;
 #pragma unroll
-        for (int j = 0; j < RB; ++j) {
-            const int r = r0 + j;
+        for (int j = 0; j < RPG; ++j) {
+            const int r = tg + GR * j;
             if (r >= NR) break;
-            const float ss = ((wsum[j][0] + wsum[j][1]) + wsum[j][2]) + wsum[j][3];
+            const float ss = ((wsum[j][tg][0] + wsum[j][tg][1]) + wsum[j][tg][2]) + wsum[j][tg][3];
             const float inv = rsqrt_cr(ss * (1.0f / (float)n) + a.eps);
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
@@ -230,7 +230,6 @@ struct PreNorm {
                 }
             }
         }
-        __syncthreads();   // wsum is reused by the next pass
     }
 };
 
