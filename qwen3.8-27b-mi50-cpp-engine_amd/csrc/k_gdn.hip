@@ -79,14 +79,17 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     const PendArea Q = pend_area(a.pend, a.kh, a.vh, (int)(par ^ 1u));  // this call's rows (write)
     const int npend = a.npend_ptr ? *a.npend_ptr : a.npend_imm;
 
-    __shared__ float skp[kMaxRows][kD], sdp[kMaxRows][kD], sdc[kMaxRows];
+    __shared__ __attribute__((aligned(16))) float skp[kMaxRows][kD];
+    __shared__ float sdp[kMaxRows][kD], sdc[kMaxRows];
     __shared__ float scv[kMaxRows][3 * kD];        // conv'd q | k | v of this head (bf16 values)
     __shared__ float sz[kMaxRows][kD];
-    __shared__ float sq[kMaxRows][kD], sk[kMaxRows][kD];
+    __shared__ __attribute__((aligned(16))) float sq[kMaxRows][kD];
+    __shared__ __attribute__((aligned(16))) float sk[kMaxRows][kD];
     __shared__ float pA[2][4][kD], pB[2][4][kD];
     __shared__ float smix[kMaxRows][kD];
     __shared__ float red[kMaxRows][2][3];
     __shared__ float sab[2][kMaxRows];
+    __shared__ float srow[kMaxRows][4];          // per row: kq, beta, decay
     extern __shared__ uint4 sy[];                  // FUSE_AB: in_a row | in_b row | nr ynorm rows
 
     // ================= phase A: every global load of the block =================
@@ -212,7 +215,13 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     for (int p = 0; p < npend; ++p) {
         const float dp = sdp[p][d], dc = sdc[p];
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(skp[p][g * kJ + j], dp, dc * st[j]);
+        for (int j4 = 0; j4 < kJ; j4 += 4) {
+            const float4 kp = *(const float4*)&skp[p][g * kJ + j4];
+            st[j4] = __builtin_fmaf(kp.x, dp, dc * st[j4]);
+            st[j4 + 1] = __builtin_fmaf(kp.y, dp, dc * st[j4 + 1]);
+            st[j4 + 2] = __builtin_fmaf(kp.z, dp, dc * st[j4 + 2]);
+            st[j4 + 3] = __builtin_fmaf(kp.w, dp, dc * st[j4 + 3]);
+        }
     }
     if (npend > 0) {
         float* Sw = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
@@ -258,22 +267,33 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
         sk[n][e] = skv;
         if (owner) Q.khat[((size_t)n * a.kh + kk) * kD + e] = skv;
     }
+    if (t < nr) {   // the rows' scalars, once: k^.q^, beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt))
+        const int n = t;
+        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
+        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
+        srow[n][0] = ((red[n][0][2] + red[n][1][2]) * invq) * invk;
+        srow[n][1] = qsigmoid(sab[1][n]);
+        srow[n][2] = qexp(-(Aexp * qsoftplus(sab[0][n] + dtb)));
+    }
     __syncthreads();
 
     // the rows, in order: one barrier each (pA / pB alternate between two buffers)
     for (int n = 0; n < nr; ++n) {
-        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
-        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
-        const float kq = ((red[n][0][2] + red[n][1][2]) * invq) * invk;
-        const float beta = qsigmoid(sab[1][n]);
-        const float sp = qsoftplus(sab[0][n] + dtb);
-        const float decay = qexp(-(Aexp * sp));
+        const float kq = srow[n][0], beta = srow[n][1], decay = srow[n][2];
         const float vv = scv[n][2 * kD + d];
         float accA = 0.0f, accB = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            accA = __builtin_fmaf(st[j], sk[n][g * kJ + j], accA);
-            accB = __builtin_fmaf(st[j], sq[n][g * kJ + j], accB);
+        for (int j4 = 0; j4 < kJ; j4 += 4) {
+            const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
+            const float4 q4 = *(const float4*)&sq[n][g * kJ + j4];
+            accA = __builtin_fmaf(st[j4], k4.x, accA);
+            accB = __builtin_fmaf(st[j4], q4.x, accB);
+            accA = __builtin_fmaf(st[j4 + 1], k4.y, accA);
+            accB = __builtin_fmaf(st[j4 + 1], q4.y, accB);
+            accA = __builtin_fmaf(st[j4 + 2], k4.z, accA);
+            accB = __builtin_fmaf(st[j4 + 2], q4.z, accB);
+            accA = __builtin_fmaf(st[j4 + 3], k4.w, accA);
+            accB = __builtin_fmaf(st[j4 + 3], q4.w, accB);
         }
         pA[n & 1][g][d] = accA;
         pB[n & 1][g][d] = accB;
@@ -283,7 +303,13 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
         const float delta = (vv - decay * A) * beta;
         const float mixed = __builtin_fmaf(delta, kq, decay * B);
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(sk[n][g * kJ + j], delta, decay * st[j]);
+        for (int j4 = 0; j4 < kJ; j4 += 4) {
+            const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
+            st[j4] = __builtin_fmaf(k4.x, delta, decay * st[j4]);
+            st[j4 + 1] = __builtin_fmaf(k4.y, delta, decay * st[j4 + 1]);
+            st[j4 + 2] = __builtin_fmaf(k4.z, delta, decay * st[j4 + 2]);
+            st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
+        }
         if (g == 0) {
             Q.delta[((size_t)n * a.vh + h) * kD + d] = delta;
             smix[n][d] = mixed;
