@@ -88,6 +88,36 @@ def cpu_baseline(cfg_dict, q27o):
                       f"(1 token/round); weight generation {gen_s:.1f} s not timed"}
 
 
+COPY_BYTES = 1 << 28       # calibration copy: 256 MiB read + 256 MiB written per launch
+
+
+def kernel_only(q27x, args):
+    """The dominant kernel alone (gate|up with its norm prologue, 20 launches cycling the layers)
+    and a plain copy of COPY_BYTES (10 launches), so that a rocprofv3 --pmc pass sees both."""
+    import ctypes
+    cfg = q27x.default_config(spec_k=args.k, ctx=args.prompt + 256)
+    eng = q27x.Engine(cfg, SEED)
+    eng.prefill(np.random.default_rng(SEED).integers(0, cfg.vocab, 64).astype(np.int32))
+    ms, b = eng.bench_kernel(0, 1, args.k + 1, 20)
+    eng.close()
+    t = ctypes.c_float()
+    q27x.call("q27x_bench_stream", 1, COPY_BYTES, 4, 4, 10, ctypes.byref(t))
+    print(json.dumps({"kernel_us": round(ms * 1e3, 2), "kernel_bytes": b, "copy_bytes": COPY_BYTES,
+                      "copy_us": round(t.value * 1e3, 2)}), flush=True)
+    return 0
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading for the calibration copy)."""
+    path = os.path.join(ROOT, "profiles", "gate_up_k2_pmc_traffic.json")
+    try:
+        with open(path) as fh:
+            return json.load(fh).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +128,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forced", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches (profilers that cannot follow graphs)")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant kernel (gate|up) and the calibration copy, for rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.no_graph:
         os.environ["Q27X_GRAPH"] = "0"
@@ -110,6 +142,8 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     q27x.call("q27x_set_device", 0)
+    if args.kernel_only:
+        return kernel_only(q27x, args)
     K = args.k
     rounds_total = args.warmup + args.steps
     ctx = args.prompt + rounds_total * (K + 1) + 128
@@ -192,10 +226,11 @@ def main():
         "plain_decode_tok_s": round(plain_tps, 2),
         "verify_step": {"ms": round(vms, 4), "bytes": vbytes, "GB_s": round(v_gbs, 1),
                         "frac_of_hbm_peak": round(v_gbs / HBM_PEAK_GBS, 4), "rows": K + 1},
-        "roofline": {"bound": "hbm", "kernel": "k_proj<NR=3, NSTEP=5, RPW=1, EPI_SWIGLU> (gate|up + SwiGLU + quantize)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_proj<3, 5, 1, 2, true, true, 16> (gate|up: post-norm prologue, W8A8, SwiGLU + quantize)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": kbytes,
-                     "us_per_launch": round(kms * 1e3, 2)},
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "bytes_per_launch": kbytes, "us_per_launch": round(kms * 1e3, 2)},
         "kernels": kernels,
         "prefill_s": round(prefill_s, 3),
         "cpu_baseline": cpu,
