@@ -298,8 +298,8 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
-// One weight row per wave step (two rows per step measured slower on MI355X, with and without
-// the prologue).
+// One weight row per wave step: two rows per step (more bytes in flight per wave) measured slower
+// on MI355X for every shape here, with and without the prologue.
 template <int NR, int NSTEP, int EPI, bool FULL, bool PRE>
 static int run_proj(const ProjArgs& a, hipStream_t s) {
     return run_proj_rpw<NR, NSTEP, EPI, FULL, PRE, 1>(a, s);
