@@ -138,8 +138,29 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         prefetch();
         __builtin_amdgcn_sched_barrier(0);
         pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
+    } else if constexpr (FULL) {
+        // activation stage by LDS DMA (global_load_lds: each lane's 16-byte code word and 4-byte
+        // scale land at the wave's LDS base + lane offset, no registers), requested together with
+        // the weight prefetch; the barrier below waits for both
+#pragma unroll
+        for (int j = 0; j < NSTG; ++j) {
+            const int i0 = j * NT + 64 * wave;              // first stage element of this wave
+            const int i = i0 + lane;
+            if (i0 < NR * SL && i < NR * SL) {
+                const int n = i / SL, s = i - n * SL;
+                __builtin_amdgcn_global_load_lds((const void*)(a.xq + (size_t)n * a.xst + 16 * s),
+                                                 (__attribute__((address_space(3))) void*)&sx[i0], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(a.xs + (size_t)n * (a.xst >> 4) + s),
+                                                 (__attribute__((address_space(3))) void*)&ssc[i0], 4, 0, 0);
+            }
+        }
+        prefetch();
+        __builtin_amdgcn_s_waitcnt(0);                   // LDS DMA writes complete before the barrier
     } else {
-        // activation stage: every load issued before any LDS write (one round trip)
+        // activation stage: every load issued before any LDS write (one round trip). When the
+        // stage is small its registers coexist with the weight prefetch, which is then requested
+        // before the stage is written, so the two round trips overlap.
+        constexpr bool EARLY = NSTG <= 5;
         uint4 tv[NSTG];
         float ts[NSTG];
 #pragma unroll
@@ -153,12 +174,17 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
                 ts[j] = a.xs[(size_t)n * (a.xst >> 4) + s];
             }
         }
+        if constexpr (EARLY) {
+            __builtin_amdgcn_sched_barrier(0);
+            prefetch();
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int j = 0; j < NSTG; ++j) {
             const int i = threadIdx.x + j * NT;
             if (i < NR * SL) { sx[i] = tv[j]; ssc[i] = ts[j]; }
         }
-        prefetch();
+        if constexpr (!EARLY) prefetch();
     }
     __syncthreads();
     const int vi = lane / LPV;                         // the value this lane holds after the tree
