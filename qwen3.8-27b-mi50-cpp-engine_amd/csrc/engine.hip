@@ -94,6 +94,7 @@ struct q27x_ctx {
     uint16_t *pb = nullptr, *qh = nullptr, *ao = nullptr, *gout = nullptr;
     uint16_t *cat = nullptr, *mtp_hin = nullptr, *mtp_res = nullptr, *hprev = nullptr, *hcatch = nullptr;
     float* attn_work = nullptr; int max_splits = 0;
+    float* sw_part = nullptr; unsigned* sw_cnt = nullptr;   // SwiGLU units split over blocks
     float* pval = nullptr; uint32_t* pidx = nullptr; int pstride = 4096;
     int32_t* out_ring = nullptr; int ring_cap = 0;
     int32_t* forced = nullptr; int forced_cap = 0;
@@ -351,6 +352,7 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
         ProjArgs gu{};
         gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
         gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f; gu.stop = &d->stop;
+        gu.sw_part = x->sw_part; gu.sw_cnt = x->sw_cnt;
         set_pre(gu, norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr));
         if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
         ProjArgs dn{};
@@ -437,6 +439,7 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     ProjArgs gu{};
     gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
     gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f; gu.stop = &d->stop;
+    gu.sw_part = x->sw_part; gu.sw_cnt = x->sw_cnt;
     set_pre(gu, norm_of(x, x->mtp_res, 1, Y.post_norm, po, 1, nullptr, nullptr));
     if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
     ProjArgs dn{};
@@ -621,7 +624,8 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     if ((size_t)x->att > maxk) maxk = x->att;
     const size_t xqn = R * (2 * maxk + I);
     const size_t pbn = R * (size_t)((x->qr + 2 * x->kvr) > (x->nqkv + x->nz) ? (x->qr + 2 * x->kvr) : (x->nqkv + x->nz));
-    sb += sizeof(Dctl) + R * H * 2 * 4 + R * H * 4 + xqn + xqn / 16 * 4 + R * (size_t)x->nz * 2 + kArriveLines * 256 + 256;
+    sb += sizeof(Dctl) + R * H * 2 * 4 + R * H * 4 + xqn + xqn / 16 * 4 + R * (size_t)x->nz * 2 + 256;
+    sb += (size_t)kSwMaxSplit * 16 * R * 4 + kSwMaxSplit * 4 + 512;
     sb += pbn * 2 + 2 * R * (size_t)x->att * 2 + R * 2 * H * 2 + R * H * 2 * 3 + H * 2;
     sb += attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4 + R * (size_t)x->pstride * 8;
     x->ring_cap = c.ctx + 64; x->forced_cap = c.ctx + 64; x->prompt_cap = c.ctx + 64;
@@ -665,6 +669,8 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     x->hcatch = (uint16_t*)salloc(x, R * H * 2);
     x->hprev = (uint16_t*)salloc(x, H * 2);
     x->attn_work = (float*)salloc(x, attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4);
+    x->sw_part = (float*)salloc(x, (size_t)kSwMaxSplit * 16 * R * 4);
+    x->sw_cnt = (unsigned*)salloc(x, kSwMaxSplit * 4);
     x->pval = (float*)salloc(x, R * (size_t)x->pstride * 4);
     x->pidx = (uint32_t*)salloc(x, R * (size_t)x->pstride * 4);
     x->out_ring = (int32_t*)salloc(x, (size_t)x->ring_cap * 4);
@@ -1076,13 +1082,13 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
         } else if (which == 6) {   // gate|up from pre-quantized rows (no prologue), for comparison
             p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
             p.act_q = x->xq + x->act_off; p.act_s = x->xs + x->act_off / 16; p.act_stride = I;
-            p.gscale = 1.0f;
+            p.gscale = 1.0f; p.sw_part = x->sw_part; p.sw_cnt = x->sw_cnt;
             epi = EPI_SWIGLU;
             b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * (1 + 4.0 / 16) + (double)nr * I * (1 + 4.0 / 16);
         } else if (which == 1) {   // post-norm prologue, SwiGLU + quantize epilogue
             p.W = Y.gu.w; p.WS = Y.gu.s; p.rows = 2 * I; p.K = H;
             p.act_q = x->xq + x->act_off; p.act_s = x->xs + x->act_off / 16; p.act_stride = I;
-            p.gscale = 1.0f;
+            p.gscale = 1.0f; p.sw_part = x->sw_part; p.sw_cnt = x->sw_cnt;
             set_pre(p, norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr));
             epi = EPI_SWIGLU;
             b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * I * (1 + 4.0 / 16);

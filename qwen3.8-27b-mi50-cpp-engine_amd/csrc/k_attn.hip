@@ -107,7 +107,6 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     const int nqr = nact * G;                       // query vectors of this kv head
     const int kvrows = a.nkv * kHD;
     const int ms = a.max_splits;
-    const int gpr = kHD / a.kv_group;               // scale groups per head row
     const int gsh = __builtin_ctz(a.kv_group);      // kv_group is a power of two
     __shared__ float kd[kSplit * kKStride];
     __shared__ float vd[kSplit * kHD];

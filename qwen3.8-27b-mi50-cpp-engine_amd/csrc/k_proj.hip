@@ -7,10 +7,11 @@
 //   int d = sdot4 x 4 (exact int32), acc = fmaf((float)d, ws64 * xs16, acc)
 // then the 64 lane sums meet in the shfl_down tree -- the reference's order
 // (src/q27_fp8.hip:3814-3871), kept so results match its host restatement bit for bit.
-// Pipelining: each weight register is refilled with the next row group's slab as soon as its
-// dot products have issued, so a full group of loads stays in flight through the reduction and
-// the epilogue; epilogue inputs are requested before those refills (vector-memory counters
-// retire in order, so a later load would make its wait drain the prefetch).
+// Pipelining: each weight register is refilled with the next row group's slab once its dot
+// products have issued (the compiler issues the group's refills together, which measured faster
+// than spreading them over the steps), so a full group of loads stays in flight through the
+// reduction and the epilogue; epilogue inputs are requested before those refills (vector-memory
+// counters retire in order, so a later load would make its wait drain the prefetch).
 #include <stdlib.h>
 
 #include <type_traits>
@@ -55,89 +56,98 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
 //   EPI_STORE: the grid's waves deal the groups round-robin: wave gw (of nw = gridDim.x * NW)
 //     takes groups gw, gw + nw, ..., so every wave streams within one group of the same number
 //     of bytes and the NW waves of a block read adjacent rows at the same time.
-//   EPI_SWIGLU: the 32-row units (16 gate rows | 16 up rows = one 16-output quantization group)
-//     are dealt round-robin to the blocks' UPB unit slots (unit u: block u % gridDim.x, slot and
-//     round from u / gridDim.x); the WPU waves of a slot stream 32 / WPU rows of its unit each, a
-//     barrier closes every round and the slot's first wave applies SwiGLU + quantize.
+//   EPI_SWIGLU (RPW = 1): the 32-row units (16 gate rows | 16 up rows = one 16-output quantization
+//     group) are dealt so that every block streams the same number of rows. With
+//     nunits = F * nb + E, block b takes the whole units b, b + nb, ..., b + (F-1) nb; the E
+//     leftover units are cut into quarters (4 gate rows + the matching 4 up rows = 4 outputs)
+//     dealt round-robin over the blocks. A block's rows are dealt round-robin to its waves and
+//     their dot products meet in LDS; after one barrier the block applies SwiGLU + quantize to its
+//     whole units. A quarter's 4 SwiGLU values go to the scratch area with agent-scope stores and
+//     count on the unit's arrival counter; the wave that brings the count to 4 takes the exact
+//     max over the unit's 16 values, quantizes them and resets the counter. No block waits for
+//     another.
 // FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
 // quantize of the raw input rows (a.pre), computed by every block (K = NSTEP * 1024, NW = 16).
-template <int NW> struct SwigluShape {
-    static constexpr int WPU = (NW >= 8) ? 2 : 4;     // waves per unit
-    static constexpr int UPB = NW / WPU;               // unit slots per block
-    static constexpr int RW = 32 / WPU;                // rows per wave per unit
-};
+constexpr int kSwRows = 288;     // SwiGLU rows one block may hold: 32 F + 8 (quarters per block)
 template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE, int NW>
 __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr int SL = NSTEP * 64;
     constexpr int NT = NW * 64;
     constexpr int NSTG = (NR * SL + NT - 1) / NT;      // staging loads per thread
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
-    using SW = SwigluShape<NW>;
-    constexpr int GPU_ = SW::RW / RPW;                 // SwiGLU: groups per wave per unit
-    static_assert(EPI != EPI_SWIGLU || (SW::RW % RPW == 0 && NW % SW::WPU == 0), "SwiGLU shape");
+    static_assert(EPI != EPI_SWIGLU || RPW == 1, "SwiGLU deals single rows");
     static_assert(!PRE || NW == 16, "the norm prologue runs on 16-wave blocks");
     __shared__ uint4 sx[NR * SL];
     __shared__ float ssc[NR * SL];
-    __shared__ float sacc[(EPI == EPI_SWIGLU) ? 2 * SW::UPB * 32 * NR : 1];
+    __shared__ float sacc[(EPI == EPI_SWIGLU) ? kSwRows * NR : 1];
     __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
     if (a.stop && *a.stop) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
-    const int nb = gridDim.x;
+    const int nb = gridDim.x, bi = blockIdx.x;
     // group sequence of this wave: index i = 0 .. niter-1
-    const int slot = wave / SW::WPU, sub = wave % SW::WPU;
-    const int nunits = (a.rows + 31) >> 5;
     const int ngroups = (a.rows + RPW - 1) / RPW;
-    const int gw = blockIdx.x * NW + wave, nw = nb * NW;
+    const int gw = bi * NW + wave, nw = nb * NW;
+    const int nunits = a.rows >> 5, F = nunits / nb, E = nunits - F * nb;
+    const int nq = 4 * E, myq = (nq > bi) ? (nq - 1 - bi) / nb + 1 : 0;   // leftover quarters
     int niter;
     if constexpr (EPI == EPI_SWIGLU) {
-        const int per_round = nb * SW::UPB;
-        const int rounds = (nunits - (int)blockIdx.x + per_round - 1) / per_round;   // slot 0's
-        niter = rounds * GPU_;                         // the same for every wave of the block
+        const int nrb = 32 * F + 8 * myq;              // this block's rows
+        niter = (nrb > wave) ? (nrb - 1 - wave) / NW + 1 : 0;
     } else {
         niter = (gw < ngroups) ? (ngroups - 1 - gw) / nw + 1 : 0;
     }
-    auto unit_of = [&](int i) __attribute__((always_inline)) {
-        return (int)blockIdx.x + nb * (slot + SW::UPB * (i / GPU_));
-    };
-    auto valid = [&](int i) __attribute__((always_inline)) {
-        if constexpr (EPI == EPI_SWIGLU) return i < niter && unit_of(i) < nunits;
-        else return i < niter;
-    };
+    auto valid = [&](int i) __attribute__((always_inline)) { return i < niter; };
     auto row_of = [&](int i, int r) __attribute__((always_inline)) {
-        if constexpr (EPI == EPI_SWIGLU) return unit_of(i) * 32 + sub * SW::RW + RPW * (i % GPU_) + r;
-        else return (gw + i * nw) * RPW + r;
+        if constexpr (EPI == EPI_SWIGLU) {
+            const int j = wave + NW * i;               // the block's local row
+            if (j < 32 * F) return (bi + nb * (j >> 5)) * 32 + (j & 31);
+            const int m = (j - 32 * F) >> 3, r8 = (j - 32 * F) & 7;
+            const int p = bi + nb * m, u = F * nb + (p >> 2), q = p & 3;
+            return u * 32 + (r8 < 4 ? 4 * q + r8 : 12 + 4 * q + r8);
+        } else {
+            return (gw + i * nw) * RPW + r;
+        }
     };
     uint4 W[RPW][NSTEP];
     float S[RPW][NSTEP];
-    auto ld = [&](int i, int r, int t) __attribute__((always_inline)) {
-        int row = row_of(i, r);
+    // Loads are issued on every path: a group past the wave's last (ok == false) reads the first
+    // 16 bytes of the weights instead, so no branch merges a path that loaded with one that did
+    // not, and each wait the compiler places counts exactly the loads still owed to later groups
+    // (a merge of the two would make it wait for all of them).
+    // rg: the group's first row (wave-uniform), computed once per group
+    auto ld = [&](int rg, int r, int t, bool ok) __attribute__((always_inline)) {
+        int row = rg + r;
         row = row < a.rows ? row : a.rows - 1;
         const int s = t * 64 + lane;
         if (FULL || s < nslab) {
-            W[r][t] = ld_nt16(a.W + (size_t)row * K + 16 * s);
-            S[r][t] = a.WS[(size_t)row * ng64 + (s >> 2)];
+            W[r][t] = ld_nt16(ok ? a.W + (size_t)row * K + 16 * s : a.W);
+            S[r][t] = *(ok ? a.WS + (size_t)row * ng64 + (s >> 2) : a.WS);
         } else {
             W[r][t] = make_uint4(0u, 0u, 0u, 0u);
             S[r][t] = 0.0f;
         }
     };
     auto prefetch = [&]() __attribute__((always_inline)) {
-        if (valid(0)) {
+        const bool ok = valid(0);
+        const int rg = __builtin_amdgcn_readfirstlane(row_of(0, 0));
 #pragma unroll
-            for (int t = 0; t < NSTEP; ++t)
+        for (int t = 0; t < NSTEP; ++t)
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) ld(0, r, t);
-        }
+            for (int r = 0; r < RPW; ++r) ld(rg, r, t, ok);
     };
     if constexpr (PRE) {
-        // input rows first, then the weights, so waiting for the rows leaves the weights in flight
+        // input rows first, then the weights, so waiting for the rows leaves the weights in flight.
+        // With two rows per 256-thread group (NR > 4) the held rows and the prefetch do not fit
+        // in 128 registers together; the weights are then requested after the norm.
         PreNorm<NSTEP, NR> pn;
+        constexpr bool EARLY = PreNorm<NSTEP, NR>::RPG == 1;
         pn.load(a.pre);
         __builtin_amdgcn_sched_barrier(0);
-        prefetch();
+        if constexpr (EARLY) prefetch();
         __builtin_amdgcn_sched_barrier(0);
         pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
+        if constexpr (!EARLY) prefetch();
     } else if constexpr (FULL) {
         // activation stage by LDS DMA (global_load_lds: each lane's 16-byte code word and 4-byte
         // scale land at the wave's LDS base + lane offset, no registers), requested together with
@@ -155,7 +165,13 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
         }
         prefetch();
-        __builtin_amdgcn_s_waitcnt(0);                   // LDS DMA writes complete before the barrier
+        // this wave's LDS DMA writes are complete before the barrier: they are older than the
+        // prefetch's 2 NSTEP RPW loads, which stay in flight (vector-memory counts retire in
+        // order). A plain barrier plus an acquire fence, because the release half of
+        // __syncthreads would wait for the prefetch as well.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NSTEP * RPW));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     } else {
         // activation stage: every load issued before any LDS write (one round trip). When the
         // stage is small its registers coexist with the weight prefetch, which is then requested
@@ -186,91 +202,106 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         }
         if constexpr (!EARLY) prefetch();
     }
-    __syncthreads();
+    if constexpr (PRE || !FULL) __syncthreads();
     const int vi = lane / LPV;                         // the value this lane holds after the tree
     const bool holder = (lane % LPV) == 0 && vi < V;
     const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
     const uint32_t* resw = (const uint32_t*)a.res;
     for (int i = 0; i < niter; ++i) {
-        const bool vnow = valid(i);
-        if (vnow) {
-            // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use
-            uint32_t rw = 0u;
-            size_t ridx = 0;
-            if (EPI == EPI_STORE && resw) {
-                int row = row_of(i, hr);
-                row = row < a.rows ? row : a.rows - 1;
-                ridx = (size_t)hn * a.rstride + row;
-                rw = a.res_bf16 ? resw[ridx >> 1] : resw[ridx];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            float acc[P];
-#pragma unroll
-            for (int v = 0; v < P; ++v) acc[v] = 0.0f;
-            auto body = [&](auto reload) __attribute__((always_inline)) {
-#pragma unroll
-                for (int t = 0; t < NSTEP; ++t) {
-                    const int s = t * 64 + lane;
-#pragma unroll
-                    for (int n = 0; n < NR; ++n) {
-                        const uint4 xa = sx[n * SL + s];
-                        const float sa = ssc[n * SL + s];
-#pragma unroll
-                        for (int r = 0; r < RPW; ++r) {
-                            const int d = dot16(W[r][t], xa);
-                            acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
-                        }
-                    }
-                    if constexpr (decltype(reload)::value) {
-#pragma unroll
-                        for (int r = 0; r < RPW; ++r) ld(i + 1, r, t);
-                    }
-                }
-            };
-            if (valid(i + 1)) body(std::true_type{});
-            else body(std::false_type{});
-            const float tv = tree_t<P>(acc, lane) * a.alpha;
-            if constexpr (EPI == EPI_STORE) {
-                const int row = row_of(i, hr);
-                if (holder && row < a.rows) {
-                    float v = tv;
-                    if (resw) {
-                        const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
-                                                    : __uint_as_float(rw);
-                        if (a.res_round) v = bfr(v);
-                        v = v + a.rs * rv;
-                    }
-                    const size_t yi = (size_t)hn * a.ystride + row;
-                    if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
-                    else ((float*)a.y)[yi] = v;
-                }
-            } else {
-                float* sw = sacc + (((i / GPU_) & 1) * SW::UPB + slot) * 32 * NR;
-                if (holder) sw[(sub * SW::RW + RPW * (i % GPU_) + hr) * NR + hn] = tv;
-            }
+        const bool more = valid(i + 1);
+        const int rg_next = __builtin_amdgcn_readfirstlane(row_of(i + 1, 0));
+        // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use; loaded
+        // (from a harmless address) also when there is none, for the reason given at ld
+        size_t ridx = 0;
+        uint32_t rw = 0u;
+        if constexpr (EPI == EPI_STORE) {
+            int row = row_of(i, hr);
+            row = row < a.rows ? row : a.rows - 1;
+            ridx = (size_t)hn * a.rstride + row;
+            rw = *(resw ? resw + (a.res_bf16 ? (ridx >> 1) : ridx) : (const uint32_t*)a.W);
         }
-        if constexpr (EPI == EPI_SWIGLU) {
-            // end of a round: 32 rows [16 gate | 16 up] -> 16 outputs, one quantization group;
-            // double-buffered partials, one barrier per round
-            if (i % GPU_ == GPU_ - 1) {
-                __syncthreads();
-                if (sub == 0 && vnow) {
-                    const float* sw = sacc + (((i / GPU_) & 1) * SW::UPB + slot) * 32 * NR;
-                    const int unit = unit_of(i), j = lane & 15;
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[P];
 #pragma unroll
-                    for (int nn = 0; nn < NR; ++nn) {
-                        const float gv = sw[j * NR + nn], uv = sw[(16 + j) * NR + nn];
-                        const float swv = gv / (1.0f + qexp(-gv));
-                        const float v = swv * uv * a.gscale;
-                        const float mx = max_xor(fabsf(v), 16);
-                        const float sc = mx * (1.0f / 127.0f);
-                        const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
-                        if (lane < 16) {
-                            a.act_q[(size_t)nn * a.act_stride + unit * 16 + j] = qcode(v, inv);
-                            if (j == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
-                        }
-                    }
+        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+            const int s = t * 64 + lane;
+#pragma unroll
+            for (int n = 0; n < NR; ++n) {
+                const uint4 xa = sx[n * SL + s];
+                const float sa = ssc[n * SL + s];
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const int d = dot16(W[r][t], xa);
+                    acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
                 }
+            }
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) ld(rg_next, r, t, more);
+        }
+        const float tv = tree_t<P>(acc, lane) * a.alpha;
+        if constexpr (EPI == EPI_STORE) {
+            const int row = row_of(i, hr);
+            if (holder && row < a.rows) {
+                float v = tv;
+                if (resw) {
+                    const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
+                                                : __uint_as_float(rw);
+                    if (a.res_round) v = bfr(v);
+                    v = v + a.rs * rv;
+                }
+                const size_t yi = (size_t)hn * a.ystride + row;
+                if (a.out_bf16) ((uint16_t*)a.y)[yi] = f2bf(v);
+                else ((float*)a.y)[yi] = v;
+            }
+        } else {
+            if (holder) sacc[(wave + NW * i) * NR + hn] = tv;
+        }
+    }
+    if constexpr (EPI == EPI_SWIGLU) {
+        __syncthreads();
+        // v = silu(g) * u * gscale for output j (rows j and 16 + j of its unit)
+        auto swiglu = [&](float gv, float uv) __attribute__((always_inline)) {
+            const float swv = gv / (1.0f + qexp(-gv));
+            return swv * uv * a.gscale;
+        };
+        // 16 outputs in lanes j = lane & 15 -> one per-16 group: exact max, scale, codes
+        auto quant16 = [&](float v, int unit, int nn) __attribute__((always_inline)) {
+            const float mx = max_xor(fabsf(v), 16);
+            const float sc = mx * (1.0f / 127.0f);
+            const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+            if (lane < 16) {
+                a.act_q[(size_t)nn * a.act_stride + unit * 16 + lane] = qcode(v, inv);
+                if (lane == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
+            }
+        };
+        const int j = lane & 15;
+        for (int k = wave; k < F; k += NW) {           // whole units
+            const int unit = bi + nb * k;
+#pragma unroll
+            for (int nn = 0; nn < NR; ++nn)
+                quant16(swiglu(sacc[(32 * k + j) * NR + nn], sacc[(32 * k + 16 + j) * NR + nn]), unit, nn);
+        }
+        for (int m = 0; m < myq; ++m) {                // leftover quarters
+            if (wave != (F + m) % NW) continue;
+            const int p = bi + nb * m, e = p >> 2, q = p & 3, unit = F * nb + e, c = lane & 3;
+            float* part = a.sw_part + (size_t)e * 16 * NR;   // [16 outputs][NR]
+            const int lr = 32 * F + 8 * m;
+#pragma unroll
+            for (int nn = 0; nn < NR; ++nn) {
+                const float v = swiglu(sacc[(lr + c) * NR + nn], sacc[(lr + 4 + c) * NR + nn]);
+                if (lane < 4) st_agent(part + (4 * q + c) * NR + nn, v);
+            }
+            __builtin_amdgcn_s_waitcnt(0);             // the stores are acknowledged before counting
+            unsigned prev = 0u;
+            if (lane == 0) prev = add_agent(a.sw_cnt + e, 1u);
+            prev = (unsigned)__builtin_amdgcn_readfirstlane((int)prev);
+            if (prev == 3u) {                          // the unit's fourth quarter: finish it
+#pragma unroll
+                for (int nn = 0; nn < NR; ++nn)
+                    quant16(__hip_atomic_load(part + j * NR + nn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), unit, nn);
+                if (lane == 0) st_agent(a.sw_cnt + e, 0u);
             }
         }
     }
@@ -307,8 +338,14 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
     constexpr int NW = (PRE || EPI == EPI_SWIGLU) ? 16 : 4;
     int grid;
     if (EPI == EPI_SWIGLU) {
-        const int nunits = (a.rows + 31) >> 5;
+        const int nunits = a.rows >> 5;
         grid = nunits < num_cus() ? nunits : num_cus();
+        const int F = nunits / grid, E = nunits - F * grid;
+        if (32 * F + 8 * ((4 * E + grid - 1) / grid) > kSwRows || E > kSwMaxSplit || (E && (!a.sw_part || !a.sw_cnt))) {
+            set_error("proj: SwiGLU shape rows=%d over %d blocks needs %s", a.rows, grid,
+                      (E && (!a.sw_part || !a.sw_cnt)) ? "the split-unit scratch" : "more LDS than it has");
+            return Q27X_E_SHAPE;
+        }
     } else if (NW == 16) {
         const int ngroups = (a.rows + RPW - 1) / RPW;
         const int nb = (ngroups + NW - 1) / NW;
@@ -380,7 +417,7 @@ static int route_nr(const ProjArgs& a, int nr, hipStream_t s) {
 
 static int route(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     const bool full = (a.K & 1023) == 0;
-    if (epi == EPI_SWIGLU) return full ? route_nr<EPI_SWIGLU, true>(a, nr, s) : route_nr<EPI_SWIGLU, false>(a, nr, s);
+    if (epi == EPI_SWIGLU) return full ? route_nr<EPI_SWIGLU, true>(a, nr, s) : -2;   // K = 1024 k only
     return full ? route_nr<EPI_STORE, true>(a, nr, s) : route_nr<EPI_STORE, false>(a, nr, s);
 }
 

@@ -92,6 +92,11 @@ __device__ __forceinline__ float qsilu(float x) { return x / (1.0f + qexp(-x)); 
 __device__ __forceinline__ float qsoftplus(float x) { return (x > 20.0f) ? x : qlog1p(qexp(x)); }
 __device__ __forceinline__ float rsqrt_cr(float x) { return 1.0f / __builtin_sqrtf(x); }
 
+// s_waitcnt immediate that waits until at most n (<= 63) vector-memory operations of this wave
+// are outstanding and leaves the export and LDS/scalar counters alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // ---------------------------------------------------------------- reductions
 // shfl_down tree over the 64 lanes (offsets 32..1); the result is valid in lane 0.
 __device__ __forceinline__ float tree64(float x) {
@@ -102,6 +107,14 @@ __device__ __forceinline__ float tree64(float x) {
 __device__ __forceinline__ float max_xor(float x, int width) {   // exact max over `width` lanes
 #pragma unroll
     for (int o = width >> 1; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+// The same max over the 4 lanes of a quad with DPP quad permutes (a VALU operand route, no LDS
+// crossbar): lane l reads lane l ^ 2 (quad_perm [2,3,0,1]), then l ^ 1 ([1,0,3,2]). The max of the
+// same four values in any order is the same float.
+__device__ __forceinline__ float max_quad(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false)));
     return x;
 }
 

@@ -41,13 +41,17 @@ struct ProjArgs {
     // EPI_STORE: y = v (+ rs*res); res_round rounds v through bf16 before the add
     void* y; int ystride; int out_bf16;
     const void* res; int res_bf16; int rstride; float rs; int res_round;
-    // EPI_SWIGLU: the weight rows interleave 16 gate rows and 16 up rows per block of 32
+    // EPI_SWIGLU: the weight rows interleave 16 gate rows and 16 up rows per block of 32.
+    // sw_part / sw_cnt: scratch for units split over blocks (kSwMaxSplit units of 16 x kMaxRows
+    // floats, kSwMaxSplit counters that start at zero and are left at zero)
     int8_t* act_q; float* act_s; int act_stride; float gscale;
+    float* sw_part; unsigned* sw_cnt;
     const int* stop;             // early exit when *stop != 0
     // norm prologue: instead of xq/xs, every block stages the RMSNorm + quantize of the raw rows
     // described by `pre` (K = pre.n); block 0 also writes pre's side outputs (hcopy, y, xq/xs)
     int has_pre; NormArgs pre;
 };
+constexpr int kSwMaxSplit = 256;
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
 
 // bf16 GEMV: y = W x (fp32 / bf16 out) or, argmax mode, per-block (val, idx) partials

@@ -167,9 +167,22 @@ struct PreNorm {
         }
     }
     // sxw: the LDS code stage as 32-bit words ([NR][SL] slabs of 4 words); ssc: [NR][SL] scales;
-    // wsum: __shared__ float[RPG][GR][4]
+    // wsum: __shared__ float[RPG][GR][4]. Block 0 (writer) also stores the side outputs; the other
+    // blocks run a copy without them, and the bf16 rounding of the normalized values is compiled
+    // in only where it is used (side output y or quant_bf16), about halving their instructions.
     __device__ __forceinline__ void finish(const NormArgs& a, uint32_t* sxw, float* ssc, int SL,
                                            float (*wsum)[GR][4], bool writer) {
+        if (writer) {
+            if (a.quant_bf16) fin<true, true>(a, sxw, ssc, SL, wsum);
+            else fin<true, false>(a, sxw, ssc, SL, wsum);
+        } else {
+            if (a.quant_bf16) fin<false, true>(a, sxw, ssc, SL, wsum);
+            else fin<false, false>(a, sxw, ssc, SL, wsum);
+        }
+    }
+    template <bool WR, bool QB>
+    __device__ __forceinline__ void fin(const NormArgs& a, uint32_t* sxw, float* ssc, int SL,
+                                        float (*wsum)[GR][4]) {
         const int t = threadIdx.x & 255, tg = threadIdx.x >> 8, lane = t & 63, wv = t >> 6;
         constexpr int n = NCH * 1024;
 #pragma unroll
@@ -180,7 +193,7 @@ struct PreNorm {
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 const float* v = xv[j][i];
-                if (writer && a.hcopy)
+                if (WR && a.hcopy)
                     *(uint2*)(a.hcopy + (size_t)r * n + i * 1024 + 4 * t) =
                         make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
                                    (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
@@ -203,19 +216,19 @@ struct PreNorm {
                 const int k = i * 1024 + 4 * t;
                 const float wf[4] = {__uint_as_float(wb[i].x << 16), __uint_as_float(wb[i].x & 0xFFFF0000u),
                                      __uint_as_float(wb[i].y << 16), __uint_as_float(wb[i].y & 0xFFFF0000u)};
-                float nm[4], q[4], mx = 0.0f;
+                float q[4], mx = 0.0f;
                 uint16_t yb[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    nm[e] = xv[j][i][e] * inv * (a.plus + wf[e]);
-                    yb[e] = f2bf(nm[e]);
-                    q[e] = a.quant_bf16 ? bf2f(yb[e]) : nm[e];
+                    const float nm = xv[j][i][e] * inv * (a.plus + wf[e]);
+                    if constexpr (WR || QB) yb[e] = f2bf(nm);
+                    q[e] = QB ? bf2f(yb[e]) : nm;
                     mx = fmaxf(mx, fabsf(q[e]));
                 }
-                if (writer && a.y)
+                if (WR && a.y)
                     *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
                                                                            (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
-                mx = max_xor(mx, 4);
+                mx = max_quad(mx);
                 const float s = mx * g * (1.0f / 127.0f);
                 const float qi = (s > 0.0f) ? (g / s) : 0.0f;
                 uint32_t pk = 0;
@@ -224,7 +237,7 @@ struct PreNorm {
                 const int slab = 64 * i + (t >> 2);
                 sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
                 if ((t & 3) == 0) ssc[r * SL + slab] = s;
-                if (writer && a.xq) {
+                if (WR && a.xq) {
                     *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
                     if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
                 }

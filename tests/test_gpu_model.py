@@ -57,6 +57,26 @@ def test_tiny_spec_rounds_match_oracle(tiny_pair):
         assert a == b, f"round {r}: gpu {a} oracle {b}"
 
 
+@pytest.mark.parametrize("inter", [5120, 6144])
+def test_tiny_split_swiglu_units_match_oracle(gpu, O, inter):
+    """gate|up with more 32-row SwiGLU units than blocks (one block per CU): 320 units leave 64
+    units split into quarters over the blocks (one quarter per block), 384 units leave 128 (two
+    quarters on every block); the split units' codes must be the bits of the oracle's."""
+    X = gpu
+    cfg = tiny(X, spec_k=2, inter=inter)
+    eng = X.Engine(cfg, SEED)
+    om = O.Model(cfg, SEED)
+    p = prompt_of(cfg, 19, seed=inter)
+    assert eng.prefill(p) == om.prefill(p)
+    hg = eng.read("hprev", -1, np.uint16, cfg.hidden)
+    assert np.array_equal(hg, om.tensor("hprev", -1, np.uint16))
+    for r in range(6):
+        a, b = eng.spec_round(), om.spec_round()
+        assert a == b, f"inter {inter} round {r}: gpu {a} oracle {b}"
+    eng.close()
+    om.close()
+
+
 def test_tiny_spec_equals_plain_and_forced(gpu, O):
     X = gpu
     for k in (1, 2, 3, 7):
