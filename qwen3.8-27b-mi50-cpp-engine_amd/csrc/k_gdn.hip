@@ -66,7 +66,6 @@ __device__ __forceinline__ PendArea pend_area(void* p, int kh, int vh, int which
 
 template <int CONV, int FUSE_AB>
 __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, size_t hist_off) {
-    if (a.stop && *a.stop) return;
     const int h = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int d = t & (kD - 1), g = t >> 7;
@@ -164,6 +163,7 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     }
 
     // ================= phase B: on-chip work =================
+    if (a.stop && *a.stop) return;                // read once the loads are in flight
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int p = g + 4 * u;

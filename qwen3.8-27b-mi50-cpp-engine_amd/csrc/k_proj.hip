@@ -81,7 +81,8 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     __shared__ float ssc[NR * SL];
     __shared__ float sacc[(EPI == EPI_SWIGLU) ? kSwRows * NR : 1];
     __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
-    if (a.stop && *a.stop) return;
+    // The round's stop flag is read once the prologue's loads are in flight (before any store),
+    // so its read does not add a memory round trip in front of them.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
     const int nb = gridDim.x, bi = blockIdx.x;
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (EARLY) prefetch();
         __builtin_amdgcn_sched_barrier(0);
+        if (a.stop && *a.stop) return;
         pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
         if constexpr (!EARLY) prefetch();
     } else if constexpr (FULL) {
@@ -165,6 +167,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
         }
         prefetch();
+        if (a.stop && *a.stop) return;
         // this wave's LDS DMA writes are complete before the barrier: they are older than the
         // prefetch's 2 NSTEP RPW loads, which stay in flight (vector-memory counts retire in
         // order). A plain barrier plus an acquire fence, because the release half of
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             if (i < NR * SL) { sx[i] = tv[j]; ssc[i] = ts[j]; }
         }
         if constexpr (!EARLY) prefetch();
+        if (a.stop && *a.stop) return;
     }
     if constexpr (PRE || !FULL) __syncthreads();
     const int vi = lane / LPV;                         // the value this lane holds after the tree
