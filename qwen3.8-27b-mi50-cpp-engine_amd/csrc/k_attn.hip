@@ -18,7 +18,7 @@ constexpr int kHD = 128;
 constexpr int kMaxQ = kMaxRows * 8;   // rows x GQA heads per kv head held by one block
 
 __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
-    if (a.stop && *a.stop) return;
+    if (stopped(a.stop)) return;
     const int r = blockIdx.y;
     if (a.nact_ptr && r >= *a.nact_ptr) return;
     const int pos = (a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm) + r;
@@ -98,7 +98,7 @@ constexpr int kKStride = kHD + 4;
 constexpr int kAttnThreads = 512;
 template <int NQW, int QPT>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
-    if (a.stop && *a.stop) return;
+    if (stopped(a.stop)) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
     const int nact = a.nact_ptr ? *a.nact_ptr : nr;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 // time with coalesced loads; x sigmoid(gate) -> bf16 -> per-16 quantize.
 constexpr int kCombChunk = 32;
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
-    if (a.stop && *a.stop) return;
+    if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
     if (a.nact_ptr && r >= *a.nact_ptr) return;
     const int pos0 = a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm;

@@ -28,7 +28,7 @@ int hip_fail(hipError_t e, const char* what) {
 constexpr int kNormMaxChunks = 8;   // n <= 8192
 template <int NCH>
 __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
-    if (a.stop && *a.stop) return;
+    if (stopped(a.stop)) return;
     __shared__ float wsum[1][4];
     norm_rows<NCH, 1>(a, blockIdx.x, 1, wsum);
 }

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     }
 
     // ================= phase B: on-chip work =================
-    if (a.stop && *a.stop) return;                // read once the loads are in flight
+    if (stopped(a.stop)) return;                // read once the loads are in flight
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int p = g + 4 * u;

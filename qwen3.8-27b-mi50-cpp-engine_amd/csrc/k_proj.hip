@@ -130,12 +130,11 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         }
     };
     auto prefetch = [&]() __attribute__((always_inline)) {
-        const bool ok = valid(0);
         const int rg = __builtin_amdgcn_readfirstlane(row_of(0, 0));
 #pragma unroll
         for (int t = 0; t < NSTEP; ++t)
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) ld(rg, r, t, ok);
+            for (int r = 0; r < RPW; ++r) ld(rg, r, t, valid(0));
     };
     if constexpr (PRE) {
         // input rows first, then the weights, so waiting for the rows leaves the weights in flight.
@@ -147,7 +146,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (EARLY) prefetch();
         __builtin_amdgcn_sched_barrier(0);
-        if (a.stop && *a.stop) return;
+        if (stopped(a.stop)) return;
         pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
         if constexpr (!EARLY) prefetch();
     } else if constexpr (FULL) {
@@ -167,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
         }
         prefetch();
-        if (a.stop && *a.stop) return;
+        if (stopped(a.stop)) return;
         // this wave's LDS DMA writes are complete before the barrier: they are older than the
         // prefetch's 2 NSTEP RPW loads, which stay in flight (vector-memory counts retire in
         // order). A plain barrier plus an acquire fence, because the release half of
@@ -204,7 +203,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             if (i < NR * SL) { sx[i] = tv[j]; ssc[i] = ts[j]; }
         }
         if constexpr (!EARLY) prefetch();
-        if (a.stop && *a.stop) return;
+        if (stopped(a.stop)) return;
     }
     if constexpr (PRE || !FULL) __syncthreads();
     const int vi = lane / LPV;                         // the value this lane holds after the tree
@@ -494,7 +493,7 @@ template <int NR, int NSTEP, int RPW, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, int upw) {
     constexpr int CH = NSTEP * 64;
     __shared__ float sxf[NR * CH * 8];
-    if (a.stop && *a.stop) return;
+    if (stopped(a.stop)) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nch = K >> 3;
     const int ngroups = (a.rows + RPW - 1) / RPW;
@@ -657,7 +656,7 @@ int launch_gemv(const GemvArgs& a, int argmax_mode, int nr, int* nblocks_out, hi
 __global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pval, const uint32_t* __restrict__ pidx,
                                                       int pstride, int nblocks, int32_t* __restrict__ idx,
                                                       float* __restrict__ val, const int* stop) {
-    if (stop && *stop) return;
+    if (stopped(stop)) return;
     const int n = blockIdx.x;
     __shared__ float sv[4];
     __shared__ uint32_t si[4];

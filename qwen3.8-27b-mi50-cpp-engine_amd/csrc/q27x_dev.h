@@ -97,6 +97,14 @@ __device__ __forceinline__ float rsqrt_cr(float x) { return 1.0f / __builtin_sqr
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// The round's stop flag (null: never stopped), read through the constant address space so it is
+// a scalar load: a vector load would make the wait for it (vmcnt) also wait for every weight load
+// issued before it. The flag does not change while a kernel that reads it runs.
+__device__ __forceinline__ bool stopped(const int* p) {
+    typedef __attribute__((address_space(4))) const int cint;
+    return p && *(cint*)p;
+}
+
 // ---------------------------------------------------------------- reductions
 // shfl_down tree over the 64 lanes (offsets 32..1); the result is valid in lane 0.
 __device__ __forceinline__ float tree64(float x) {
