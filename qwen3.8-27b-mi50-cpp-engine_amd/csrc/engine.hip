@@ -324,8 +324,7 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
             a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
             a.pos0_ptr = &d->pos; a.work = x->attn_work; a.max_splits = x->max_splits; a.sl2e = x->sl2e;
             a.out = x->ao; a.xq = xa; a.xs = sa; a.stop = &d->stop;
-            if ((rc = launch_attn_prep(a, nr, s))) return rc;
-            if ((rc = launch_attn(a, nr, s))) return rc;
+            if ((rc = launch_attn(a, nr, s, true))) return rc;
             o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.xq = xa; o.xst = x->att; o.xs = sa;
         } else {
             // in_qkv | in_z (raw bf16 rows; the conv runs inside the GDN kernel)
@@ -426,9 +425,8 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
     a.pos0_ptr = &d->mtp_dpos0; a.nact_ptr = &d->mtp_nact; a.work = x->attn_work; a.max_splits = x->max_splits;
     a.sl2e = x->sl2e; a.out = x->ao; a.xq = xa; a.xs = sa; a.stop = &d->stop;
-    if ((rc = launch_attn_prep(a, nr, s))) return rc;
-    if (kv_only) return Q27X_OK;
-    if ((rc = launch_attn(a, nr, s))) return rc;
+    if (kv_only) return launch_attn_prep(a, nr, s);
+    if ((rc = launch_attn(a, nr, s, true))) return rc;
     // o-proj rounded to bf16 before the residual add
     ProjArgs o{};
     o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.alpha = 1.0f; o.xq = xa; o.xst = x->att; o.xs = sa;

@@ -17,51 +17,39 @@ namespace q27x {
 constexpr int kHD = 128;
 constexpr int kMaxQ = kMaxRows * 8;   // rows x GQA heads per kv head held by one block
 
-__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
-    if (stopped(a.stop)) return;
-    const int r = blockIdx.y;
-    if (a.nact_ptr && r >= *a.nact_ptr) return;
-    const int pos = (a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm) + r;
-    const int l = threadIdx.x;
-    const int u = blockIdx.x;
-    const bool isq = u < a.nq;
-    const int head = isq ? u : u - a.nq;
-    const int qw = a.gate ? 2 * kHD : kHD;
-    const int qrows = a.nq * qw, kvrows = a.nkv * kHD;
-    const uint16_t* row = a.qkv + (size_t)r * a.qkv_stride;
-    const uint16_t* src = isq ? row + (size_t)head * qw : row + qrows + (size_t)head * kHD;
-    const uint16_t* wgt = isq ? a.q_norm_w : a.k_norm_w;
+// RMSNorm (1 + w) and rotate-half RoPE of one head row at position pos by one wave: lane l holds
+// dims l and l + 64 of the head's 128 bf16 values at src.
+__device__ __forceinline__ void norm_rope(const AttnArgs& a, const uint16_t* src, const uint16_t* wgt, int pos,
+                                          int l, float& y0, float& y1) {
     const float x0 = bf2f(src[l]), x1 = bf2f(src[l + 64]);
+    const float wg0 = bf2f(wgt[l]), wg1 = bf2f(wgt[l + 64]);
+    // the RoPE table entries are read by every lane (in bounds for any lane) with the inputs
+    const int half = a.rot >> 1;
+    const int f = (a.rot <= 64) ? (l & (half - 1)) : l;
+    const float c = a.rope_cos[(size_t)pos * half + f], s = a.rope_sin[(size_t)pos * half + f];
     const float w0 = tree64(x0 * x0), w1 = tree64(x1 * x1);
     const float ss = __shfl(w0, 0, 64) + __shfl(w1, 0, 64);
     const float inv = rsqrt_cr(ss * (1.0f / (float)kHD) + a.eps);
-    float y0 = x0 * inv * (1.0f + bf2f(wgt[l]));
-    float y1 = x1 * inv * (1.0f + bf2f(wgt[l + 64]));
-    const int half = a.rot >> 1;
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
+    y0 = x0 * inv * (1.0f + wg0);
+    y1 = x1 * inv * (1.0f + wg1);
     if (a.rot <= 64) {
         const float pv = __shfl_xor(y0, half, 64);
         if (l < a.rot) {
             const float rv = (l < half) ? -pv : pv;
-            const int f = l & (half - 1);
-            y0 = y0 * cs[f] + rv * sn[f];
+            y0 = y0 * c + rv * s;
         }
     } else {   // rot == 128: dims l and l+64 are partners
-        const float c = cs[l], s = sn[l];
         const float n0 = y0 * c + (-y1) * s;
         const float n1 = y1 * c + y0 * s;
         y0 = n0; y1 = n1;
     }
-    if (isq) {
-        uint16_t* dst = a.qh + (size_t)r * a.nq * kHD + (size_t)head * kHD;
-        dst[l] = f2bf(y0);
-        dst[l + 64] = f2bf(y1);
-        return;
-    }
-    const uint16_t* vsrc = row + qrows + kvrows + (size_t)head * kHD;
-    const float v0 = bf2f(vsrc[l]), v1 = bf2f(vsrc[l + 64]);
-    const size_t off = (size_t)pos * kvrows + (size_t)head * kHD;
+}
+
+// K (normed, roped: y0, y1) and V (raw: v0, v1) of one kv head row -> int8 codes with one fp32
+// scale per kv_group at cache element offset off; deq gets code * scale, the values the attention
+// reads back.
+__device__ __forceinline__ void store_kv(const AttnArgs& a, float y0, float y1, float v0, float v1, size_t off,
+                                         int l, float (&deq)[4]) {
     const int G = a.kv_group;
     const float vals[4] = { y0, y1, v0, v1 };
 #pragma unroll
@@ -73,9 +61,37 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
         const int dd = l + ((q & 1) ? 64 : 0);
         int8_t* c8 = (q < 2) ? a.kc : a.vc;
         float* cs8 = (q < 2) ? a.ks : a.vs;
-        c8[off + dd] = qcode(v, qi);
+        const int8_t code = qcode(v, qi);
+        c8[off + dd] = code;
         if ((dd % G) == 0) cs8[(off + dd) / G] = sc;
+        deq[q] = (float)code * sc;
     }
+}
+
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    if (stopped(a.stop)) return;
+    const int r = blockIdx.y;
+    if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
+    const int pos = (a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm) + r;
+    const int l = threadIdx.x;
+    const int u = blockIdx.x;
+    const bool isq = u < a.nq;
+    const int head = isq ? u : u - a.nq;
+    const int qw = a.gate ? 2 * kHD : kHD;
+    const int qrows = a.nq * qw, kvrows = a.nkv * kHD;
+    const uint16_t* row = a.qkv + (size_t)r * a.qkv_stride;
+    const uint16_t* src = isq ? row + (size_t)head * qw : row + qrows + (size_t)head * kHD;
+    float y0, y1;
+    norm_rope(a, src, isq ? a.q_norm_w : a.k_norm_w, pos, l, y0, y1);
+    if (isq) {
+        uint16_t* dst = a.qh + (size_t)r * a.nq * kHD + (size_t)head * kHD;
+        dst[l] = f2bf(y0);
+        dst[l + 64] = f2bf(y1);
+        return;
+    }
+    const uint16_t* vsrc = row + qrows + kvrows + (size_t)head * kHD;
+    float deq[4];
+    store_kv(a, y0, y1, bf2f(vsrc[l]), bf2f(vsrc[l + 64]), (size_t)pos * kvrows + (size_t)head * kHD, l, deq);
 }
 
 size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
@@ -96,13 +112,17 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
 // Dynamic LDS: queries [nqr][128] fp32 | p [nqr][65] fp32.
 constexpr int kKStride = kHD + 4;
 constexpr int kAttnThreads = 512;
-template <int NQW, int QPT>
+// PREP: the block also does the prep of its rows (the grid then holds one split per block): the
+// queries of its kv head are normed and roped here instead of read back, and the split that holds
+// the step's new positions computes their K and V, writes them to the cache and puts the
+// dequantized values straight into its tile.
+template <int NQW, int QPT, bool PREP>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
-    const int nact = a.nact_ptr ? *a.nact_ptr : nr;
-    const int pos0 = a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm;
+    const int nact = a.nact_ptr ? ld_uniform(a.nact_ptr) : nr;
+    const int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
     const int Lmax = pos0 + nact;
     const int nqr = nact * G;                       // query vectors of this kv head
     const int kvrows = a.nkv * kHD;
@@ -122,6 +142,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
         const int k0 = s * kSplit;
         const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
+        // keys [kn0, nk) are this step's new positions (PREP: computed below, not read)
+        const int kn0 = PREP ? ((pos0 - k0 > 0) ? (pos0 - k0 < nk ? pos0 - k0 : nk) : 0) : nk;
         // ---- loads: thread covers 16-byte words i = t and t + 512 (K words 0..511, V 512..1023)
         uint4 kv4[2];
         float scl[2];
@@ -130,14 +152,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
             kv4[u] = make_uint4(0u, 0u, 0u, 0u);
             scl[u] = 0.0f;
-            if (k < nk) {
+            if (k < kn0) {
                 const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + 16 * c;
                 kv4[u] = *(const uint4*)((isv ? a.vc : a.kc) + off);
                 scl[u] = (isv ? a.vs : a.ks)[off >> gsh];
             }
         }
         uint4 q4[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
-        if (!staged_q) {
+        if (!PREP && !staged_q) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int i = t + kAttnThreads * u;   // query vector i/16, 8 dims (i%16)*8
@@ -148,10 +170,51 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 }
             }
         }
+        // (before the barrier: these write only the query stage and the new keys' tile rows,
+        // which the dequantization below leaves alone, and their loads overlap the tile's)
+        if (PREP && !staged_q) {
+            // queries: one wave per query vector (row r, GQA head g): norm, RoPE, bf16
+            const int qw = a.gate ? 2 * kHD : kHD;
+            // (unrolled over the wave's NQW vectors with clamped indices, so every load is issued
+            // before the first wait)
+            float qy[NQW][2];
+#pragma unroll
+            for (int i = 0; i < NQW; ++i) {
+                const int qi = wv + (kAttnThreads / 64) * i, qc = qi < nqr ? qi : nqr - 1;
+                const int r = qc / G, g = qc - r * G;
+                const uint16_t* src = a.qkv + (size_t)r * a.qkv_stride + (size_t)(kvh * G + g) * qw;
+                norm_rope(a, src, a.q_norm_w, pos0 + r, lane, qy[i][0], qy[i][1]);
+            }
+#pragma unroll
+            for (int i = 0; i < NQW; ++i) {
+                const int qi = wv + (kAttnThreads / 64) * i;
+                if (qi < nqr) {
+                    qf[qi * kHD + lane] = bfr(qy[i][0]);
+                    qf[qi * kHD + 64 + lane] = bfr(qy[i][1]);
+                }
+            }
+            // new positions of this split: one wave per key
+            const int qrows = a.nq * qw;
+            for (int k = kn0 + wv; k < nk; k += kAttnThreads / 64) {
+                const int pos = k0 + k, r = pos - pos0;
+                const uint16_t* row = a.qkv + (size_t)r * a.qkv_stride;
+                const uint16_t* ksrc = row + qrows + (size_t)kvh * kHD;
+                const uint16_t* vsrc = row + qrows + kvrows + (size_t)kvh * kHD;
+                float y0, y1, deq[4];
+                norm_rope(a, ksrc, a.k_norm_w, pos, lane, y0, y1);
+                store_kv(a, y0, y1, bf2f(vsrc[lane]), bf2f(vsrc[lane + 64]), (size_t)pos * kvrows + (size_t)kvh * kHD,
+                         lane, deq);
+                kd[k * kKStride + lane] = deq[0];
+                kd[k * kKStride + 64 + lane] = deq[1];
+                vd[k * kHD + lane] = deq[2];
+                vd[k * kHD + 64 + lane] = deq[3];
+            }
+        }
         __syncthreads();                           // the previous split's tiles are consumed
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
+            if (k >= kn0 && k < nk) continue;      // a new position (PREP)
             const uint32_t w4[4] = {kv4[u].x, kv4[u].y, kv4[u].z, kv4[u].w};
             float* dst = isv ? &vd[k * kHD + 16 * c] : &kd[k * kKStride + 16 * c];
 #pragma unroll
@@ -164,7 +227,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 *(float4*)(dst + 4 * e4) = f;
             }
         }
-        if (!staged_q) {
+        if (!PREP && !staged_q) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int i = t + kAttnThreads * u;
@@ -177,8 +240,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                                        __uint_as_float(q4[u].w << 16), __uint_as_float(q4[u].w & 0xFFFF0000u));
                 }
             }
-            staged_q = true;
         }
+        staged_q = true;
         __syncthreads();
         // ---- scores + split softmax: lane = key, this wave's queries wv + 8 i
         {
@@ -272,8 +335,8 @@ constexpr int kCombChunk = 32;
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
-    if (a.nact_ptr && r >= *a.nact_ptr) return;
-    const int pos0 = a.pos0_ptr ? *a.pos0_ptr : a.pos0_imm;
+    if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
+    const int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
     const int L = pos0 + r + 1;
     const int ns = (L + kSplit - 1) / kSplit;
     const int ms = a.max_splits;
@@ -341,30 +404,40 @@ int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
     return Q27X_E_SHAPE;
 }
 
-int launch_attn(const AttnArgs& a, int nr, hipStream_t s) {
-    if (int rc = attn_check(a, nr)) return rc;
-    if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
+template <bool PREP>
+static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
     const int nqr = nr * (a.nq / a.nkv);
     const size_t lds = (size_t)nqr * (kHD + kSplit + 1) * 4;
     static bool lds_set = false;                  // queries + p of up to 64 query vectors: 49 KiB
     if (!lds_set) {
         const int mx = 64 * (kHD + kSplit + 1) * 4;
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<1, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<2, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<3, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<6, 3>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<8, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<1, 1, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<2, 1, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<3, 2, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<4, 2, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<6, 3, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<8, 4, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
         lds_set = true;
     }
+    // one split per block (max_splits covers the whole context)
     const dim3 grid(a.max_splits, a.nkv);
-    if (nqr <= 8) hipLaunchKernelGGL((k_attn_split<1, 1>), grid, dim3(kAttnThreads), lds, s, a, nr);
-    else if (nqr <= 16) hipLaunchKernelGGL((k_attn_split<2, 1>), grid, dim3(kAttnThreads), lds, s, a, nr);
-    else if (nqr <= 24) hipLaunchKernelGGL((k_attn_split<3, 2>), grid, dim3(kAttnThreads), lds, s, a, nr);
-    else if (nqr <= 32) hipLaunchKernelGGL((k_attn_split<4, 2>), grid, dim3(kAttnThreads), lds, s, a, nr);
-    else if (nqr <= 48) hipLaunchKernelGGL((k_attn_split<6, 3>), grid, dim3(kAttnThreads), lds, s, a, nr);
-    else hipLaunchKernelGGL((k_attn_split<8, 4>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    if (nqr <= 8) hipLaunchKernelGGL((k_attn_split<1, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 16) hipLaunchKernelGGL((k_attn_split<2, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 24) hipLaunchKernelGGL((k_attn_split<3, 2, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 32) hipLaunchKernelGGL((k_attn_split<4, 2, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else if (nqr <= 48) hipLaunchKernelGGL((k_attn_split<6, 3, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
+    else hipLaunchKernelGGL((k_attn_split<8, 4, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
     Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+// prep_fused: the split kernel does the prep as well (no k_attn_prep launch before it)
+int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
+    if (int rc = attn_check(a, nr)) return rc;
+    if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
+    if (prep_fused && !(a.rot == kHD || a.rot <= 64)) { set_error("attn: rot=%d unsupported", a.rot); return Q27X_E_SHAPE; }
+    const int rc = prep_fused ? launch_split<true>(a, nr, s) : launch_split<false>(a, nr, s);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr), dim3(kHD), 0, s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;

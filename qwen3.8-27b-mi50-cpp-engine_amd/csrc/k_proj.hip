@@ -27,6 +27,13 @@ template <int V> struct Pow2 {
     static constexpr int value = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : V <= 32 ? 32 : 64;
 };
 
+// shfl_down levels O, O/2, ..., 1 (down_add: DPP for offsets <= 8)
+template <int O>
+__device__ __forceinline__ float down_tree(float y) {
+    if constexpr (O == 0) return y;
+    else return down_tree<O / 2>(down_add<O>(y));
+}
+
 // Transposed shfl tree: P values per lane, each reduced over the 64 lanes with exactly the pairs
 // of the shfl_down tree (offsets 32..1; a + b and b + a are the same float); value v ends in lane
 // v * (64 / P). The halving levels exchange half of the values per step, so P values cost
@@ -46,10 +53,7 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
             x[v] = keep + __shfl_xor(send, o, 64);
         }
     }
-    float y = x[0];
-#pragma unroll
-    for (int o = 32 / P; o > 0; o >>= 1) y = y + __shfl_down(y, o, 64);
-    return y;
+    return down_tree<32 / P>(x[0]);
 }
 
 // Work assignment. A row group is RPW consecutive weight rows.

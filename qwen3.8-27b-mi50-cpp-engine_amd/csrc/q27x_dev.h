@@ -104,12 +104,37 @@ __device__ __forceinline__ bool stopped(const int* p) {
     typedef __attribute__((address_space(4))) const int cint;
     return p && *(cint*)p;
 }
+// A device-resident int that no kernel writes while the reader runs (round positions, counts),
+// read the same way: a scalar load whose wait does not wait for vector loads.
+__device__ __forceinline__ int ld_uniform(const int* p) {
+    typedef __attribute__((address_space(4))) const int cint;
+    return *(cint*)p;
+}
 
 // ---------------------------------------------------------------- reductions
-// shfl_down tree over the 64 lanes (offsets 32..1); the result is valid in lane 0.
+// x of lane l + N in the same 16-lane row (DPP row_shl:N, a VALU operand route instead of an LDS
+// crossbar shuffle; lanes past the row's end read 0). It equals __shfl_down(x, N) in every lane l
+// with l % 16 + N < 16 -- in a halving tree with offsets N <= 8, every lane whose sum is used.
+template <int N>
+__device__ __forceinline__ float dpp_down(float x) {
+    static_assert(N >= 1 && N <= 15, "row_shl");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
+}
+// One level of a shfl_down halving tree: offsets 32 and 16 cross rows (LDS shuffle), 8..1 by DPP.
+template <int O>
+__device__ __forceinline__ float down_add(float x) {
+    if constexpr (O >= 16) return x + __shfl_down(x, O, 64);
+    else return x + dpp_down<O>(x);
+}
+// shfl_down tree over the 64 lanes (offsets 32..1, the same pairs in the same order); the result
+// is valid in lane 0.
 __device__ __forceinline__ float tree64(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = x + __shfl_down(x, o, 64);
+    x = down_add<32>(x);
+    x = down_add<16>(x);
+    x = down_add<8>(x);
+    x = down_add<4>(x);
+    x = down_add<2>(x);
+    x = down_add<1>(x);
     return x;
 }
 __device__ __forceinline__ float max_xor(float x, int width) {   // exact max over `width` lanes

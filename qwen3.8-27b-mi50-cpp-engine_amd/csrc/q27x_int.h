@@ -114,7 +114,8 @@ struct AttnArgs {
     const int* stop;
 };
 int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s);
-int launch_attn(const AttnArgs& a, int nr, hipStream_t s);
+// prep_fused: the split kernel also norms/ropes the rows and writes the new K/V (no prep launch)
+int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused = false);
 size_t attn_work_floats(int nq, int hd, int max_splits, int nr);
 
 // ---------------------------------------------------------------- synthetic weights

@@ -77,6 +77,20 @@ def test_tiny_split_swiglu_units_match_oracle(gpu, O, inter):
     om.close()
 
 
+def test_tiny_rounds_across_a_key_split_match_oracle(tiny_pair):
+    """Verify rows whose positions straddle a 64-key attention split (e.g. 62, 63 | 64): the split
+    that holds the new positions computes their K/V itself, and the next split sees them in the
+    cache; tokens and the final residual bits must be the oracle's."""
+    X, cfg, eng, om = tiny_pair
+    p = prompt_of(cfg, 60, seed=11)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(8):
+        a, b = eng.spec_round(), om.spec_round()
+        assert a == b, f"round {r}: gpu {a} oracle {b}"
+    hg = eng.read("hprev", -1, np.uint16, cfg.hidden)
+    assert np.array_equal(hg, om.tensor("hprev", -1, np.uint16))
+
+
 def test_tiny_spec_equals_plain_and_forced(gpu, O):
     X = gpu
     for k in (1, 2, 3, 7):
