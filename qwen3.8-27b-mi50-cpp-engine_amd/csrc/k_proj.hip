@@ -56,18 +56,19 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
     return down_tree<32 / P>(x[0]);
 }
 
-// Work assignment. A row group is RPW consecutive weight rows.
-//   EPI_STORE: the grid's waves deal the groups round-robin: wave gw (of nw = gridDim.x * NW)
-//     takes groups gw, gw + nw, ..., so every wave streams within one group of the same number
-//     of bytes and the NW waves of a block read adjacent rows at the same time.
+// Work assignment. A row group is RPW consecutive weight rows. Each block owns a list of groups;
+// its waves take them one at a time from a counter in LDS (a wave that is served sooner takes
+// more), so the block's waves finish together.
+//   EPI_STORE: block b owns the groups b NW + w + i nw (w < NW, nw = gridDim.x * NW), so the
+//     waves of the grid stream adjacent rows at the same time.
 //   EPI_SWIGLU (RPW = 1): the 32-row units (16 gate rows | 16 up rows = one 16-output quantization
 //     group) are dealt so that every block streams the same number of rows. With
 //     nunits = F * nb + E, block b takes the whole units b, b + nb, ..., b + (F-1) nb; the E
 //     leftover units are cut into quarters (4 gate rows + the matching 4 up rows = 4 outputs)
-//     dealt round-robin over the blocks. A block's rows are dealt round-robin to its waves and
-//     their dot products meet in LDS; after one barrier the block applies SwiGLU + quantize to its
-//     whole units. A quarter's 4 SwiGLU values go to the scratch area with agent-scope stores and
-//     count on the unit's arrival counter; the wave that brings the count to 4 takes the exact
+//     dealt round-robin over the blocks. The dot products of a block's rows meet in LDS; after
+//     one barrier the block applies SwiGLU + quantize to its whole units. A quarter's 4 SwiGLU
+//     values go to the scratch area with agent-scope stores and count on the unit's arrival
+//     counter; the wave that brings the count to 4 takes the exact
 //     max over the unit's 16 values, quantizes them and resets the counter. No block waits for
 //     another.
 // FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
@@ -90,28 +91,31 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslab = K >> 4, ng64 = K >> 6;
     const int nb = gridDim.x, bi = blockIdx.x;
-    // group sequence of this wave: index i = 0 .. niter-1
+    // The block's row groups form a list j = 0 .. nrb-1; wave w starts with group w, then takes
+    // the next unclaimed group from a block counter in LDS, so waves that get their bytes sooner
+    // do more groups and the block's waves finish together.
     const int ngroups = (a.rows + RPW - 1) / RPW;
-    const int gw = bi * NW + wave, nw = nb * NW;
+    const int nw = nb * NW;
     const int nunits = a.rows >> 5, F = nunits / nb, E = nunits - F * nb;
     const int nq = 4 * E, myq = (nq > bi) ? (nq - 1 - bi) / nb + 1 : 0;   // leftover quarters
-    int niter;
+    int nrb;
     if constexpr (EPI == EPI_SWIGLU) {
-        const int nrb = 32 * F + 8 * myq;              // this block's rows
-        niter = (nrb > wave) ? (nrb - 1 - wave) / NW + 1 : 0;
-    } else {
-        niter = (gw < ngroups) ? (ngroups - 1 - gw) / nw + 1 : 0;
+        nrb = 32 * F + 8 * myq;                        // this block's rows
+    } else {                                           // groups bi*NW + w + i*nw of the grid
+        const int fr = ngroups / nw, rem = ngroups - fr * nw - bi * NW;
+        nrb = fr * NW + (rem < 0 ? 0 : (rem > NW ? NW : rem));
     }
-    auto valid = [&](int i) __attribute__((always_inline)) { return i < niter; };
-    auto row_of = [&](int i, int r) __attribute__((always_inline)) {
+    __shared__ unsigned s_next;                        // groups handed out after the first NW
+    if (threadIdx.x == 0) s_next = 0u;
+    auto valid = [&](int j) __attribute__((always_inline)) { return j < nrb; };
+    auto row_of = [&](int j, int r) __attribute__((always_inline)) {
         if constexpr (EPI == EPI_SWIGLU) {
-            const int j = wave + NW * i;               // the block's local row
             if (j < 32 * F) return (bi + nb * (j >> 5)) * 32 + (j & 31);
             const int m = (j - 32 * F) >> 3, r8 = (j - 32 * F) & 7;
             const int p = bi + nb * m, u = F * nb + (p >> 2), q = p & 3;
             return u * 32 + (r8 < 4 ? 4 * q + r8 : 12 + 4 * q + r8);
         } else {
-            return (gw + i * nw) * RPW + r;
+            return (bi * NW + (j % NW) + (j / NW) * nw) * RPW + r;
         }
     };
     uint4 W[RPW][NSTEP];
@@ -134,11 +138,11 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         }
     };
     auto prefetch = [&]() __attribute__((always_inline)) {
-        const int rg = __builtin_amdgcn_readfirstlane(row_of(0, 0));
+        const int rg = __builtin_amdgcn_readfirstlane(row_of(wave, 0));
 #pragma unroll
         for (int t = 0; t < NSTEP; ++t)
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) ld(rg, r, t, valid(0));
+            for (int r = 0; r < RPW; ++r) ld(rg, r, t, valid(wave));
     };
     if constexpr (PRE) {
         // input rows first, then the weights, so waiting for the rows leaves the weights in flight.
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         // prefetch's 2 NSTEP RPW loads, which stay in flight (vector-memory counts retire in
         // order). A plain barrier plus an acquire fence, because the release half of
         // __syncthreads would wait for the prefetch as well.
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NSTEP * RPW));
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NSTEP * RPW) & ~(15 << 8));   // and the LDS counter
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     } else {
@@ -214,15 +218,18 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     const bool holder = (lane % LPV) == 0 && vi < V;
     const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
     const uint32_t* resw = (const uint32_t*)a.res;
-    for (int i = 0; i < niter; ++i) {
-        const bool more = valid(i + 1);
-        const int rg_next = __builtin_amdgcn_readfirstlane(row_of(i + 1, 0));
+    for (int j = wave; j < nrb;) {
+        unsigned jn = 0u;
+        if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int jnext = NW + __builtin_amdgcn_readfirstlane((int)jn);
+        const bool more = valid(jnext);
+        const int rg_next = __builtin_amdgcn_readfirstlane(row_of(jnext, 0));
         // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use; loaded
         // (from a harmless address) also when there is none, for the reason given at ld
         size_t ridx = 0;
         uint32_t rw = 0u;
         if constexpr (EPI == EPI_STORE) {
-            int row = row_of(i, hr);
+            int row = row_of(j, hr);
             row = row < a.rows ? row : a.rows - 1;
             ridx = (size_t)hn * a.rstride + row;
             rw = *(resw ? resw + (a.res_bf16 ? (ridx >> 1) : ridx) : (const uint32_t*)a.W);
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         }
         const float tv = tree_t<P>(acc, lane) * a.alpha;
         if constexpr (EPI == EPI_STORE) {
-            const int row = row_of(i, hr);
+            const int row = row_of(j, hr);
             if (holder && row < a.rows) {
                 float v = tv;
                 if (resw) {
@@ -263,8 +270,9 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
                 else ((float*)a.y)[yi] = v;
             }
         } else {
-            if (holder) sacc[(wave + NW * i) * NR + hn] = tv;
+            if (holder) sacc[j * NR + hn] = tv;
         }
+        j = jnext;
     }
     if constexpr (EPI == EPI_SWIGLU) {
         __syncthreads();
