@@ -230,50 +230,62 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     }
     // a/b logits: pair (which, n) per wave, lane-chunk order (chunk c on lane c%64, fmaf per
     // element), shfl tree, bf16 rounding as k_bf16_gemv2_tile (src/q27_util.hip:158-162)
-    if (FUSE_AB) {
-        for (int pi = wv; pi < 2 * nr; pi += 8) {
-            const int which = pi & 1, n = pi >> 1;
-            const uint4* wrow = sy + (size_t)which * hc;
-            const uint4* yrow = sy + (size_t)(2 + n) * hc;
-            float acc = 0.0f;
-            for (int c = lane; c < hc; c += 64) {
-                const uint4 w = wrow[c], y = yrow[c];
-                acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(y.x << 16), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(y.x & 0xFFFF0000u), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(y.y << 16), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(y.y & 0xFFFF0000u), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(y.z << 16), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(y.z & 0xFFFF0000u), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(y.w << 16), acc);
-                acc = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(y.w & 0xFFFF0000u), acc);
+    // The row scalars come from two independent chains that run on different waves at once:
+    // waves 0..5 take the a/b logits and turn each into its row scalar at once (decay from a,
+    // beta from b); waves 6 and 7 take the q/k norms of whole rows (both 64-element halves, each
+    // reduced by the tree, summed first half + second half) and write q^, k^ and k^.q^.
+    constexpr int kAbW = 6;
+    if (wv < kAbW) {
+        if (FUSE_AB) {
+            for (int pi = wv; pi < 2 * nr; pi += kAbW) {
+                const int which = pi & 1, n = pi >> 1;
+                const uint4* wrow = sy + (size_t)which * hc;
+                const uint4* yrow = sy + (size_t)(2 + n) * hc;
+                float acc = 0.0f;
+                for (int c = lane; c < hc; c += 64) {
+                    const uint4 w = wrow[c], y = yrow[c];
+                    acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(y.x << 16), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(y.x & 0xFFFF0000u), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(y.y << 16), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(y.y & 0xFFFF0000u), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(y.z << 16), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(y.z & 0xFFFF0000u), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(y.w << 16), acc);
+                    acc = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(y.w & 0xFFFF0000u), acc);
+                }
+                acc = tree64(acc);
+                if (lane == 0) {   // beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt))
+                    const float v = bfr(acc);
+                    if (which) srow[n][1] = qsigmoid(v);
+                    else srow[n][2] = qexp(-(Aexp * qsoftplus(v + dtb)));
+                }
             }
-            acc = tree64(acc);
-            if (lane == 0) sab[which][n] = bfr(acc);
+        } else if (t < nr) {
+            srow[t][1] = qsigmoid(sab[1][t]);
+            srow[t][2] = qexp(-(Aexp * qsoftplus(sab[0][t] + dtb)));
         }
-    }
-    // q/k L2 norms and k^.q^ of row n on the wave pair (2m, 2m+1), element e = 64 (w&1) + lane
-    const int e = 64 * (wv & 1) + lane;
-    for (int n = wv >> 1; n < nr; n += 4) {
-        const float qv = scv[n][e], kv = scv[n][kD + e];
-        const float r0 = tree64(qv * qv), r1 = tree64(kv * kv), r2 = tree64(qv * kv);
-        if (lane == 0) { red[n][wv & 1][0] = r0; red[n][wv & 1][1] = r1; red[n][wv & 1][2] = r2; }
-    }
-    __syncthreads();
-    for (int n = wv >> 1; n < nr; n += 4) {
-        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
-        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
-        const float skv = scv[n][kD + e] * invk;
-        sq[n][e] = scv[n][e] * invq;
-        sk[n][e] = skv;
-        if (owner) Q.khat[((size_t)n * a.kh + kk) * kD + e] = skv;
-    }
-    if (t < nr) {   // the rows' scalars, once: k^.q^, beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt))
-        const int n = t;
-        const float invq = rsqrt_cr((red[n][0][0] + red[n][1][0]) + 1e-6f) * 0.0883883476f;
-        const float invk = rsqrt_cr((red[n][0][1] + red[n][1][1]) + 1e-6f);
-        srow[n][0] = ((red[n][0][2] + red[n][1][2]) * invq) * invk;
-        srow[n][1] = qsigmoid(sab[1][n]);
-        srow[n][2] = qexp(-(Aexp * qsoftplus(sab[0][n] + dtb)));
+    } else {
+        for (int n = wv - kAbW; n < nr; n += 8 - kAbW) {
+            const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
+            const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
+            const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
+            const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
+            const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
+            const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
+            const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
+            const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
+            const float invk = rsqrt_cr(ssk + 1e-6f);
+            const float kh0 = k0 * invk, kh1 = k1 * invk;
+            sq[n][lane] = q0 * invq;
+            sq[n][64 + lane] = q1 * invq;
+            sk[n][lane] = kh0;
+            sk[n][64 + lane] = kh1;
+            if (owner) {
+                Q.khat[((size_t)n * a.kh + kk) * kD + lane] = kh0;
+                Q.khat[((size_t)n * a.kh + kk) * kD + 64 + lane] = kh1;
+            }
+            if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
+        }
     }
     __syncthreads();
 
@@ -318,7 +330,8 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     }
     __syncthreads();
 
-    // output norm + gate + quantize, row n on the wave pair (2m, 2m+1)
+    // output norm + gate + quantize, row n on the wave pair (2m, 2m+1), element e = 64 (w&1) + lane
+    const int e = 64 * (wv & 1) + lane;
     for (int n = wv >> 1; n < nr; n += 4) {
         const float mx = smix[n][e];
         const float r3 = tree64(mx * mx);
