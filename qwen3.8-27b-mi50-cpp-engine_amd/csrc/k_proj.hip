@@ -59,8 +59,10 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
 // Work assignment. A row group is RPW consecutive weight rows. Each block owns a list of groups;
 // its waves take them one at a time from a counter in LDS (a wave that is served sooner takes
 // more), so the block's waves finish together.
-//   EPI_STORE: block b owns the groups b NW + w + i nw (w < NW, nw = gridDim.x * NW), so the
-//     waves of the grid stream adjacent rows at the same time.
+//   EPI_STORE: with 4-wave blocks (K = 17408 and the unaligned shapes, several blocks per CU),
+//     block b owns the groups b NW + w + i nw (w < NW, nw = gridDim.x * NW); with 16-wave
+//     blocks (one per CU) it owns the groups b + i gridDim.x, so every block gets the same count
+//     to within one. Either way the waves of the grid stream adjacent rows at the same time.
 //   EPI_SWIGLU (RPW = 1): the 32-row units (16 gate rows | 16 up rows = one 16-output quantization
 //     group) are dealt so that every block streams the same number of rows. With
 //     nunits = F * nb + E, block b takes the whole units b, b + nb, ..., b + (F-1) nb; the E
@@ -101,6 +103,8 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     int nrb;
     if constexpr (EPI == EPI_SWIGLU) {
         nrb = 32 * F + 8 * myq;                        // this block's rows
+    } else if constexpr (NW == 16) {                   // groups bi + i*nb of the grid
+        nrb = (ngroups - bi + nb - 1) / nb;
     } else {                                           // groups bi*NW + w + i*nw of the grid
         const int fr = ngroups / nw, rem = ngroups - fr * nw - bi * NW;
         nrb = fr * NW + (rem < 0 ? 0 : (rem > NW ? NW : rem));
@@ -115,7 +119,8 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             const int p = bi + nb * m, u = F * nb + (p >> 2), q = p & 3;
             return u * 32 + (r8 < 4 ? 4 * q + r8 : 12 + 4 * q + r8);
         } else {
-            return (bi * NW + (j % NW) + (j / NW) * nw) * RPW + r;
+            if constexpr (NW == 16) return (bi + j * nb) * RPW + r;
+            else return (bi * NW + (j % NW) + (j / NW) * nw) * RPW + r;
         }
     };
     uint4 W[RPW][NSTEP];
@@ -334,11 +339,11 @@ static int num_cus() {
     return g_ncu;
 }
 
-// Launch shape. The norm-prologue and SwiGLU kernels run one 16-wave block per CU (the prologue
-// is then computed once per CU; SwiGLU deals its units over 8 slots per block). The plain store
-// kernels run 4-wave blocks, wpc waves per CU (16 for the K <= 6144 shapes, 8 for K = 17408 whose
-// 17 KiB-per-row prefetch holds ~250 VGPRs). Overridable for launch-shape sweeps (Q27X_WPC5,
-// Q27X_WPC17).
+// Launch shape. The norm-prologue, SwiGLU and aligned K <= 6144 kernels run one 16-wave block per
+// CU (the prologue is then computed once per CU; a block's waves share one row list). K = 17408
+// (a 17 KiB-per-row prefetch in ~190 VGPRs) and the unaligned shapes run 4-wave blocks, wpc
+// waves per CU (8 for K = 17408, 16 otherwise): for K = 17408 one 8-wave block per CU measured
+// slower. Overridable for launch-shape sweeps (Q27X_WPC5, Q27X_WPC17).
 static int env_knob(const char* name, int def, int lo, int hi) {
     const char* v = getenv(name);
     if (!v || !*v) return def;
@@ -350,7 +355,7 @@ static int knob_wpc17() { static const int v = env_knob("Q27X_WPC17", 8, 4, 16);
 
 template <int NR, int NSTEP, int EPI, bool FULL, bool PRE, int RPW>
 static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
-    constexpr int NW = (PRE || EPI == EPI_SWIGLU) ? 16 : 4;
+    constexpr int NW = (PRE || EPI == EPI_SWIGLU || (FULL && NSTEP < 17)) ? 16 : 4;
     int grid;
     if (EPI == EPI_SWIGLU) {
         const int nunits = a.rows >> 5;
@@ -608,11 +613,170 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, int upw) {
     }
 }
 
+// Aligned form (K = NSTEP * 512, 16-byte aligned activation rows): one 16-wave block per CU.
+// Block b owns the row groups b + i * gridDim.x; wave w starts with group w and then takes the
+// next unclaimed group from an LDS counter, so the block's waves finish together. Each step's
+// weights are refilled with the next group's right after they are used (one group in flight per
+// wave, no register copies). The activation rows are staged as fp32 with 16-byte loads issued
+// before the first group's weights. Same per-row arithmetic as k_gemv, so the same bits. MODE 1
+// merges the waves' running argmax in LDS and writes one partial per block.
+template <int NR, int NSTEP, int RPW, int MODE>
+__global__ __launch_bounds__(1024) void k_gemv_full(GemvArgs a) {
+    constexpr int NW = 16, NT = NW * 64, CH = NSTEP * 64, NCK = NR * CH, SI = (NCK + NT - 1) / NT;
+    __shared__ float sxf[NR * CH * 8];
+    __shared__ unsigned s_next;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K = a.K;
+    const int ngroups = (a.rows + RPW - 1) / RPW;
+    const int nb = gridDim.x, bi = blockIdx.x;
+    const int nrb = (ngroups - bi + nb - 1) / nb;      // this block's groups (the launch has nb <= ngroups)
+    if (threadIdx.x == 0) s_next = 0u;
+    uint4 W[RPW][NSTEP];
+    // a group past the block's last reads the first 16 bytes of the weights instead (branch-free,
+    // so each wait the compiler places counts only the loads owed to later steps)
+    auto ld = [&](int rg, int r, int t, bool ok) __attribute__((always_inline)) {
+        int row = rg + r;
+        row = row < a.rows ? row : a.rows - 1;
+        W[r][t] = ld_nt16(ok ? a.W + (size_t)row * K + 8 * (t * 64 + lane) : a.W);
+    };
+    // activation rows first, then the first group's weights: waiting for the rows leaves the
+    // weights in flight
+    uint4 xv[SI];
+#pragma unroll
+    for (int u = 0; u < SI; ++u) {
+        const int i = threadIdx.x + u * NT;
+        const int n = i / CH, c = i - n * CH;
+        xv[u] = *(const uint4*)((i < NCK) ? a.x + (size_t)n * a.xst + 8 * c : a.x);
+    }
+    {
+        const int rg = __builtin_amdgcn_readfirstlane((bi + wave * nb) * RPW);
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) ld(rg, r, t, wave < nrb);
+    }
+    if (stopped(a.stop)) return;
+#pragma unroll
+    for (int u = 0; u < SI; ++u) {
+        const int i = threadIdx.x + u * NT;
+        if (i < NCK) {
+            const int n = i / CH, c = i - n * CH;
+            float* d = &sxf[n * CH * 8 + 8 * c];
+            const uint4 v = xv[u];
+            *(float4*)d = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                                      __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+            *(float4*)(d + 4) = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                                            __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+        }
+    }
+    __syncthreads();
+    float bv = -__builtin_huge_valf();                 // MODE 1: lane n < NR keeps row n's best
+    uint32_t bx = 0xFFFFFFFFu;
+    for (int j = wave; j < nrb;) {
+        unsigned jn = 0u;
+        if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int jnext = NW + __builtin_amdgcn_readfirstlane((int)jn);
+        const bool more = jnext < nrb;
+        const int rg_next = __builtin_amdgcn_readfirstlane((bi + jnext * nb) * RPW);
+        float acc[RPW][NR];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int n = 0; n < NR; ++n) acc[r][n] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+            const int c = t * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const uint4 w = W[r][t];
+                float wf[8];
+                wf[0] = __uint_as_float(w.x << 16); wf[1] = __uint_as_float(w.x & 0xFFFF0000u);
+                wf[2] = __uint_as_float(w.y << 16); wf[3] = __uint_as_float(w.y & 0xFFFF0000u);
+                wf[4] = __uint_as_float(w.z << 16); wf[5] = __uint_as_float(w.z & 0xFFFF0000u);
+                wf[6] = __uint_as_float(w.w << 16); wf[7] = __uint_as_float(w.w & 0xFFFF0000u);
+#pragma unroll
+                for (int n = 0; n < NR; ++n) {
+                    const float4 x0 = *(const float4*)&sxf[n * CH * 8 + 8 * c];
+                    const float4 x1 = *(const float4*)&sxf[n * CH * 8 + 8 * c + 4];
+                    float v = acc[r][n];
+                    v = __builtin_fmaf(wf[0], x0.x, v); v = __builtin_fmaf(wf[1], x0.y, v);
+                    v = __builtin_fmaf(wf[2], x0.z, v); v = __builtin_fmaf(wf[3], x0.w, v);
+                    v = __builtin_fmaf(wf[4], x1.x, v); v = __builtin_fmaf(wf[5], x1.y, v);
+                    v = __builtin_fmaf(wf[6], x1.z, v); v = __builtin_fmaf(wf[7], x1.w, v);
+                    acc[r][n] = v;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) ld(rg_next, r, t, more);
+            __builtin_amdgcn_sched_barrier(0);          // keeps each step's activation reads in the step
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int n = 0; n < NR; ++n) acc[r][n] = __shfl(tree64(acc[r][n]), 0, 64);
+        const int row0 = (bi + j * nb) * RPW;
+        if (MODE == 0) {
+            if (lane < RPW * NR) {
+                const int r = lane % RPW, n = lane / RPW, row = row0 + r;
+                float v = 0.0f;
+#pragma unroll
+                for (int rr = 0; rr < RPW; ++rr)
+#pragma unroll
+                    for (int nn = 0; nn < NR; ++nn) if (rr == r && nn == n) v = acc[rr][nn];
+                if (row < a.rows) {
+                    if (a.out_bf16) ((uint16_t*)a.y)[(size_t)n * a.ystride + row] = f2bf(v);
+                    else ((float*)a.y)[(size_t)n * a.ystride + row] = v;
+                }
+            }
+        } else if (lane < NR) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const int row = row0 + r;
+                float v = 0.0f;
+#pragma unroll
+                for (int nn = 0; nn < NR; ++nn) if (nn == lane) v = acc[r][nn];
+                if (row < a.rows && finitef(v)) am_merge(bv, bx, v, (uint32_t)row);
+            }
+        }
+        j = jnext;
+    }
+    if constexpr (MODE == 1) {                         // one partial per block and row
+        __shared__ float sbv[NW][NR];
+        __shared__ uint32_t sbx[NW][NR];
+        if (lane < NR) { sbv[wave][lane] = bv; sbx[wave][lane] = bx; }
+        __syncthreads();
+        if (threadIdx.x < NR) {
+            const int n = threadIdx.x;
+            for (int w = 0; w < NW; ++w)
+                if (sbx[w][n] != 0xFFFFFFFFu) am_merge(bv, bx, sbv[w][n], sbx[w][n]);
+            a.pval[(size_t)n * a.pstride + bi] = bv;
+            a.pidx[(size_t)n * a.pstride + bi] = bx;
+        }
+    }
+}
+
 template <int NR, int MODE>
 static int gemv_k(const GemvArgs& a, hipStream_t s, int* nb) {
     const int ns = (a.K + 511) / 512;
     constexpr int RPW = 2;
     const int ngroups = (a.rows + RPW - 1) / RPW;
+    const bool aligned = a.K == ns * 512 && !((uintptr_t)a.x & 15) && !(a.xst & 7);
+    if (aligned && (ns == 1 || ns == 2 || ns == 4 || ns == 10)) {
+        int grid = a.rows < num_cus() ? a.rows : num_cus();
+        if (MODE == 1 && grid > a.pstride) grid = a.pstride;
+        if (grid < 1) return -2;
+        if (nb) *nb = grid;
+#define Q27X_GF(NS) hipLaunchKernelGGL((k_gemv_full<NR, NS, 1, MODE>), dim3(grid), dim3(1024), 0, s, a)
+        switch (ns) {
+            case 1: Q27X_GF(1); break;
+            case 2: Q27X_GF(2); break;
+            case 4: Q27X_GF(4); break;
+            default: Q27X_GF(10); break;
+        }
+#undef Q27X_GF
+        Q27X_HIP(hipGetLastError());
+        return Q27X_OK;
+    }
     int wmax = num_cus() * 8;
     if (MODE == 1 && wmax > a.pstride) wmax = a.pstride & ~3;
     const int upw = (ngroups + wmax - 1) / wmax;
