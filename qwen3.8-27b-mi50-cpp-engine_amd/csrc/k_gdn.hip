@@ -16,9 +16,12 @@
 // back once, then continues. The commit uses exactly the update the row already received, so the
 // committed state is bit-identical to stepping the accepted rows one at a time.
 // Conv (CONV = 1, the engine path; k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439): the raw
-// projection rows are convolved here. The committed shift register lives in `pend` in two parity
-// areas (read `par`, write `1 - par`), because the q and k channels of a key head are read by all
-// the value heads that share it and written by one of them.
+// projection rows are convolved here; the committed shift register lives in `pend`.
+// Every pending value in `pend` (k^, the raw q|k|v input channels, the shift register) is kept
+// per value head, although the q and k channels belong to the key head that several value heads
+// share: each block then reads and rewrites only its own entries (in place, each entry by one
+// thread, reads consumed before the first barrier), so no call has to wait for a shared word
+// before its loads or publish one after its stores.
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
@@ -29,36 +32,33 @@ constexpr int kNT = 512;              // threads per block: 4 key groups x 128 v
 constexpr int kJ = kD / 4;            // key rows per thread (32)
 constexpr int kStg = 8;               // staging loads per thread per batch
 
-// pend buffer: header (parity, grid counter) | two parity areas of khat [R][KH][D] |
-// delta [R][VH][D] | decay [R][VH] (fp32) | raw [2][R][NQKV] bf16 | hist [2][NQKV][4] bf16 |
-// work [R][NQKV] bf16 (conv output of the kernel-tier entry). A call reads area `par` and writes
-// area 1-par; the last block of the grid flips par.
+// pend buffer: header (256 B, unused) | khat [R][VH][D] | delta [R][VH][D] | decay [R][VH] (fp32) |
+// raw [R][VH][3D] bf16 (each value head's q|k|v input channels of the pending rows; the
+// kernel-tier conv uses the same area as [R][NQKV]) | hist [VH][3D][4] bf16 (shift registers) |
+// work [R][NQKV] bf16 (conv output of the kernel-tier entry).
 __host__ __device__ static inline size_t hdr_bytes() { return 256; }
-__host__ __device__ static inline size_t area_floats(int kh, int vh) {
-    return (size_t)kMaxRows * ((size_t)kh * kD + (size_t)vh * kD + vh);
+__host__ __device__ static inline size_t area_floats(int vh) {
+    return (size_t)kMaxRows * (2 * (size_t)vh * kD + vh);
 }
 size_t gdn_pend_raw_offset(int kh, int vh, int d) {
-    (void)d;
-    return hdr_bytes() + 2 * area_floats(kh, vh) * 4;
+    (void)kh; (void)d;
+    return hdr_bytes() + area_floats(vh) * 4;
 }
 static size_t gdn_hist_offset(int kh, int vh, int d) {
-    const size_t nqkv = (size_t)(2 * kh + vh) * d;
-    return gdn_pend_raw_offset(kh, vh, d) + 2 * (size_t)kMaxRows * nqkv * 2;
+    return gdn_pend_raw_offset(kh, vh, d) + (size_t)kMaxRows * vh * 3 * kD * 2;
+}
+static size_t gdn_work_offset(int kh, int vh, int d) {
+    return gdn_hist_offset(kh, vh, d) + (size_t)vh * 3 * kD * 4 * 2;
 }
 size_t gdn_pend_bytes(int kh, int vh, int d) {
     const size_t nqkv = (size_t)(2 * kh + vh) * d;
-    return gdn_hist_offset(kh, vh, d) + 2 * nqkv * 4 * 2 + (size_t)kMaxRows * nqkv * 2;
+    return gdn_work_offset(kh, vh, d) + (size_t)kMaxRows * nqkv * 2;
 }
-static size_t gdn_work_offset(int kh, int vh, int d) {
-    const size_t nqkv = (size_t)(2 * kh + vh) * d;
-    return gdn_hist_offset(kh, vh, d) + 2 * nqkv * 4 * 2;
-}
-struct PendHdr { unsigned par; unsigned gcnt; };
 struct PendArea { float* khat; float* delta; float* decay; };
-__device__ __forceinline__ PendArea pend_area(void* p, int kh, int vh, int which) {
-    float* b = (float*)((char*)p + hdr_bytes()) + (size_t)which * area_floats(kh, vh);
+__device__ __forceinline__ PendArea pend_area(void* p, int vh) {
+    float* b = (float*)((char*)p + hdr_bytes());
     PendArea v;
-    v.khat = b;  b += (size_t)kMaxRows * kh * kD;
+    v.khat = b;  b += (size_t)kMaxRows * vh * kD;
     v.delta = b; b += (size_t)kMaxRows * vh * kD;
     v.decay = b;
     return v;
@@ -70,12 +70,9 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int d = t & (kD - 1), g = t >> 7;
     const int ratio = a.vh / a.kh, kk = h / ratio;
-    const bool owner = (h % ratio) == 0;           // writes the shared q/k channels
-    const int KD = a.kh * kD, nqkv = 2 * KD + a.vh * kD;
-    PendHdr* hdr = (PendHdr*)a.pend;
-    const unsigned par = hdr->par & 1u;
-    const PendArea P = pend_area(a.pend, a.kh, a.vh, (int)par);        // pending rows (read)
-    const PendArea Q = pend_area(a.pend, a.kh, a.vh, (int)(par ^ 1u));  // this call's rows (write)
+    const bool owner = (h % ratio) == 0;           // writes the shared conv history output
+    const int KD = a.kh * kD;
+    const PendArea P = pend_area(a.pend, a.vh);     // pending rows: read first, then this call's rows
     const int npend = a.npend_ptr ? *a.npend_ptr : a.npend_imm;
 
     __shared__ __attribute__((aligned(16))) float skp[kMaxRows][kD];
@@ -102,7 +99,7 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int p = g + 4 * u;
-        pk[u] = (p < npend) ? P.khat[((size_t)p * a.kh + kk) * kD + d] : 0.0f;
+        pk[u] = (p < npend) ? P.khat[((size_t)p * a.vh + h) * kD + d] : 0.0f;
         pd[u] = (p < npend) ? P.delta[((size_t)p * a.vh + h) * kD + d] : 0.0f;
     }
     const float pdc = (t < npend) ? P.decay[(size_t)t * a.vh + h] : 0.0f;
@@ -114,17 +111,17 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     for (int n = 0; n < kMaxRows; ++n) xr[n] = (t < 3 * kD && n < nr) ? a.qkv[(size_t)n * a.qkv_stride + ch] : (uint16_t)0;
     uint2 cw = make_uint2(0u, 0u), hs = make_uint2(0u, 0u);
     uint16_t pr[kMaxRows];
-    const uint16_t* raw_r = (const uint16_t*)((const char*)a.pend + raw_off) + (size_t)par * kMaxRows * nqkv;
-    uint16_t* raw_w = (uint16_t*)((char*)a.pend + raw_off) + (size_t)(par ^ 1u) * kMaxRows * nqkv;
-    const uint16_t* hist_r = (const uint16_t*)((const char*)a.pend + hist_off) + (size_t)par * nqkv * 4;
-    uint16_t* hist_w = (uint16_t*)((char*)a.pend + hist_off) + (size_t)(par ^ 1u) * nqkv * 4;
+    // this value head's raw channels [R][VH][3D] and shift registers [VH][3D][4]
+    const size_t rstr = (size_t)a.vh * 3 * kD;
+    uint16_t* raw = (uint16_t*)((char*)a.pend + raw_off) + (size_t)h * 3 * kD;
+    uint16_t* hist = (uint16_t*)((char*)a.pend + hist_off) + (size_t)h * 3 * kD * 4;
     if (CONV) {
         if (t < 3 * kD) {
             cw = *(const uint2*)(a.conv_w + (size_t)ch * 4);
-            hs = *(const uint2*)(hist_r + (size_t)ch * 4);
+            hs = *(const uint2*)(hist + (size_t)cl * 4);
         }
 #pragma unroll
-        for (int p = 0; p < kMaxRows; ++p) pr[p] = (t < 3 * kD && p < npend) ? raw_r[(size_t)p * nqkv + ch] : (uint16_t)0;
+        for (int p = 0; p < kMaxRows; ++p) pr[p] = (t < 3 * kD && p < npend) ? raw[(size_t)p * rstr + cl] : (uint16_t)0;
     }
     // (d) gate rows z: threads 384..511
     uint16_t zr[kMaxRows];
@@ -177,13 +174,10 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
 #pragma unroll
             for (int p = 0; p < kMaxRows; ++p)
                 if (p < npend) { h0 = h1; h1 = h2; h2 = pr[p]; }
-            const bool own = (cl >= 2 * kD) || owner;
-            if (own) {
-                *(uint2*)(hist_w + (size_t)ch * 4) = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2);
-                if (a.conv_hist) {
-                    a.conv_hist[(size_t)ch * 3] = h0; a.conv_hist[(size_t)ch * 3 + 1] = h1;
-                    a.conv_hist[(size_t)ch * 3 + 2] = h2;
-                }
+            *(uint2*)(hist + (size_t)cl * 4) = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2);
+            if (a.conv_hist && ((cl >= 2 * kD) || owner)) {
+                a.conv_hist[(size_t)ch * 3] = h0; a.conv_hist[(size_t)ch * 3 + 1] = h1;
+                a.conv_hist[(size_t)ch * 3 + 2] = h2;
             }
             const float w0 = __uint_as_float(cw.x << 16), w1 = __uint_as_float(cw.x & 0xFFFF0000u);
             const float w2 = __uint_as_float(cw.y << 16), w3 = __uint_as_float(cw.y & 0xFFFF0000u);
@@ -196,7 +190,7 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
                 acc = __builtin_fmaf(bf2f(h2), w2, acc);
                 acc = __builtin_fmaf(bf2f(x), w3, acc);
                 h0 = h1; h1 = h2; h2 = x;
-                if (own) raw_w[(size_t)n * nqkv + ch] = x;
+                raw[(size_t)n * rstr + cl] = x;
                 scv[n][cl] = bf2f(f2bf(qsilu(acc)));
             }
         } else {
@@ -280,10 +274,8 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
             sq[n][64 + lane] = q1 * invq;
             sk[n][lane] = kh0;
             sk[n][64 + lane] = kh1;
-            if (owner) {
-                Q.khat[((size_t)n * a.kh + kk) * kD + lane] = kh0;
-                Q.khat[((size_t)n * a.kh + kk) * kD + 64 + lane] = kh1;
-            }
+            P.khat[((size_t)n * a.vh + h) * kD + lane] = kh0;
+            P.khat[((size_t)n * a.vh + h) * kD + 64 + lane] = kh1;
             if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
         }
     }
@@ -323,10 +315,10 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
             st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
         }
         if (g == 0) {
-            Q.delta[((size_t)n * a.vh + h) * kD + d] = delta;
+            P.delta[((size_t)n * a.vh + h) * kD + d] = delta;
             smix[n][d] = mixed;
         }
-        if (t == 0) Q.decay[(size_t)n * a.vh + h] = decay;
+        if (t == 0) P.decay[(size_t)n * a.vh + h] = decay;
     }
     __syncthreads();
 
@@ -353,13 +345,6 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
             a.xq[k] = qcode(yv, qi);
             if ((e & 15) == 0) a.xs[k >> 4] = sc;
         }
-    }
-    // the last block of the grid flips the parity (every block read it at its start; what this
-    // call wrote is read by the next call, after the kernel boundary)
-    if (t == 0 &&
-        __hip_atomic_fetch_add(&hdr->gcnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(gridDim.x - 1)) {
-        st_agent(&hdr->gcnt, 0u);
-        st_agent(&hdr->par, par ^ 1u);
     }
 }
 
