@@ -118,6 +118,7 @@ constexpr int kAttnThreads = 512;
 // dequantized values straight into its tile.
 template <int NQW, int QPT, bool PREP>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
+    warm_args(a);
     if (stopped(a.stop)) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
@@ -250,21 +251,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 #pragma unroll
             for (int i = 0; i < NQW; ++i) acc[i] = 0.0f;
             const float* kr = &kd[k * kKStride];
+            // a wave with fewer than NQW queries computes its missing ones on query 0 (discarded
+            // below): no branch inside the loop, so the LDS reads of several steps are in flight
+            // together instead of one read and one wait per step
+            int qrow[NQW];
+#pragma unroll
+            for (int i = 0; i < NQW; ++i) qrow[i] = (wv + 8 * i < nqr) ? (wv + 8 * i) * kHD : 0;
 #pragma unroll 4
             for (int c = 0; c < kHD / 4; ++c) {
                 const float4 kv = *(const float4*)(kr + 4 * c);
 #pragma unroll
                 for (int i = 0; i < NQW; ++i) {
-                    const int qi = wv + 8 * i;
-                    if (qi < nqr) {               // wave-uniform
-                        const float4 q = *(const float4*)&qf[qi * kHD + 4 * c];
-                        float v = acc[i];
-                        v = __builtin_fmaf(q.x, kv.x, v);
-                        v = __builtin_fmaf(q.y, kv.y, v);
-                        v = __builtin_fmaf(q.z, kv.z, v);
-                        v = __builtin_fmaf(q.w, kv.w, v);
-                        acc[i] = v;
-                    }
+                    const float4 q = *(const float4*)&qf[qrow[i] + 4 * c];
+                    float v = acc[i];
+                    v = __builtin_fmaf(q.x, kv.x, v);
+                    v = __builtin_fmaf(q.y, kv.y, v);
+                    v = __builtin_fmaf(q.z, kv.z, v);
+                    v = __builtin_fmaf(q.w, kv.w, v);
+                    acc[i] = v;
                 }
             }
 #pragma unroll

@@ -111,6 +111,21 @@ __device__ __forceinline__ int ld_uniform(const int* p) {
     return *(cint*)p;
 }
 
+// Request every 64-byte line of a kernel's argument struct at once, at the start: the compiler
+// otherwise loads each argument near its first use, and every scalar-cache miss on the argument
+// segment (written once per graph, cold by the time the launch runs) is a memory round trip in
+// the middle of the prologue. One scalar load per line, one wait; later reads of any argument hit
+// the scalar cache.
+template <typename T>
+__device__ __forceinline__ void warm_args(const T& a) {
+    const char* p = (const char*)&a;
+#pragma unroll
+    for (int off = 0; off < (int)sizeof(T); off += 64) {
+        const int v = *(const int*)(p + off);
+        asm volatile("" ::"s"(v));
+    }
+}
+
 // ---------------------------------------------------------------- reductions
 // x of lane l + N in the same 16-lane row (DPP row_shl:N, a VALU operand route instead of an LDS
 // crossbar shuffle; lanes past the row's end read 0). It equals __shfl_down(x, N) in every lane l
