@@ -28,7 +28,7 @@ __device__ __forceinline__ void norm_rope(const AttnArgs& a, const uint16_t* src
     const int f = (a.rot <= 64) ? (l & (half - 1)) : l;
     const float c = a.rope_cos[(size_t)pos * half + f], s = a.rope_sin[(size_t)pos * half + f];
     const float w0 = tree64(x0 * x0), w1 = tree64(x1 * x1);
-    const float ss = __shfl(w0, 0, 64) + __shfl(w1, 0, 64);
+    const float ss = bcast0(w0) + bcast0(w1);
     const float inv = rsqrt_cr(ss * (1.0f / (float)kHD) + a.eps);
     y0 = x0 * inv * (1.0f + wg0);
     y1 = x1 * inv * (1.0f + wg1);

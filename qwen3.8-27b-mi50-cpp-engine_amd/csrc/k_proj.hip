@@ -50,6 +50,8 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
             const uint32_t lo = __float_as_uint(x[v]), hi = __float_as_uint(x[v + h]);
             const float send = __uint_as_float((lo & up) | (hi & ~up));
             const float keep = __uint_as_float((hi & up) | (lo & ~up));
+            // (an LDS-crossbar shuffle: the lane swaps used by tree64 changed how the compiler
+            // places the next group's refills here and made the store kernels slower)
             x[v] = keep + __shfl_xor(send, o, 64);
         }
     }
@@ -575,7 +577,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, int upw) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int n = 0; n < NR; ++n) acc[r][n] = __shfl(tree64(acc[r][n]), 0, 64);
+            for (int n = 0; n < NR; ++n) acc[r][n] = bcast0(tree64(acc[r][n]));
         const int row0 = g * RPW;
         if (MODE == 0) {
             if (lane < RPW * NR) {
@@ -713,7 +715,7 @@ __global__ __launch_bounds__(1024) void k_gemv_full(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int n = 0; n < NR; ++n) acc[r][n] = __shfl(tree64(acc[r][n]), 0, 64);
+            for (int n = 0; n < NR; ++n) acc[r][n] = bcast0(tree64(acc[r][n]));
         const int row0 = (bi + j * nb) * RPW;
         if (MODE == 0) {
             if (lane < RPW * NR) {

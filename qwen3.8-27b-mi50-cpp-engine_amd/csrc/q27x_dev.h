@@ -135,10 +135,24 @@ __device__ __forceinline__ float dpp_down(float x) {
     static_assert(N >= 1 && N <= 15, "row_shl");
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
 }
-// One level of a shfl_down halving tree: offsets 32 and 16 cross rows (LDS shuffle), 8..1 by DPP.
+// x of lane l ^ 32 and of lane l ^ 16, by the gfx950 lane-swap instructions (VALU, no LDS
+// crossbar): v_permlane32_swap on two copies of x leaves the upper half-wave's values in the lower
+// lanes of the second result and the lower half's in the upper lanes of the first;
+// v_permlane16_swap does the same for odd/even 16-lane rows.
+__device__ __forceinline__ float xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+// One level of a shfl_down halving tree: offsets 32 and 16 cross rows (lane swaps: lane l reads
+// l ^ O, which is l + O in every lane whose sum the tree uses), 8..1 by DPP.
 template <int O>
 __device__ __forceinline__ float down_add(float x) {
-    if constexpr (O >= 16) return x + __shfl_down(x, O, 64);
+    if constexpr (O == 32) return x + xor32(x);
+    else if constexpr (O == 16) return x + xor16(x);
     else return x + dpp_down<O>(x);
 }
 // shfl_down tree over the 64 lanes (offsets 32..1, the same pairs in the same order); the result
@@ -152,9 +166,21 @@ __device__ __forceinline__ float tree64(float x) {
     x = down_add<1>(x);
     return x;
 }
-__device__ __forceinline__ float max_xor(float x, int width) {   // exact max over `width` lanes
-#pragma unroll
-    for (int o = width >> 1; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+// lane 0's value in every lane (a scalar read, no crossbar)
+__device__ __forceinline__ float bcast0(float x) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+// Exact max over aligned groups of `width` (a power of two <= 64) lanes, in every lane of the
+// group: quads by DPP quad permutes (l ^ 1, l ^ 2), then 8 and 16 lanes by DPP half-row and row
+// mirrors (each pairs the two halves of the group, which already hold their own maxima), then the
+// lane swaps for 32 and 64. The max of the same values in any order is the same float.
+__device__ __forceinline__ float max_xor(float x, int width) {
+    if (width >= 2) x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false)));
+    if (width >= 4) x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false)));
+    if (width >= 8) x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false)));
+    if (width >= 16) x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false)));
+    if (width >= 32) x = fmaxf(x, xor16(x));
+    if (width >= 64) x = fmaxf(x, xor32(x));
     return x;
 }
 // The same max over the 4 lanes of a quad with DPP quad permutes (a VALU operand route, no LDS
