@@ -113,11 +113,17 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     }
     __shared__ unsigned s_next;                        // groups handed out after the first NW
     if (threadIdx.x == 0) s_next = 0u;
+    // SwiGLU: rows still owed per quarter / whole unit of the block (quarters first in the list)
+    __shared__ unsigned s_gcnt[(EPI == EPI_SWIGLU) ? kSwRows / 8 : 1];
+    __shared__ int8_t s_code[(EPI == EPI_SWIGLU) ? (kSwRows / 32) * NR * 16 : 1];
+    __shared__ float s_scale[(EPI == EPI_SWIGLU) ? (kSwRows / 32) * NR : 1];
+    if constexpr (EPI == EPI_SWIGLU)
+        for (int i = threadIdx.x; i < kSwRows / 8; i += NT) s_gcnt[i] = 0u;
     auto valid = [&](int j) __attribute__((always_inline)) { return j < nrb; };
     auto row_of = [&](int j, int r) __attribute__((always_inline)) {
         if constexpr (EPI == EPI_SWIGLU) {
-            if (j < 32 * F) return (bi + nb * (j >> 5)) * 32 + (j & 31);
-            const int m = (j - 32 * F) >> 3, r8 = (j - 32 * F) & 7;
+            if (j >= 8 * myq) return (bi + nb * ((j - 8 * myq) >> 5)) * 32 + ((j - 8 * myq) & 31);
+            const int m = j >> 3, r8 = j & 7;
             const int p = bi + nb * m, u = F * nb + (p >> 2), q = p & 3;
             return u * 32 + (r8 < 4 ? 4 * q + r8 : 12 + 4 * q + r8);
         } else {
@@ -225,6 +231,61 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     const bool holder = (lane % LPV) == 0 && vi < V;
     const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
     const uint32_t* resw = (const uint32_t*)a.res;
+    // v = silu(g) * u * gscale for output j (rows j and 16 + j of its unit)
+    auto swiglu = [&](float gv, float uv) __attribute__((always_inline)) {
+        const float swv = gv / (1.0f + qexp(-gv));
+        return swv * uv * a.gscale;
+    };
+    // 16 values in lanes c = lane & 15 -> one per-16 group: exact max, scale, codes
+    auto quant16 = [&](float v, int8_t& code, float& sc) __attribute__((always_inline)) {
+        const float mx = max_xor(fabsf(v), 16);
+        sc = mx * (1.0f / 127.0f);
+        const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        code = qcode(v, inv);
+    };
+    // The wave that stores the last row of a whole unit quantizes the unit into LDS; the wave that
+    // stores the last row of a leftover quarter hands its 4 SwiGLU values to the unit's other
+    // blocks (agent-scope stores, then the unit's arrival counter; the fourth arrival quantizes
+    // the unit). Quarters come first in the block's list, so their exchange overlaps the streaming.
+    auto finish = [&](int j) __attribute__((always_inline)) {
+        const int c16 = lane & 15;
+        if (j >= 8 * myq) {
+            const int k = (j - 8 * myq) >> 5, lr = 8 * myq + 32 * k;
+#pragma unroll
+            for (int nn = 0; nn < NR; ++nn) {
+                int8_t code;
+                float sc;
+                quant16(swiglu(sacc[(lr + c16) * NR + nn], sacc[(lr + 16 + c16) * NR + nn]), code, sc);
+                if (lane < 16) s_code[(k * NR + nn) * 16 + c16] = code;
+                if (lane == 0) s_scale[k * NR + nn] = sc;
+            }
+        } else {
+            const int m = j >> 3, p = bi + nb * m, e = p >> 2, q = p & 3, unit = F * nb + e, c = lane & 3;
+            float* part = a.sw_part + (size_t)e * 16 * NR;   // [16 outputs][NR]
+#pragma unroll
+            for (int nn = 0; nn < NR; ++nn) {
+                const float v = swiglu(sacc[(8 * m + c) * NR + nn], sacc[(8 * m + 4 + c) * NR + nn]);
+                if (lane < 4) st_agent(part + (4 * q + c) * NR + nn, v);
+            }
+            __builtin_amdgcn_s_waitcnt(0);             // the stores are acknowledged before counting
+            unsigned prev = 0u;
+            if (lane == 0) prev = add_agent(a.sw_cnt + e, 1u);
+            prev = (unsigned)__builtin_amdgcn_readfirstlane((int)prev);
+            if (prev == 3u) {                          // the unit's fourth quarter: finish it
+#pragma unroll
+                for (int nn = 0; nn < NR; ++nn) {
+                    int8_t code;
+                    float sc;
+                    quant16(__hip_atomic_load(part + c16 * NR + nn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), code, sc);
+                    if (lane < 16) a.act_q[(size_t)nn * a.act_stride + unit * 16 + c16] = code;
+                    if (lane == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
+                }
+                if (lane == 0) st_agent(a.sw_cnt + e, 0u);
+            }
+            // nothing of this path left in flight, so the loop's waits stay those of the plain path
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+    };
     for (int j = wave; j < nrb;) {
         unsigned jn = 0u;
         if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -278,53 +339,28 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
         } else {
             if (holder) sacc[j * NR + hn] = tv;
+            // (LDS operations of a wave complete in order: the row's values are in LDS before
+            // its count, and a wave that reads the count as complete reads them after it)
+            const bool isq = j < 8 * myq;
+            unsigned prev = 0u;
+            if (lane == 0)
+                prev = __hip_atomic_fetch_add(&s_gcnt[isq ? (j >> 3) : myq + ((j - 8 * myq) >> 5)], 1u,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            prev = (unsigned)__builtin_amdgcn_readfirstlane((int)prev);
+            if (prev == (isq ? 7u : 31u)) {
+                asm volatile("" ::: "memory");
+                finish(j);
+            }
         }
         j = jnext;
     }
     if constexpr (EPI == EPI_SWIGLU) {
+        // the whole units' codes and scales, quantized in the loop, written out together
         __syncthreads();
-        // v = silu(g) * u * gscale for output j (rows j and 16 + j of its unit)
-        auto swiglu = [&](float gv, float uv) __attribute__((always_inline)) {
-            const float swv = gv / (1.0f + qexp(-gv));
-            return swv * uv * a.gscale;
-        };
-        // 16 outputs in lanes j = lane & 15 -> one per-16 group: exact max, scale, codes
-        auto quant16 = [&](float v, int unit, int nn) __attribute__((always_inline)) {
-            const float mx = max_xor(fabsf(v), 16);
-            const float sc = mx * (1.0f / 127.0f);
-            const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
-            if (lane < 16) {
-                a.act_q[(size_t)nn * a.act_stride + unit * 16 + lane] = qcode(v, inv);
-                if (lane == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + unit] = sc;
-            }
-        };
-        const int j = lane & 15;
-        for (int k = wave; k < F; k += NW) {           // whole units
-            const int unit = bi + nb * k;
-#pragma unroll
-            for (int nn = 0; nn < NR; ++nn)
-                quant16(swiglu(sacc[(32 * k + j) * NR + nn], sacc[(32 * k + 16 + j) * NR + nn]), unit, nn);
-        }
-        for (int m = 0; m < myq; ++m) {                // leftover quarters
-            if (wave != (F + m) % NW) continue;
-            const int p = bi + nb * m, e = p >> 2, q = p & 3, unit = F * nb + e, c = lane & 3;
-            float* part = a.sw_part + (size_t)e * 16 * NR;   // [16 outputs][NR]
-            const int lr = 32 * F + 8 * m;
-#pragma unroll
-            for (int nn = 0; nn < NR; ++nn) {
-                const float v = swiglu(sacc[(lr + c) * NR + nn], sacc[(lr + 4 + c) * NR + nn]);
-                if (lane < 4) st_agent(part + (4 * q + c) * NR + nn, v);
-            }
-            __builtin_amdgcn_s_waitcnt(0);             // the stores are acknowledged before counting
-            unsigned prev = 0u;
-            if (lane == 0) prev = add_agent(a.sw_cnt + e, 1u);
-            prev = (unsigned)__builtin_amdgcn_readfirstlane((int)prev);
-            if (prev == 3u) {                          // the unit's fourth quarter: finish it
-#pragma unroll
-                for (int nn = 0; nn < NR; ++nn)
-                    quant16(__hip_atomic_load(part + j * NR + nn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), unit, nn);
-                if (lane == 0) st_agent(a.sw_cnt + e, 0u);
-            }
+        for (int i = threadIdx.x; i < F * NR * 16; i += NT) {
+            const int k = i / (NR * 16), nn = (i / 16) % NR, c = i & 15;
+            a.act_q[(size_t)nn * a.act_stride + (bi + nb * k) * 16 + c] = s_code[i];
+            if (c == 0) a.act_s[(size_t)nn * (a.act_stride >> 4) + bi + nb * k] = s_scale[k * NR + nn];
         }
     }
 }
