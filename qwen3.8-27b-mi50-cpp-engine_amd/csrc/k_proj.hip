@@ -69,10 +69,12 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
 //     group) are dealt so that every block streams the same number of rows. With
 //     nunits = F * nb + E, block b takes the whole units b, b + nb, ..., b + (F-1) nb; the E
 //     leftover units are cut into quarters (4 gate rows + the matching 4 up rows = 4 outputs)
-//     dealt round-robin over the blocks. The dot products of a block's rows meet in LDS; after
-//     one barrier the block applies SwiGLU + quantize to its whole units. A quarter's 4 SwiGLU
-//     values go to the scratch area with agent-scope stores and count on the unit's arrival
-//     counter; the wave that brings the count to 4 takes the exact
+//     dealt round-robin over the blocks (a block's quarters come first in its list). The dot
+//     products of a block's rows meet in LDS, and an LDS counter per unit / quarter counts its
+//     rows: the wave that stores the last row of a whole unit applies SwiGLU + quantize to it
+//     (codes and scales staged in LDS, written out by the block at the end); for a quarter it
+//     sends the 4 SwiGLU values to the scratch area with agent-scope stores and counts on the
+//     unit's arrival counter; the wave that brings the count to 4 takes the exact
 //     max over the unit's 16 values, quantizes them and resets the counter. No block waits for
 //     another.
 // FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
