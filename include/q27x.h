@@ -115,6 +115,36 @@ int q27x_proj_rows(const q27x_i8g_t* w, const int8_t* xq, int xstride, const flo
 int q27x_proj_partials(const q27x_i8g_t* w, const int8_t* xq, int xstride, int32_t* part,
                        int nr, q27x_stream_t s);
 
+/* ---- Prefill ingest GEMM on int8 MFMA (per-(row, group) scales) ----
+ * The reference's layer-split prefill quantizes per K group of gs = 1024 columns (or the whole K)
+ * and runs one rocBLAS int8 gemm_ex per group into int32 slabs, then sums the slabs in fp32
+ * (src/q27_epi.hip:1-8). These three entry points are that data path on gfx950 MFMA. */
+
+/* Weights, per-64 mirror -> per-(row, group) (replaces q27_i8g64_to_row_conv,
+ * src/q27_epi.hip:36-47; math at 14-35): sg = max of the group's gs/64 per-64 scales;
+ * inv = sg>0 ? 1/sg : 0; code = clamp(rint((w*s64)*inv), -127, 127). w, s64 [rows][K], [rows][K/64]
+ * -> wg [rows][K], sg [rows][K/gs]; wg may be w (in place, as the reference). gs % 64 == 0, K % gs == 0. */
+int q27x_i8g64_to_grp(const int8_t* w, const float* s64, int rows, int K, int gs, int8_t* wg,
+                      float* sg, q27x_stream_t s);
+
+/* Activations per (token, group) (the quantizer q27_quant_group, src/q27_epi.hip:64-75, that the
+ * reference fuses into its prefill norms and requant kernels, src/q27_epi.hip:80-186), here on fp32
+ * rows: sc = max|v|*(1/127); qi = sc>0 ? 1/sc : 0; code = clamp(rint(v*qi), -127, 127).
+ * x [M] rows of xstride floats (16-byte aligned) -> xq [M][K], xs [M][K/gs]. K % gs == 0. */
+int q27x_quant_tok_groups(const float* x, int xstride, int M, int K, int gs, int8_t* xq, float* xs,
+                          q27x_stream_t s);
+
+/* y[t][n] = alpha * sum over groups g (ascending) of fmaf((float)acc_g[t][n], sw[n][g]*sx[t][g], .)
+ *           (+ rs * res[t][n]),  acc_g = the exact int32 dot of group g.
+ * Replaces q27_rb_gemm_i8g (src/q27_rb.cpp:43-55) together with its fp32 slab epilogue
+ * q27_epi_f32r (src/q27_epi.hip:189-203, 235-243, 257-262), without the int32 slabs in memory.
+ * w [N][K] + sw [N][K/gs]; x [M][K] + sx [M][K/gs]; y rows of ldy floats; res may be NULL (rows of
+ * ldr floats). Kernel geometry: N % 128 == 0, K % 128 == 0, gs % 128 == 0, K/gs <= 20, w and x
+ * 16-byte aligned; any M >= 1. Other shapes return Q27X_E_SHAPE. */
+int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha,
+                  const int8_t* x, const float* sx, int M, float* y, int ldy, const float* res,
+                  int ldr, float rs, q27x_stream_t s);
+
 /* R9 / lm_head bf16 GEMV of nr rows (replaces q27_bf16_gemv2_tile, include/q27_nr.h:75-76):
  *   y[n][r] = sum_k bf16(W[r][k]) * bf16(x[n][k]) in fp32; out_bf16 selects bf16 / fp32 out.
  * K % 8 == 0. */

@@ -176,6 +176,66 @@ void q27o_quant_weights_i8g64(const float* w, int rows, int K, int8_t* wq, float
         q27o_quant_f32(w + (size_t)r * K, K, 64, wq + (size_t)r * K, ws + (size_t)r * (K / 64));
 }
 
+/* ------------------------------------------------------------------ prefill GEMM (per group) */
+/* Weights, per-64 mirror -> per-(row, group of gs): src/q27_epi.hip:14-35 (q27_k_i8g64_to_grp).
+ * sg = max of the group's per-64 scales; inv = sg>0 ? 1/sg : 0; code = clamp(rint((w*s64)*inv)). */
+void q27o_i8g64_to_grp(const int8_t* w, const float* s64, int rows, int K, int gs, int8_t* wg, float* sg) {
+    const int ns = K / 64, ng = K / gs;
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < ng; ++g) {
+            float mx = 0.0f;
+            for (int i = 0; i < gs / 64; ++i) mx = fmaxf(mx, s64[(size_t)r * ns + g * (gs / 64) + i]);
+            const float inv = (mx > 0.0f) ? 1.0f / mx : 0.0f;
+            sg[(size_t)r * ng + g] = mx;
+            for (int k = g * gs; k < (g + 1) * gs; ++k)
+                wg[(size_t)r * K + k] = q_code((float)w[(size_t)r * K + k] * s64[(size_t)r * ns + (k >> 6)], inv);
+        }
+}
+
+/* Activations per (token, group of gs): q27_quant_group, src/q27_epi.hip:64-75 (the same
+ * sc = mx*(1/127), inv = 1/sc form as q27o_quant_f32). Row t of x at x + t*xstride. */
+void q27o_quant_tok_groups(const float* x, int xstride, int M, int K, int gs, int8_t* xq, float* xs) {
+    for (int t = 0; t < M; ++t)
+        q27o_quant_f32(x + (size_t)t * xstride, K, gs, xq + (size_t)t * K, xs + (size_t)t * (K / gs));
+}
+
+/* The int32 slabs of src/q27_rb.cpp:43-55: part[g][t][n] = sum over group g of x[t][k]*w[n][k]. */
+void q27o_gemm_i8g_partials(const int8_t* w, int N, int K, int gs, const int8_t* x, int M, int32_t* part) {
+    const int ng = K / gs;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n)
+        for (int t = 0; t < M; ++t)
+            for (int g = 0; g < ng; ++g) {
+                int32_t acc = 0;
+                const int8_t* wr = w + (size_t)n * K + (size_t)g * gs;
+                const int8_t* xr = x + (size_t)t * K + (size_t)g * gs;
+                for (int k = 0; k < gs; ++k) acc += (int32_t)wr[k] * (int32_t)xr[k];
+                part[((size_t)g * M + t) * N + n] = acc;
+            }
+}
+
+/* The slab-sum epilogue, src/q27_epi.hip:189-203 (q27_slab4) and 235-243 (q27_k_epi_f32r):
+ * o = 0; for g ascending: o = fmaf((float)acc_g, sw[n][g]*sx[t][g], o); y = o*alpha (+ rs*res). */
+void q27o_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
+                   const float* sx, int M, float* y, int ldy, const float* res, int ldr, float rs) {
+    const int ng = K / gs;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n)
+        for (int t = 0; t < M; ++t) {
+            float o = 0.0f;
+            for (int g = 0; g < ng; ++g) {
+                int32_t acc = 0;
+                const int8_t* wr = w + (size_t)n * K + (size_t)g * gs;
+                const int8_t* xr = x + (size_t)t * K + (size_t)g * gs;
+                for (int k = 0; k < gs; ++k) acc += (int32_t)wr[k] * (int32_t)xr[k];
+                o = fmaf((float)acc, sw[(size_t)n * ng + g] * sx[(size_t)t * ng + g], o);
+            }
+            o = o * alpha;
+            if (res) o = o + rs * res[(size_t)t * ldr + n];
+            y[(size_t)t * ldy + n] = o;
+        }
+}
+
 /* R16: src/q27_nvfp4.hip:3984-4031 (natural order here): sw = g/(1+e^-g); v = sw*u*gscale. */
 void q27o_swiglu_quant_rows(const float* gate, const float* up, int stride, int8_t* xq,
                             float* xs, int n, float in_scale, int nr) {

@@ -100,6 +100,13 @@ void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride
                     int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
                     uint16_t* out, int8_t* xq, float* xs);
 
+/* ---- prefill GEMM, per-(row, group) int8 (src/q27_rb.cpp:43-55, src/q27_epi.hip:14-75, 189-243) ---- */
+void q27o_i8g64_to_grp(const int8_t* w, const float* s64, int rows, int K, int gs, int8_t* wg, float* sg);
+void q27o_quant_tok_groups(const float* x, int xstride, int M, int K, int gs, int8_t* xq, float* xs);
+void q27o_gemm_i8g_partials(const int8_t* w, int N, int K, int gs, const int8_t* x, int M, int32_t* part);
+void q27o_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
+                   const float* sx, int M, float* y, int ldy, const float* res, int ldr, float rs);
+
 /* ---- R18 / R20 ---- */
 void q27o_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val);
 int  q27o_accept(const int32_t* nx, const int32_t* dt, int k, int32_t* committed);

@@ -37,6 +37,10 @@ _SIGS = {
     "q27o_swiglu_quant_rows": ([VP, VP, I, VP, VP, I, F, I], None),
     "q27o_proj_rows": ([VP, VP, F, I, I, VP, I, VP, VP, I, I], None),
     "q27o_proj_partials": ([VP, I, I, VP, I, VP, I], None),
+    "q27o_i8g64_to_grp": ([VP, VP, I, I, I, VP, VP], None),
+    "q27o_quant_tok_groups": ([VP, I, I, I, I, VP, VP], None),
+    "q27o_gemm_i8g_partials": ([VP, I, I, I, VP, I, VP], None),
+    "q27o_gemm_i8g": ([VP, VP, I, I, I, F, VP, VP, I, VP, I, VP, I, F], None),
     "q27o_proj_rows_epi": ([VP, VP, F, I, I, VP, I, VP, VP, I, I, VP, I, I, F, I], None),
     "q27o_bf16_gemv_rows": ([VP, I, I, VP, I, VP, I, I], None),
     "q27o_rowsumsq": ([VP, I], F), "q27o_headsum": ([VP, VP, I], F),

@@ -72,6 +72,9 @@ _SIGS = {
     "q27x_quant_weights_i8g64": ([VP, I, I, VP, VP, VP], I),
     "q27x_proj_rows": ([VP, VP, I, VP, VP, I, I, VP, I, I, F, I, VP], I),
     "q27x_proj_partials": ([VP, VP, I, VP, I, VP], I),
+    "q27x_i8g64_to_grp": ([VP, VP, I, I, I, VP, VP, VP], I),
+    "q27x_quant_tok_groups": ([VP, I, I, I, I, VP, VP, VP], I),
+    "q27x_gemm_i8g": ([VP, VP, I, I, I, F, VP, VP, I, VP, I, VP, I, F, VP], I),
     "q27x_bf16_gemv_rows": ([VP, I, I, VP, I, VP, I, I, I, VP], I),
     "q27x_rmsnorm_quant_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, VP, I, F, I, VP], I),
     "q27x_swiglu_quant_rows": ([VP, VP, I, VP, VP, I, F, I, VP], I),
