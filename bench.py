@@ -107,6 +107,46 @@ def kernel_only(q27x, args):
     return 0
 
 
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published
+
+
+def prefill_gemm(q27x, reps=20):
+    """The prefill ingest GEMM on int8 MFMA (q27x_gemm_i8g) at BASELINE config 4's shape: M = 4096
+    tokens x N = 17408 (gate) x K = 5120, 1024-column groups, seeded codes and scales resident on
+    the device; device events around `reps` back-to-back launches."""
+    import ctypes
+    M, N, K, gs = 4096, 17408, 5120, 1024
+    rng = np.random.default_rng(SEED)
+    host = [rng.integers(-127, 127, (N, K), dtype=np.int8, endpoint=True),
+            rng.uniform(1e-4, 2e-3, (N, K // gs)).astype(np.float32),
+            rng.integers(-127, 127, (M, K), dtype=np.int8, endpoint=True),
+            rng.uniform(1e-3, 5e-2, (M, K // gs)).astype(np.float32)]
+    bufs = [q27x.DevBuf(array=h) for h in host]
+    y = q27x.DevBuf(M * N * 4)
+    args = (bufs[0].ptr, bufs[1].ptr, N, K, gs, 1.0, bufs[2].ptr, bufs[3].ptr, M, y.ptr, N, None, N, 0.0, None)
+    e0, e1, ms = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_float()
+    q27x.call("q27x_event_create", ctypes.byref(e0))
+    q27x.call("q27x_event_create", ctypes.byref(e1))
+    for _ in range(3):
+        q27x.call("q27x_gemm_i8g", *args)
+    q27x.call("q27x_event_record", e0, None)
+    for _ in range(reps):
+        q27x.call("q27x_gemm_i8g", *args)
+    q27x.call("q27x_event_record", e1, None)
+    q27x.call("q27x_device_sync")
+    q27x.call("q27x_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+    for e in (e0, e1):
+        q27x.call("q27x_event_destroy", e)
+    for b in bufs + [y]:
+        b.free()
+    us = ms.value * 1e3 / reps
+    tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    return {"kernel": "k_gemm_i8g<128> (per-(row, group) int8 MFMA, fp32 group-sum epilogue)",
+            "shape": {"M": M, "N": N, "K": K, "gs": gs}, "us_per_launch": round(us, 1),
+            "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS (int8, dense)",
+            "frac": round(tops / INT8_PEAK_TOPS, 4)}
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading for the calibration copy)."""
@@ -128,6 +168,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forced", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches (profilers that cannot follow graphs)")
+    ap.add_argument("--prefill-gemm-only", action="store_true",
+                    help="only the int8-MFMA prefill GEMM leg (for rocprofv3 passes on it)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate|up) and the calibration copy, for rocprofv3 --pmc passes")
     args = ap.parse_args()
@@ -144,6 +186,9 @@ def main():
     q27x.call("q27x_set_device", 0)
     if args.kernel_only:
         return kernel_only(q27x, args)
+    if args.prefill_gemm_only:
+        print(json.dumps({"prefill_gemm": prefill_gemm(q27x)}), flush=True)
+        return 0
     K = args.k
     rounds_total = args.warmup + args.steps
     ctx = args.prompt + rounds_total * (K + 1) + 128
@@ -200,6 +245,8 @@ def main():
         kernels[name] = {"us": round(ms_ * 1e3, 2), "GB_s": round(b_ / (ms_ / 1e3) / 1e9, 1)}
     log(f"kernels: {kernels}")
     eng.close()
+    pg = prefill_gemm(q27x)
+    log(f"prefill GEMM: {pg}")
 
     cpu = None
     if not args.no_cpu:
@@ -233,6 +280,7 @@ def main():
                      "bytes_per_launch": kbytes, "us_per_launch": round(kms * 1e3, 2)},
         "kernels": kernels,
         "prefill_s": round(prefill_s, 3),
+        "prefill_gemm": pg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -139,7 +139,7 @@ int q27x_quant_tok_groups(const float* x, int xstride, int M, int K, int gs, int
  * Replaces q27_rb_gemm_i8g (src/q27_rb.cpp:43-55) together with its fp32 slab epilogue
  * q27_epi_f32r (src/q27_epi.hip:189-203, 235-243, 257-262), without the int32 slabs in memory.
  * w [N][K] + sw [N][K/gs]; x [M][K] + sx [M][K/gs]; y rows of ldy floats; res may be NULL (rows of
- * ldr floats). Kernel geometry: N % 128 == 0, K % 128 == 0, gs % 128 == 0, K/gs <= 20, w and x
+ * ldr floats). Kernel geometry: N % 128 == 0, K % 64 == 0, gs % 64 == 0, K/gs <= 20, w and x
  * 16-byte aligned; any M >= 1. Other shapes return Q27X_E_SHAPE. */
 int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha,
                   const int8_t* x, const float* sx, int M, float* y, int ldy, const float* res,

@@ -18,11 +18,11 @@
 // change them; the fp32 part runs per output in the reference's group order.
 //
 // GEMM tiling: a 256-thread block computes a 128-token x 128-row tile; wave w owns the 64 x 64
-// quarter (w / 2, w % 2) as 2 x 2 v_mfma_i32_32x32x32_i8 tiles. K advances 128 bytes per step
-// through a double-buffered LDS stage whose rows are padded to 144 bytes, so the 32 rows that
-// one operand read touches start in distinct banks. The next step's tiles are loaded into
-// registers while the current step is multiplied. At the end of each group the int32 tiles are
-// folded into fp32 accumulators with the group's scales (staged in LDS for the whole K at the
+// quarter (w / 2, w % 2) as 2 x 2 v_mfma_i32_32x32x32_i8 tiles. K advances 64 bytes per stage
+// through a ring of 6 LDS stages filled by LDS DMA five stages ahead of the multiply, so about
+// 80 KiB per CU stay in flight to cover the memory latency (one stage ahead measured 16% of
+// the int8 peak: every stage waited for its own loads). At the end of each group the int32 tiles
+// are folded into fp32 accumulators with the group's scales (staged in LDS for the whole K at the
 // start) and restarted from zero.
 #include "q27x_dev.h"
 #include "q27x_int.h"
@@ -32,9 +32,14 @@ namespace q27x {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kGM = 128, kGN = 128, kGK = 128;    // block tile: tokens x weight rows x K bytes
-constexpr int kGLd = kGK + 16;                     // LDS row pitch (bytes)
+constexpr int kGM = 128, kGK = 64;                // block tile: 128 tokens x BN weight rows, 64 K bytes per stage
 constexpr int kGMaxG = 20;                         // groups per row held in LDS (K / GS)
+// stages in the LDS ring: 3 for 128-row tiles (two blocks per CU), 4 for 256-row tiles (one)
+template <int BN> struct GemmCfg {
+    static constexpr int S = BN == 128 ? 3 : 4;
+    static constexpr int Stage = (kGM + BN) * kGK; // bytes per stage: A rows, then B rows
+    static constexpr int NI = Stage / 4096;        // 1 KiB transfers per wave per stage
+};
 
 struct GemmArgs {
     const int8_t* w;    // [N][K] per-(row, group) codes
@@ -47,89 +52,116 @@ struct GemmArgs {
     int M, N, K, gs, ng, ldy, ldr;
 };
 
+template <int BN>
 __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
-    __shared__ __align__(16) int8_t sA[2][kGM * kGLd];
-    __shared__ __align__(16) int8_t sB[2][kGN * kGLd];
+    constexpr int kGS = GemmCfg<BN>::S, kGStage = GemmCfg<BN>::Stage, NI = GemmCfg<BN>::NI;
+    constexpr int JT = BN / 64;                    // 32-row weight tiles per wave
+    __shared__ __align__(16) int8_t sR[kGS * kGStage];
     __shared__ float sSx[kGM * kGMaxG];
-    __shared__ float sSw[kGN * kGMaxG];
+    __shared__ float sSw[BN * kGMaxG];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int n0 = blockIdx.x * kGN, m0 = blockIdx.y * kGM;
+    const int wm = wave >> 1, wn = wave & 1;       // wave tile: tokens 64 wm .., weight rows (BN / 2) wn ..
+    // Tile order. Blocks are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8), and each
+    // XCD has its own L2; block b therefore takes tile (b % 8) * T/8 + b / 8 of a grouped order
+    // (groups of 4 token tiles, weight tile major within a group), so each XCD streams one
+    // contiguous run of that order: with 32 token tiles, its own 4 token tiles (kept in its L2)
+    // against every weight tile, and the 32 blocks it runs at once share 4 token tiles and 8
+    // weight tiles. When T is not a multiple of 8 the order is the plain one.
+    const int nt = a.N / BN, mt = (a.M + kGM - 1) / kGM, T = nt * mt;
+    const int b = blockIdx.x;
+    const int tile = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int grp = tile / (4 * nt), fm = grp * 4, gsz = (mt - fm < 4) ? mt - fm : 4;
+    const int within = tile - grp * 4 * nt;
+    const int m0 = (fm + within % gsz) * kGM, n0 = (within / gsz) * BN;
     const int K = a.K, ng = a.ng, spg = a.gs / kGK, nsteps = K / kGK;
 
-    // the block's scales for every group (rows past M read row M - 1; their outputs are not stored)
+    // Stage layout: rows of 64 bytes, A rows 0..127 then B rows 0..BN-1; chunk c (16 bytes) of row R
+    // sits in slot c ^ ((R >> 1) & 3) of its row, so the 8 consecutive rows one operand read serves
+    // at a time (same c) fall in 8 different 16-byte bank groups. DMA: instruction i (< NI) of wave
+    // w fills stage bytes 1 KiB (NI w + i) .. +1 KiB = stage rows 16 (NI w + i) .. +16; lane l writes
+    // row 16 (NI w + i) + l / 4, slot l % 4, so it loads that row's chunk (l % 4) ^ ((row >> 1) & 3).
+    const int8_t* gp[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int rs = 16 * (NI * wave + i) + (lane >> 2);         // stage row
+        const int r = rs < kGM ? rs : rs - kGM;
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        if (rs < kGM) {
+            const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;       // rows past M repeat row M - 1
+            gp[i] = a.x + (size_t)t * K + 16 * c;
+        } else {
+            gp[i] = a.w + (size_t)(n0 + r) * K + 16 * c;
+        }
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)sR;
+    auto issue = [&](int step, int slot) __attribute__((always_inline)) {
+        const uint32_t base = lds0 + slot * kGStage + 1024 * NI * wave;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) lds_dma16(gp[i] + step * kGK, __builtin_amdgcn_readfirstlane(base + 1024 * i));
+    };
+
+    // the first stages, then the block's scales for every group (rows past M read row M - 1;
+    // their outputs are not stored)
+#pragma unroll
+    for (int p = 0; p < kGS - 1; ++p) issue(p < nsteps ? p : 0, p);
     for (int i = tid; i < kGM * ng; i += 256) {
         const int r = i / ng, g = i - r * ng;
         const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;
         sSx[r * kGMaxG + g] = a.sx[(size_t)t * ng + g];
+    }
+    for (int i = tid; i < BN * ng; i += 256) {
+        const int r = i / ng, g = i - r * ng;
         sSw[r * kGMaxG + g] = a.sw[(size_t)(n0 + r) * ng + g];
     }
+    __syncthreads();
 
-    // register stage: thread tid moves the 16-byte chunks c = tid + 256 q (q < 4) of each tile,
-    // chunk c = row c / 8, bytes 16 (c % 8) .. +16 of the step (8 threads cover one 128-byte row).
-    // (Plain code rather than lambdas: captured arrays were moved to LDS by the compiler.)
-    const int crow = tid >> 3, ccol = (tid & 7) * 16;
-    const int8_t* xp[4];
-    const int8_t* wp[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int row = crow + 32 * q;
-        const int t = (m0 + row < a.M) ? m0 + row : a.M - 1;
-        xp[q] = a.x + (size_t)t * K + ccol;
-        wp[q] = a.w + (size_t)(n0 + row) * K + ccol;
-    }
-    uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-#define Q27X_GLOAD(k0)                                                                              \
-    ra0 = *(const uint4*)(xp[0] + (k0)); rb0 = *(const uint4*)(wp[0] + (k0));                       \
-    ra1 = *(const uint4*)(xp[1] + (k0)); rb1 = *(const uint4*)(wp[1] + (k0));                       \
-    ra2 = *(const uint4*)(xp[2] + (k0)); rb2 = *(const uint4*)(wp[2] + (k0));                       \
-    ra3 = *(const uint4*)(xp[3] + (k0)); rb3 = *(const uint4*)(wp[3] + (k0));
-#define Q27X_SSTORE(buf)                                                                            \
-    *(uint4*)&sA[buf][(crow) * kGLd + ccol] = ra0; *(uint4*)&sB[buf][(crow) * kGLd + ccol] = rb0;   \
-    *(uint4*)&sA[buf][(crow + 32) * kGLd + ccol] = ra1; *(uint4*)&sB[buf][(crow + 32) * kGLd + ccol] = rb1; \
-    *(uint4*)&sA[buf][(crow + 64) * kGLd + ccol] = ra2; *(uint4*)&sB[buf][(crow + 64) * kGLd + ccol] = rb2; \
-    *(uint4*)&sA[buf][(crow + 96) * kGLd + ccol] = ra3; *(uint4*)&sB[buf][(crow + 96) * kGLd + ccol] = rb3;
-
-    v16i acc[2][2];
-    float facc[2][2][16];
+    v16i acc[2][JT];
+    float facc[2][JT][16];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < JT; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0; facc[i][j][r] = 0.0f; }
 
     // operand rows of this lane: A row (token) wm*64 + 32 i + lane % 32, B row (weight row)
-    // wn*64 + 32 j + lane % 32; both take bytes 16 (lane / 32) .. +16 of each 32-byte K slice, so
-    // A and B pair the same K positions
-    const int arow = wm * 64 + (lane & 31), brow = wn * 64 + (lane & 31), kh = (lane >> 5) * 16;
-
-    Q27X_GLOAD(0)
-    Q27X_SSTORE(0)
-    __syncthreads();
+    // wn*BN/2 + 32 j + lane % 32; both take chunk 2 kk + lane / 32 of the stage's 32-byte K slice
+    // kk, so A and B pair the same K positions
+    const int arow = wm * 64 + (lane & 31), brow = wn * (BN / 2) + (lane & 31);
+    const int swa = (arow >> 1) & 3, swb = (brow >> 1) & 3, kh = lane >> 5;
     for (int s = 0; s < nsteps; ++s) {
-        const int buf = s & 1;
-        // the step after the last reloads step 0 into the idle buffer (nothing reads it), so
-        // every iteration issues the same loads and the compiler's waits stay exact
-        const int kn = (s + 1 < nsteps ? s + 1 : 0) * kGK;
-        Q27X_GLOAD(kn)
+        // this wave's transfers for stage s are done once at most the NI (kGS - 2) issued after
+        // them are outstanding (vector-memory counts retire in order); after the barrier every
+        // wave's are, and every wave has finished reading stage s - 1, whose slot is refilled now
+        // with stage s + kGS - 1 (past the end: stage 0 again, never read, so every iteration
+        // issues the same transfers and the count stays exact)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(NI * (kGS - 2)));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_sched_barrier(0);
+        const int sn = s + kGS - 1;
+        issue(sn < nsteps ? sn : 0, sn % kGS);
+        const int8_t* st = sR + (s % kGS) * kGStage;
 #pragma unroll
         for (int kk = 0; kk < kGK / 32; ++kk) {
-            v4i av0 = *(const v4i*)&sA[buf][arow * kGLd + kk * 32 + kh];
-            v4i av1 = *(const v4i*)&sA[buf][(arow + 32) * kGLd + kk * 32 + kh];
-            v4i bv0 = *(const v4i*)&sB[buf][brow * kGLd + kk * 32 + kh];
-            v4i bv1 = *(const v4i*)&sB[buf][(brow + 32) * kGLd + kk * 32 + kh];
-            acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av0, bv0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av0, bv1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av1, bv0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av1, bv1, acc[1][1], 0, 0, 0);
+            const int c = 2 * kk + kh;
+            v4i av[2], bv[JT];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) av[i] = *(const v4i*)(st + (arow + 32 * i) * kGK + ((c ^ swa) << 4));
+#pragma unroll
+            for (int j = 0; j < JT; ++j) bv[j] = *(const v4i*)(st + (kGM + brow + 32 * j) * kGK + ((c ^ swb) << 4));
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
         if ((s + 1) % spg == 0) {
             // fold the group: accumulator element r of a 32 x 32 tile is row
             // 8 (r / 4) + 4 (lane / 32) + r % 4, column lane % 32
             const int g = (s + 1) / spg - 1;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < JT; ++j) {
                 const float swv = sSw[(brow + 32 * j) * kGMaxG + g];
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
@@ -142,17 +174,15 @@ __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
                     }
             }
         }
-        Q27X_SSTORE(buf ^ 1)
-        __syncthreads();
     }
-#undef Q27X_GLOAD
-#undef Q27X_SSTORE
+    // no transfer may still be writing LDS when the block ends
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+        for (int j = 0; j < JT; ++j) {
+            const int n = n0 + wn * (BN / 2) + 32 * j + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -253,17 +283,19 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
         set_error("q27x_gemm_i8g: bad arguments");
         return Q27X_E_ARG;
     }
-    if ((N % kGN) || (K % kGK) || (gs % kGK) || (K % gs) || K / gs > kGMaxG || ((uintptr_t)w & 15) ||
+    if ((N % 128) || (K % kGK) || (gs % kGK) || (K % gs) || K / gs > kGMaxG || ((uintptr_t)w & 15) ||
         ((uintptr_t)x & 15)) {
-        set_error("q27x_gemm_i8g: no kernel for N %d, K %d, gs %d (N %% %d, K %% %d, gs %% %d must be 0, "
-                  "K/gs <= %d, 16-byte aligned codes)", N, K, gs, kGN, kGK, kGK, kGMaxG);
+        set_error("q27x_gemm_i8g: no kernel for N %d, K %d, gs %d (N %% 128, K %% %d, gs %% %d must be 0, "
+                  "K/gs <= %d, 16-byte aligned codes)", N, K, gs, kGK, kGK, kGMaxG);
         return Q27X_E_SHAPE;
     }
     GemmArgs a{};
     a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = y; a.res = res; a.alpha = alpha; a.rs = rs;
     a.M = M; a.N = N; a.K = K; a.gs = gs; a.ng = K / gs; a.ldy = ldy; a.ldr = ldr;
-    hipLaunchKernelGGL(k_gemm_i8g, dim3((unsigned)(N / kGN), (unsigned)((M + kGM - 1) / kGM)), dim3(256), 0,
-                       (hipStream_t)s, a);
+    // 128-row weight tiles: two blocks per CU (LDS 68 KiB, 220 registers per lane). 256-row tiles
+    // (one block per CU, 433 registers) measured 1-8% slower at the prefill shapes.
+    const unsigned mt = (unsigned)((M + kGM - 1) / kGM);
+    hipLaunchKernelGGL(k_gemm_i8g<128>, dim3((unsigned)(N / 128) * mt), dim3(256), 0, (hipStream_t)s, a);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

@@ -97,6 +97,19 @@ __device__ __forceinline__ float rsqrt_cr(float x) { return 1.0f / __builtin_sqr
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// LDS DMA of 16 bytes per lane: lane l's 16 bytes from g land at LDS byte address lds + 16 l
+// (lds wave-uniform). Issued from inline asm: with the builtin form the compiler makes every
+// later LDS read of the wave wait for all of its outstanding vector-memory loads, which would
+// serialize a multi-stage pipeline; here the transfer is invisible to the compiler, and the caller
+// waits for it (s_waitcnt vmcnt, counting these in issue order) before it reads the destination.
+// M0 carries the LDS base for the one instruction and is restored after it.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save) : "s"(lds), "v"(g) : "memory");
+}
+
 // The round's stop flag (null: never stopped), read through the constant address space so it is
 // a scalar load: a vector load would make the wait for it (vmcnt) also wait for every weight load
 // issued before it. The flag does not change while a kernel that reads it runs.
