@@ -18,12 +18,13 @@
 // change them; the fp32 part runs per output in the reference's group order.
 //
 // GEMM tiling: a 256-thread block computes a 128-token x 128-row tile; wave w owns the 64 x 64
-// quarter (w / 2, w % 2) as 2 x 2 v_mfma_i32_32x32x32_i8 tiles. K advances 64 bytes per stage
-// through a ring of 6 LDS stages filled by LDS DMA five stages ahead of the multiply, so about
-// 80 KiB per CU stay in flight to cover the memory latency (one stage ahead measured 16% of
-// the int8 peak: every stage waited for its own loads). At the end of each group the int32 tiles
-// are folded into fp32 accumulators with the group's scales (staged in LDS for the whole K at the
-// start) and restarted from zero.
+// quarter (w / 2, w % 2) as 2 x 2 v_mfma_i32_32x32x32_i8 tiles, and two blocks share a CU. K
+// advances 64 bytes per stage through a ring of 4 LDS stages (3 when the scales of 17+ groups
+// take the room) filled by LDS DMA ahead of the multiply, so 96-128 KiB per CU stay in flight
+// to cover the memory latency (one stage ahead measured 16% of the int8 peak: every stage waited
+// for its own loads). At the end of each group the int32 tiles are folded into fp32
+// accumulators with the group's scales (staged in LDS for the whole K at the start) and
+// restarted from zero.
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
@@ -35,8 +36,8 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kGM = 128, kGK = 64;                // block tile: 128 tokens x BN weight rows, 64 K bytes per stage
 constexpr int kGMaxG = 20;                         // groups per row held in LDS (K / GS)
 // stages in the LDS ring: 3 for 128-row tiles (two blocks per CU), 4 for 256-row tiles (one)
-template <int BN> struct GemmCfg {
-    static constexpr int S = BN == 128 ? 3 : 4;
+template <int BN, int NS> struct GemmCfg {
+    static constexpr int S = NS;
     static constexpr int Stage = (kGM + BN) * kGK; // bytes per stage: A rows, then B rows
     static constexpr int NI = Stage / 4096;        // 1 KiB transfers per wave per stage
 };
@@ -52,13 +53,16 @@ struct GemmArgs {
     int M, N, K, gs, ng, ldy, ldr;
 };
 
-template <int BN>
+template <int BN, int NS>
 __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
-    constexpr int kGS = GemmCfg<BN>::S, kGStage = GemmCfg<BN>::Stage, NI = GemmCfg<BN>::NI;
+    constexpr int kGS = GemmCfg<BN, NS>::S, kGStage = GemmCfg<BN, NS>::Stage, NI = GemmCfg<BN, NS>::NI;
     constexpr int JT = BN / 64;                    // 32-row weight tiles per wave
     __shared__ __align__(16) int8_t sR[kGS * kGStage];
-    __shared__ float sSx[kGM * kGMaxG];
-    __shared__ float sSw[BN * kGMaxG];
+    // the block's scales, [row][ng] floats: 128 token rows, then BN weight rows (dynamic LDS,
+    // sized by the launch to the group count, so short K leaves room for a deeper ring)
+    extern __shared__ float sScl[];
+    float* sSx = sScl;
+    float* sSw = sScl + kGM * a.ng;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;       // wave tile: tokens 64 wm .., weight rows (BN / 2) wn ..
     // Tile order. Blocks are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8), and each
@@ -107,11 +111,11 @@ __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
     for (int i = tid; i < kGM * ng; i += 256) {
         const int r = i / ng, g = i - r * ng;
         const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;
-        sSx[r * kGMaxG + g] = a.sx[(size_t)t * ng + g];
+        sSx[r * ng + g] = a.sx[(size_t)t * ng + g];
     }
     for (int i = tid; i < BN * ng; i += 256) {
         const int r = i / ng, g = i - r * ng;
-        sSw[r * kGMaxG + g] = a.sw[(size_t)(n0 + r) * ng + g];
+        sSw[r * ng + g] = a.sw[(size_t)(n0 + r) * ng + g];
     }
     __syncthreads();
 
@@ -162,13 +166,13 @@ __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
             const int g = (s + 1) / spg - 1;
 #pragma unroll
             for (int j = 0; j < JT; ++j) {
-                const float swv = sSw[(brow + 32 * j) * kGMaxG + g];
+                const float swv = sSw[(brow + 32 * j) * ng + g];
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int tr = wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        const float sc = swv * sSx[tr * kGMaxG + g];
+                        const float sc = swv * sSx[tr * ng + g];
                         facc[i][j][r] = __builtin_fmaf((float)acc[i][j][r], sc, facc[i][j][r]);
                         acc[i][j][r] = 0;
                     }
@@ -292,10 +296,15 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
     GemmArgs a{};
     a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = y; a.res = res; a.alpha = alpha; a.rs = rs;
     a.M = M; a.N = N; a.K = K; a.gs = gs; a.ng = K / gs; a.ldy = ldy; a.ldr = ldr;
-    // 128-row weight tiles: two blocks per CU (LDS 68 KiB, 220 registers per lane). 256-row tiles
-    // (one block per CU, 433 registers) measured 1-8% slower at the prefill shapes.
+    // 128-row weight tiles: two blocks per CU (220 registers per lane). 256-row tiles (one block
+    // per CU, 433 registers) measured 1-8% slower at the prefill shapes.
     const unsigned mt = (unsigned)((M + kGM - 1) / kGM);
-    hipLaunchKernelGGL(k_gemm_i8g<128>, dim3((unsigned)(N / 128) * mt), dim3(256), 0, (hipStream_t)s, a);
+    // ring depth: 4 stages (64 KiB) while the scales leave two blocks per CU room, else 3
+    const size_t scl = (size_t)(kGM + 128) * a.ng * sizeof(float);
+    if (64 * 1024 + scl <= 80 * 1024)
+        hipLaunchKernelGGL((k_gemm_i8g<128, 4>), dim3((unsigned)(N / 128) * mt), dim3(256), scl, (hipStream_t)s, a);
+    else
+        hipLaunchKernelGGL((k_gemm_i8g<128, 3>), dim3((unsigned)(N / 128) * mt), dim3(256), scl, (hipStream_t)s, a);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
