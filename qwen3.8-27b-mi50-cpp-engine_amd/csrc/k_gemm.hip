@@ -33,13 +33,14 @@ namespace q27x {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kGM = 128, kGK = 64;                // block tile: 128 tokens x BN weight rows, 64 K bytes per stage
+constexpr int kGN = 128, kGK = 64;                // block tile: BM tokens x 128 weight rows, 64 K bytes per stage
 constexpr int kGMaxG = 20;                         // groups per row held in LDS (K / GS)
-// stages in the LDS ring: 3 for 128-row tiles (two blocks per CU), 4 for 256-row tiles (one)
-template <int BN, int NS> struct GemmCfg {
-    static constexpr int S = NS;
-    static constexpr int Stage = (kGM + BN) * kGK; // bytes per stage: A rows, then B rows
-    static constexpr int NI = Stage / 4096;        // 1 KiB transfers per wave per stage
+template <int BM, int NS> struct GemmCfg {
+    static constexpr int S = NS;                   // stages in the LDS ring
+    static constexpr int NW = BM / 32;             // waves: BM / 64 token rows x 2 weight columns of 64
+    static constexpr int Stage = (BM + kGN) * kGK; // bytes per stage: A rows, then B rows
+    static constexpr int NI = Stage / (1024 * NW); // 1 KiB transfers per wave per stage
+    static_assert(Stage % (1024 * NW) == 0, "whole transfers per wave");
 };
 
 struct GemmArgs {
@@ -53,10 +54,11 @@ struct GemmArgs {
     int M, N, K, gs, ng, ldy, ldr;
 };
 
-template <int BN, int NS>
-__global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
-    constexpr int kGS = GemmCfg<BN, NS>::S, kGStage = GemmCfg<BN, NS>::Stage, NI = GemmCfg<BN, NS>::NI;
-    constexpr int JT = BN / 64;                    // 32-row weight tiles per wave
+template <int BM, int NS>
+__global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
+    constexpr int kGS = GemmCfg<BM, NS>::S, kGStage = GemmCfg<BM, NS>::Stage, NI = GemmCfg<BM, NS>::NI;
+    constexpr int kGM = BM, BN = kGN, NT = BM * 2;
+    constexpr int JT = 2;                          // 32-row weight tiles per wave
     __shared__ __align__(16) int8_t sR[kGS * kGStage];
     // the block's scales, [row][ng] floats: 128 token rows, then BN weight rows (dynamic LDS,
     // sized by the launch to the group count, so short K leaves room for a deeper ring)
@@ -108,12 +110,12 @@ __global__ __launch_bounds__(256) void k_gemm_i8g(GemmArgs a) {
     // their outputs are not stored)
 #pragma unroll
     for (int p = 0; p < kGS - 1; ++p) issue(p < nsteps ? p : 0, p);
-    for (int i = tid; i < kGM * ng; i += 256) {
+    for (int i = tid; i < kGM * ng; i += NT) {
         const int r = i / ng, g = i - r * ng;
         const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;
         sSx[r * ng + g] = a.sx[(size_t)t * ng + g];
     }
-    for (int i = tid; i < BN * ng; i += 256) {
+    for (int i = tid; i < BN * ng; i += NT) {
         const int r = i / ng, g = i - r * ng;
         sSw[r * ng + g] = a.sw[(size_t)(n0 + r) * ng + g];
     }
@@ -296,15 +298,22 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
     GemmArgs a{};
     a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = y; a.res = res; a.alpha = alpha; a.rs = rs;
     a.M = M; a.N = N; a.K = K; a.gs = gs; a.ng = K / gs; a.ldy = ldy; a.ldr = ldr;
-    // 128-row weight tiles: two blocks per CU (220 registers per lane). 256-row tiles (one block
-    // per CU, 433 registers) measured 1-8% slower at the prefill shapes.
-    const unsigned mt = (unsigned)((M + kGM - 1) / kGM);
-    // ring depth: 4 stages (64 KiB) while the scales leave two blocks per CU room, else 3
-    const size_t scl = (size_t)(kGM + 128) * a.ng * sizeof(float);
-    if (64 * 1024 + scl <= 80 * 1024)
-        hipLaunchKernelGGL((k_gemm_i8g<128, 4>), dim3((unsigned)(N / 128) * mt), dim3(256), scl, (hipStream_t)s, a);
-    else
-        hipLaunchKernelGGL((k_gemm_i8g<128, 3>), dim3((unsigned)(N / 128) * mt), dim3(256), scl, (hipStream_t)s, a);
+    // Weight tiles of 128 rows (256-row tiles need 433 registers per lane, one block per CU, and
+    // measured 1-8% slower). Token tiles of 256 (8 waves, one block per CU, a 5-stage ring) from
+    // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
+    // two blocks per CU, a 4-stage ring, or 3 when 17+ groups' scales take the room).
+    if (M >= 512) {
+        const unsigned mt = (unsigned)((M + 255) / 256);
+        const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);
+        hipLaunchKernelGGL((k_gemm_i8g<256, 5>), dim3((unsigned)(N / kGN) * mt), dim3(512), scl, (hipStream_t)s, a);
+    } else {
+        const unsigned mt = (unsigned)((M + 127) / 128);
+        const size_t scl = (size_t)(128 + kGN) * a.ng * sizeof(float);
+        if (64 * 1024 + scl <= 80 * 1024)
+            hipLaunchKernelGGL((k_gemm_i8g<128, 4>), dim3((unsigned)(N / kGN) * mt), dim3(256), scl, (hipStream_t)s, a);
+        else
+            hipLaunchKernelGGL((k_gemm_i8g<128, 3>), dim3((unsigned)(N / kGN) * mt), dim3(256), scl, (hipStream_t)s, a);
+    }
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

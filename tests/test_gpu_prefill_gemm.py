@@ -54,6 +54,8 @@ def oracle_gemm(O, w, sw, x, sx, gs, alpha, res=None, rs=0.0):
     (300, 384, 5120, 5120, True),      # one group over the whole K (per-token scales)
     (130, 256, 17408, 1024, False),    # down's K: 17 groups
     (257, 128, 6144, 1024, True),      # out_proj's K
+    (600, 256, 5120, 1024, True),      # 256-token tiles, ragged last tile
+    (1024, 384, 17408, 1024, False),   # 256-token tiles, 17 groups
 ])
 def test_gemm_i8g(gpu, O, M, N, K, gs, with_res):
     rng = np.random.default_rng(0x51E70400 + M + N + K)
