@@ -81,17 +81,18 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
     const int m0 = (fm + within % gsz) * kGM, n0 = (within / gsz) * BN;
     const int K = a.K, ng = a.ng, spg = a.gs / kGK, nsteps = K / kGK;
 
-    // Stage layout: rows of 64 bytes, A rows 0..127 then B rows 0..BN-1; chunk c (16 bytes) of row R
-    // sits in slot c ^ ((R >> 1) & 3) of its row, so the 8 consecutive rows one operand read serves
-    // at a time (same c) fall in 8 different 16-byte bank groups. DMA: instruction i (< NI) of wave
+    // Stage layout: rows of 64 bytes, A rows 0..BM-1 then B rows 0..BN-1; chunk c (16 bytes) of row
+    // R sits in slot c ^ ((R >> 2) & 3) of its row, so the 16 consecutive rows one operand read
+    // serves at a time (same c) fill the 16 distinct 16-byte positions of a 256-byte bank window
+    // (SQ_LDS_BANK_CONFLICT reads 0; with (R >> 1) & 3 it was 17% of busy cycles). DMA: instruction i (< NI) of wave
     // w fills stage bytes 1 KiB (NI w + i) .. +1 KiB = stage rows 16 (NI w + i) .. +16; lane l writes
-    // row 16 (NI w + i) + l / 4, slot l % 4, so it loads that row's chunk (l % 4) ^ ((row >> 1) & 3).
+    // row 16 (NI w + i) + l / 4, slot l % 4, so it loads that row's chunk (l % 4) ^ ((row >> 2) & 3).
     const int8_t* gp[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int rs = 16 * (NI * wave + i) + (lane >> 2);         // stage row
         const int r = rs < kGM ? rs : rs - kGM;
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
         if (rs < kGM) {
             const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;       // rows past M repeat row M - 1
             gp[i] = a.x + (size_t)t * K + 16 * c;
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
     // wn*BN/2 + 32 j + lane % 32; both take chunk 2 kk + lane / 32 of the stage's 32-byte K slice
     // kk, so A and B pair the same K positions
     const int arow = wm * 64 + (lane & 31), brow = wn * (BN / 2) + (lane & 31);
-    const int swa = (arow >> 1) & 3, swb = (brow >> 1) & 3, kh = lane >> 5;
+    const int swa = (arow >> 2) & 3, swb = (brow >> 2) & 3, kh = lane >> 5;
     for (int s = 0; s < nsteps; ++s) {
         // this wave's transfers for stage s are done once at most the NI (kGS - 2) issued after
         // them are outstanding (vector-memory counts retire in order); after the barrier every
