@@ -141,7 +141,7 @@ def prefill_gemm(q27x, reps=20):
         b.free()
     us = ms.value * 1e3 / reps
     tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    return {"kernel": "k_gemm_i8g<256, 5> (256-token x 128-row tiles, per-(row, group) int8 MFMA, fp32 group-sum epilogue)",
+    return {"kernel": "k_gemm_i8g_rs (256-token x 128-row tiles, register-staged 128-byte stages, per-(row, group) int8 MFMA, fp32 group-sum epilogue)",
             "shape": {"M": M, "N": N, "K": K, "gs": gs}, "us_per_launch": round(us, 1),
             "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS (int8, dense)",
             "frac": round(tops / INT8_PEAK_TOPS, 4)}

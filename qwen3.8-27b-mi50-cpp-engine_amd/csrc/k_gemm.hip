@@ -202,6 +202,149 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
         }
 }
 
+// The same GEMM for 256-token tiles with register-staged loads and 128-byte stages: each thread
+// moves six 16-byte chunks per stage with plain vector loads, issued three stages ahead into two
+// register sets, and writes them to a double-buffered LDS stage one iteration before the
+// multiply; 16 MFMAs per wave between barriers. The loop is unrolled by two so the register sets
+// are named at compile time; nsteps (K / 128) must be even. Rows are 128 bytes, chunk c of row R
+// in slot c ^ ((R >> 1) & 7) (the 16 rows one operand read serves fill a 256-byte bank window).
+// Same fold and tile order as k_gemm_i8g.
+__global__ __launch_bounds__(512) void k_gemm_i8g_rs(GemmArgs a) {
+    constexpr int BM = 256, BN = kGN, NT = 512, KB = 128, kStage = (BM + BN) * KB;
+    __shared__ __align__(16) int8_t sR[2 * kStage];
+    extern __shared__ float sScl[];
+    float* sSx = sScl;
+    float* sSw = sScl + BM * a.ng;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nt = a.N / BN, mt = (a.M + BM - 1) / BM, T = nt * mt;
+    const int b = blockIdx.x;
+    const int tile = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int grp = tile / (4 * nt), fm = grp * 4, gsz = (mt - fm < 4) ? mt - fm : 4;
+    const int within = tile - grp * 4 * nt;
+    const int m0 = (fm + within % gsz) * BM, n0 = (within / gsz) * BN;
+    const int K = a.K, ng = a.ng, spg = a.gs / KB, nsteps = K / KB;
+
+    // thread tid moves chunk q = tid + 512 k (k < 6) of each stage: stage row q / 8 (A rows
+    // first), natural chunk q % 8 of that row, stored at slot (q % 8) ^ ((row >> 1) & 7)
+    const int8_t* gp[6];
+    int lo[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const int q = tid + NT * k, rs = q >> 3, c = q & 7;
+        const int r = rs < BM ? rs : rs - BM;
+        if (rs < BM) {
+            const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;
+            gp[k] = a.x + (size_t)t * K + 16 * c;
+        } else {
+            gp[k] = a.w + (size_t)(n0 + r) * K + 16 * c;
+        }
+        lo[k] = rs * KB + ((c ^ ((r >> 1) & 7)) << 4);
+    }
+    uint4 ra0, ra1, ra2, ra3, ra4, ra5, rb0, rb1, rb2, rb3, rb4, rb5;
+#define Q27X_LD(R0, R1, R2, R3, R4, R5, step)                                                       \
+    { const int k0_ = (step) * KB;                                                                  \
+      R0 = *(const uint4*)(gp[0] + k0_); R1 = *(const uint4*)(gp[1] + k0_);                         \
+      R2 = *(const uint4*)(gp[2] + k0_); R3 = *(const uint4*)(gp[3] + k0_);                         \
+      R4 = *(const uint4*)(gp[4] + k0_); R5 = *(const uint4*)(gp[5] + k0_); }
+#define Q27X_ST(R0, R1, R2, R3, R4, R5, slot)                                                       \
+    { int8_t* d_ = sR + (slot) * kStage;                                                            \
+      *(uint4*)(d_ + lo[0]) = R0; *(uint4*)(d_ + lo[1]) = R1; *(uint4*)(d_ + lo[2]) = R2;           \
+      *(uint4*)(d_ + lo[3]) = R3; *(uint4*)(d_ + lo[4]) = R4; *(uint4*)(d_ + lo[5]) = R5; }
+
+    for (int i = tid; i < BM * ng; i += NT) {
+        const int r = i / ng, g = i - r * ng;
+        const int t = (m0 + r < a.M) ? m0 + r : a.M - 1;
+        sSx[r * ng + g] = a.sx[(size_t)t * ng + g];
+    }
+    for (int i = tid; i < BN * ng; i += NT) {
+        const int r = i / ng, g = i - r * ng;
+        sSw[r * ng + g] = a.sw[(size_t)(n0 + r) * ng + g];
+    }
+    // stages 0 and 1 in flight, stage 0 to LDS, stage 2 in flight behind stage 1
+    Q27X_LD(ra0, ra1, ra2, ra3, ra4, ra5, 0)
+    Q27X_LD(rb0, rb1, rb2, rb3, rb4, rb5, 1)
+    Q27X_ST(ra0, ra1, ra2, ra3, ra4, ra5, 0)
+    Q27X_LD(ra0, ra1, ra2, ra3, ra4, ra5, 2 < nsteps ? 2 : 0)
+    __syncthreads();
+
+    v16i acc[2][2];
+    float facc[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0; facc[i][j][r] = 0.0f; }
+    const int arow = wm * 64 + (lane & 31), brow = wn * 64 + (lane & 31);
+    const int swa = (arow >> 1) & 7, swb = (brow >> 1) & 7, kh = lane >> 5;
+
+    // iteration s: multiply stage s (LDS slot s % 2); store stage s + 1 (register set (s + 1) % 2)
+    // into the other slot; reload that set with stage s + 3 (past the end: stage 0, stored into a
+    // slot nobody reads again); barrier
+#define Q27X_ITER(S_, N0, N1, N2, N3, N4, N5)                                                       \
+    {                                                                                               \
+        const int s_ = (S_);                                                                        \
+        const int8_t* st = sR + (s_ & 1) * kStage;                                                  \
+_Pragma("unroll")                                                                                   \
+        for (int kk = 0; kk < KB / 32; ++kk) {                                                      \
+            const int c = 2 * kk + kh;                                                              \
+            v4i av[2], bv[2];                                                                       \
+_Pragma("unroll")                                                                                   \
+            for (int i = 0; i < 2; ++i) av[i] = *(const v4i*)(st + (arow + 32 * i) * KB + ((c ^ swa) << 4)); \
+_Pragma("unroll")                                                                                   \
+            for (int j = 0; j < 2; ++j) bv[j] = *(const v4i*)(st + (BM + brow + 32 * j) * KB + ((c ^ swb) << 4)); \
+_Pragma("unroll")                                                                                   \
+            for (int i = 0; i < 2; ++i)                                                             \
+_Pragma("unroll")                                                                                   \
+                for (int j = 0; j < 2; ++j)                                                         \
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0); \
+        }                                                                                           \
+        if ((s_ + 1) % spg == 0) {                                                                  \
+            const int g = (s_ + 1) / spg - 1;                                                       \
+_Pragma("unroll")                                                                                   \
+            for (int j = 0; j < 2; ++j) {                                                           \
+                const float swv = sSw[(brow + 32 * j) * ng + g];                                    \
+_Pragma("unroll")                                                                                   \
+                for (int i = 0; i < 2; ++i)                                                         \
+_Pragma("unroll")                                                                                   \
+                    for (int r = 0; r < 16; ++r) {                                                  \
+                        const int tr = wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); \
+                        const float sc = swv * sSx[tr * ng + g];                                    \
+                        facc[i][j][r] = __builtin_fmaf((float)acc[i][j][r], sc, facc[i][j][r]);     \
+                        acc[i][j][r] = 0;                                                           \
+                    }                                                                               \
+            }                                                                                       \
+        }                                                                                           \
+        Q27X_ST(N0, N1, N2, N3, N4, N5, (s_ + 1) & 1)                                               \
+        Q27X_LD(N0, N1, N2, N3, N4, N5, s_ + 3 < nsteps ? s_ + 3 : 0)                               \
+        __syncthreads();                                                                            \
+    }
+    for (int s = 0; s < nsteps; s += 2) {
+        Q27X_ITER(s, rb0, rb1, rb2, rb3, rb4, rb5)        // stage s + 1 sits in the b set
+        Q27X_ITER(s + 1, ra0, ra1, ra2, ra3, ra4, ra5)    // stage s + 2 in the a set
+    }
+#undef Q27X_ITER
+#undef Q27X_LD
+#undef Q27X_ST
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (t < a.M) {
+                    float o = facc[i][j][r] * a.alpha;
+                    if (a.res) o = o + a.rs * a.res[(size_t)t * a.ldr + n];
+                    a.y[(size_t)t * a.ldy + n] = o;
+                }
+            }
+        }
+}
+
 // Weights: per-64 mirror -> per-(row, group) codes and scales; one 256-thread block per row.
 // In place when wg == w (each element is read and written by the same thread).
 __global__ __launch_bounds__(256) void k_i8g64_to_grp(const int8_t* w, const float* s64, int K, int gs,
@@ -303,7 +446,11 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
     // measured 1-8% slower). Token tiles of 256 (8 waves, one block per CU, a 5-stage ring) from
     // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
     // two blocks per CU, a 4-stage ring, or 3 when 17+ groups' scales take the room).
-    if (M >= 512) {
+    if (M >= 512 && K % 256 == 0 && gs % 128 == 0) {
+        const unsigned mt = (unsigned)((M + 255) / 256);
+        const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);
+        hipLaunchKernelGGL(k_gemm_i8g_rs, dim3((unsigned)(N / kGN) * mt), dim3(512), scl, (hipStream_t)s, a);
+    } else if (M >= 512) {
         const unsigned mt = (unsigned)((M + 255) / 256);
         const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);
         hipLaunchKernelGGL((k_gemm_i8g<256, 5>), dim3((unsigned)(N / kGN) * mt), dim3(512), scl, (hipStream_t)s, a);
