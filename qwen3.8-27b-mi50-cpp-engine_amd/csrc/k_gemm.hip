@@ -205,7 +205,8 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
 // The same GEMM for 256-token tiles with register-staged loads and 128-byte stages: each thread
 // moves six 16-byte chunks per stage with plain vector loads, issued three stages ahead into two
 // register sets, and writes them to a double-buffered LDS stage one iteration before the
-// multiply; 16 MFMAs per wave between barriers. The loop is unrolled by two so the register sets
+// multiply; 16 MFMAs per wave between barriers, each 32-byte slice's operands read from LDS
+// while the previous slice multiplies. The loop is unrolled by two so the register sets
 // are named at compile time; nsteps (K / 128) must be even. Rows are 128 bytes, chunk c of row R
 // in slot c ^ ((R >> 1) & 7) (the 16 rows one operand read serves fill a 256-byte bank window).
 // Same fold and tile order as k_gemm_i8g.
@@ -286,19 +287,26 @@ __global__ __launch_bounds__(512) void k_gemm_i8g_rs(GemmArgs a) {
     {                                                                                               \
         const int s_ = (S_);                                                                        \
         const int8_t* st = sR + (s_ & 1) * kStage;                                                  \
+        v4i av[2][2], bv[2][2];                                                                     \
+_Pragma("unroll")                                                                                   \
+        for (int i = 0; i < 2; ++i) av[0][i] = *(const v4i*)(st + (arow + 32 * i) * KB + ((kh ^ swa) << 4)); \
+_Pragma("unroll")                                                                                   \
+        for (int j = 0; j < 2; ++j) bv[0][j] = *(const v4i*)(st + (BM + brow + 32 * j) * KB + ((kh ^ swb) << 4)); \
 _Pragma("unroll")                                                                                   \
         for (int kk = 0; kk < KB / 32; ++kk) {                                                      \
-            const int c = 2 * kk + kh;                                                              \
-            v4i av[2], bv[2];                                                                       \
+            const int cu = kk & 1, nx = cu ^ 1;                                                     \
+            if (kk + 1 < KB / 32) {                                                                 \
+                const int c = 2 * (kk + 1) + kh;                                                    \
 _Pragma("unroll")                                                                                   \
-            for (int i = 0; i < 2; ++i) av[i] = *(const v4i*)(st + (arow + 32 * i) * KB + ((c ^ swa) << 4)); \
+                for (int i = 0; i < 2; ++i) av[nx][i] = *(const v4i*)(st + (arow + 32 * i) * KB + ((c ^ swa) << 4)); \
 _Pragma("unroll")                                                                                   \
-            for (int j = 0; j < 2; ++j) bv[j] = *(const v4i*)(st + (BM + brow + 32 * j) * KB + ((c ^ swb) << 4)); \
+                for (int j = 0; j < 2; ++j) bv[nx][j] = *(const v4i*)(st + (BM + brow + 32 * j) * KB + ((c ^ swb) << 4)); \
+            }                                                                                       \
 _Pragma("unroll")                                                                                   \
             for (int i = 0; i < 2; ++i)                                                             \
 _Pragma("unroll")                                                                                   \
                 for (int j = 0; j < 2; ++j)                                                         \
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0); \
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[cu][i], bv[cu][j], acc[i][j], 0, 0, 0); \
         }                                                                                           \
         if ((s_ + 1) % spg == 0) {                                                                  \
             const int g = (s_ + 1) / spg - 1;                                                       \
