@@ -54,8 +54,10 @@ def oracle_gemm(O, w, sw, x, sx, gs, alpha, res=None, rs=0.0):
     (300, 384, 5120, 5120, True),      # one group over the whole K (per-token scales)
     (130, 256, 17408, 1024, False),    # down's K: 17 groups
     (257, 128, 6144, 1024, True),      # out_proj's K
-    (600, 256, 5120, 1024, True),      # 256-token tiles, ragged last tile
-    (1024, 384, 17408, 1024, False),   # 256-token tiles, 17 groups
+    (600, 256, 5120, 1024, True),      # 256-token tiles (register-staged), ragged last tile
+    (1024, 384, 17408, 1024, False),   # 256-token tiles (register-staged), 17 groups
+    (520, 128, 1152, 1152, True),      # 256-token tiles, K % 256 != 0: the LDS-DMA ring
+    (777, 256, 3200, 640, False),      # 256-token tiles, K % 256 != 0, 5 groups of 640
 ])
 def test_gemm_i8g(gpu, O, M, N, K, gs, with_res):
     rng = np.random.default_rng(0x51E70400 + M + N + K)
