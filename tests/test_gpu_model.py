@@ -57,6 +57,23 @@ def test_tiny_spec_rounds_match_oracle(tiny_pair):
         assert a == b, f"round {r}: gpu {a} oracle {b}"
 
 
+def test_tiny_k7_rounds_match_oracle(gpu, O):
+    # the widest chain (K = 7: 8 verify rows through every layer, the 8-row projection and
+    # attention forms), round by round against the oracle
+    X = gpu
+    cfg = tiny(X, spec_k=7)
+    eng = X.Engine(cfg, SEED)
+    om = O.Model(cfg, SEED)
+    p = prompt_of(cfg, 33, seed=11)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(10):
+        a = eng.spec_round()
+        b = om.spec_round()
+        assert a == b, f"round {r}: gpu {a} oracle {b}"
+    eng.close()
+    om.close()
+
+
 @pytest.mark.parametrize("inter", [5120, 6144])
 def test_tiny_split_swiglu_units_match_oracle(gpu, O, inter):
     """gate|up with more 32-row SwiGLU units than blocks (one block per CU): 320 units leave 64
