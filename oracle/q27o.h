@@ -21,6 +21,10 @@
  * sequences are reproducible bit for bit. Their accuracy against libm is pinned by tests.
  *
  * parity pinning: see tests/test_oracle_*.py (closed forms, fp64 brute force, invariants).
+ * parity unpinned: the composition of the MTP draft layer inside q27o_model_spec_round (the order
+ * of the fc halves, the layer's own KV cache and the draft hand-off; src/q27_main.cpp:2551-2618,
+ * 7346-7411). Its operators are pinned one by one, but the reference's only check of the
+ * composed layer needs the real checkpoint. Draft tokens never change committed tokens.
  */
 #ifndef Q27O_H
 #define Q27O_H
