@@ -191,6 +191,13 @@ int q27x_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, 
                     int d, uint16_t* out, int out_stride, int8_t* xq, float* xs,
                     int nr, q27x_stream_t s);
 
+/* R12 commit without new rows: apply the npend pending rows that the last q27x_gdn_verify call
+ * left in `pend` (the accepted prefix) to S and conv_hist, leaving nothing pending (the next
+ * q27x_gdn_verify passes npend = 0). Replaces the snapshot-bank restore of the reference's round
+ * tail (src/q27_main.cpp:2933-2941) for callers that need the committed state materialised. */
+int q27x_gdn_commit(float* S, uint16_t* conv_hist, void* pend, int npend, int kh, int vh, int d,
+                    q27x_stream_t s);
+
 /* R14 attention prep for nr consecutive positions pos0..pos0+nr-1 (replaces
  * q27_attn_prep_tp_nr, include/q27_nr.h:84-86; math at src/q27_attn.hip:156-253):
  * per head RMSNorm(1+w) over head_dim, rotate-half RoPE on the first rot dims using the
@@ -247,7 +254,8 @@ typedef struct q27x_config {
     int kv_group;        /* 32: fp32 scale per 32 KV elements */
     float rms_eps;       /* 1e-6 */
     int head_double_residual; /* 1: final-norm input bf16(bf16(r1)+r2) as the reference */
-    int mtp_swap;        /* Q27_MTP_SWAP (0: embedding half first) */
+    int mtp_swap;        /* Q27_MTP_SWAP (1, the reference default, src/q27_main.cpp:3367: the
+                            embedding half first, src/q27_mtp_defs.h:94-95; 0: the hidden half first) */
     int mtp_plus_one;    /* Q27_MTP_PO (1) */
     int spec;            /* Q27_SPEC: 1 = speculative decode */
     int spec_k;          /* Q27_SPEC_K: drafts per round, [1, 7] */
@@ -263,6 +271,10 @@ typedef struct q27x_stats {
     long long acc_hist[9];     /* rounds with >= j accepted drafts, j = 0..8 */
     double decode_ms;          /* wall clock of the decode loop (no load, no prefill) */
     double prefill_ms;
+    /* per-round phases summed over the rounds (Q27_SPEC_T, src/q27_main.cpp:6731-6733), from
+     * device clock stamps: draft (round start to the last draft's argmax), verify layers (to the
+     * head norm), head (final norm, lm_head, argmax), tail (acceptance, rollback, hand-off) */
+    double draft_ms, verify_ms, head_ms, tail_ms;
 } q27x_stats;
 
 typedef struct q27x_ctx q27x_ctx;
@@ -293,15 +305,30 @@ int q27x_prefill(q27x_ctx* ctx, const int32_t* ids, int n, int32_t* first_token)
 int q27x_decode_step(q27x_ctx* ctx, int32_t* out_token);
 /* One chained-MTP speculative round (spec_round, src/q27_main.cpp:2702-2958): K drafts, an
  * NR = K+1 row verify, greedy acceptance, rollback and hand-off, all on the device. Returns the
- * committed tokens (ncommit = nacc+1 <= K+1). */
+ * committed tokens (ncommit = nacc+1 <= K+1). As in the reference's decode loop (6391), a round runs
+ * only while pos + K < ctx; closer to the end of the context this call takes one plain step
+ * (ncommit = 1), and at pos == ctx it returns Q27X_E_RANGE. */
 int q27x_spec_round(q27x_ctx* ctx, int32_t* out_tokens, int* ncommit);
+/* R2 MTP draft layer on its own (mtp_pass_nr, src/q27_main.cpp:2551-2618; single-row twin
+ * mtp_draft_step 7346-7411): nr (1..8) rows of (hidden row, token) at draft positions
+ * dpos0 .. dpos0+nr-1 of the MTP layer's own KV cache (written by the call): fc over
+ * [norm(emb) | norm(h)], the full-attention decoder layer, and for head_row >= 0 mtp.norm + the
+ * shared lm_head + argmax of that row. Device buffers: hrows [nr][hidden] bf16, toks [nr] int32;
+ * res [nr][hidden] bf16 receives the layer's residual rows (nullable), token one int32 (nullable).
+ * Ordered after prior work on stream s, and later work on s waits for it. Uses the context's
+ * scratch: not concurrent with other calls on the same context. */
+int q27x_mtp_draft(q27x_ctx* ctx, const uint16_t* hrows, const int32_t* toks, int nr, int dpos0,
+                   int head_row, uint16_t* res, int32_t* token, q27x_stream_t s);
 /* Forced-acceptance mode: drafts are taken from this token stream (the trunk's own greedy
  * continuation, positions after the prompt) instead of the MTP argmax; the draft and verify work
  * is unchanged. n = 0 switches it off. */
 int q27x_set_forced_drafts(q27x_ctx* ctx, const int32_t* toks, int n);
 /* Decode loop (src/q27_main.cpp:6382-6696): after q27x_prefill, generate until max_new tokens
- * are committed (including the first token from prefill). spec = 1 runs speculative rounds
- * (with the device-side graph and a one-round-lagged host mailbox), 0 plain steps. */
+ * are committed (including the first token from prefill) or the context is full. spec = 1 runs
+ * speculative rounds (with the device-side graph and a one-round-lagged host mailbox) while
+ * pos + K < ctx and plain steps after that (6391); spec = 0 plain steps. out receives the first
+ * min(committed, max_new) tokens of the request (a round may commit past max_new; those tokens
+ * are kept and a later call continues after them). */
 int q27x_generate(q27x_ctx* ctx, int max_new, int spec, int32_t* out, int* n_out,
                   q27x_stats* st);
 /* Exactly n speculative rounds (spec = 1) or plain steps (spec = 0) from the current state, launched

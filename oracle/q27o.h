@@ -20,11 +20,12 @@
  * polynomial, basic IEEE operations only), used identically on the device, so that greedy token
  * sequences are reproducible bit for bit. Their accuracy against libm is pinned by tests.
  *
- * parity pinning: see tests/test_oracle_*.py (closed forms, fp64 brute force, invariants).
- * parity unpinned: the composition of the MTP draft layer inside q27o_model_spec_round (the order
- * of the fc halves, the layer's own KV cache and the draft hand-off; src/q27_main.cpp:2551-2618,
- * 7346-7411). Its operators are pinned one by one, but the reference's only check of the
- * composed layer needs the real checkpoint. Draft tokens never change committed tokens.
+ * parity pinning: see tests/test_oracle_*.py (closed forms, fp64 brute force, invariants). The
+ * MTP draft layer's composition (src/q27_main.cpp:2551-2618: fc halves, the decoder layer on its
+ * own KV cache, the four bf16-rounded down slices, mtp.norm + lm_head) is pinned against a float64
+ * forward written from its definition, with planted composition mistakes shown to fail
+ * (tests/test_oracle_mtp.py); the draft hand-off by spec == plain greedy under forced drafts with
+ * planted wrong tokens (tests/test_oracle_model.py).
  */
 #ifndef Q27O_H
 #define Q27O_H
@@ -135,6 +136,10 @@ int  q27o_model_prefill(q27o_model* m, const int32_t* ids, int n);          /* r
 int  q27o_model_decode_step(q27o_model* m);                                 /* returns token */
 int  q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced); /* ncommit */
 int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx);
+/* one MTP pass (mtp_pass_nr, src/q27_main.cpp:2551-2618) over nr rows at draft positions dpos0..;
+ * res [nr][H] bf16 out, logits [vocab] of head_row (may be NULL); returns the head row's argmax */
+int  q27o_model_mtp_pass(q27o_model* m, int nr, const uint16_t* hrows, const int32_t* toks, int dpos0,
+                         int head_row, uint16_t* res, float* logits);
 double q27o_model_weight_bytes(const q27o_model* m);
 /* access to named tensors / buffers for the tests */
 void* q27o_model_tensor(q27o_model* m, const char* name, int layer, size_t* bytes);

@@ -58,6 +58,7 @@ _SIGS = {
     "q27o_model_reset": ([VP], None), "q27o_model_prefill": ([VP, VP, I], I),
     "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
     "q27o_model_verify_rows": ([VP, I, VP, VP], I),
+    "q27o_model_mtp_pass": ([VP, I, VP, VP, I, I, VP, VP], I),
     "q27o_model_weight_bytes": ([VP], D),
     "q27o_model_tensor": ([VP, ctypes.c_char_p, I, VP], VP),
 }
@@ -121,6 +122,24 @@ class Model:
         f = None if forced is None else np.ascontiguousarray(forced, dtype=np.int32)
         n = lib().q27o_model_spec_round(self.m, out.ctypes.data, ptr(f))
         return out[:n].tolist()
+
+    def verify_rows(self, toks):
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        nx = np.zeros(8, np.int32)
+        lib().q27o_model_verify_rows(self.m, len(toks), toks.ctypes.data, nx.ctypes.data)
+        return nx[: len(toks)].tolist()
+
+    def mtp_pass(self, hrows, toks, dpos0, head_row):
+        """One MTP pass over rows (hrows [nr][H] bf16 bits, toks [nr]) at draft positions
+        dpos0..; returns (argmax of head_row, residual rows [nr][H] bf16, head-row logits)."""
+        hrows = np.ascontiguousarray(hrows, dtype=np.uint16)
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        nr = len(toks)
+        res = np.zeros((nr, self.cfg.hidden), np.uint16)
+        logits = np.zeros(self.cfg.vocab, np.float32)
+        t = lib().q27o_model_mtp_pass(self.m, nr, hrows.ctypes.data, toks.ctypes.data, dpos0, head_row,
+                                      res.ctypes.data, logits.ctypes.data)
+        return t, res, logits
 
     def tensor(self, name, layer, dtype):
         nb = ctypes.c_size_t(0)

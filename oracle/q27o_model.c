@@ -15,7 +15,7 @@ enum {
     T_IN_QKV = 10, T_IN_Z = 11, T_IN_A = 12, T_IN_B = 13, T_A_LOG = 14, T_DT_BIAS = 15,
     T_GDN_NORM = 16, T_CONV_W = 17, T_OUT_PROJ = 18,
     T_Q = 20, T_K = 21, T_V = 22, T_Q_NORM = 23, T_K_NORM = 24, T_O = 25,
-    T_GATE = 30, T_UP = 31, T_DOWN = 32,
+    T_GATE = 30, T_UP = 31, T_DOWN = 32, T_DOWN_S0 = 33,   /* MTP down slices: 33..36 */
     T_EMB = 40, T_FINAL_NORM = 41, T_LM_HEAD = 42,
     T_PRE_EMB = 50, T_PRE_HID = 51, T_FC0 = 52, T_FC1 = 53, T_MTP_NORM = 54
 };
@@ -36,6 +36,7 @@ typedef struct {
     i8m o;
     /* MLP */
     i8m gate, up, down;
+    i8m down4[4];            /* MTP layer only: down as four column slices (src/q27_main.cpp:2605-2612) */
     /* state */
     int8_t *kc, *vc; float *ks, *vs;
     float* S; uint16_t* conv_hist; void* pend;
@@ -56,6 +57,10 @@ struct q27o_model {
     uint16_t *hprev, *hcatch;     /* [H], [8][H] */
     uint16_t* hfinal;             /* [rows][H] last verify's final residual rows */
     uint16_t* hchain;             /* [H] */
+    /* the last round's drafts (dt: what the verify saw; dt_raw: the MTP argmax before any forced
+     * replacement), verify argmaxes and acceptance */
+    int32_t dt[8], dt_raw[8], nx[8];
+    int nacc_last;
     double wbytes;
 };
 
@@ -115,13 +120,19 @@ static void gen_attn(q27o_model* m, layer_t* Y, int code) {
     Y->ks = (float*)calloc(kvn / c->kv_group, 4); Y->vs = (float*)calloc(kvn / c->kv_group, 4);
     m->wbytes += (double)(qr + 2 * kvr) * H * (1.0 + 4.0 / 64) + (double)H * c->n_q * c->head_dim * (1.0 + 4.0 / 64);
 }
-static void gen_mlp(q27o_model* m, layer_t* Y, int code) {
+/* slices: 0 = one down matrix [H][I] (trunk layers); 4 = four [H][I/4] column slices, each its
+ * own per-64-scaled tensor (the MTP layer, whose reference checkpoint stores mtp down as four
+ * K = 4352 tensors, src/q27_main.cpp:2605-2612) */
+static void gen_mlp(q27o_model* m, layer_t* Y, int code, int slices) {
     const q27o_cfg* c = &m->c;
     Y->in_norm = gen_bf16(m->seed, tid(code, T_IN_NORM), c->hidden, 0.02f, 0.0f);
     Y->post_norm = gen_bf16(m->seed, tid(code, T_POST_NORM), c->hidden, 0.02f, 0.0f);
     Y->gate = gen_i8(m->seed, tid(code, T_GATE), c->inter, c->hidden);
     Y->up = gen_i8(m->seed, tid(code, T_UP), c->inter, c->hidden);
-    Y->down = gen_i8(m->seed, tid(code, T_DOWN), c->hidden, c->inter);
+    if (slices)
+        for (int j = 0; j < 4; ++j) Y->down4[j] = gen_i8(m->seed, tid(code, T_DOWN_S0 + j), c->hidden, c->inter / 4);
+    else
+        Y->down = gen_i8(m->seed, tid(code, T_DOWN), c->hidden, c->inter);
     m->wbytes += 3.0 * c->inter * c->hidden * (1.0 + 4.0 / 64) + 4.0 * c->hidden;
 }
 
@@ -135,7 +146,7 @@ q27o_model* q27o_model_create(const q27o_cfg* c, uint64_t seed) {
         layer_t* Y = &m->L[L];
         const int code = L + 1;
         Y->is_attn = is_attn_layer(c, L);
-        gen_mlp(m, Y, code);
+        gen_mlp(m, Y, code, 0);
         if (Y->is_attn) { gen_attn(m, Y, code); continue; }
         Y->qkvz = alloc_i8(nqkv + nz, H);
         gen_i8_into(seed, tid(code, T_IN_QKV), nqkv, H, Y->qkvz.w, Y->qkvz.s);
@@ -154,7 +165,7 @@ q27o_model* q27o_model_create(const q27o_cfg* c, uint64_t seed) {
                      2.0 * 2 * c->gdn_vh * H + 2.0 * 4 * nqkv + 2.0 * (2 * c->gdn_vh + D);
     }
     /* MTP layer: a full-attention decoder layer (src/q27_mtp_defs.h:22-33) */
-    gen_mlp(m, &m->mtp, 1000);
+    gen_mlp(m, &m->mtp, 1000, 1);
     m->mtp.is_attn = 1;
     gen_attn(m, &m->mtp, 1000);
     m->pre_emb = gen_bf16(seed, tid(1000, T_PRE_EMB), H, 0.02f, 0.0f);
@@ -181,6 +192,7 @@ q27o_model* q27o_model_create(const q27o_cfg* c, uint64_t seed) {
 static void free_layer(layer_t* Y) {
     free(Y->in_norm); free(Y->post_norm);
     free_i8(&Y->gate); free_i8(&Y->up); free_i8(&Y->down);
+    for (int j = 0; j < 4; ++j) free_i8(&Y->down4[j]);
     if (Y->is_attn) {
         free_i8(&Y->qkv); free(Y->q_norm); free(Y->k_norm); free_i8(&Y->o);
         free(Y->kc); free(Y->vc); free(Y->ks); free(Y->vs);
@@ -306,7 +318,7 @@ static void verify(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
  * draft positions dpos0 + r. Leaves the layer's residual rows in res (bf16 [nr][H]); returns the
  * head row's argmax (head_row >= 0) or -1. */
 static int mtp_pass(q27o_model* m, int nr, const uint16_t* const* hrows, const int32_t* toks,
-                    int dpos0, int head_row, uint16_t* res) {
+                    int dpos0, int head_row, uint16_t* res, float* logits_out) {
     const q27o_cfg* c = &m->c;
     layer_t* Y = &m->mtp;
     const int H = c->hidden, I = c->inter;
@@ -356,19 +368,23 @@ static int mtp_pass(q27o_model* m, int nr, const uint16_t* const* hrows, const i
     q27o_proj_rows(Y->gate.w, Y->gate.s, 1.0f, I, H, xa, H, sa, f0, I, nr);
     q27o_proj_rows(Y->up.w, Y->up.s, 1.0f, I, H, xa, H, sa, f1, I, nr);
     q27o_swiglu_quant_rows(f0, f1, I, xa, sa, I, 1.0f, nr);
-    /* down: one K = inter projection added into the bf16 residual (the reference runs it as four
-     * K = 4352 NVFP4 slices, src/q27_main.cpp:2606-2612, a consequence of its kernel shapes) */
-    q27o_proj_rows_epi(Y->down.w, Y->down.s, 1.0f, H, I, xa, I, sa, res, H, 1, res, 1, H, 1.0f, nr);
+    /* down as four K = inter/4 column slices, each projected on its own and added into the bf16
+     * residual, which is rounded to bf16 after every slice (src/q27_main.cpp:2605-2612:
+     * q27_proj_nvfp4_down_nrs into fp32 pd, then q27_add_inplace(nrm, pd) per slice) */
+    const int I4 = I / 4;
+    for (int j = 0; j < 4; ++j)
+        q27o_proj_rows_epi(Y->down4[j].w, Y->down4[j].s, 1.0f, H, I4, xa + (size_t)j * I4, I,
+                           sa + (size_t)j * (I4 / 16), res, H, 1, res, 1, H, 1.0f, nr);
     int tok = -1;
     if (head_row >= 0) {
         q27o_rmsnorm_quant_rows(res + (size_t)head_row * H, 1, H, m->mtp_norm, 1.0f, c->rms_eps, H, NULL, t1, H,
                                 NULL, NULL, 1, 1.0f, 1);
-        float* logits = (float*)malloc((size_t)c->vocab * 4);
+        float* logits = logits_out ? logits_out : (float*)malloc((size_t)c->vocab * 4);
         q27o_bf16_gemv_rows(m->lm_head, c->vocab, H, t1, H, logits, c->vocab, 1);
         int32_t ix; float vv;
         q27o_argmax_rows(logits, c->vocab, c->vocab, 1, &ix, &vv);
         tok = ix;
-        free(logits);
+        if (!logits_out) free(logits);
     }
     free(cat); free(t1); free(xa); free(sa); free(f0); free(f1); free(pb); free(qh); free(ao);
     return tok;
@@ -398,7 +414,7 @@ int q27o_model_prefill(q27o_model* m, const int32_t* ids, int n) {
         const int cn = (n - 1 - p0 < 8) ? n - 1 - p0 : 8;
         const uint16_t* hr[8];
         for (int r = 0; r < cn; ++r) hr[r] = hall + (size_t)(p0 + r) * H;
-        mtp_pass(m, cn, hr, ids + p0 + 1, p0, -1, res);
+        mtp_pass(m, cn, hr, ids + p0 + 1, p0, -1, res, NULL);
     }
     free(res);
     memcpy(m->hprev, hall + (size_t)(n - 1) * H, (size_t)H * 2);
@@ -416,6 +432,18 @@ int q27o_model_decode_step(q27o_model* m) {
     m->pos += 1;
     m->tok = nx;
     return nx;
+}
+
+/* One MTP pass on its own (the kernel-tier q27x_mtp_draft): nr rows (hidden rows hrows [nr][H]
+ * bf16, tokens toks) at draft positions dpos0.. of the layer's KV cache; writes the layer's
+ * residual rows res [nr][H] bf16 and, for head_row >= 0, that row's logits [vocab] fp32; returns
+ * the head row's argmax (or -1). */
+int q27o_model_mtp_pass(q27o_model* m, int nr, const uint16_t* hrows, const int32_t* toks, int dpos0,
+                        int head_row, uint16_t* res, float* logits) {
+    const uint16_t* hr[8];
+    if (nr < 1 || nr > 8) return -2;
+    for (int r = 0; r < nr; ++r) hr[r] = hrows + (size_t)r * m->c.hidden;
+    return mtp_pass(m, nr, hr, toks, dpos0, head_row, res, logits);
 }
 
 int q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
@@ -436,7 +464,8 @@ int q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced) {
         for (int cc = 0; cc < m->ncatch; ++cc) { hr[nrm] = m->hcatch + (size_t)cc * H; tk[nrm] = m->catch_tok[cc]; ++nrm; }
         hr[nrm] = m->hprev; tk[nrm] = m->tok; ++nrm;
         const int dpos0 = m->pos - 1 - m->ncatch;
-        int d0 = mtp_pass(m, nrm, hr, tk, dpos0, nrm - 1, res);
+        int d0 = mtp_pass(m, nrm, hr, tk, dpos0, nrm - 1, res, NULL);
+        m->dt_raw[0] = d0;
         if (forced) d0 = forced[0];
         dt[0] = d0;
         memcpy(m->hchain, res + (size_t)(nrm - 1) * H, (size_t)H * 2);
@@ -445,7 +474,8 @@ int q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced) {
     for (int j = 1; j < K; ++j) {
         const uint16_t* hr[1] = { m->hchain };
         const int32_t tk[1] = { dt[j - 1] };
-        int dj = mtp_pass(m, 1, hr, tk, m->pos - 1 + j, 0, res);
+        int dj = mtp_pass(m, 1, hr, tk, m->pos - 1 + j, 0, res, NULL);
+        m->dt_raw[j] = dj;
         if (forced) dj = forced[j];
         dt[j] = dj;
         memcpy(m->hchain, res, (size_t)H * 2);
@@ -456,6 +486,12 @@ int q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced) {
     verify(m, K + 1, toks, nx);
     /* [3] greedy acceptance; [4] rollback = commit only rows 0..nacc; hand-off */
     const int nacc = q27o_accept(nx, dt, K, out);
+    for (int j = 0; j < 8; ++j) {
+        m->dt[j] = j < K ? dt[j] : 0;
+        m->nx[j] = j <= K ? nx[j] : 0;
+        if (j >= K) m->dt_raw[j] = 0;
+    }
+    m->nacc_last = nacc;
     m->gdn_npend = nacc + 1;
     for (int j = 0; j < nacc; ++j) {
         memcpy(m->hcatch + (size_t)j * H, m->hfinal + (size_t)j * H, (size_t)H * 2);
@@ -485,8 +521,44 @@ void* q27o_model_tensor(q27o_model* m, const char* name, int layer, size_t* byte
     else if (!strcmp(name, "gate_w")) { p = Y->gate.w; b = (size_t)c->inter * H; }
     else if (!strcmp(name, "gate_s")) { p = Y->gate.s; b = (size_t)c->inter * (H / 64) * 4; }
     else if (!strcmp(name, "conv_w") && !Y->is_attn) { p = Y->conv_w; b = (size_t)nqkv * 4 * 2; }
+    else if (!strcmp(name, "ks") && Y->is_attn) { p = Y->ks; b = (size_t)c->ctx * c->n_kv * c->head_dim / c->kv_group * 4; }
+    else if (!strcmp(name, "vc") && Y->is_attn) { p = Y->vc; b = (size_t)c->ctx * c->n_kv * c->head_dim; }
+    else if (!strcmp(name, "vs") && Y->is_attn) { p = Y->vs; b = (size_t)c->ctx * c->n_kv * c->head_dim / c->kv_group * 4; }
+    else if (!strcmp(name, "hcatch")) { p = m->hcatch; b = (size_t)8 * H * 2; }
+    else if (!strcmp(name, "hchain")) { p = m->hchain; b = (size_t)H * 2; }
+    else if (!strcmp(name, "dt")) { p = m->dt; b = 8 * 4; }
+    else if (!strcmp(name, "dt_raw")) { p = m->dt_raw; b = 8 * 4; }
+    else if (!strcmp(name, "nx")) { p = m->nx; b = 8 * 4; }
+    else if (!strcmp(name, "catch_tok")) { p = m->catch_tok; b = 8 * 4; }
     else if (!strcmp(name, "pos")) { static int v; v = m->pos; p = &v; b = 4; }
     else if (!strcmp(name, "tok")) { static int v2; v2 = m->tok; p = &v2; b = 4; }
+    else if (!strcmp(name, "ncatch")) { static int v3; v3 = m->ncatch; p = &v3; b = 4; }
+    else if (!strcmp(name, "nacc")) { static int v4; v4 = m->nacc_last; p = &v4; b = 4; }
+    /* weights of a layer (layer < 0: the MTP layer) and the MTP globals, for float64 forwards */
+    else if (!strcmp(name, "in_norm")) { p = Y->in_norm; b = (size_t)H * 2; }
+    else if (!strcmp(name, "post_norm")) { p = Y->post_norm; b = (size_t)H * 2; }
+    else if (!strcmp(name, "up_w")) { p = Y->up.w; b = (size_t)c->inter * H; }
+    else if (!strcmp(name, "up_s")) { p = Y->up.s; b = (size_t)c->inter * (H / 64) * 4; }
+    else if (!strcmp(name, "down_w") && Y->down.w) { p = Y->down.w; b = (size_t)H * c->inter; }
+    else if (!strcmp(name, "down_s") && Y->down.s) { p = Y->down.s; b = (size_t)H * (c->inter / 64) * 4; }
+    else if (!strncmp(name, "down4_w", 7) && Y->down4[0].w) {
+        const int j = name[7] - '0'; if (j >= 0 && j < 4) { p = Y->down4[j].w; b = (size_t)H * (c->inter / 4); } }
+    else if (!strncmp(name, "down4_s", 7) && Y->down4[0].s) {
+        const int j = name[7] - '0'; if (j >= 0 && j < 4) { p = Y->down4[j].s; b = (size_t)H * (c->inter / 256) * 4; } }
+    else if (!strcmp(name, "qkv_w") && Y->is_attn) { p = Y->qkv.w; b = (size_t)Y->qkv.rows * H; }
+    else if (!strcmp(name, "qkv_s") && Y->is_attn) { p = Y->qkv.s; b = (size_t)Y->qkv.rows * (H / 64) * 4; }
+    else if (!strcmp(name, "q_norm") && Y->is_attn) { p = Y->q_norm; b = (size_t)c->head_dim * 2; }
+    else if (!strcmp(name, "k_norm") && Y->is_attn) { p = Y->k_norm; b = (size_t)c->head_dim * 2; }
+    else if (!strcmp(name, "o_w") && Y->is_attn) { p = Y->o.w; b = (size_t)H * Y->o.K; }
+    else if (!strcmp(name, "o_s") && Y->is_attn) { p = Y->o.s; b = (size_t)H * (Y->o.K / 64) * 4; }
+    else if (!strcmp(name, "fc0_w")) { p = m->fc0.w; b = (size_t)H * H; }
+    else if (!strcmp(name, "fc0_s")) { p = m->fc0.s; b = (size_t)H * (H / 64) * 4; }
+    else if (!strcmp(name, "fc1_w")) { p = m->fc1.w; b = (size_t)H * H; }
+    else if (!strcmp(name, "fc1_s")) { p = m->fc1.s; b = (size_t)H * (H / 64) * 4; }
+    else if (!strcmp(name, "pre_emb")) { p = m->pre_emb; b = (size_t)H * 2; }
+    else if (!strcmp(name, "pre_hid")) { p = m->pre_hid; b = (size_t)H * 2; }
+    else if (!strcmp(name, "mtp_norm")) { p = m->mtp_norm; b = (size_t)H * 2; }
+    else if (!strcmp(name, "final_norm")) { p = m->final_norm; b = (size_t)H * 2; }
     if (bytes) *bytes = b;
     return p;
 }

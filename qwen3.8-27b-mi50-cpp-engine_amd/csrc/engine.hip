@@ -28,7 +28,7 @@ enum {
     T_IN_QKV = 10, T_IN_Z = 11, T_IN_A = 12, T_IN_B = 13, T_A_LOG = 14, T_DT_BIAS = 15,
     T_GDN_NORM = 16, T_CONV_W = 17, T_OUT_PROJ = 18,
     T_Q = 20, T_K = 21, T_V = 22, T_Q_NORM = 23, T_K_NORM = 24, T_O = 25,
-    T_GATE = 30, T_UP = 31, T_DOWN = 32,
+    T_GATE = 30, T_UP = 31, T_DOWN = 32, T_DOWN_S0 = 33,   // MTP down slices: 33..36
     T_EMB = 40, T_FINAL_NORM = 41, T_LM_HEAD = 42,
     T_PRE_EMB = 50, T_PRE_HID = 51, T_FC0 = 52, T_FC1 = 53, T_MTP_NORM = 54
 };
@@ -43,6 +43,7 @@ struct LayerDev {
     uint16_t *gdn_norm = nullptr, *conv_w = nullptr; Mat out_proj;
     Mat qkv; uint16_t *q_norm = nullptr, *k_norm = nullptr; Mat o;
     Mat gu, down;
+    Mat down4[4];   // MTP layer: down as four column slices of I/4 (src/q27_main.cpp:2605-2612)
     int8_t *kc = nullptr, *vc = nullptr; float *ks = nullptr, *vs = nullptr;
     float* S = nullptr; uint16_t* conv_hist = nullptr; void* pend = nullptr;
 };
@@ -53,6 +54,7 @@ struct Dctl {
     int catch_tok[8];
     int dt[8], nx[8];
     float nxval[8];
+    int dt_raw[8];      // the MTP argmax of each draft, before a forced replacement
     int vtok[8];
     int mtp_nact, mtp_dpos0, mtp_head, mtp_out;
     int mtp_tok[8];
@@ -61,6 +63,12 @@ struct Dctl {
     int nacc_last, ncommit_last, err, pad0;
     long long acc_hist[9];
     long long accepted;
+    // per-round phase timing (the reference's Q27_SPEC_T buckets, src/q27_main.cpp:2705-2707,
+    // 6731-6733), in device wall-clock ticks: stamps of the current round and running sums of
+    // draft (round start -> last draft's argmax), verify layers (-> head norm), head (-> acceptance)
+    // and tail (acceptance, rollback and hand-off)
+    unsigned long long t_begin, t_draft, t_verify, t_pad;
+    unsigned long long sp_t[4];
 };
 
 struct Mailbox { volatile int round; volatile int committed; volatile int ncommit; volatile int stop; volatile int tok[8]; };
@@ -105,6 +113,7 @@ struct q27x_ctx {
     int n_prompt = 0;
     hipGraphExec_t g_spec = nullptr, g_plain = nullptr;
     int g_spec_k = 0;
+    int wclk_khz = 0;      // device wall clock (s_memrealtime) rate
     float sl2e = 0.0f;
 };
 
@@ -135,13 +144,26 @@ __device__ __forceinline__ void copy_row(uint16_t* dst, const uint16_t* src, int
     for (int i = threadIdx.x * 8; i < H; i += blockDim.x * 8) *(uint4*)(dst + i) = *(const uint4*)(src + i);
 }
 // draft 0 rows: the catch-up rows then (h_prev, tok) (src/q27_main.cpp:2737-2744)
+// A round writes positions pos .. pos + K: it needs pos + K < ctx, the reference's condition for a
+// speculative round (src/q27_main.cpp:6391). The host never launches one past it; if it happens
+// anyway the round raises the device error, stops, and tells the host through the mailbox.
+__device__ __forceinline__ void raise_range(Dctl* d, Mailbox* mb) {
+    d->err = 6;
+    d->stop = 1;
+    if (mb) {
+        mb->stop = 1;
+        __threadfence_system();
+        mb->round = d->rounds + 1;
+    }
+}
 __global__ __launch_bounds__(256) void k_round_begin(Dctl* d, uint16_t* mtp_hin, const uint16_t* hcatch,
-                                                     const uint16_t* hprev, int H, int K) {
+                                                     const uint16_t* hprev, Mailbox* mb, int H, int K) {
     if (d->stop) return;
-    if (d->pos + K + 1 > d->ctx) {
-        if (threadIdx.x == 0) { d->err = 6; d->stop = 1; }
+    if (d->pos + K >= d->ctx) {
+        if (threadIdx.x == 0) raise_range(d, mb);
         return;
     }
+    if (threadIdx.x == 0) d->t_begin = __builtin_amdgcn_s_memrealtime();
     const int nc = d->ncatch;
     for (int r = 0; r < nc; ++r) copy_row(mtp_hin + (size_t)r * H, hcatch + (size_t)r * H, H);
     copy_row(mtp_hin + (size_t)nc * H, hprev, H);
@@ -162,7 +184,9 @@ __global__ __launch_bounds__(256) void k_draft_post(Dctl* d, uint16_t* mtp_hin, 
     if (d->stop) return;
     __shared__ int s_tok;
     if (threadIdx.x == 0) {
+        if (j + 1 == K) d->t_draft = __builtin_amdgcn_s_memrealtime();
         int t = d->mtp_out;
+        d->dt_raw[j] = t;
         if (d->forced_on) {
             const int fi = d->pos - d->forced_base + 1 + j;
             if (fi >= 0 && fi < d->forced_n) t = forced[fi];
@@ -192,7 +216,9 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
                                                 int32_t* ring, int ring_cap, Mailbox* mb, int H, int K) {
     if (d->stop) return;
     __shared__ int s_nacc;
+    __shared__ unsigned long long s_t0;
     if (threadIdx.x == 0) {
+        s_t0 = __builtin_amdgcn_s_memrealtime();
         int nacc = 0;
         while (nacc < K && d->nx[nacc] == d->dt[nacc]) ++nacc;
         s_nacc = nacc;
@@ -202,13 +228,12 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
     for (int j = 0; j < nacc; ++j) copy_row(hcatch + (size_t)j * H, hfinal + (size_t)j * H, H);
     copy_row(hprev, hfinal + (size_t)nacc * H, H);
     if (threadIdx.x == 0) {
+        // every committed token goes to the ring (a round that passes max_new still advanced the
+        // state by ncommit positions; a later call continues after them)
         const int ncommit = nacc + 1;
         int c = d->committed;
-        int emitted = 0;
-        for (int j = 0; j < ncommit && c < d->max_new; ++j, ++emitted) {
+        for (int j = 0; j < ncommit; ++j, ++c)
             if (c < ring_cap) ring[c] = d->nx[j];
-            ++c;
-        }
         for (int j = 0; j < nacc; ++j) d->catch_tok[j] = d->nx[j];
         d->ncatch = nacc;
         d->tok = d->nx[nacc];
@@ -229,12 +254,16 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
             __threadfence_system();
             mb->round = d->rounds;
         }
+        d->sp_t[0] += d->t_draft - d->t_begin;
+        d->sp_t[1] += d->t_verify - d->t_draft;
+        d->sp_t[2] += s_t0 - d->t_verify;
+        d->sp_t[3] += __builtin_amdgcn_s_memrealtime() - s_t0;
     }
 }
 // plain greedy step bookkeeping (src/q27_main.cpp:6462-6466, 6680-6695)
-__global__ void k_plain_pre(Dctl* d) {
+__global__ void k_plain_pre(Dctl* d, Mailbox* mb) {
     if (d->stop || threadIdx.x) return;
-    if (d->pos + 1 > d->ctx) { d->err = 6; d->stop = 1; return; }
+    if (d->pos >= d->ctx) { raise_range(d, mb); return; }
     d->vtok[0] = d->tok;
 }
 __global__ __launch_bounds__(256) void k_plain_post(Dctl* d, const uint16_t* hfinal, uint16_t* hprev, int32_t* ring,
@@ -243,7 +272,7 @@ __global__ __launch_bounds__(256) void k_plain_post(Dctl* d, const uint16_t* hfi
     copy_row(hprev, hfinal, H);
     if (threadIdx.x == 0) {
         const int c = d->committed;
-        if (c < d->max_new && c < ring_cap) ring[c] = d->nx[0];
+        if (c < ring_cap) ring[c] = d->nx[0];
         d->committed = c + 1;
         d->tok = d->nx[0];
         d->pos += 1;
@@ -366,6 +395,7 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
     hn.x = x->xres; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->hid : nullptr;
     hn.hout = hout ? hout : x->hfinal; hn.w = x->final_norm; hn.plus = 1.0f; hn.eps = c.rms_eps; hn.n = H;
     hn.y = head ? x->ynorm : nullptr; hn.ystride = H; hn.in_scale = 1.0f; hn.stop = &d->stop;
+    hn.stamp = &d->t_verify;
     if ((rc = launch_norm(hn, nr, s))) return rc;
     if (head) {
         GemvArgs ga{};
@@ -440,11 +470,17 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     gu.sw_part = x->sw_part; gu.sw_cnt = x->sw_cnt;
     set_pre(gu, norm_of(x, x->mtp_res, 1, Y.post_norm, po, 1, nullptr, nullptr));
     if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
-    ProjArgs dn{};
-    dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f; dn.xq = xact; dn.xst = I;
-    dn.xs = sact; dn.y = x->mtp_res; dn.ystride = H; dn.out_bf16 = 1; dn.res = x->mtp_res; dn.res_bf16 = 1;
-    dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
-    if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
+    // down as four K = I/4 column slices, each added into the bf16 residual with its own bf16
+    // rounding (src/q27_main.cpp:2605-2612: one fp32 slice projection, then q27_add_inplace)
+    const int I4 = I / 4;
+    for (int j = 0; j < 4; ++j) {
+        ProjArgs dn{};
+        dn.W = Y.down4[j].w; dn.WS = Y.down4[j].s; dn.rows = H; dn.K = I4; dn.alpha = 1.0f;
+        dn.xq = xact + (size_t)j * I4; dn.xst = I; dn.xs = sact + (size_t)j * (I4 / 16);
+        dn.y = x->mtp_res; dn.ystride = H; dn.out_bf16 = 1; dn.res = x->mtp_res; dn.res_bf16 = 1;
+        dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
+        if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
+    }
     if (head) {
         NormArgs hn{};
         hn.x = x->mtp_res; hn.x_bf16 = 1; hn.xstride = H; hn.w = x->mtp_norm; hn.plus = 1.0f; hn.eps = c.rms_eps;
@@ -473,7 +509,8 @@ static int enqueue_spec_round(q27x_ctx* x) {
     const int K = x->c.spec_k, H = x->H;
     Dctl* d = x->dctl;
     int rc;
-    hipLaunchKernelGGL(k_round_begin, dim3(1), dim3(256), 0, x->stream, d, x->mtp_hin, x->hcatch, x->hprev, H, K);
+    hipLaunchKernelGGL(k_round_begin, dim3(1), dim3(256), 0, x->stream, d, x->mtp_hin, x->hcatch, x->hprev, x->mbox_dev,
+                       H, K);
     Q27X_HIP(hipGetLastError());
     for (int j = 0; j < K; ++j) {
         if ((rc = mtp_pass(x, j == 0 ? K + 1 : 1, 1, 0))) return rc;
@@ -487,7 +524,7 @@ static int enqueue_spec_round(q27x_ctx* x) {
     return Q27X_OK;
 }
 static int enqueue_plain_step(q27x_ctx* x) {
-    hipLaunchKernelGGL(k_plain_pre, dim3(1), dim3(64), 0, x->stream, x->dctl);
+    hipLaunchKernelGGL(k_plain_pre, dim3(1), dim3(64), 0, x->stream, x->dctl, x->mbox_dev);
     Q27X_HIP(hipGetLastError());
     int rc = verify_pass(x, 1, 1, nullptr);
     if (rc) return rc;
@@ -595,6 +632,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return fail(hip_fail(e, "hipSetDevice"));
     if ((e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking)) != hipSuccess) return fail(hip_fail(e, "hipStreamCreate"));
+    if ((e = hipDeviceGetAttribute(&x->wclk_khz, hipDeviceAttributeWallClockRate, device)) != hipSuccess) return fail(hip_fail(e, "hipDeviceGetAttribute"));
     if (int rc0 = gdn_set_lds_limit()) return fail(rc0);
     // weight arena
     const size_t H = x->H, I = x->I, V = x->V;
@@ -606,7 +644,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
         if (is_attn_layer(c, l)) { wb += i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 2 * 128 * 2 + 512; ++n_attn; }
         else wb += i8b(x->nqkv + x->nz, H) + 2 * (size_t)c.gdn_vh * H * 2 + (size_t)x->nqkv * 4 * 2 + i8b(H, x->nz) + 4096;
     }
-    wb += 2 * H * 2 + i8b(2 * I, H) + i8b(H, I) + i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 1024;   // MTP
+    wb += 2 * H * 2 + i8b(2 * I, H) + 4 * i8b(H, I / 4) + i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 4096;   // MTP
     wb += 3 * H * 2 + 2 * i8b(H, H) + 2 * V * H * 2 + H * 2 + 8192;
     x->wcap = wb;
     if ((e = hipMalloc((void**)&x->warena, wb)) != hipSuccess) return fail(hip_fail(e, "hipMalloc(weights)"));
@@ -739,13 +777,22 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     int rc;
 #define GEN(m, rows, K) if ((rc = gen_i8m(x, m, rows, K))) return rc
 #define VEC(dst, t, n, sd, mn, uni) if (!((dst) = gen_vec(x, seed, t, n, sd, mn, uni))) { set_error("weight generation"); return Q27X_E_NOMEM; }
-    auto mlp = [&](LayerDev& Y, int code) -> int {
+    // slices: 0 = one down matrix (trunk layers), 4 = four [H][I/4] column slices (the MTP layer)
+    auto mlp = [&](LayerDev& Y, int code, int slices) -> int {
         int r2;
         VEC(Y.in_norm, tid(code, T_IN_NORM), H, 0.02f, 0.0f, 0);
         VEC(Y.post_norm, tid(code, T_POST_NORM), H, 0.02f, 0.0f, 0);
         if ((r2 = gen_i8m(x, Y.gu, 2 * I, H))) return r2;
         if ((r2 = launch_gen_i8(Y.gu.w, Y.gu.s, I, H, tensor_key(seed, tid(code, T_GATE)), 1, 0, s))) return r2;
         if ((r2 = launch_gen_i8(Y.gu.w, Y.gu.s, I, H, tensor_key(seed, tid(code, T_UP)), 1, 1, s))) return r2;
+        if (slices) {
+            for (int j = 0; j < 4; ++j) {
+                if ((r2 = gen_i8m(x, Y.down4[j], H, I / 4))) return r2;
+                if ((r2 = launch_gen_i8(Y.down4[j].w, Y.down4[j].s, H, I / 4, tensor_key(seed, tid(code, T_DOWN_S0 + j)),
+                                        0, 0, s))) return r2;
+            }
+            return Q27X_OK;
+        }
         if ((r2 = gen_i8m(x, Y.down, H, I))) return r2;
         if ((r2 = launch_gen_i8(Y.down.w, Y.down.s, H, I, tensor_key(seed, tid(code, T_DOWN)), 0, 0, s))) return r2;
         return Q27X_OK;
@@ -767,7 +814,7 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     for (int l = 0; l < c.n_layers; ++l) {
         LayerDev& Y = x->L[l];
         const int code = l + 1;
-        if ((rc = mlp(Y, code))) return rc;
+        if ((rc = mlp(Y, code, 0))) return rc;
         if (Y.is_attn) { if ((rc = attn(Y, code))) return rc; continue; }
         GEN(Y.qkvz, x->nqkv + x->nz, H);
         if ((rc = launch_gen_i8(Y.qkvz.w, Y.qkvz.s, x->nqkv, H, tensor_key(seed, tid(code, T_IN_QKV)), 0, 0, s))) return rc;
@@ -782,7 +829,7 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
         GEN(Y.out_proj, H, x->nz);
         if ((rc = launch_gen_i8(Y.out_proj.w, Y.out_proj.s, H, x->nz, tensor_key(seed, tid(code, T_OUT_PROJ)), 0, 0, s))) return rc;
     }
-    if ((rc = mlp(x->mtp, 1000))) return rc;
+    if ((rc = mlp(x->mtp, 1000, 4))) return rc;
     if ((rc = attn(x->mtp, 1000))) return rc;
     VEC(x->pre_emb, tid(1000, T_PRE_EMB), H, 0.02f, 0.0f, 0);
     VEC(x->pre_hid, tid(1000, T_PRE_HID), H, 0.02f, 0.0f, 0);
@@ -882,25 +929,68 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
     return Q27X_OK;
 }
 
+// The graph of a speculative round (spec = 1) or a plain step (spec = 0), built on first use.
+static int ensure_graph(q27x_ctx* x, int spec) {
+    if (!use_graphs()) return Q27X_OK;
+    hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
+    if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
+    if (!*g) {
+        int rc = build_graph(x, spec, g);
+        if (rc) return rc;
+        if (spec) x->g_spec_k = x->c.spec_k;
+    }
+    return Q27X_OK;
+}
 static int run_step(q27x_ctx* x, int spec) {
     if (use_graphs()) {
-        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
-        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
-        if (!*g) {
-            int rc = build_graph(x, spec, g);
-            if (rc) return rc;
-            if (spec) x->g_spec_k = x->c.spec_k;
-        }
-        Q27X_HIP(hipGraphLaunch(*g, x->stream));
+        int rc = ensure_graph(x, spec);
+        if (rc) return rc;
+        Q27X_HIP(hipGraphLaunch(spec ? x->g_spec : x->g_plain, x->stream));
         return Q27X_OK;
     }
     return spec ? enqueue_spec_round(x) : enqueue_plain_step(x);
 }
 
+// Start of every decode call: wait for the stream, read the control block into h, and re-arm it
+// for a call that may commit up to max_new tokens in total. A call that reached its budget left
+// stop = 1; the next call clears it, so decode continues from the current state. A device error
+// stays set and is reported (a new prompt resets it).
+static int arm(q27x_ctx* x, int max_new, Dctl* h) {
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    Q27X_HIP(hipMemcpy(h, x->dctl, sizeof *h, hipMemcpyDeviceToHost));
+    if (h->err) return check_device_err(x);
+    const int stop = h->committed >= max_new ? 1 : 0;
+    int rc = set_ints(x, 2, DOFF(max_new), max_new, DOFF(stop), stop);
+    if (rc) return rc;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    h->max_new = max_new;
+    h->stop = stop;
+    memset((void*)x->mbox, 0, sizeof(Mailbox));   // no kernel is in flight
+    return Q27X_OK;
+}
+
+static void fill_stats(q27x_ctx* x, q27x_stats* st, const Dctl& h0, const Dctl& h, long long committed, double ms) {
+    if (!st) return;
+    memset(st, 0, sizeof *st);
+    st->rounds = h.rounds - h0.rounds;
+    st->committed = committed;
+    st->accepted = h.accepted - h0.accepted;
+    for (int j = 0; j < 9; ++j) st->acc_hist[j] = h.acc_hist[j] - h0.acc_hist[j];
+    st->decode_ms = ms;
+    const double tick_ms = x->wclk_khz > 0 ? 1.0 / x->wclk_khz : 0.0;
+    st->draft_ms = (double)(h.sp_t[0] - h0.sp_t[0]) * tick_ms;
+    st->verify_ms = (double)(h.sp_t[1] - h0.sp_t[1]) * tick_ms;
+    st->head_ms = (double)(h.sp_t[2] - h0.sp_t[2]) * tick_ms;
+    st->tail_ms = (double)(h.sp_t[3] - h0.sp_t[3]) * tick_ms;
+}
+
 int q27x_decode_step(q27x_ctx* x, int32_t* out_token) {
     if (!x || !x->prefilled) { set_error("q27x_decode_step: no prefill"); return Q27X_E_STATE; }
-    int rc = run_step(x, 0);
+    Dctl h;
+    int rc = arm(x, 0x7fffffff, &h);
     if (rc) return rc;
+    if (h.pos >= x->c.ctx) { set_error("context capacity exhausted (ctx=%d)", x->c.ctx); return Q27X_E_RANGE; }
+    if ((rc = run_step(x, 0))) return rc;
     Q27X_HIP(hipStreamSynchronize(x->stream));
     if ((rc = check_device_err(x))) return rc;
     int32_t t = 0;
@@ -909,17 +999,55 @@ int q27x_decode_step(q27x_ctx* x, int32_t* out_token) {
     return Q27X_OK;
 }
 
+// One round. As in the reference's decode loop, a speculative round runs only while pos + K < ctx
+// (src/q27_main.cpp:6391); nearer the end of the context the call takes a plain step (ncommit = 1).
 int q27x_spec_round(q27x_ctx* x, int32_t* out_tokens, int* ncommit) {
     if (!x || !x->prefilled) { set_error("q27x_spec_round: no prefill"); return Q27X_E_STATE; }
-    int rc = run_step(x, 1);
+    Dctl h;
+    int rc = arm(x, 0x7fffffff, &h);
     if (rc) return rc;
+    if (h.pos >= x->c.ctx) { set_error("context capacity exhausted (ctx=%d)", x->c.ctx); return Q27X_E_RANGE; }
+    const int spec = h.pos + x->c.spec_k < x->c.ctx;
+    if ((rc = run_step(x, spec))) return rc;
     Q27X_HIP(hipStreamSynchronize(x->stream));
     if ((rc = check_device_err(x))) return rc;
-    Dctl h;
     Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
-    if (ncommit) *ncommit = h.ncommit_last;
-    if (out_tokens) for (int j = 0; j < h.ncommit_last; ++j) out_tokens[j] = h.nx[j];
+    const int nc = spec ? h.ncommit_last : 1;
+    if (ncommit) *ncommit = nc;
+    if (out_tokens) for (int j = 0; j < nc; ++j) out_tokens[j] = h.nx[j];
     return Q27X_OK;
+}
+
+int q27x_mtp_draft(q27x_ctx* x, const uint16_t* hrows, const int32_t* toks, int nr, int dpos0, int head_row,
+                   uint16_t* res, int32_t* token, q27x_stream_t s) {
+    if (!x || !hrows || !toks || nr < 1 || nr > kMaxRows || dpos0 < 0 || dpos0 + nr > x->c.ctx || head_row >= nr ||
+        (token && head_row < 0)) {
+        set_error("q27x_mtp_draft: bad arguments (nr=%d dpos0=%d head_row=%d)", nr, dpos0, head_row);
+        return Q27X_E_ARG;
+    }
+    if (!x->loaded) { set_error("q27x_mtp_draft: no weights"); return Q27X_E_STATE; }
+    const int H = x->H;
+    hipEvent_t e;
+    Q27X_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    int rc = Q27X_OK;
+    auto run = [&]() -> int {
+        Q27X_HIP(hipEventRecord(e, (hipStream_t)s));
+        Q27X_HIP(hipStreamWaitEvent(x->stream, e, 0));
+        Q27X_HIP(hipMemcpyAsync(x->mtp_hin, hrows, (size_t)nr * H * 2, hipMemcpyDeviceToDevice, x->stream));
+        Q27X_HIP(hipMemcpyAsync(x->dctl->mtp_tok, toks, (size_t)nr * 4, hipMemcpyDeviceToDevice, x->stream));
+        int r = set_ints(x, 4, DOFF(mtp_nact), nr, DOFF(mtp_dpos0), dpos0, DOFF(mtp_head), head_row < 0 ? 0 : head_row,
+                         DOFF(stop), 0);
+        if (r) return r;
+        if ((r = mtp_pass(x, nr, head_row >= 0, 0))) return r;
+        if (res) Q27X_HIP(hipMemcpyAsync(res, x->mtp_res, (size_t)nr * H * 2, hipMemcpyDeviceToDevice, x->stream));
+        if (token) Q27X_HIP(hipMemcpyAsync(token, &x->dctl->mtp_out, 4, hipMemcpyDeviceToDevice, x->stream));
+        Q27X_HIP(hipEventRecord(e, x->stream));
+        Q27X_HIP(hipStreamWaitEvent((hipStream_t)s, e, 0));
+        return Q27X_OK;
+    };
+    rc = run();
+    (void)hipEventDestroy(e);
+    return rc;
 }
 
 int q27x_set_forced_drafts(q27x_ctx* x, const int32_t* toks, int n) {
@@ -934,37 +1062,47 @@ int q27x_set_forced_drafts(q27x_ctx* x, const int32_t* toks, int n) {
     return Q27X_OK;
 }
 
+// The decode loop (src/q27_main.cpp:6382-6696). Steps are launched with two in flight; the host
+// learns each one's outcome from the pinned mailbox one step late. Near the end of the context
+// (when the position bound of the launched steps says the next round might not fit) it drains
+// the stream, reads the exact position, and switches to plain steps once pos + K >= ctx, as the
+// reference does (6391); the request ends when max_new tokens are committed or the context is full.
 int q27x_generate(q27x_ctx* x, int max_new, int spec, int32_t* out, int* n_out, q27x_stats* st) {
     if (!x || !x->prefilled || max_new < 1 || !out) { set_error("q27x_generate: bad arguments"); return Q27X_E_ARG; }
-    if (max_new > x->ring_cap) { set_error("q27x_generate: max_new exceeds capacity"); return Q27X_E_RANGE; }
-    int rc = set_ints(x, 1, DOFF(max_new), max_new);
-    if (rc) return rc;
+    if (max_new > x->ring_cap) max_new = x->ring_cap;   // a request never commits more than the context holds
     Dctl h0;
-    Q27X_HIP(hipMemcpyAsync(&h0, x->dctl, sizeof h0, hipMemcpyDeviceToHost, x->stream));
-    Q27X_HIP(hipStreamSynchronize(x->stream));
-    if (h0.committed >= max_new) rc = set_ints(x, 1, DOFF(stop), 1);
+    int rc = arm(x, max_new, &h0);
     if (rc) return rc;
-    // build the graph outside the timed loop
-    if (use_graphs()) {
-        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
-        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
-        if (!*g) { if ((rc = build_graph(x, spec, g))) return rc; if (spec) x->g_spec_k = x->c.spec_k; }
-    }
+    const int K = x->c.spec_k, ctx = x->c.ctx;
+    // graphs built outside the timed loop (the plain one is needed at the context edge)
+    if ((rc = ensure_graph(x, 0))) return rc;
+    if (spec && (rc = ensure_graph(x, 1))) return rc;
     Q27X_HIP(hipStreamSynchronize(x->stream));
     const auto t0 = std::chrono::steady_clock::now();
-    // two rounds in flight: a round is launched once the one before the previous has landed
     std::vector<hipEvent_t> ev(2, nullptr);
     for (auto& e : ev) Q27X_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     long long launched = 0;
-    const int max_rounds = x->c.ctx;
-    while (launched < max_rounds) {
+    long long pos_hi = h0.pos;              // bound of the position after every launched step
+    int mode = spec ? 1 : 0;
+    bool done = h0.stop != 0;
+    while (!done && launched < (long long)ctx + 2) {
         if (launched >= 2) {
-            Q27X_HIP(hipEventSynchronize(ev[launched & 1]));
+            if ((rc = (int)hipEventSynchronize(ev[launched & 1])) != 0) { rc = hip_fail((hipError_t)rc, "hipEventSynchronize"); break; }
             if (x->mbox->stop || x->mbox->committed >= max_new) break;
         }
-        if ((rc = run_step(x, spec))) break;
-        Q27X_HIP(hipEventRecord(ev[launched & 1], x->stream));
+        if (pos_hi + (mode ? K + 1 : 1) > ctx) {
+            if ((rc = (int)hipStreamSynchronize(x->stream)) != 0) { rc = hip_fail((hipError_t)rc, "hipStreamSynchronize"); break; }
+            Dctl h;
+            if ((rc = (int)hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost)) != 0) { rc = hip_fail((hipError_t)rc, "hipMemcpy"); break; }
+            if (h.stop || h.err || h.committed >= max_new) break;
+            pos_hi = h.pos;
+            if (mode && h.pos + K >= ctx) mode = 0;
+            if (!mode && h.pos >= ctx) break;
+        }
+        if ((rc = run_step(x, mode))) break;
+        if ((rc = (int)hipEventRecord(ev[launched & 1], x->stream)) != 0) { rc = hip_fail((hipError_t)rc, "hipEventRecord"); break; }
         ++launched;
+        pos_hi += mode ? K + 1 : 1;
     }
     Q27X_HIP(hipStreamSynchronize(x->stream));
     const auto t1 = std::chrono::steady_clock::now();
@@ -976,31 +1114,19 @@ int q27x_generate(q27x_ctx* x, int max_new, int spec, int32_t* out, int* n_out, 
     const int n = h.committed < max_new ? h.committed : max_new;
     Q27X_HIP(hipMemcpy(out, x->out_ring, (size_t)n * 4, hipMemcpyDeviceToHost));
     if (n_out) *n_out = n;
-    if (st) {
-        memset(st, 0, sizeof *st);
-        st->rounds = h.rounds - h0.rounds;
-        st->committed = n - h0.committed;
-        st->accepted = h.accepted - h0.accepted;
-        for (int j = 0; j < 9; ++j) st->acc_hist[j] = h.acc_hist[j] - h0.acc_hist[j];
-        st->decode_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
-    }
+    fill_stats(x, st, h0, h, h.committed - h0.committed, std::chrono::duration<double, std::milli>(t1 - t0).count());
     return Q27X_OK;
 }
 
 // Exactly n rounds (spec) or plain steps back to back from the current state, one graph launch
 // each, no host synchronisation in between; stats over those rounds (wall clock around the launches
-// and the final synchronisation).
+// and the final synchronisation). A round past the end of the context is an error (Q27X_E_RANGE).
 int q27x_run_rounds(q27x_ctx* x, int n, int spec, q27x_stats* st) {
     if (!x || !x->prefilled || n < 1) { set_error("q27x_run_rounds: bad arguments"); return Q27X_E_ARG; }
-    int rc = set_ints(x, 1, DOFF(max_new), 0x7fffffff);
-    if (rc) return rc;
-    if (use_graphs()) {
-        hipGraphExec_t* g = spec ? &x->g_spec : &x->g_plain;
-        if (spec && x->g_spec && x->g_spec_k != x->c.spec_k) { (void)hipGraphExecDestroy(x->g_spec); x->g_spec = nullptr; }
-        if (!*g) { if ((rc = build_graph(x, spec, g))) return rc; if (spec) x->g_spec_k = x->c.spec_k; }
-    }
     Dctl h0;
-    Q27X_HIP(hipMemcpyAsync(&h0, x->dctl, sizeof h0, hipMemcpyDeviceToHost, x->stream));
+    int rc = arm(x, 0x7fffffff, &h0);
+    if (rc) return rc;
+    if ((rc = ensure_graph(x, spec))) return rc;
     Q27X_HIP(hipStreamSynchronize(x->stream));
     const auto t0 = std::chrono::steady_clock::now();
     for (int i = 0; i < n && !rc; ++i) rc = run_step(x, spec);
@@ -1010,14 +1136,7 @@ int q27x_run_rounds(q27x_ctx* x, int n, int spec, q27x_stats* st) {
     if ((rc = check_device_err(x))) return rc;
     Dctl h;
     Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
-    if (st) {
-        memset(st, 0, sizeof *st);
-        st->rounds = h.rounds - h0.rounds;
-        st->committed = h.committed - h0.committed;
-        st->accepted = h.accepted - h0.accepted;
-        for (int j = 0; j < 9; ++j) st->acc_hist[j] = h.acc_hist[j] - h0.acc_hist[j];
-        st->decode_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
-    }
+    fill_stats(x, st, h0, h, h.committed - h0.committed, std::chrono::duration<double, std::milli>(t1 - t0).count());
     return Q27X_OK;
 }
 
@@ -1137,6 +1256,19 @@ int q27x_debug_read(q27x_ctx* x, const char* name, int layer, void* dst, size_t 
     if (!strcmp(name, "S") && Y->S) { src = Y->S; n = (size_t)x->c.gdn_vh * 128 * 128 * 4; }
     else if (!strcmp(name, "conv_hist") && Y->conv_hist) { src = Y->conv_hist; n = (size_t)x->nqkv * 3 * 2; }
     else if (!strcmp(name, "kc") && Y->kc) { src = Y->kc; n = kvn; }
+    else if (!strcmp(name, "vc") && Y->vc) { src = Y->vc; n = kvn; }
+    else if (!strcmp(name, "ks") && Y->ks) { src = Y->ks; n = kvn / x->c.kv_group * 4; }
+    else if (!strcmp(name, "vs") && Y->vs) { src = Y->vs; n = kvn / x->c.kv_group * 4; }
+    else if (!strcmp(name, "mtp_res")) { src = x->mtp_res; n = (size_t)kMaxRows * x->H * 2; }
+    else if (!strcmp(name, "hcatch")) { src = x->hcatch; n = (size_t)kMaxRows * x->H * 2; }
+    else if (!strcmp(name, "dt")) { src = x->dctl->dt; n = 8 * 4; }
+    else if (!strcmp(name, "dt_raw")) { src = x->dctl->dt_raw; n = 8 * 4; }
+    else if (!strcmp(name, "nx")) { src = x->dctl->nx; n = 8 * 4; }
+    else if (!strcmp(name, "catch_tok")) { src = x->dctl->catch_tok; n = 8 * 4; }
+    else if (!strcmp(name, "ncatch")) { src = &x->dctl->ncatch; n = 4; }
+    else if (!strcmp(name, "mtp_head")) { src = &x->dctl->mtp_head; n = 4; }
+    else if (!strcmp(name, "pos")) { src = &x->dctl->pos; n = 4; }
+    else if (!strcmp(name, "tok")) { src = &x->dctl->tok; n = 4; }
     else if (!strcmp(name, "hprev")) { src = x->hprev; n = (size_t)x->H * 2; }
     else if (!strcmp(name, "hfinal")) { src = x->hfinal; n = (size_t)kMaxRows * x->H * 2; }
     else if (!strcmp(name, "emb")) { src = x->emb; n = (size_t)x->V * x->H * 2; }

@@ -29,6 +29,7 @@ constexpr int kNormMaxChunks = 8;   // n <= 8192
 template <int NCH>
 __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
     if (stopped(a.stop)) return;
+    if (a.stamp && blockIdx.x == 0 && threadIdx.x == 0) *a.stamp = __builtin_amdgcn_s_memrealtime();
     __shared__ float wsum[1][4];
     norm_rows<NCH, 1>(a, blockIdx.x, 1, wsum);
 }

@@ -392,6 +392,7 @@ __global__ __launch_bounds__(256) void k_gdn_conv(const uint16_t* __restrict__ r
     uint16_t h0 = hist[3 * c], h1 = hist[3 * c + 1], h2 = hist[3 * c + 2];
     for (int p = 0; p < npend; ++p) { h0 = h1; h1 = h2; h2 = pend_raw[(size_t)p * nconv + c]; }
     hist[3 * c] = h0; hist[3 * c + 1] = h1; hist[3 * c + 2] = h2;
+    if (nr == 0) return;   // commit only
     const float w0 = bf2f(conv_w[4 * c]), w1 = bf2f(conv_w[4 * c + 1]);
     const float w2 = bf2f(conv_w[4 * c + 2]), w3 = bf2f(conv_w[4 * c + 3]);
     for (int n = 0; n < nr; ++n) {
@@ -412,6 +413,26 @@ int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_
                        nconv, conv_w, conv_hist, pend_raw, npend_ptr, npend_imm, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
+}
+
+// Commit only: apply the npend pending rows of `pend` to S (the update each row already received,
+// the same fmaf as k_gdn's commit), write S back, and leave nothing pending. One block per value
+// head, thread (g, d) holds key rows 32 g .. 32 g + 31 of value column d.
+__global__ __launch_bounds__(kNT) void k_gdn_commit(float* __restrict__ S, const void* pend, int vh, int npend) {
+    const int h = blockIdx.x, t = threadIdx.x, d = t & (kD - 1), g = t >> 7;
+    const PendArea P = pend_area(const_cast<void*>(pend), vh);
+    float* Sp = S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
+    float st[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
+    for (int p = 0; p < npend; ++p) {
+        const float dp = P.delta[((size_t)p * vh + h) * kD + d], dc = P.decay[(size_t)p * vh + h];
+        const float* kp = P.khat + ((size_t)p * vh + h) * kD + g * kJ;
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(kp[j], dp, dc * st[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) Sp[(size_t)j * kD] = st[j];
 }
 
 }  // namespace q27x
@@ -447,4 +468,24 @@ extern "C" int q27x_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const ui
     g.npend_imm = npend; g.kh = kh; g.vh = vh; g.d = d; g.eps = 1e-6f;
     g.out = out; g.out_stride = out_stride; g.xq = xq; g.xs = xs;
     return launch_gdn(g, nr, (hipStream_t)s);
+}
+
+// Kernel-tier commit without new rows: the conv shift registers and S take the npend pending rows
+// that q27x_gdn_verify left in `pend` (the accepted prefix of its last call). Afterwards nothing is
+// pending: the next q27x_gdn_verify call passes npend = 0.
+extern "C" int q27x_gdn_commit(float* S, uint16_t* conv_hist, void* pend, int npend, int kh, int vh, int d,
+                               q27x_stream_t s) {
+    if (!S || !conv_hist || !pend || npend < 0 || npend > kMaxRows || d != 128 || kh < 1 || vh % kh) {
+        set_error("q27x_gdn_commit: bad arguments");
+        return Q27X_E_ARG;
+    }
+    if (npend == 0) return Q27X_OK;
+    const int nconv = (2 * kh + vh) * d;
+    uint16_t* pend_raw = (uint16_t*)((char*)pend + gdn_pend_raw_offset(kh, vh, d));
+    int rc = launch_gdn_conv(nullptr, 0, nullptr, 0, nconv, nullptr, conv_hist, pend_raw, nullptr, npend, 0,
+                             (hipStream_t)s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_gdn_commit, dim3(vh), dim3(kNT), 0, (hipStream_t)s, S, (const void*)pend, vh, npend);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
 }

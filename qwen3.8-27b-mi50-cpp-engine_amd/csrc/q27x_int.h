@@ -32,6 +32,7 @@ struct NormArgs {
     int8_t* xq; float* xs; int quant_bf16; float in_scale;
     const int* stop;
     const int* row_sel;                           // optional: process only row *row_sel (into row 0)
+    unsigned long long* stamp;                    // optional: block 0 stores the wall clock at its start
 };
 // ---------------------------------------------------------------- projection
 enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2 };

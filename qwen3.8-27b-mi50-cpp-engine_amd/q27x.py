@@ -45,6 +45,8 @@ class Stats(ctypes.Structure):
         ("rounds", ctypes.c_longlong), ("committed", ctypes.c_longlong),
         ("accepted", ctypes.c_longlong), ("acc_hist", ctypes.c_longlong * 9),
         ("decode_ms", ctypes.c_double), ("prefill_ms", ctypes.c_double),
+        ("draft_ms", ctypes.c_double), ("verify_ms", ctypes.c_double),
+        ("head_ms", ctypes.c_double), ("tail_ms", ctypes.c_double),
     ]
 
 
@@ -95,6 +97,8 @@ _SIGS = {
     "q27x_reset": ([VP], I), "q27x_prefill": ([VP, VP, I, VP], I),
     "q27x_decode_step": ([VP, VP], I), "q27x_spec_round": ([VP, VP, VP], I),
     "q27x_set_forced_drafts": ([VP, VP, I], I),
+    "q27x_mtp_draft": ([VP, VP, VP, I, I, I, VP, VP, VP], I),
+    "q27x_gdn_commit": ([VP, VP, VP, I, I, I, I, VP], I),
     "q27x_generate": ([VP, I, I, VP, VP, VP], I),
     "q27x_bench_verify": ([VP, I, I, VP], I),
     "q27x_run_rounds": ([VP, I, I, VP], I),
@@ -250,6 +254,23 @@ class Engine:
         b = ctypes.c_double(0)
         call("q27x_bench_kernel", self.ctx, layer, which, nr, iters, ctypes.byref(ms), ctypes.byref(b))
         return ms.value, b.value
+
+    def mtp_draft(self, hrows, toks, dpos0, head_row):
+        """One MTP pass (q27x_mtp_draft) on host arrays: hrows [nr][hidden] bf16 bits, toks [nr];
+        returns (head-row argmax or None, residual rows [nr][hidden] bf16)."""
+        hrows = np.ascontiguousarray(hrows, dtype=np.uint16)
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        nr = len(toks)
+        dh, dt = DevBuf(array=hrows), DevBuf(array=toks)
+        dres, dtok = DevBuf(nr * self.cfg.hidden * 2), DevBuf(4)
+        call("q27x_mtp_draft", self.ctx, dh.ptr, dt.ptr, nr, dpos0, head_row, dres.ptr,
+             dtok.ptr if head_row >= 0 else None, None)
+        call("q27x_device_sync")
+        res = dres.download(np.uint16, (nr, self.cfg.hidden))
+        tok = int(dtok.download(np.int32, (1,))[0]) if head_row >= 0 else None
+        for b in (dh, dt, dres, dtok):
+            b.free()
+        return tok, res
 
     def read(self, name, layer, dtype, count):
         out = np.empty(count, dtype=dtype)

@@ -145,3 +145,81 @@ def attention_rows(qh, gate_vals, Kd, Vd, nq, nkv, hd, pos0, nr):
                 o = o * sigmoid(gate_vals[r, h * hd:(h + 1) * hd])
             out[r, h * hd:(h + 1) * hd] = o
     return out
+
+
+def dequant_rows(wq, ws):
+    """int8 weights [rows][K] with per-64 scales [rows][K/64] -> float64."""
+    return wq.astype(np.float64) * np.repeat(ws.astype(np.float64), 64, axis=1)
+
+
+def mtp_forward(W, c, hrows, toks, pos0, swap_halves=False, plus_one=None, drop_o=False):
+    """The MTP draft layer in float64, from its definition: rows r = (hidden h_r, token t_r) at
+    positions pos0 + r;
+      x_r = [norm_e(emb[t_r]) | norm_h(h_r)]   (embedding half first when mtp_swap is set)
+      res = fc x                                (fc = [fc0 | fc1] over the two halves)
+      res += o_proj(attention(norm_in(res)))   (a full-attention decoder layer: per-head norms
+                                                 (1 + w), rotate-half RoPE on the first rot dims,
+                                                 causal GQA over the rows, output * sigmoid(gate))
+      res += down(silu(gate(n)) * up(n)),  n = norm_post(res)
+      logits_r = lm_head norm_mtp(res_r)
+    W holds the oracle's weights (int8 + scales, bf16 vectors); c the config dict. The keyword
+    arguments plant a mistake (for showing that the comparison detects it). Returns (res [nr][H],
+    logits [nr][vocab]), float64; every activation stays unquantized."""
+    H, hd, nq, nkv = c["hidden"], c["head_dim"], c["n_q"], c["n_kv"]
+    po = float(c["mtp_plus_one"]) if plus_one is None else plus_one
+    eps = c["rms_eps"]
+    nr = len(toks)
+    e = bf2f(W["emb"].reshape(-1, H)[np.asarray(toks)]).astype(np.float64)
+    h = bf2f(hrows).reshape(nr, H).astype(np.float64)
+    ne = rmsnorm(e, bf2f(W["pre_emb"]), po, eps)
+    nh = rmsnorm(h, bf2f(W["pre_hid"]), po, eps)
+    first, second = (ne, nh) if c["mtp_swap"] else (nh, ne)
+    if swap_halves:
+        first, second = second, first
+    res = first @ dequant_rows(W["fc0_w"], W["fc0_s"]).T + second @ dequant_rows(W["fc1_w"], W["fc1_s"]).T
+    # attention block
+    x = rmsnorm(res, bf2f(W["in_norm"]), po, eps)
+    qkv = x @ dequant_rows(W["qkv_w"], W["qkv_s"]).T
+    qw = 2 * hd if c["attn_gate"] else hd
+    qrows = nq * qw
+    rot, theta = c["rot_dims"], c["rope_theta"]
+    qn, kn = bf2f(W["q_norm"]).astype(np.float64), bf2f(W["k_norm"]).astype(np.float64)
+    Q = np.zeros((nr, nq, hd))
+    G = np.zeros((nr, nq, hd))
+    Kh = np.zeros((nr, nkv, hd))
+    Vh = np.zeros((nr, nkv, hd))
+    for r in range(nr):
+        for hh in range(nq):
+            q = qkv[r, hh * qw: hh * qw + hd]
+            q = q / np.sqrt((q * q).mean() + eps) * (1.0 + qn)
+            Q[r, hh] = rope_rotate(q, pos0 + r, rot, theta)
+            if c["attn_gate"]:
+                G[r, hh] = qkv[r, hh * qw + hd: hh * qw + 2 * hd]
+        for kv in range(nkv):
+            k = qkv[r, qrows + kv * hd: qrows + (kv + 1) * hd]
+            k = k / np.sqrt((k * k).mean() + eps) * (1.0 + kn)
+            Kh[r, kv] = rope_rotate(k, pos0 + r, rot, theta)
+            Vh[r, kv] = qkv[r, qrows + nkv * hd + kv * hd: qrows + nkv * hd + (kv + 1) * hd]
+    att = np.zeros((nr, nq * hd))
+    grp = nq // nkv
+    for r in range(nr):
+        for hh in range(nq):
+            kv = hh // grp
+            sc = Kh[: r + 1, kv] @ Q[r, hh] / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            o = (p @ Vh[: r + 1, kv]) / p.sum()
+            if c["attn_gate"]:
+                o = o * sigmoid(G[r, hh])
+            att[r, hh * hd:(hh + 1) * hd] = o
+    if not drop_o:
+        res = res + att @ dequant_rows(W["o_w"], W["o_s"]).T
+    # MLP
+    x = rmsnorm(res, bf2f(W["post_norm"]), po, eps)
+    g = x @ dequant_rows(W["gate_w"], W["gate_s"]).T
+    u = x @ dequant_rows(W["up_w"], W["up_s"]).T
+    a = silu(g) * u
+    Wd = np.concatenate([dequant_rows(W[f"down4_w{j}"], W[f"down4_s{j}"]) for j in range(4)], axis=1)
+    res = res + a @ Wd.T
+    xn = rmsnorm(res, bf2f(W["mtp_norm"]), 1.0, eps)
+    logits = xn @ bf2f(W["lm_head"]).reshape(-1, H).astype(np.float64).T
+    return res, logits

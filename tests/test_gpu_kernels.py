@@ -232,11 +232,14 @@ def gdn_inputs(rng, O, nr, kh=16, vh=48, d=128):
         b=rng.uniform(-4, 0, (nr, vh)).astype(np.float32))
 
 
-def test_gdn_verify_config1(gpu, O):
+@pytest.mark.parametrize("rollback", [0, 1, 2])
+def test_gdn_verify_config1(gpu, O, rollback):
     """BASELINE config 1 GDN core: 3 verify rows, state ~N(0, 0.1), a/b ~U(-4, 0), then a second
-    call that commits an accepted prefix (rollback) -- both compared bit for bit."""
+    call that commits an accepted prefix of rollback + 1 rows (the rest rolled back), then the
+    commit-only entry for that call's accepted prefix followed by a call with nothing pending --
+    all compared bit for bit with the oracle."""
     X = gpu
-    rng = np.random.default_rng(0x51E70001)
+    rng = np.random.default_rng(0x51E70001 + 17 * rollback)
     kh, vh, d, nr = 16, 48, 128, 3
     nqkv, nz = (2 * kh + vh) * d, vh * d
     S = (rng.standard_normal((vh, d, d)) * 0.1).astype(np.float32)
@@ -251,8 +254,12 @@ def test_gdn_verify_config1(gpu, O):
     dpend = X.DevBuf(X.lib().q27x_gdn_pend_bytes(kh, vh, d, 8))
     dpend.zero()
     dconv, dA, ddt, dnw = dev(X, conv_w), dev(X, A_log), dev(X, dt_bias), dev(X, norm_w)
-    rollback = int(rng.integers(0, 3))
-    for call_i, npend in enumerate([0, rollback + 1]):
+    for call_i, npend in enumerate([0, rollback + 1, 2 - rollback + 1]):
+        if call_i == 2:
+            # commit the previous call's accepted prefix on its own, then run with nothing pending;
+            # the oracle gets the same prefix as npend of one call
+            X.call("q27x_gdn_commit", dS.ptr, dh.ptr, dpend.ptr, npend, kh, vh, d, None)
+        gpu_npend = 0 if call_i == 2 else npend
         inp = gdn_inputs(rng, O, nr, kh, vh, d)
         out_o = np.empty((nr, nz), np.uint16)
         xq_o, xs_o = np.empty((nr, nz), np.int8), np.empty((nr, nz // 16), np.float32)
@@ -263,7 +270,7 @@ def test_gdn_verify_config1(gpu, O):
         dq, dzz, da, db = dev(X, inp["qkv"]), dev(X, inp["z"]), dev(X, inp["a"]), dev(X, inp["b"])
         dout, dxq, dxs = X.DevBuf(nr * nz * 2), X.DevBuf(nr * nz), X.DevBuf(nr * nz // 4)
         X.call("q27x_gdn_verify", dq.ptr, nqkv, dzz.ptr, nz, da.ptr, db.ptr, vh, dA.ptr, ddt.ptr, dnw.ptr, dconv.ptr,
-               dS.ptr, dh.ptr, dpend.ptr, npend, kh, vh, d, dout.ptr, nz, dxq.ptr, dxs.ptr, nr, None)
+               dS.ptr, dh.ptr, dpend.ptr, gpu_npend, kh, vh, d, dout.ptr, nz, dxq.ptr, dxs.ptr, nr, None)
         X.call("q27x_device_sync")
         same(f"gdn out (call {call_i})", dout.download(np.uint16, (nr, nz)), out_o)
         same(f"gdn codes (call {call_i})", dxq.download(np.int8, (nr, nz)), xq_o)
@@ -344,3 +351,30 @@ def test_accept(gpu):
         nacc, ncommit = dn.download(np.int32, (2,))
         assert nacc == exp and ncommit == exp + 1
         assert dc.download(np.int32, (8,))[: ncommit].tolist() == nx[: ncommit]
+
+
+def test_mtp_draft_entry_matches_oracle(gpu, O):
+    """Kernel-tier MTP draft layer (q27x_mtp_draft) against the oracle's mtp_pass on the tiny
+    geometry: a 3-row pass at positions 0..2 (head row 2), a 2-row pass at 3..4 that attends to
+    the cache (head row 1), and a catch-up row that overwrites position 1 -- residual rows, the
+    drafted tokens and the layer's whole KV cache bit for bit."""
+    X = gpu
+    cfg = X.tiny_config(spec_k=2, n_layers=4)
+    eng = X.Engine(cfg, 0x51E70003)
+    om = O.Model(cfg, 0x51E70003)
+    rng = np.random.default_rng(0x51E7A010)
+    H = cfg.hidden
+    h = O.f2bf(rng.standard_normal((6, H)).astype(np.float32))
+    t = rng.integers(0, cfg.vocab, 6).astype(np.int32)
+    for rows, dpos0, head in ((slice(0, 3), 0, 2), (slice(3, 5), 3, 1), (slice(5, 6), 1, 0), (slice(0, 2), 4, -1)):
+        tg, rg = eng.mtp_draft(h[rows], t[rows], dpos0, head)
+        to, ro, _ = om.mtp_pass(h[rows], t[rows], dpos0, head)
+        same(f"mtp residual rows at {dpos0}", rg, ro)
+        if head >= 0:
+            assert tg == to, (dpos0, tg, to)
+    n = cfg.ctx * cfg.n_kv * cfg.head_dim
+    for name, dt, cnt in (("kc", np.int8, n), ("vc", np.int8, n), ("ks", np.float32, n // cfg.kv_group),
+                          ("vs", np.float32, n // cfg.kv_group)):
+        same(f"mtp cache {name}", eng.read(name, -1, dt, cnt), om.tensor(name, -1, dt)[:cnt])
+    eng.close()
+    om.close()

@@ -151,3 +151,191 @@ def test_full_geometry_spec_equals_plain(gpu):
     assert forced == plain
     assert stf.acc_hist[2] >= stf.rounds - 1
     eng.close()
+
+
+# ---------------------------------------------------------------- drafts and hand-off
+def kv_bytes(cfg):
+    return cfg.ctx * cfg.n_kv * cfg.head_dim
+
+
+def check_round_state(eng, om, cfg, tag, gdn_layer=0):
+    """Everything a round leaves behind, GPU against oracle, bit for bit: the drafts (what the
+    verify saw and the MTP argmax before any forcing), the verify argmaxes, the hand-off (catch-up
+    rows and tokens, h_prev), the MTP chain residual, the MTP layer's KV cache, and one GDN layer's
+    committed state."""
+    H, K = cfg.hidden, cfg.spec_k
+    g_dt, o_dt = eng.read("dt", -1, np.int32, 8)[:K], om.tensor("dt", -1, np.int32)[:K]
+    assert g_dt.tolist() == o_dt.tolist(), (tag, "drafts", g_dt, o_dt)
+    g_raw, o_raw = eng.read("dt_raw", -1, np.int32, 8)[:K], om.tensor("dt_raw", -1, np.int32)[:K]
+    assert g_raw.tolist() == o_raw.tolist(), (tag, "MTP argmax", g_raw, o_raw)
+    g_nx, o_nx = eng.read("nx", -1, np.int32, 8)[:K + 1], om.tensor("nx", -1, np.int32)[:K + 1]
+    assert g_nx.tolist() == o_nx.tolist(), (tag, "verify argmax", g_nx, o_nx)
+    nc = int(eng.read("ncatch", -1, np.int32, 1)[0])
+    assert nc == int(om.tensor("ncatch", -1, np.int32)[0]), (tag, "ncatch")
+    if nc:
+        assert eng.read("catch_tok", -1, np.int32, 8)[:nc].tolist() == om.tensor("catch_tok", -1, np.int32)[:nc].tolist()
+        hc_g = eng.read("hcatch", -1, np.uint16, 8 * H)[: nc * H]
+        hc_o = om.tensor("hcatch", -1, np.uint16)[: nc * H]
+        assert np.array_equal(hc_g, hc_o), (tag, "catch-up rows")
+    assert np.array_equal(eng.read("hprev", -1, np.uint16, H), om.tensor("hprev", -1, np.uint16)), (tag, "h_prev")
+    head = int(eng.read("mtp_head", -1, np.int32, 1)[0])
+    chain = eng.read("mtp_res", -1, np.uint16, 8 * H)[head * H:(head + 1) * H]
+    assert np.array_equal(chain, om.tensor("hchain", -1, np.uint16)), (tag, "MTP chain residual")
+    n = kv_bytes(cfg)
+    for name, dt, cnt in (("kc", np.int8, n), ("vc", np.int8, n), ("ks", np.float32, n // cfg.kv_group),
+                          ("vs", np.float32, n // cfg.kv_group)):
+        assert np.array_equal(eng.read(name, -1, dt, cnt).view(np.uint8), om.tensor(name, -1, dt)[:cnt].view(np.uint8)), \
+            (tag, "MTP cache " + name)
+    S_g = eng.read("S", gdn_layer, np.float32, cfg.gdn_vh * 128 * 128)
+    assert np.array_equal(S_g.view(np.uint32), om.tensor("S", gdn_layer, np.float32).view(np.uint32)), (tag, "GDN S")
+
+
+@pytest.mark.parametrize("k", [2, 7])
+def test_tiny_drafts_and_handoff_match_oracle(gpu, O, k):
+    """Natural acceptance, round by round: drafts, MTP argmax, MTP chain residual and KV cache,
+    hand-off and GDN state are the oracle's bits (on random weights the MTP rarely matches the
+    trunk, so this checks the draft layer itself)."""
+    X = gpu
+    cfg = tiny(X, spec_k=k)
+    eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
+    p = prompt_of(cfg, 23, seed=40 + k)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(6):
+        a, b = eng.spec_round(), om.spec_round()
+        assert a == b, (k, r, a, b)
+        check_round_state(eng, om, cfg, f"K={k} round {r}")
+    eng.close()
+    om.close()
+
+
+def corrupted_stream(plain, vocab, seed, density=0.3):
+    rng = np.random.default_rng(seed)
+    s = np.array(plain, np.int32)
+    bad = rng.random(len(s)) < density
+    bad[0] = False
+    s[bad] = (s[bad] + 1 + rng.integers(0, 7, bad.sum())) % vocab
+    return s
+
+
+@pytest.mark.parametrize("k", [2, 7])
+def test_tiny_partial_acceptance_matches_oracle(gpu, O, k):
+    """Forced drafts from the trunk's own greedy stream with wrong tokens planted at seeded
+    positions: every acceptance length 0..K occurs, so the rollback of 0 < nacc < K rows, the
+    catch-up rows of the next draft and the deferred GDN commit all run on the GPU; each round's
+    state is the oracle's, and the committed stream is plain greedy."""
+    X = gpu
+    cfg = tiny(X, spec_k=k)
+    eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
+    p = prompt_of(cfg, 19, seed=60 + k)
+    n = len(p)
+    first = om.prefill(p)
+    plain = [first] + [om.decode_step() for _ in range(120)]
+    forced = corrupted_stream(plain, cfg.vocab, seed=70 + k, density=0.12 if k == 7 else 0.3)
+    assert eng.prefill(p) == om.prefill(p) == first
+    eng.set_forced(forced)
+    out, seen = [first], set()
+    for r in range(14):
+        b0 = int(om.tensor("pos", -1, np.int32)[0]) - n
+        d = list(forced[b0 + 1:b0 + 1 + k])
+        got_o = om.spec_round(forced=np.array(d + [0] * 8, np.int32))
+        got_g = eng.spec_round()
+        assert got_g == got_o, (k, r, got_g, got_o)
+        seen.add(len(got_o) - 1)
+        check_round_state(eng, om, cfg, f"K={k} forced round {r}")
+        out.extend(got_o)
+    assert out == plain[:len(out)]
+    assert 0 in seen and any(0 < s < k for s in seen), (k, sorted(seen))
+    eng.set_forced([])
+    eng.close()
+    om.close()
+
+
+def test_generate_continues_after_its_budget(tiny_pair):
+    """A generate call that reached max_new leaves the context ready: the next generate (larger
+    budget), a plain step and a spec round continue the oracle's greedy stream."""
+    X, cfg, eng, om = tiny_pair
+    p = prompt_of(cfg, 17, seed=21)
+    first = om.prefill(p)
+    plain = [first] + [om.decode_step() for _ in range(40)]
+    assert eng.prefill(p) == first
+    a, _ = eng.generate(10, spec=True)
+    assert a == plain[:10]
+    b, st = eng.generate(20, spec=True)
+    assert b == plain[:20] and st.committed >= 1
+    eng.decode_step()
+    eng.spec_round()
+    c = int(eng.read("pos", -1, np.int32, 1)[0]) - len(p) + 1     # tokens committed so far
+    stream, _ = eng.generate(c, spec=True)                         # budget already met: reads them
+    assert len(stream) == c and stream == plain[:c], (stream, plain[:c])
+
+
+def test_generate_runs_to_the_end_of_the_context(gpu, O):
+    """max_new past the context: speculative rounds while pos + K < ctx, then plain steps, and the
+    request ends with the context full (src/q27_main.cpp:6384, 6391) -- no error, and the tokens are
+    the oracle's plain greedy stream to the last position."""
+    X = gpu
+    cfg = tiny(X, spec_k=3, ctx=64)
+    eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
+    p = prompt_of(cfg, 40, seed=5)
+    first = om.prefill(p)
+    plain = [first] + [om.decode_step() for _ in range(cfg.ctx - len(p))]
+    assert eng.prefill(p) == first
+    out, st = eng.generate(200, spec=True)
+    assert out == plain, (len(out), len(plain))
+    assert int(eng.read("pos", -1, np.int32, 1)[0]) == cfg.ctx
+    # forced acceptance (K+1 per round) reaches the edge with larger steps
+    eng.prefill(p)
+    eng.set_forced(np.array(plain + [0] * 16, np.int32))
+    out2, st2 = eng.generate(200, spec=True)
+    assert out2 == plain
+    eng.set_forced([])
+    with pytest.raises(X.Q27XError):
+        eng.spec_round()                     # pos == ctx: nothing left to run
+    eng.close()
+    om.close()
+
+
+def test_round_phase_times_are_reported(tiny_pair):
+    X, cfg, eng, om = tiny_pair
+    eng.prefill(prompt_of(cfg, 12, seed=2))
+    st = eng.run_rounds(5, spec=True)
+    assert st.rounds == 5
+    parts = [st.draft_ms, st.verify_ms, st.head_ms, st.tail_ms]
+    assert all(v > 0 for v in parts), parts
+    assert sum(parts) < st.decode_ms * 1.05, (parts, st.decode_ms)
+
+
+def test_full_width_rounds_match_oracle(gpu, O):
+    """BASELINE widths (hidden 5120, inter 17408, vocab 62080, GDN 16/48 heads, attention 32q/8kv,
+    kv_group 32, MTP layer on) at 4 layers (3 GDN + 1 attention), against the oracle: prefill of
+    64 tokens, natural rounds and forced rounds with planted wrong drafts (partial acceptance),
+    each round's tokens, drafts, hand-off, MTP state and GDN state bit for bit. These are the
+    engine's full-width kernel instantiations (norm prologues at K = 5120, split SwiGLU units, the
+    32q/8kv attention, the 62080-row lm_head with argmax partials)."""
+    X = gpu
+    cfg = X.default_config(spec_k=2, n_layers=4, ctx=256)
+    eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
+    p = prompt_of(cfg, 64, seed=31)
+    first = om.prefill(p)
+    assert eng.prefill(p) == first
+    assert np.array_equal(eng.read("hprev", -1, np.uint16, cfg.hidden), om.tensor("hprev", -1, np.uint16))
+    for r in range(3):
+        a, b = eng.spec_round(), om.spec_round()
+        assert a == b, (r, a, b)
+        check_round_state(eng, om, cfg, f"full width round {r}")
+    # partial acceptance at full width
+    om.prefill(p)
+    plain = [first] + [om.decode_step() for _ in range(16)]
+    forced = corrupted_stream(plain, cfg.vocab, seed=33, density=0.35)
+    assert eng.prefill(p) == om.prefill(p)
+    eng.set_forced(forced)
+    n = len(p)
+    for r in range(4):
+        b0 = int(om.tensor("pos", -1, np.int32)[0]) - n
+        d = list(forced[b0 + 1:b0 + 3])
+        got_o = om.spec_round(forced=np.array(d + [0] * 8, np.int32))
+        got_g = eng.spec_round()
+        assert got_g == got_o, (r, got_g, got_o)
+        check_round_state(eng, om, cfg, f"full width forced round {r}")
+    eng.close()
+    om.close()
