@@ -221,6 +221,18 @@ int q27x_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
                    int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
                    void* work, uint16_t* out, int8_t* xq, float* xs, q27x_stream_t s);
 
+/* q27x_attn_rows without the `work` argument and without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The split partials live in one file-scope
+ * device array of 32.5 MiB per GPU (held until the process ends), so nr x nq x ceil((pos0+nr)/64)
+ * may be at most 65536 (e.g. 8 rows x 32 query heads at 16384 positions); larger calls return
+ * Q27X_E_RANGE. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race. Same kernels and the same bits as q27x_attn_rows. */
+int q27x_attn_rows_noalloc(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
+                           const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
+                           int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
+                           uint16_t* out, int8_t* xq, float* xs, q27x_stream_t s);
+
 /* R18 argmax of nr rows of n logits: non-finite filtered, ties -> lowest index, all non-finite
  * -> index 0 / value -inf (replaces q27_argmax_val, include/q27.h:348; src/q27_elem.hip:216-322). */
 int q27x_argmax_rows(const float* logits, int n, int ld, int nr, int32_t* idx, float* val,

@@ -9,6 +9,8 @@
 //   owns (split, kv head) for all rows and all GQA heads: K/V tile dequantised into LDS once,
 //   scores by 16-lane dot products, two-pass softmax in base 2, p.V in key order; the combine
 //   merges splits in order, applies sigmoid(gate) and quantises for o_proj.
+#include <mutex>
+
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
@@ -487,4 +489,59 @@ extern "C" int q27x_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int 
     a.sl2e = (float)((1.0 / sqrt((double)hd)) * 1.4426950408889634);
     a.out = out; a.xq = xq; a.xs = xs;
     return launch_attn(a, nr, (hipStream_t)s);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+// Scratch of q27x_attn_rows_noalloc: the split partials of one call, o [nr][nq][splits][128] |
+// m | l, at most kNoAllocRows (row, query head, split) triples -- 32 query heads x 8 rows x 256
+// splits of 64 keys (16384 positions): 32.5 MiB of device memory, held on every GPU the library
+// runs on until the process ends. Every partial the combine reads is written earlier in the same
+// call, so nothing in it has to start at zero.
+namespace q27x {
+constexpr size_t kNoAllocRows = 65536;
+constexpr size_t kNoAllocFloats = kNoAllocRows * (kHD + 2);
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+// Device address of `scratch` on the current device. The array's name in host code is only a
+// host-side stand-in, so the address is looked up once per device (with that device current) and
+// kept; kernels and copies get this pointer, never the name.
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_dev[kMaxDevices];
+static int scratch_ptr(float** out) {
+    int dev = 0;
+    Q27X_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) { set_error("attn: device %d out of range", dev); return Q27X_E_ARG; }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) { set_error("attn: no device address for the scratch array"); return Q27X_E_HIP; }
+        g_scratch_dev[dev] = (float*)p;
+    }
+    *out = g_scratch_dev[dev];
+    return Q27X_OK;
+}
+}  // namespace q27x
+
+extern "C" int q27x_attn_rows_noalloc(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride, const int8_t* kc,
+                                      const float* ks, const int8_t* vc, const float* vs, int kv_group, int nq, int nkv,
+                                      int hd, int gate, int pos0, int nr, uint16_t* out, int8_t* xq, float* xs,
+                                      q27x_stream_t s) {
+    if (!qh || (gate && !qkv_gate) || !kc || !ks || !vc || !vs || !out || pos0 < 0 || nq < 1 || nr < 1 || hd != kHD) {
+        set_error("q27x_attn_rows_noalloc: bad arguments");
+        return Q27X_E_ARG;
+    }
+    const size_t splits = ((size_t)pos0 + nr + kSplit - 1) / kSplit;
+    if ((size_t)nr * nq * splits > kNoAllocRows) {
+        set_error("q27x_attn_rows_noalloc: nr x nq x splits = %zu exceeds the scratch limit of %zu "
+                  "(e.g. 8 rows x 32 heads at 16384 positions)", (size_t)nr * nq * splits, kNoAllocRows);
+        return Q27X_E_RANGE;
+    }
+    float* w = nullptr;
+    const int rc = scratch_ptr(&w);
+    if (rc) return rc;
+    return q27x_attn_rows(qh, qkv_gate, qkv_stride, kc, ks, vc, vs, kv_group, nq, nkv, hd, gate, pos0, nr, w, out, xq,
+                          xs, s);
 }

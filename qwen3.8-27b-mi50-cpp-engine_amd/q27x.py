@@ -87,6 +87,7 @@ _SIGS = {
                              I, VP], I),
     "q27x_attn_work_bytes": ([I, I, I, I], SZ),
     "q27x_attn_rows": ([VP, VP, I, VP, VP, VP, VP, I, I, I, I, I, I, I, VP, VP, VP, VP, VP], I),
+    "q27x_attn_rows_noalloc": ([VP, VP, I, VP, VP, VP, VP, I, I, I, I, I, I, I, VP, VP, VP, VP], I),
     "q27x_argmax_rows": ([VP, I, I, I, VP, VP, VP], I),
     "q27x_accept": ([VP, VP, I, VP, VP, VP], I),
     "q27x_math_test": ([VP, VP, I, I, VP], I),
