@@ -57,35 +57,236 @@ def verify_bytes(c, ctx_len, nr):
     return total
 
 
-def cpu_baseline(cfg_dict, q27o):
+def host_info():
+    """CPU model, logical CPUs and the OpenMP thread count the oracle runs with."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    return {"cpu_model": model, "nproc": os.cpu_count(), "omp_threads": threads}
+
+
+def best_of(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return min(ts), float(np.median(ts))
+
+
+def cpu_baseline(cfg_dict, q27o, k):
     """The oracle's integer path (int8 x int8 -> int32 per 16, fp32 scaling, OpenMP over output rows)
-    on a bounded sample: a 4-layer slice (3 GDN + 1 attention) of the full-width model plus the
-    lm_head, verifying 3 rows; scaled to 64 layers and to committed tok/s at one token per round."""
+    on a bounded sample of one round: the (k+1)-row verify of a 4-layer full-width slice (3 GDN + 1
+    attention) with the lm_head, the lm_head alone, and one single-row MTP draft pass with its head.
+    A round is 16 x (slice - lm_head) + lm_head + k drafts (one token per round at natural
+    acceptance on random weights)."""
     d = dict(cfg_dict)
     d["n_layers"] = 4
     d["ctx"] = 256
     t0 = time.time()
     m = q27o.Model(d, SEED)
     gen_s = time.time() - t0
-    prompt = np.random.default_rng(1).integers(0, d["vocab"], 8).astype(np.int32)
-    m.prefill(prompt)
-    toks = np.array([1, 2, 3], np.int32)
-    nx = np.zeros(8, np.int32)
     lib = q27o.lib()
-    times = []
-    for _ in range(3):
-        t = time.time()
-        lib.q27o_model_verify_rows(m.m, 3, toks.ctypes.data, nx.ctypes.data)
-        times.append(time.time() - t)
+    H, V = d["hidden"], d["vocab"]
+    prompt = np.random.default_rng(1).integers(0, V, 8).astype(np.int32)
+    m.prefill(prompt)
+    toks = np.arange(1, k + 2, dtype=np.int32)
+    nx = np.zeros(8, np.int32)
+    t_slice, _ = best_of(lambda: lib.q27o_model_verify_rows(m.m, k + 1, toks.ctypes.data, nx.ctypes.data), 3)
+    lm = m.tensor("lm_head", -1, np.uint16)
+    y = q27o.f2bf(np.random.default_rng(2).standard_normal((k + 1, H)).astype(np.float32))
+    logits = np.empty((k + 1, V), np.float32)
+    idx, val = np.empty(8, np.int32), np.empty(8, np.float32)
+
+    def head():
+        lib.q27o_bf16_gemv_rows(lm.ctypes.data, V, H, y.ctypes.data, H, logits.ctypes.data, V, k + 1)
+        lib.q27o_argmax_rows(logits.ctypes.data, V, V, k + 1, idx.ctypes.data, val.ctypes.data)
+    t_head, _ = best_of(head, 3)
+    del lm
+    hrow = y[:1].copy()
+    t_draft, _ = best_of(lambda: m.mtp_pass(hrow, toks[:1], 8, 0), 3)
     m.close()
-    t4 = min(times)
-    # head (lm_head) counted once, layers scaled 4 -> 64
-    round_s = t4 * (cfg_dict["n_layers"] / 4.0)
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    return {"value": round(1.0 / round_s, 4), "unit": "committed tok/s", "cores": cores, "kind": "port",
-            "sample": f"3-row verify of a 4-layer full-width slice (3 GDN + 1 attention) + lm_head, best of 3 "
-                      f"({t4:.2f} s), scaled x{cfg_dict['n_layers'] // 4} to one round at natural acceptance "
-                      f"(1 token/round); weight generation {gen_s:.1f} s not timed"}
+    scale = cfg_dict["n_layers"] / 4.0
+    round_s = scale * max(t_slice - t_head, 0.0) + t_head + k * t_draft
+    info = host_info()
+    return {"value": round(1.0 / round_s, 4), "unit": "committed tok/s", "cores": info["omp_threads"],
+            "kind": "port", **info,
+            "sample": f"best of 3: {k + 1}-row verify of a 4-layer full-width slice (3 GDN + 1 attention) + "
+                      f"lm_head {t_slice:.3f} s, lm_head alone {t_head:.3f} s, one MTP draft pass {t_draft:.3f} s; "
+                      f"round = {scale:.0f} x (slice - lm_head) + lm_head + {k} drafts = {round_s:.2f} s at one "
+                      f"token per round; weight generation {gen_s:.1f} s not timed"}
+
+
+# ---------------------------------------------------------------- BASELINE configs 0-2
+CFG_SHAPES = dict(H=5120, I=17408, KH=16, VH=48, D=128, NQ=32, NKV=8, HD=128, GROUP=32, NR=3)
+
+
+def cpu_configs(q27o, attn_ctx, reps=5):
+    """BASELINE configs 0-2 on the host through the oracle's kernel-tier functions (OpenMP over
+    output rows), on seeded synthetic inputs of the BASELINE shapes; best and median of reps."""
+    L = q27o.lib()
+    c = CFG_SHAPES
+    H, I, nr, D, VH, KH = c["H"], c["I"], c["NR"], c["D"], c["VH"], c["KH"]
+    rng = np.random.default_rng(SEED)
+    i8 = 1.0 + 4.0 / 64
+    out = {}
+
+    def i8w(rows, K):
+        return (rng.integers(-127, 128, (rows, K), dtype=np.int8),
+                rng.uniform(1e-4, 2e-3, (rows, K // 64)).astype(np.float32))
+
+    def bf(shape, std=1.0, mean=0.0):
+        return q27o.f2bf((mean + rng.standard_normal(shape) * std).astype(np.float32))
+
+    # config 0: one 3-row W8A8 projection [17408 x 5120], fp32 out
+    W, WS = i8w(I, H)
+    xq = rng.integers(-127, 128, (nr, H), dtype=np.int8)
+    xs = rng.uniform(1e-3, 5e-2, (nr, H // 16)).astype(np.float32)
+    y = np.empty((nr, I), np.float32)
+    tmin, tmed = best_of(lambda: L.q27o_proj_rows(W.ctypes.data, WS.ctypes.data, 1.0, I, H, xq.ctypes.data, H,
+                                                  xs.ctypes.data, y.ctypes.data, I, nr), reps)
+    b0 = I * H * i8 + nr * H * (1 + 4.0 / 16) + nr * I * 4
+    out["config0_projection"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3),
+                                 "bytes": b0, "GB_s": round(b0 / tmin / 1e9, 2)}
+    del W, WS
+    # shared: the layer input (fp32 residual rows), its norm + quantize
+    xres = rng.standard_normal((nr, H)).astype(np.float32)
+    nw = bf((H,), 0.02)
+    hq = np.empty((nr, H), np.int8)
+    hs = np.empty((nr, H // 16), np.float32)
+    hb = np.empty((nr, H), np.uint16)
+    yn = np.empty((nr, H), np.uint16)
+
+    def norm():
+        L.q27o_rmsnorm_quant_rows(xres.ctypes.data, 0, H, nw.ctypes.data, 1.0, 1e-6, H, hb.ctypes.data, yn.ctypes.data,
+                                  H, hq.ctypes.data, hs.ctypes.data, 0, 1.0, nr)
+    # config 1: one GDN layer's mixer
+    nqkv, nz = (2 * KH + VH) * D, VH * D
+    Wz, Sz = i8w(nqkv + nz, H)
+    Wo, So = i8w(H, nz)
+    in_a, in_b = bf((VH, H), 0.02), bf((VH, H), 0.02)
+    A_log = q27o.f2bf(rng.uniform(0, 2.7, VH).astype(np.float32))
+    dtb = bf((VH,), 0.1)
+    gnw = bf((D,), 0.02, 1.0)
+    conv_w = bf((nqkv, 4), 0.3)
+    S = (rng.standard_normal((VH, D, D)) * 0.1).astype(np.float32)
+    hist = bf((nqkv, 3))
+    pend = np.zeros(L.q27o_gdn_pend_bytes(KH, VH, D, 8), np.uint8)
+    pb = np.empty((nr, nqkv + nz), np.uint16)
+    ab = np.empty((2, nr, VH), np.float32)
+    tmp = np.empty((nr, VH), np.float32)
+    gout = np.empty((nr, nz), np.uint16)
+    gq, gs = np.empty((nr, nz), np.int8), np.empty((nr, nz // 16), np.float32)
+    r1 = np.empty((nr, H), np.float32)
+
+    def gdn_layer():
+        norm()
+        L.q27o_proj_rows_epi(Wz.ctypes.data, Sz.ctypes.data, 1.0, nqkv + nz, H, hq.ctypes.data, H, hs.ctypes.data,
+                             pb.ctypes.data, nqkv + nz, 1, None, 0, 0, 0.0, nr)
+        for j, w in enumerate((in_a, in_b)):
+            L.q27o_bf16_gemv_rows(w.ctypes.data, VH, H, yn.ctypes.data, H, tmp.ctypes.data, VH, nr)
+            ab[j] = q27o.bf2f(q27o.f2bf(tmp))
+        L.q27o_gdn_verify(pb.ctypes.data, nqkv + nz, pb.ctypes.data + nqkv * 2, nqkv + nz, ab[0].ctypes.data, ab[1].ctypes.data, VH, A_log.ctypes.data, dtb.ctypes.data,
+                          gnw.ctypes.data, conv_w.ctypes.data, S.ctypes.data, hist.ctypes.data, pend.ctypes.data, 1,
+                          KH, VH, D, 1e-6, gout.ctypes.data, nz, gq.ctypes.data, gs.ctypes.data, nr)
+        L.q27o_proj_rows_epi(Wo.ctypes.data, So.ctypes.data, 1.0, H, nz, gq.ctypes.data, nz, gs.ctypes.data,
+                             r1.ctypes.data, H, 0, hb.ctypes.data, 1, H, 1.0, nr)
+    gdn_layer()
+    tmin, tmed = best_of(gdn_layer, reps)
+    b1 = ((nqkv + nz) * H * i8 + nr * H * 4 + nr * (nqkv + nz) * 2 + 2.0 * VH * H * 2 + nqkv * 4 * 2 +
+          2.0 * VH * D * D * 4 + H * nz * i8 + nr * H * 6)
+    out["config1_gdn_layer"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3), "bytes": b1,
+                                "GB_s": round(b1 / tmin / 1e9, 2)}
+    del Wz, Sz, Wo, So
+    # config 2: one attention layer's mixer at contexts attn_ctx
+    NQ, NKV, HD, G = c["NQ"], c["NKV"], c["HD"], c["GROUP"]
+    qr, kvr, att = NQ * 2 * HD, NKV * HD, NQ * HD
+    Wq, Sq = i8w(qr + 2 * kvr, H)
+    Wo2, So2 = i8w(H, att)
+    qn, kn = bf((HD,), 0.02), bf((HD,), 0.02)
+    qkv = np.empty((nr, qr + 2 * kvr), np.uint16)
+    qh = np.empty((nr, att), np.uint16)
+    ao = np.empty((nr, att), np.uint16)
+    aq, asc = np.empty((nr, att), np.int8), np.empty((nr, att // 16), np.float32)
+    for L0 in attn_ctx:
+        ctx = L0 + nr
+        kc = rng.integers(-127, 128, (ctx, kvr), dtype=np.int8)
+        vc = rng.integers(-127, 128, (ctx, kvr), dtype=np.int8)
+        ks = rng.uniform(1e-3, 2e-2, (ctx, kvr // G)).astype(np.float32)
+        vs = rng.uniform(1e-3, 2e-2, (ctx, kvr // G)).astype(np.float32)
+        cs, sn = np.empty(ctx * 16, np.float32), np.empty(ctx * 16, np.float32)
+        L.q27o_rope_table(ctx, 32, 1e7, cs.ctypes.data, sn.ctypes.data)
+
+        def attn_layer():
+            norm()
+            L.q27o_proj_rows_epi(Wq.ctypes.data, Sq.ctypes.data, 1.0, qr + 2 * kvr, H, hq.ctypes.data, H,
+                                 hs.ctypes.data, qkv.ctypes.data, qr + 2 * kvr, 1, None, 0, 0, 0.0, nr)
+            L.q27o_attn_prep_rows(qkv.ctypes.data, qr + 2 * kvr, qn.ctypes.data, kn.ctypes.data, cs.ctypes.data,
+                                  sn.ctypes.data, 32, kc.ctypes.data, ks.ctypes.data, vc.ctypes.data, vs.ctypes.data,
+                                  G, qh.ctypes.data, NQ, NKV, HD, 1, 1e-6, L0, nr)
+            L.q27o_attn_rows(qh.ctypes.data, qkv.ctypes.data, qr + 2 * kvr, kc.ctypes.data, ks.ctypes.data,
+                             vc.ctypes.data, vs.ctypes.data, G, NQ, NKV, HD, 1, L0, nr, ao.ctypes.data, aq.ctypes.data,
+                             asc.ctypes.data)
+            L.q27o_proj_rows_epi(Wo2.ctypes.data, So2.ctypes.data, 1.0, H, att, aq.ctypes.data, att,
+                                 asc.ctypes.data, r1.ctypes.data, H, 0, hb.ctypes.data, 1, H, 1.0, nr)
+        tmin, tmed = best_of(attn_layer, reps)
+        b2 = ((qr + 2 * kvr) * H * i8 + nr * H * 4 + nr * (qr + 2 * kvr) * 2 + 2.0 * ctx * kvr * (1 + 4.0 / G) +
+              H * att * i8 + nr * H * 6)
+        out[f"config2_attention_ctx{L0}"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3),
+                                             "bytes": b2, "GB_s": round(b2 / tmin / 1e9, 2)}
+    out["host"] = host_info()
+    return out
+
+
+def gpu_config0(q27x, iters=50, copies=6):
+    """BASELINE config 0 on the GPU through the kernel tier (q27x_proj_rows, fp32 out): 3 rows x
+    [17408 x 5120]; launches cycle through `copies` weight copies (570 MB) so none hits the
+    Infinity Cache; device events around iters launches."""
+    import ctypes
+    c = CFG_SHAPES
+    H, I, nr = c["H"], c["I"], c["NR"]
+    rng = np.random.default_rng(SEED)
+    W = rng.integers(-127, 128, (I, H), dtype=np.int8)
+    WS = rng.uniform(1e-4, 2e-3, (I, H // 64)).astype(np.float32)
+    ws = [(q27x.DevBuf(array=W), q27x.DevBuf(array=WS)) for _ in range(copies)]
+    xq = q27x.DevBuf(array=rng.integers(-127, 128, (nr, H), dtype=np.int8))
+    xs = q27x.DevBuf(array=rng.uniform(1e-3, 5e-2, (nr, H // 16)).astype(np.float32))
+    y = q27x.DevBuf(nr * I * 4)
+    hs = [q27x.I8G(w.ptr, s.ptr, 1.0, I, H) for w, s in ws]
+
+    def launch(i):
+        q27x.call("q27x_proj_rows", ctypes.byref(hs[i % copies]), xq.ptr, H, xs.ptr, y.ptr, I, 0, None, 0, 0, 0.0, nr,
+                  None)
+    e0, e1, ms = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_float()
+    q27x.call("q27x_event_create", ctypes.byref(e0))
+    q27x.call("q27x_event_create", ctypes.byref(e1))
+    for i in range(3):
+        launch(i)
+    q27x.call("q27x_event_record", e0, None)
+    for i in range(iters):
+        launch(i + 3)
+    q27x.call("q27x_event_record", e1, None)
+    q27x.call("q27x_device_sync")
+    q27x.call("q27x_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+    for e in (e0, e1):
+        q27x.call("q27x_event_destroy", e)
+    for w, s in ws:
+        w.free()
+        s.free()
+    for b in (xq, xs, y):
+        b.free()
+    i8 = 1.0 + 4.0 / 64
+    b0 = I * H * i8 + nr * H * (1 + 4.0 / 16) + nr * I * 4
+    us = ms.value * 1e3 / iters
+    return {"us": round(us, 2), "bytes": b0, "GB_s": round(b0 / (us * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(b0 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 COPY_BYTES = 1 << 28       # calibration copy: 256 MiB read + 256 MiB written per launch
@@ -177,7 +378,7 @@ def main():
         os.environ["Q27X_GRAPH"] = "0"
     if args.gpus != 1:
         print(f"bench.py: this build runs the hot path on one GPU; --gpus {args.gpus} is not supported "
-              f"(the sharded design is described in DESIGN.md)", file=sys.stderr)
+              f"(nothing here is sharded across GPUs)", file=sys.stderr)
         return 2
     q27x = _load("q27x", os.path.join(PKG, "q27x.py"))
     if q27x.gpu_count() < 1:
@@ -191,7 +392,8 @@ def main():
         return 0
     K = args.k
     rounds_total = args.warmup + args.steps
-    ctx = args.prompt + rounds_total * (K + 1) + 128
+    attn_ctx = [1024, 4096, 16384]
+    ctx = max(args.prompt + rounds_total * (K + 1) + 128, max(attn_ctx) + 64)
     cfg = q27x.default_config(spec_k=K, ctx=ctx)
     t0 = time.time()
     eng = q27x.Engine(cfg, SEED)
@@ -207,7 +409,9 @@ def main():
     st = eng.run_rounds(args.steps, spec=True)
     nat_tps = st.committed / (st.decode_ms / 1e3)
     ms_per_round = st.decode_ms / st.rounds
-    log(f"natural: {st.rounds} rounds, {st.committed} committed, {nat_tps:.1f} tok/s, {ms_per_round:.3f} ms/round")
+    phases = {n: round(getattr(st, n + "_ms") / st.rounds, 4) for n in ("draft", "verify", "head", "tail")}
+    log(f"natural: {st.rounds} rounds, {st.committed} committed, {nat_tps:.1f} tok/s, {ms_per_round:.3f} ms/round; "
+        f"phases {phases}")
 
     # ---- plain greedy (comparator, and the forced-acceptance draft stream)
     eng.prefill(prompt)
@@ -244,17 +448,36 @@ def main():
         ms_, b_ = eng.bench_kernel(0, which, K + 1, 50)
         kernels[name] = {"us": round(ms_ * 1e3, 2), "GB_s": round(b_ / (ms_ / 1e3) / 1e9, 1)}
     log(f"kernels: {kernels}")
+
+    # ---- BASELINE configs 0-2 on the GPU (3 rows; config 0 through the kernel tier, 1 and 2 on the
+    # engine's own kernels; these overwrite the context's state, so they run last)
+    gpu_cfg = {"config0_projection": gpu_config0(q27x)}
+    ms_, b_ = eng.bench_mixer(False, args.prompt, 3, 48)
+    gpu_cfg["config1_gdn_layer"] = {"us": round(ms_ * 1e3, 2), "bytes": b_, "GB_s": round(b_ / (ms_ / 1e3) / 1e9, 1)}
+    for L0 in attn_ctx:
+        ms_, b_ = eng.bench_mixer(True, L0, 3, 48)
+        gpu_cfg[f"config2_attention_ctx{L0}"] = {"us": round(ms_ * 1e3, 2), "bytes": b_,
+                                                 "GB_s": round(b_ / (ms_ / 1e3) / 1e9, 1)}
+    for v in gpu_cfg.values():
+        v["frac_of_hbm_peak"] = round(v["GB_s"] / HBM_PEAK_GBS, 4)
+    log(f"configs 0-2 (GPU): {gpu_cfg}")
     eng.close()
     pg = prefill_gemm(q27x)
     log(f"prefill GEMM: {pg}")
 
     cpu = None
+    cpu_cfg = None
     if not args.no_cpu:
         q27o = _load("q27o", os.path.join(ROOT, "oracle", "q27o.py"))
         log("cpu baseline (oracle) ...")
-        cpu = cpu_baseline(cfg.as_dict(), q27o)
+        cpu = cpu_baseline(cfg.as_dict(), q27o, K)
         log(f"cpu: {cpu}")
+        cpu_cfg = cpu_configs(q27o, attn_ctx)
+        log(f"configs 0-2 (CPU): {cpu_cfg}")
 
+    workload = (f"BASELINE config {3 if (K == 2 and args.prompt == 1024) else 4 if K == 7 else 3}: random-init "
+                f"int8 27B (64 layers: 48 GDN + 16 attention), chained MTP K={K}, {args.prompt}-token prompt, "
+                f"natural acceptance")
     out = {
         "metric": "committed tok/s (MTP K=2, 27B int8, 1 GPU) + verify-step HBM GB/s",
         "value": round(nat_tps, 2),
@@ -263,22 +486,25 @@ def main():
         "ms_per_step": round(ms_per_round, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic: seeded random-init int8 weights, 1024 uniform-random prompt ids",
-        "config": {"workload": "BASELINE config 3: random-init int8 27B (64 layers: 48 GDN + 16 attention), "
-                               "chained MTP K=2, natural acceptance",
-                   "spec_k": K, "prompt": args.prompt, "hidden": cfg.hidden, "layers": cfg.n_layers},
+        "data": f"synthetic: seeded random-init int8 weights, {args.prompt} uniform-random prompt ids",
+        "config": {"workload": workload, "spec_k": K, "prompt": args.prompt, "hidden": cfg.hidden,
+                   "layers": cfg.n_layers},
         "acceptance": {"tokens_per_round": round(st.committed / st.rounds, 3), "rounds": st.rounds,
                        "p_ge": [round(st.acc_hist[j] / st.rounds, 3) for j in range(1, K + 1)]},
+        "round_phases_ms": phases,
         "forced_acceptance": forced,
         "plain_decode_tok_s": round(plain_tps, 2),
         "verify_step": {"ms": round(vms, 4), "bytes": vbytes, "GB_s": round(v_gbs, 1),
                         "frac_of_hbm_peak": round(v_gbs / HBM_PEAK_GBS, 4), "rows": K + 1},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_proj<3, 5, 1, 2, true, true, 16> (gate|up: post-norm prologue, W8A8, SwiGLU + quantize)",
+                     "kernel": f"k_proj<{K + 1}, 5, 1, 2, true, true, 16> (gate|up: post-norm prologue, W8A8, "
+                               f"SwiGLU + quantize)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
                      "bytes_per_launch": kbytes, "us_per_launch": round(kms * 1e3, 2)},
         "kernels": kernels,
+        "configs_gpu": gpu_cfg,
+        "configs_cpu": cpu_cfg,
         "prefill_s": round(prefill_s, 3),
         "prefill_gemm": pg,
         "cpu_baseline": cpu,

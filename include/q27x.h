@@ -356,6 +356,13 @@ int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
  * Infinity Cache; reports ms per launch and its algorithmic bytes (weights + scales + input rows +
  * outputs). Overwrites the context's activation scratch. */
 int q27x_bench_kernel(q27x_ctx* ctx, int layer, int which, int nr, int iters, float* ms, double* bytes);
+/* BASELINE configs 1 and 2 on the engine's own kernels: the mixer half of one layer (attn = 0:
+ * GDN -- in_qkv|in_z with the input-norm prologue, the GDN kernel, out_proj + residual; attn = 1:
+ * q|k|v with the prologue, attention over positions 0..pos+nr-1, o_proj + residual) for nr rows at
+ * position pos, averaged over iters launches that cycle through the layers of that kind; reports
+ * ms per layer and its algorithmic bytes. Overwrites the recurrent state, the KV cache and the
+ * activation scratch (prefill again before decoding). */
+int q27x_bench_mixer(q27x_ctx* ctx, int attn, int pos, int nr, int iters, float* ms, double* bytes);
 /* HBM calibration (no reference counterpart): a streaming read (mode 0) or plain copy (mode 1) of
  * `bytes` per launch, cycling through 1 GiB so no launch hits the 256 MB Infinity Cache; grid =
  * CUs x blocks_per_cu blocks of 256 threads, `unroll` (1, 2, 4, 8) 16-byte loads in flight per

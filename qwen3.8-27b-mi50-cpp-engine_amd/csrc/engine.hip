@@ -313,10 +313,9 @@ static NormArgs norm_of(q27x_ctx* x, const void* src, int src_bf16, const uint16
 }
 static void set_pre(ProjArgs& p, const NormArgs& n) { p.has_pre = 1; p.pre = n; }
 
-// run_layer_tp_nr on one card for nr rows: tokens d->vtok, positions d->pos.., GDN commits
-// d->gdn_npend pending rows. head: 0 = final residual rows only, 1 = + final norm, lm_head and
-// argmax into d->nx. hout: where the final residual rows go (default ctx->hfinal).
-static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
+// One layer of the verify pass (run_layer_tp_nr, src/q27_main.cpp:2271-2489) for nr rows; mlp = 0
+// stops after the mixer half (attention or GDN, then o_proj / out_proj + residual).
+static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
     const q27x_config& c = x->c;
     hipStream_t s = x->stream;
     Dctl* d = x->dctl;
@@ -324,7 +323,7 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
     int8_t* xa = x->xq;  float* sa = x->xs;
     int8_t* xact = x->xq + x->act_off;  float* sact = x->xs + x->act_off / 16;
     int rc;
-    for (int l = 0; l < c.n_layers; ++l) {
+    {
         LayerDev& Y = x->L[l];
         // input norm. Layer 0: the bf16 embedding rows, quantizing the bf16 normed rows
         // (q27_rmsnorm_quant_fp8); later layers: the fp32 residual r2, quantizing the fp32 normed
@@ -376,6 +375,7 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
             o.W = Y.out_proj.w; o.WS = Y.out_proj.s; o.rows = H; o.K = x->nz; o.xq = xa; o.xst = x->nz; o.xs = sa;
         }
         if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
+        if (!mlp) return Q27X_OK;
         // post norm of r1 (fp32, quantize the fp32 normed rows, h = bf16(r1)): gate|up prologue
         ProjArgs gu{};
         gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
@@ -390,6 +390,20 @@ static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
         dn.res = x->hid; dn.res_bf16 = 1; dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
         if ((rc = launch_proj(dn, EPI_STORE, nr, s))) return rc;
     }
+    return Q27X_OK;
+}
+
+// run_layer_tp_nr on one card for nr rows: tokens d->vtok, positions d->pos.., GDN commits
+// d->gdn_npend pending rows. head: 0 = final residual rows only, 1 = + final norm, lm_head and
+// argmax into d->nx. hout: where the final residual rows go (default ctx->hfinal).
+static int verify_pass(q27x_ctx* x, int nr, int head, uint16_t* hout) {
+    const q27x_config& c = x->c;
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    const int H = x->H;
+    int rc;
+    for (int l = 0; l < c.n_layers; ++l)
+        if ((rc = layer_pass(x, l, nr, 1))) return rc;
     // head (src/q27_main.cpp:2457-2481): final residual rows, final norm, lm_head, argmax
     NormArgs hn{};
     hn.x = x->xres; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->hid : nullptr;
@@ -1245,6 +1259,58 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
     *ms = t / (float)iters;
     *bytes = b;
     return rc;
+}
+
+// The mixer half of one verify layer (GDN -- in_qkv|in_z with its input-norm
+// prologue, the GDN kernel, out_proj + residual; config 2: attention -- q|k|v with its prologue,
+// the attention over positions 0 .. pos+nr-1, o_proj + residual), timed with device events over
+// iters launches that cycle through the layers of that kind (layer 0 excluded: its prologue reads
+// the embedding), so no launch finds its weights in the Infinity Cache. Runs at position pos; the
+// control block is restored afterwards, but the layers' recurrent state, KV cache and the
+// activation scratch are overwritten (prefill again before decoding).
+int q27x_bench_mixer(q27x_ctx* x, int attn, int pos, int nr, int iters, float* ms, double* bytes) {
+    if (!x || !x->loaded || nr < 1 || nr > kMaxRows || iters < 1 || !ms || !bytes || pos < 0 || pos + nr > x->c.ctx) {
+        set_error("q27x_bench_mixer: bad arguments");
+        return Q27X_E_ARG;
+    }
+    const q27x_config& c = x->c;
+    std::vector<int> ls;
+    for (int l = 1; l < c.n_layers; ++l)
+        if (x->L[l].is_attn == (attn ? 1 : 0)) ls.push_back(l);
+    if (ls.empty()) { set_error("q27x_bench_mixer: no layer of that kind"); return Q27X_E_ARG; }
+    Dctl h0;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    Q27X_HIP(hipMemcpy(&h0, x->dctl, sizeof h0, hipMemcpyDeviceToHost));
+    int rc = set_ints(x, 3, DOFF(pos), pos, DOFF(stop), 0, DOFF(gdn_npend), 0);
+    if (rc) return rc;
+    const double H = x->H, i8 = 1.0 + 4.0 / 64;
+    double b;
+    if (attn) {
+        const double qkvr = x->qr + 2 * x->kvr;
+        b = qkvr * H * i8 + nr * H * 4 + nr * qkvr * 2 +
+            2.0 * (pos + nr) * x->kvr * (1.0 + 4.0 / c.kv_group) + H * x->att * i8 + nr * H * 6;
+    } else {
+        const double rows = x->nqkv + x->nz;
+        b = rows * H * i8 + nr * H * 4 + nr * rows * 2 + 2.0 * c.gdn_vh * H * 2 + (double)x->nqkv * 4 * 2 +
+            2.0 * c.gdn_vh * 128 * 128 * 4 + H * x->nz * i8 + nr * H * 6;
+    }
+    hipEvent_t e0, e1;
+    Q27X_HIP(hipEventCreate(&e0));
+    Q27X_HIP(hipEventCreate(&e1));
+    for (int i = 0; i < 3 && !rc; ++i) rc = layer_pass(x, ls[(size_t)i % ls.size()], nr, 0);
+    if (!rc) rc = (int)hipEventRecord(e0, x->stream);
+    for (int i = 0; i < iters && !rc; ++i) rc = layer_pass(x, ls[(size_t)(i + 3) % ls.size()], nr, 0);
+    if (!rc) rc = (int)hipEventRecord(e1, x->stream);
+    float t = 0.0f;
+    if (!rc) rc = (int)hipEventSynchronize(e1);
+    if (!rc) rc = (int)hipEventElapsedTime(&t, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc) return rc < 0 ? rc : hip_fail((hipError_t)rc, "q27x_bench_mixer");
+    Q27X_HIP(hipMemcpy(x->dctl, &h0, sizeof h0, hipMemcpyHostToDevice));
+    *ms = t / (float)iters;
+    *bytes = b;
+    return Q27X_OK;
 }
 
 int q27x_debug_read(q27x_ctx* x, const char* name, int layer, void* dst, size_t bytes) {

@@ -104,6 +104,7 @@ _SIGS = {
     "q27x_bench_verify": ([VP, I, I, VP], I),
     "q27x_run_rounds": ([VP, I, I, VP], I),
     "q27x_bench_kernel": ([VP, I, I, I, I, VP, VP], I),
+    "q27x_bench_mixer": ([VP, I, I, I, I, VP, VP], I),
     "q27x_debug_read": ([VP, ctypes.c_char_p, I, VP, SZ], I),
     "q27x_bench_stream": ([I, SZ, I, I, I, VP], I),
 }
@@ -272,6 +273,12 @@ class Engine:
         for b in (dh, dt, dres, dtok):
             b.free()
         return tok, res
+
+    def bench_mixer(self, attn, pos, nr, iters):
+        ms = ctypes.c_float(0)
+        b = ctypes.c_double(0)
+        call("q27x_bench_mixer", self.ctx, 1 if attn else 0, pos, nr, iters, ctypes.byref(ms), ctypes.byref(b))
+        return ms.value, b.value
 
     def read(self, name, layer, dtype, count):
         out = np.empty(count, dtype=dtype)
