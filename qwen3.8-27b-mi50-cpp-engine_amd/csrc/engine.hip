@@ -45,7 +45,8 @@ struct LayerDev {
     Mat gu, down;
     Mat down4[4];   // MTP layer: down as four column slices of I/4 (src/q27_main.cpp:2605-2612)
     int8_t *kc = nullptr, *vc = nullptr; float *ks = nullptr, *vs = nullptr;
-    float* S = nullptr; uint16_t* conv_hist = nullptr; void* pend = nullptr;
+    float* S = nullptr; void* pend = nullptr;
+    uint16_t* conv_st = nullptr;   // per q|k|v channel: committed conv history + pending raw inputs (16 bf16)
 };
 
 // device control block (the Dev NR fields of src/q27_main.cpp:360-379 plus the round's tokens)
@@ -103,6 +104,7 @@ struct q27x_ctx {
     uint16_t *cat = nullptr, *mtp_hin = nullptr, *mtp_res = nullptr, *hprev = nullptr, *hcatch = nullptr;
     float* attn_work = nullptr; int max_splits = 0;
     float* sw_part = nullptr; unsigned* sw_cnt = nullptr;   // SwiGLU units split over blocks
+    float* gab = nullptr;          // GDN row scalars of the current layer: [2][kMaxRows][vh] decay, beta
     float* pval = nullptr; uint32_t* pidx = nullptr; int pstride = 4096;
     int32_t* out_ring = nullptr; int ring_cap = 0;
     int32_t* forced = nullptr; int forced_cap = 0;
@@ -330,10 +332,10 @@ static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
         // rows (q27_rmsnorm_hostss_fp8_b). Side outputs h = bf16(x), y = bf16(normed) (GDN a/b).
         NormArgs nin;
         if (l == 0) {
-            nin = norm_of(x, nullptr, 1, Y.in_norm, 1.0f, 1, x->hid, x->ynorm);
+            nin = norm_of(x, nullptr, 1, Y.in_norm, 1.0f, 1, x->hid, nullptr);
             nin.emb = x->emb; nin.tok = d->vtok;
         } else {
-            nin = norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, x->ynorm);
+            nin = norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, nullptr);
         }
         ProjArgs o{};
         o.alpha = 1.0f; o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
@@ -357,17 +359,21 @@ static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
         } else {
             // in_qkv | in_z (raw bf16 rows; the conv runs inside the GDN kernel)
             const int rows = Y.qkvz.rows;
+            // the q|k|v channels are convolved in the projection's epilogue (with the deferred
+            // commit of their history), the z rows stored raw
             ProjArgs p{};
             p.alpha = 1.0f; p.stop = &d->stop;
             p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = rows; p.K = H;
             p.y = x->pb; p.ystride = rows; p.out_bf16 = 1;
+            p.conv_w = Y.conv_w; p.conv_st = Y.conv_st; p.nconv = x->nqkv; p.npend_ptr = &d->gdn_npend;
+            // ... and the rows' (decay, beta) from the in_a / in_b dot products
+            p.in_a = Y.in_a; p.in_b = Y.in_b; p.A_log = Y.A_log; p.dt_bias = Y.dt_bias; p.ab_vh = c.gdn_vh;
+            p.ab_out = x->gab;
             set_pre(p, nin);
-            if ((rc = launch_proj(p, EPI_STORE, nr, s))) return rc;
+            if ((rc = launch_proj(p, EPI_CONV, nr, s))) return rc;
             GdnArgs g{};
             g.qkv = x->pb; g.qkv_stride = rows; g.z = x->pb + x->nqkv; g.z_stride = rows;
-            g.in_a = Y.in_a; g.in_b = Y.in_b; g.ynorm = x->ynorm; g.ystride = H; g.H = H;
-            g.A_log = Y.A_log; g.dt_bias = Y.dt_bias; g.norm_w = Y.gdn_norm;
-            g.conv_w = Y.conv_w; g.conv_hist = Y.conv_hist;
+            g.rowsc = x->gab; g.norm_w = Y.gdn_norm;
             g.S = Y.S; g.pend = Y.pend; g.npend_ptr = &d->gdn_npend;
             g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
             g.out = x->gout; g.out_stride = x->nz; g.xq = xa; g.xs = sa; g.stop = &d->stop;
@@ -667,7 +673,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     const size_t n_gdn = (size_t)(c.n_layers - n_attn);
     x->max_splits = (c.ctx + kSplit - 1) / kSplit;
     size_t sb = (n_attn + 1) * (2 * kvn + 2 * kvn / c.kv_group * 4 + 1024);
-    sb += n_gdn * ((size_t)c.gdn_vh * 128 * 128 * 4 + (size_t)x->nqkv * 3 * 2 + gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128) + 1024);
+    sb += n_gdn * ((size_t)c.gdn_vh * 128 * 128 * 4 + (size_t)x->nqkv * 32 + gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128) + 1024);
     const size_t R = kMaxRows;
     size_t maxk = (size_t)H;
     if ((size_t)x->nz > maxk) maxk = x->nz;
@@ -675,7 +681,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     const size_t xqn = R * (2 * maxk + I);
     const size_t pbn = R * (size_t)((x->qr + 2 * x->kvr) > (x->nqkv + x->nz) ? (x->qr + 2 * x->kvr) : (x->nqkv + x->nz));
     sb += sizeof(Dctl) + R * H * 2 * 4 + R * H * 4 + xqn + xqn / 16 * 4 + R * (size_t)x->nz * 2 + 256;
-    sb += (size_t)kSwMaxSplit * 16 * R * 4 + kSwMaxSplit * 4 + 512;
+    sb += (size_t)kSwMaxSplit * 16 * R * 4 + kSwMaxSplit * 4 + 512 + 2 * R * (size_t)c.gdn_vh * 4 + 256;
     sb += pbn * 2 + 2 * R * (size_t)x->att * 2 + R * 2 * H * 2 + R * H * 2 * 3 + H * 2;
     sb += attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4 + R * (size_t)x->pstride * 8;
     x->ring_cap = c.ctx + 64; x->forced_cap = c.ctx + 64; x->prompt_cap = c.ctx + 64;
@@ -693,7 +699,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
             Y.ks = (float*)salloc(x, kvn / c.kv_group * 4); Y.vs = (float*)salloc(x, kvn / c.kv_group * 4);
         } else {
             Y.S = (float*)salloc(x, (size_t)c.gdn_vh * 128 * 128 * 4);
-            Y.conv_hist = (uint16_t*)salloc(x, (size_t)x->nqkv * 3 * 2);
+            Y.conv_st = (uint16_t*)salloc(x, (size_t)x->nqkv * 32);
             Y.pend = salloc(x, gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128));
         }
     }
@@ -721,6 +727,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     x->attn_work = (float*)salloc(x, attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4);
     x->sw_part = (float*)salloc(x, (size_t)kSwMaxSplit * 16 * R * 4);
     x->sw_cnt = (unsigned*)salloc(x, kSwMaxSplit * 4);
+    x->gab = (float*)salloc(x, (size_t)2 * kMaxRows * c.gdn_vh * 4);
     x->pval = (float*)salloc(x, R * (size_t)x->pstride * 4);
     x->pidx = (uint32_t*)salloc(x, R * (size_t)x->pstride * 4);
     x->out_ring = (int32_t*)salloc(x, (size_t)x->ring_cap * 4);
@@ -881,7 +888,7 @@ int q27x_reset(q27x_ctx* x) {
             Q27X_HIP(hipMemsetAsync(Y.ks, 0, kvn / c.kv_group * 4, s)); Q27X_HIP(hipMemsetAsync(Y.vs, 0, kvn / c.kv_group * 4, s));
         } else {
             Q27X_HIP(hipMemsetAsync(Y.S, 0, (size_t)c.gdn_vh * 128 * 128 * 4, s));
-            Q27X_HIP(hipMemsetAsync(Y.conv_hist, 0, (size_t)x->nqkv * 3 * 2, s));
+            Q27X_HIP(hipMemsetAsync(Y.conv_st, 0, (size_t)x->nqkv * 32, s));
             Q27X_HIP(hipMemsetAsync(Y.pend, 0, gdn_pend_bytes(c.gdn_kh, c.gdn_vh, 128), s));
         }
     }
@@ -1201,11 +1208,16 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
         LayerDev& Y = x->L[l];
         ProjArgs p{};
         p.alpha = 1.0f; p.stop = &d->stop;
-        if (which == 0) {   // as in the verify pass: input-norm prologue over the fp32 residual rows
+        if (which == 0) {   // as in the verify pass: input-norm prologue, conv epilogue, GDN row scalars
             p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H;
             p.y = x->pb; p.ystride = Y.qkvz.rows; p.out_bf16 = 1;
-            set_pre(p, norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, x->ynorm));
-            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * p.rows * 2;
+            p.conv_w = Y.conv_w; p.conv_st = Y.conv_st; p.nconv = x->nqkv; p.npend_ptr = &d->gdn_npend;
+            p.in_a = Y.in_a; p.in_b = Y.in_b; p.A_log = Y.A_log; p.dt_bias = Y.dt_bias; p.ab_vh = c.gdn_vh;
+            p.ab_out = x->gab;
+            set_pre(p, norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, nullptr));
+            epi = EPI_CONV;
+            b = (double)p.rows * H * (1 + 4.0 / 64) + (double)nr * H * 4 + (double)nr * p.rows * 2 +
+                2.0 * c.gdn_vh * H * 2 + (double)x->nqkv * (8 + 2 * 32);
         } else if (which == 5) {   // in_qkv|in_z from pre-quantized rows (no prologue), for comparison
             p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = Y.qkvz.rows; p.K = H; p.xq = x->xq; p.xst = H; p.xs = x->xs;
             p.y = x->pb; p.ystride = Y.qkvz.rows; p.out_bf16 = 1;
@@ -1320,7 +1332,17 @@ int q27x_debug_read(q27x_ctx* x, const char* name, int layer, void* dst, size_t 
     const LayerDev* Y = (layer >= 0 && layer < x->c.n_layers) ? &x->L[layer] : &x->mtp;
     const size_t kvn = (size_t)x->c.ctx * x->kvr;
     if (!strcmp(name, "S") && Y->S) { src = Y->S; n = (size_t)x->c.gdn_vh * 128 * 128 * 4; }
-    else if (!strcmp(name, "conv_hist") && Y->conv_hist) { src = Y->conv_hist; n = (size_t)x->nqkv * 3 * 2; }
+    else if (!strcmp(name, "conv_hist") && Y->conv_st) {
+        // the committed conv history [nqkv][3] bf16, unpacked from the channel records
+        std::vector<uint16_t> rec((size_t)x->nqkv * 16), h3((size_t)x->nqkv * 3);
+        Q27X_HIP(hipStreamSynchronize(x->stream));
+        Q27X_HIP(hipMemcpy(rec.data(), Y->conv_st, rec.size() * 2, hipMemcpyDeviceToHost));
+        for (size_t ch = 0; ch < (size_t)x->nqkv; ++ch)
+            for (int i = 0; i < 3; ++i) h3[ch * 3 + i] = rec[ch * 16 + i];
+        const size_t nb = bytes < h3.size() * 2 ? bytes : h3.size() * 2;
+        memcpy(dst, h3.data(), nb);
+        return Q27X_OK;
+    }
     else if (!strcmp(name, "kc") && Y->kc) { src = Y->kc; n = kvn; }
     else if (!strcmp(name, "vc") && Y->vc) { src = Y->vc; n = kvn; }
     else if (!strcmp(name, "ks") && Y->ks) { src = Y->ks; n = kvn / x->c.kv_group * 4; }

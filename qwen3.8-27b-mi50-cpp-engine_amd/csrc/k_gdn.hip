@@ -1,27 +1,28 @@
 // k_gdn.hip -- gated-delta-rule verify of NR rows with deferred commit (R10-R12).
 //
-// Mathematics (src/q27_gdn.hip:206-372, gdn_step_body), per value head h, key head h/ratio:
+// Mathematics (src/q27_gdn.hip:206-372, gdn_step_body; the NR scan k_gdn_scan_tp, 464-592), per
+// value head h, key head h/ratio:
 //   q^ = q rsqrt(sum q^2 + 1e-6) / sqrt(128), k^ = k rsqrt(sum k^2 + 1e-6)
 //   beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt_bias))
 //   A = S^T k^, B = S^T q^, delta = (v - decay A) beta, mixed = decay B + delta (k^.q^)
-//   S <- decay S + k^ (x) delta
+//   S <- decay S + k^ (x) delta            (row by row, as the reference's scan)
 //   out = mixed rsqrt(mean(mixed^2) + eps) norm_w SiLU(z)  -> bf16 -> per-16 int8
 // Layout: S [VH][D=128][D] fp32 key-major. One 512-thread block per value head: thread (g, d)
 // holds key rows 32g..32g+31 of value column d (64 KiB of state per block in VGPRs). Every
 // global load of the block is issued before the first wait, so a call costs one memory round
-// trip plus on-chip work; the rows then run with one barrier each.
+// trip plus on-chip work; the rows then run with one barrier each. The rows are VALU-bound on the
+// block's CU (four operations per state element per row), which is why a head stays on one block:
+// splitting its columns over CUs would need a cross-block exchange for the output norm that costs
+// more than it saves at 3 rows.
+// Inputs arrive prepared: the engine convolves the q|k|v channels in the epilogue of the
+// in_qkv|in_z projection and computes each row's (decay, beta) there as well (the a/b dot products
+// and their transcendentals, k_proj), so `rowsc` holds them; the kernel-tier entry passes the a/b
+// logits instead (the scalars are then computed here) and convolves with k_gdn_conv first.
 // Rollback: instead of the reference's per-row snapshot banks (src/q27_main.cpp:2933-2941) the
 // state in HBM stays at the last committed position; each row's (k^, delta, decay) goes to
 // `pend`, and the next call first applies the rows that were accepted (npend), writes that state
 // back once, then continues. The commit uses exactly the update the row already received, so the
 // committed state is bit-identical to stepping the accepted rows one at a time.
-// Conv (CONV = 1, the engine path; k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439): the raw
-// projection rows are convolved here; the committed shift register lives in `pend`.
-// Every pending value in `pend` (k^, the raw q|k|v input channels, the shift register) is kept
-// per value head, although the q and k channels belong to the key head that several value heads
-// share: each block then reads and rewrites only its own entries (in place, each entry by one
-// thread, reads consumed before the first barrier), so no call has to wait for a shared word
-// before its loads or publish one after its stores.
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
@@ -30,25 +31,20 @@ namespace q27x {
 constexpr int kD = 128;
 constexpr int kNT = 512;              // threads per block: 4 key groups x 128 value dims
 constexpr int kJ = kD / 4;            // key rows per thread (32)
-constexpr int kStg = 8;               // staging loads per thread per batch
 
-// pend buffer: header (256 B, unused) | khat [R][VH][D] | delta [R][VH][D] | decay [R][VH] (fp32) |
-// raw [R][VH][3D] bf16 (each value head's q|k|v input channels of the pending rows; the
-// kernel-tier conv uses the same area as [R][NQKV]) | hist [VH][3D][4] bf16 (shift registers) |
-// work [R][NQKV] bf16 (conv output of the kernel-tier entry).
+// pend buffer: header (256 B) | khat [R][VH][D] | delta [R][VH][D] | decay [R][VH] (fp32) |
+// raw [R][NQKV] bf16 (pending conv inputs of the kernel-tier conv) | work [R][NQKV] bf16 (its
+// convolved rows).
 __host__ __device__ static inline size_t hdr_bytes() { return 256; }
 __host__ __device__ static inline size_t area_floats(int vh) {
     return (size_t)kMaxRows * (2 * (size_t)vh * kD + vh);
 }
 size_t gdn_pend_raw_offset(int kh, int vh, int d) {
     (void)kh; (void)d;
-    return hdr_bytes() + area_floats(vh) * 4;
-}
-static size_t gdn_hist_offset(int kh, int vh, int d) {
-    return gdn_pend_raw_offset(kh, vh, d) + (size_t)kMaxRows * vh * 3 * kD * 2;
+    return (hdr_bytes() + area_floats(vh) * 4 + 255) & ~(size_t)255;
 }
 static size_t gdn_work_offset(int kh, int vh, int d) {
-    return gdn_hist_offset(kh, vh, d) + (size_t)vh * 3 * kD * 4 * 2;
+    return gdn_pend_raw_offset(kh, vh, d) + (size_t)kMaxRows * (2 * kh + vh) * d * 2;
 }
 size_t gdn_pend_bytes(int kh, int vh, int d) {
     const size_t nqkv = (size_t)(2 * kh + vh) * d;
@@ -64,29 +60,25 @@ __device__ __forceinline__ PendArea pend_area(void* p, int vh) {
     return v;
 }
 
-template <int CONV, int FUSE_AB>
-__global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, size_t hist_off) {
+__global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
     const int h = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int d = t & (kD - 1), g = t >> 7;
     const int ratio = a.vh / a.kh, kk = h / ratio;
-    const bool owner = (h % ratio) == 0;           // writes the shared conv history output
     const int KD = a.kh * kD;
     const PendArea P = pend_area(a.pend, a.vh);     // pending rows: read first, then this call's rows
-    const int npend = a.npend_ptr ? *a.npend_ptr : a.npend_imm;
+    const int npend = a.npend_ptr ? ld_uniform(a.npend_ptr) : a.npend_imm;
 
     __shared__ __attribute__((aligned(16))) float skp[kMaxRows][kD];
     __shared__ float sdp[kMaxRows][kD], sdc[kMaxRows];
-    __shared__ float scv[kMaxRows][3 * kD];        // conv'd q | k | v of this head (bf16 values)
+    __shared__ float scv[kMaxRows][3 * kD];        // convolved q | k | v of this head (bf16 values)
     __shared__ float sz[kMaxRows][kD];
     __shared__ __attribute__((aligned(16))) float sq[kMaxRows][kD];
     __shared__ __attribute__((aligned(16))) float sk[kMaxRows][kD];
     __shared__ float pA[2][4][kD], pB[2][4][kD];
     __shared__ float smix[kMaxRows][kD];
-    __shared__ float red[kMaxRows][2][3];
-    __shared__ float sab[2][kMaxRows];
+    __shared__ float red[kMaxRows][2];
     __shared__ float srow[kMaxRows][4];          // per row: kq, beta, decay
-    extern __shared__ uint4 sy[];                  // FUSE_AB: in_a row | in_b row | nr ynorm rows
 
     // ================= phase A: every global load of the block =================
     // (a) committed state slice
@@ -103,61 +95,28 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
         pd[u] = (p < npend) ? P.delta[((size_t)p * a.vh + h) * kD + d] : 0.0f;
     }
     const float pdc = (t < npend) ? P.decay[(size_t)t * a.vh + h] : 0.0f;
-    // (c) channel t < 384 of this head: q (key head kk), k (kk), v (h)
+    // (c) channel t < 384 of this head: q (key head kk), k (kk), v (h); threads 384..511 the gate z
     const int cl = (t < 3 * kD) ? t : 0;
     const int ch = (cl < kD) ? kk * kD + cl : (cl < 2 * kD) ? KD + kk * kD + (cl - kD) : 2 * KD + h * kD + (cl - 2 * kD);
     uint16_t xr[kMaxRows];
 #pragma unroll
-    for (int n = 0; n < kMaxRows; ++n) xr[n] = (t < 3 * kD && n < nr) ? a.qkv[(size_t)n * a.qkv_stride + ch] : (uint16_t)0;
-    uint2 cw = make_uint2(0u, 0u), hs = make_uint2(0u, 0u);
-    uint16_t pr[kMaxRows];
-    // this value head's raw channels [R][VH][3D] and shift registers [VH][3D][4]
-    const size_t rstr = (size_t)a.vh * 3 * kD;
-    uint16_t* raw = (uint16_t*)((char*)a.pend + raw_off) + (size_t)h * 3 * kD;
-    uint16_t* hist = (uint16_t*)((char*)a.pend + hist_off) + (size_t)h * 3 * kD * 4;
-    if (CONV) {
-        if (t < 3 * kD) {
-            cw = *(const uint2*)(a.conv_w + (size_t)ch * 4);
-            hs = *(const uint2*)(hist + (size_t)cl * 4);
-        }
-#pragma unroll
-        for (int p = 0; p < kMaxRows; ++p) pr[p] = (t < 3 * kD && p < npend) ? raw[(size_t)p * rstr + cl] : (uint16_t)0;
-    }
-    // (d) gate rows z: threads 384..511
-    uint16_t zr[kMaxRows];
-#pragma unroll
     for (int n = 0; n < kMaxRows; ++n)
-        zr[n] = (t >= 3 * kD && n < nr) ? a.z[(size_t)n * a.z_stride + (size_t)h * kD + d] : (uint16_t)0;
-    // (e) a/b: the two weight rows and the nr normed input rows, staged through LDS
-    const int hc = a.H >> 3;                       // 8-element chunks per row
-    const int nstg = FUSE_AB ? (2 + nr) * hc : 0;
-    float ab_a = 0.0f, ab_b = 0.0f;
-    if (!FUSE_AB && t < nr) {
-        ab_a = a.a[(size_t)t * a.ab_stride + h];
-        ab_b = a.b[(size_t)t * a.ab_stride + h];
+        xr[n] = (n < nr) ? ((t < 3 * kD) ? a.qkv[(size_t)n * a.qkv_stride + ch] : a.z[(size_t)n * a.z_stride + (size_t)h * kD + d])
+                         : (uint16_t)0;
+    // (d) the row scalars: prepared (decay, beta), or the a/b logits
+    float r_a = 0.0f, r_b = 0.0f;
+    if (t < nr) {
+        if (a.rowsc) {
+            r_a = a.rowsc[(size_t)t * a.vh + h];                           // decay
+            r_b = a.rowsc[(size_t)(kMaxRows + t) * a.vh + h];              // beta
+        } else {
+            r_a = a.a[(size_t)t * a.ab_stride + h];
+            r_b = a.b[(size_t)t * a.ab_stride + h];
+        }
     }
-    const float Aexp = qexp(bf2f(a.A_log[h]));
-    const float dtb = bf2f(a.dt_bias[h]);
+    const float Aexp = a.rowsc ? 0.0f : qexp(bf2f(a.A_log[h]));
+    const float dtb = a.rowsc ? 0.0f : bf2f(a.dt_bias[h]);
     const float nw = bf2f(a.norm_w[(t & 63) + 64 * (wv & 1)]);
-    for (int base = 0; base < nstg; base += kStg * kNT) {
-        uint4 v[kStg];
-#pragma unroll
-        for (int u = 0; u < kStg; ++u) {
-            const int i = base + u * kNT + t;
-            v[u] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nstg) {
-                const int r = i / hc, c = i - r * hc;
-                const uint16_t* src = (r == 0) ? a.in_a + (size_t)h * a.H : (r == 1) ? a.in_b + (size_t)h * a.H
-                                                                                       : a.ynorm + (size_t)(r - 2) * a.ystride;
-                v[u] = *(const uint4*)(src + 8 * c);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kStg; ++u) {
-            const int i = base + u * kNT + t;
-            if (i < nstg) sy[i] = v[u];
-        }
-    }
 
     // ================= phase B: on-chip work =================
     if (stopped(a.stop)) return;                // read once the loads are in flight
@@ -167,41 +126,20 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
         if (p < npend) { skp[p][d] = pk[u]; sdp[p][d] = pd[u]; }
     }
     if (t < npend) sdc[t] = pdc;
-    if (!FUSE_AB && t < nr) { sab[0][t] = ab_a; sab[1][t] = ab_b; }
-    if (t < 3 * kD) {
-        if (CONV) {
-            uint16_t h0 = (uint16_t)(hs.x & 0xFFFFu), h1 = (uint16_t)(hs.x >> 16), h2 = (uint16_t)(hs.y & 0xFFFFu);
-#pragma unroll
-            for (int p = 0; p < kMaxRows; ++p)
-                if (p < npend) { h0 = h1; h1 = h2; h2 = pr[p]; }
-            *(uint2*)(hist + (size_t)cl * 4) = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2);
-            if (a.conv_hist && ((cl >= 2 * kD) || owner)) {
-                a.conv_hist[(size_t)ch * 3] = h0; a.conv_hist[(size_t)ch * 3 + 1] = h1;
-                a.conv_hist[(size_t)ch * 3 + 2] = h2;
-            }
-            const float w0 = __uint_as_float(cw.x << 16), w1 = __uint_as_float(cw.x & 0xFFFF0000u);
-            const float w2 = __uint_as_float(cw.y << 16), w3 = __uint_as_float(cw.y & 0xFFFF0000u);
-#pragma unroll
-            for (int n = 0; n < kMaxRows; ++n) {
-                if (n >= nr) break;
-                const uint16_t x = xr[n];
-                float acc = bf2f(h0) * w0;
-                acc = __builtin_fmaf(bf2f(h1), w1, acc);
-                acc = __builtin_fmaf(bf2f(h2), w2, acc);
-                acc = __builtin_fmaf(bf2f(x), w3, acc);
-                h0 = h1; h1 = h2; h2 = x;
-                raw[(size_t)n * rstr + cl] = x;
-                scv[n][cl] = bf2f(f2bf(qsilu(acc)));
-            }
-        } else {
-#pragma unroll
-            for (int n = 0; n < kMaxRows; ++n)
-                if (n < nr) scv[n][cl] = bf2f(xr[n]);
+    if (t < nr) {
+        if (a.rowsc) {
+            srow[t][1] = r_b;
+            srow[t][2] = r_a;
+        } else {   // beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt))
+            srow[t][1] = qsigmoid(r_b);
+            srow[t][2] = qexp(-(Aexp * qsoftplus(r_a + dtb)));
         }
-    } else {
+    }
 #pragma unroll
-        for (int n = 0; n < kMaxRows; ++n)
-            if (n < nr) sz[n][d] = bf2f(zr[n]);
+    for (int n = 0; n < kMaxRows; ++n) {
+        if (n >= nr) break;
+        if (t < 3 * kD) scv[n][cl] = bf2f(xr[n]);
+        else sz[n][d] = bf2f(xr[n]);
     }
     __syncthreads();
 
@@ -222,62 +160,26 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
 #pragma unroll
         for (int j = 0; j < kJ; ++j) Sw[(size_t)j * kD] = st[j];
     }
-    // a/b logits: pair (which, n) per wave, lane-chunk order (chunk c on lane c%64, fmaf per
-    // element), shfl tree, bf16 rounding as k_bf16_gemv2_tile (src/q27_util.hip:158-162)
-    // The row scalars come from two independent chains that run on different waves at once:
-    // waves 0..5 take the a/b logits and turn each into its row scalar at once (decay from a,
-    // beta from b); waves 6 and 7 take the q/k norms of whole rows (both 64-element halves, each
-    // reduced by the tree, summed first half + second half) and write q^, k^ and k^.q^.
-    constexpr int kAbW = 6;
-    if (wv < kAbW) {
-        if (FUSE_AB) {
-            for (int pi = wv; pi < 2 * nr; pi += kAbW) {
-                const int which = pi & 1, n = pi >> 1;
-                const uint4* wrow = sy + (size_t)which * hc;
-                const uint4* yrow = sy + (size_t)(2 + n) * hc;
-                float acc = 0.0f;
-                for (int c = lane; c < hc; c += 64) {
-                    const uint4 w = wrow[c], y = yrow[c];
-                    acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(y.x << 16), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(y.x & 0xFFFF0000u), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(y.y << 16), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(y.y & 0xFFFF0000u), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(y.z << 16), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(y.z & 0xFFFF0000u), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(y.w << 16), acc);
-                    acc = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(y.w & 0xFFFF0000u), acc);
-                }
-                acc = tree64(acc);
-                if (lane == 0) {   // beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt))
-                    const float v = bfr(acc);
-                    if (which) srow[n][1] = qsigmoid(v);
-                    else srow[n][2] = qexp(-(Aexp * qsoftplus(v + dtb)));
-                }
-            }
-        } else if (t < nr) {
-            srow[t][1] = qsigmoid(sab[1][t]);
-            srow[t][2] = qexp(-(Aexp * qsoftplus(sab[0][t] + dtb)));
-        }
-    } else {
-        for (int n = wv - kAbW; n < nr; n += 8 - kAbW) {
-            const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
-            const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
-            const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
-            const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
-            const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
-            const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
-            const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
-            const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
-            const float invk = rsqrt_cr(ssk + 1e-6f);
-            const float kh0 = k0 * invk, kh1 = k1 * invk;
-            sq[n][lane] = q0 * invq;
-            sq[n][64 + lane] = q1 * invq;
-            sk[n][lane] = kh0;
-            sk[n][64 + lane] = kh1;
-            P.khat[((size_t)n * a.vh + h) * kD + lane] = kh0;
-            P.khat[((size_t)n * a.vh + h) * kD + 64 + lane] = kh1;
-            if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
-        }
+    // q/k norms of whole rows, one wave per row: both 64-element halves, each reduced by the tree,
+    // summed first half + second half; q^, k^ and k^.q^
+    for (int n = wv; n < nr; n += kNT / 64) {
+        const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
+        const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
+        const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
+        const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
+        const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
+        const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
+        const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
+        const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
+        const float invk = rsqrt_cr(ssk + 1e-6f);
+        const float kh0 = k0 * invk, kh1 = k1 * invk;
+        sq[n][lane] = q0 * invq;
+        sq[n][64 + lane] = q1 * invq;
+        sk[n][lane] = kh0;
+        sk[n][64 + lane] = kh1;
+        P.khat[((size_t)n * a.vh + h) * kD + lane] = kh0;
+        P.khat[((size_t)n * a.vh + h) * kD + 64 + lane] = kh1;
+        if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
     }
     __syncthreads();
 
@@ -306,13 +208,15 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
         const float B = ((pB[n & 1][0][d] + pB[n & 1][1][d]) + pB[n & 1][2][d]) + pB[n & 1][3][d];
         const float delta = (vv - decay * A) * beta;
         const float mixed = __builtin_fmaf(delta, kq, decay * B);
+        if (n + 1 < nr) {                           // the state after the last row is never needed
 #pragma unroll
-        for (int j4 = 0; j4 < kJ; j4 += 4) {
-            const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
-            st[j4] = __builtin_fmaf(k4.x, delta, decay * st[j4]);
-            st[j4 + 1] = __builtin_fmaf(k4.y, delta, decay * st[j4 + 1]);
-            st[j4 + 2] = __builtin_fmaf(k4.z, delta, decay * st[j4 + 2]);
-            st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
+            for (int j4 = 0; j4 < kJ; j4 += 4) {
+                const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
+                st[j4] = __builtin_fmaf(k4.x, delta, decay * st[j4]);
+                st[j4 + 1] = __builtin_fmaf(k4.y, delta, decay * st[j4 + 1]);
+                st[j4 + 2] = __builtin_fmaf(k4.z, delta, decay * st[j4 + 2]);
+                st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
+            }
         }
         if (g == 0) {
             P.delta[((size_t)n * a.vh + h) * kD + d] = delta;
@@ -327,12 +231,12 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
     for (int n = wv >> 1; n < nr; n += 4) {
         const float mx = smix[n][e];
         const float r3 = tree64(mx * mx);
-        if (lane == 0) red[n][wv & 1][0] = r3;
+        if (lane == 0) red[n][wv & 1] = r3;
     }
     __syncthreads();
     for (int n = wv >> 1; n < nr; n += 4) {
         const float mx = smix[n][e];
-        const float inv = rsqrt_cr((red[n][0][0] + red[n][1][0]) * (1.0f / (float)kD) + a.eps);
+        const float inv = rsqrt_cr((red[n][0] + red[n][1]) * (1.0f / (float)kD) + a.eps);
         const float y = mx * inv * nw * qsilu(sz[n][e]);
         const uint16_t yb = f2bf(y);
         const size_t k = (size_t)n * a.out_stride + (size_t)h * kD + e;
@@ -350,34 +254,20 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr, size_t raw_off, 
 
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s) {
     if (a.d != kD || a.kh < 1 || a.vh % a.kh || nr < 1 || nr > kMaxRows || !a.qkv || !a.z || !a.S || !a.pend ||
-        !a.out || !a.A_log || !a.dt_bias || !a.norm_w) {
+        !a.out || !a.norm_w) {
         set_error("gdn: unsupported shape or null argument (d=%d kh=%d vh=%d nr=%d)", a.d, a.kh, a.vh, nr);
         return Q27X_E_SHAPE;
     }
     if (a.xq && a.out_stride % 16) { set_error("gdn: out_stride must be a multiple of 16"); return Q27X_E_ARG; }
-    const int fuse = (a.in_a && a.in_b && a.ynorm) ? 1 : 0;
-    if (!fuse && (!a.a || !a.b)) { set_error("gdn: a/b logits or in_a/in_b weights required"); return Q27X_E_ARG; }
-    if (fuse && (a.H < 8 || (a.H & 7) || a.H > 8192)) { set_error("gdn: H=%d unsupported for the fused a/b", a.H); return Q27X_E_SHAPE; }
-    if (a.conv_w && ((size_t)a.conv_w & 7)) { set_error("gdn: conv_w must be 8-byte aligned"); return Q27X_E_ARG; }
-    const size_t lds = fuse ? (size_t)(2 + nr) * a.H * 2 : 0;
-    const size_t ro = gdn_pend_raw_offset(a.kh, a.vh, a.d), ho = gdn_hist_offset(a.kh, a.vh, a.d);
-    if (a.conv_w) {
-        if (fuse) hipLaunchKernelGGL((k_gdn<1, 1>), dim3(a.vh), dim3(kNT), lds, s, a, nr, ro, ho);
-        else hipLaunchKernelGGL((k_gdn<1, 0>), dim3(a.vh), dim3(kNT), 0, s, a, nr, ro, ho);
-    } else {
-        if (fuse) hipLaunchKernelGGL((k_gdn<0, 1>), dim3(a.vh), dim3(kNT), lds, s, a, nr, ro, ho);
-        else hipLaunchKernelGGL((k_gdn<0, 0>), dim3(a.vh), dim3(kNT), 0, s, a, nr, ro, ho);
+    if (!a.rowsc && (!a.a || !a.b || !a.A_log || !a.dt_bias)) {
+        set_error("gdn: the row scalars or the a/b logits with A_log and dt_bias are required");
+        return Q27X_E_ARG;
     }
+    hipLaunchKernelGGL(k_gdn, dim3(a.vh), dim3(kNT), 0, s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
-int gdn_set_lds_limit() {
-    // the fused a/b stage of 8 rows at H = 8192 needs 160 KiB of dynamic LDS at most
-    const int mx = 160 * 1024 - 48 * 1024;
-    Q27X_HIP(hipFuncSetAttribute((const void*)k_gdn<1, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-    Q27X_HIP(hipFuncSetAttribute((const void*)k_gdn<0, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
-    return Q27X_OK;
-}
+int gdn_set_lds_limit() { return Q27X_OK; }
 
 // conv + SiLU with the deferred shift-register commit as a standalone kernel (the kernel-tier
 // entry; the engine convolves inside k_gdn)
@@ -418,7 +308,8 @@ int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_
 // Commit only: apply the npend pending rows of `pend` to S (the update each row already received,
 // the same fmaf as k_gdn's commit), write S back, and leave nothing pending. One block per value
 // head, thread (g, d) holds key rows 32 g .. 32 g + 31 of value column d.
-__global__ __launch_bounds__(kNT) void k_gdn_commit(float* __restrict__ S, const void* pend, int vh, int npend) {
+constexpr int kCommitT = kNT;        // commit kernel: thread (g, d), key group g < 4, column d < 128
+__global__ __launch_bounds__(kCommitT) void k_gdn_commit(float* __restrict__ S, const void* pend, int vh, int npend) {
     const int h = blockIdx.x, t = threadIdx.x, d = t & (kD - 1), g = t >> 7;
     const PendArea P = pend_area(const_cast<void*>(pend), vh);
     float* Sp = S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
@@ -485,7 +376,7 @@ extern "C" int q27x_gdn_commit(float* S, uint16_t* conv_hist, void* pend, int np
     int rc = launch_gdn_conv(nullptr, 0, nullptr, 0, nconv, nullptr, conv_hist, pend_raw, nullptr, npend, 0,
                              (hipStream_t)s);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_gdn_commit, dim3(vh), dim3(kNT), 0, (hipStream_t)s, S, (const void*)pend, vh, npend);
+    hipLaunchKernelGGL(k_gdn_commit, dim3(vh), dim3(kCommitT), 0, (hipStream_t)s, S, (const void*)pend, vh, npend);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

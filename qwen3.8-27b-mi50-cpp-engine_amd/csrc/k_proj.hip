@@ -82,6 +82,9 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
 constexpr int kSwRows = 288;     // SwiGLU rows one block may hold: 32 F + 8 (quarters per block)
 template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE, int NW>
 __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
+    constexpr bool CV = (EPI == EPI_CONV);
+    constexpr bool ST = (EPI == EPI_STORE || CV);
+    static_assert(!CV || RPW == 1, "the conv epilogue takes one row per group");
     constexpr int SL = NSTEP * 64;
     constexpr int NT = NW * 64;
     constexpr int NSTG = (NR * SL + NT - 1) / NT;      // staging loads per thread
@@ -92,6 +95,8 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     __shared__ float ssc[NR * SL];
     __shared__ float sacc[(EPI == EPI_SWIGLU) ? kSwRows * NR : 1];
     __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
+    // EPI_CONV: the bf16 normalized input rows of the blocks that compute GDN row scalars
+    __shared__ __attribute__((aligned(16))) uint16_t sybf[CV ? NR * NSTEP * 1024 : 1];
     // The round's stop flag is read once the prologue's loads are in flight (before any store),
     // so its read does not add a memory round trip in front of them.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -121,7 +126,6 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     __shared__ float s_scale[(EPI == EPI_SWIGLU) ? (kSwRows / 32) * NR : 1];
     if constexpr (EPI == EPI_SWIGLU)
         for (int i = threadIdx.x; i < kSwRows / 8; i += NT) s_gcnt[i] = 0u;
-    auto valid = [&](int j) __attribute__((always_inline)) { return j < nrb; };
     auto row_of = [&](int j, int r) __attribute__((always_inline)) {
         if constexpr (EPI == EPI_SWIGLU) {
             if (j >= 8 * myq) return (bi + nb * ((j - 8 * myq) >> 5)) * 32 + ((j - 8 * myq) & 31);
@@ -133,6 +137,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             else return (bi * NW + (j % NW) + (j / NW) * nw) * RPW + r;
         }
     };
+    auto valid = [&](int j) __attribute__((always_inline)) { return j < nrb; };
     uint4 W[RPW][NSTEP];
     float S[RPW][NSTEP];
     // Loads are issued on every path: a group past the wave's last (ok == false) reads the first
@@ -170,7 +175,9 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         if constexpr (EARLY) prefetch();
         __builtin_amdgcn_sched_barrier(0);
         if (stopped(a.stop)) return;
-        pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0);
+        uint16_t* ylds = nullptr;
+        if constexpr (CV) ylds = (bi < 2 * a.ab_vh) ? sybf : nullptr;
+        pn.finish(a.pre, (uint32_t*)sx, ssc, SL, wsum, blockIdx.x == 0, ylds);
         if constexpr (!EARLY) prefetch();
     } else if constexpr (FULL) {
         // activation stage by LDS DMA (global_load_lds: each lane's 16-byte code word and 4-byte
@@ -229,6 +236,62 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         if (stopped(a.stop)) return;
     }
     if constexpr (PRE || !FULL) __syncthreads();
+    int npend_cv = 0;
+    if constexpr (CV) npend_cv = ld_uniform(a.npend_ptr);
+    // GDN row scalars (EPI_CONV): wave 0 of blocks b < 2 ab_vh, before its rows. The bf16 GEMV of
+    // one in_a / in_b row: chunk c of 8 elements on lane c % 64 in ascending c, fmaf per element,
+    // shfl tree, bf16 rounding (k_bf16_gemv2_tile, src/q27_util.hip:114-167); then, lane n for row
+    // n, the scalar of src/q27_gdn.hip:206-372.
+    if constexpr (CV) {
+        if (wave == 0 && bi < 2 * a.ab_vh) {
+            const int which = bi & 1, head = bi >> 1;
+            const uint16_t* wrow = (which ? a.in_b : a.in_a) + (size_t)head * K;
+            constexpr int NC = NSTEP * 2;              // 8-element chunks per lane
+            float acc[NR];
+#pragma unroll
+            for (int n = 0; n < NR; ++n) acc[n] = 0.0f;
+#pragma unroll
+            for (int c0 = 0; c0 < NC; c0 += 5) {
+                uint4 wv4[5];
+#pragma unroll
+                for (int i = 0; i < 5; ++i)
+                    if (c0 + i < NC) wv4[i] = *(const uint4*)(wrow + 8 * (lane + 64 * (c0 + i)));
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    if (c0 + i >= NC) break;
+                    const uint4 w = wv4[i];
+                    const int cc = lane + 64 * (c0 + i);
+#pragma unroll
+                    for (int n = 0; n < NR; ++n) {
+                        const uint4 y = *(const uint4*)(sybf + (size_t)n * K + 8 * cc);
+                        float v = acc[n];
+                        v = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(y.x << 16), v);
+                        v = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(y.x & 0xFFFF0000u), v);
+                        v = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(y.y << 16), v);
+                        v = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(y.y & 0xFFFF0000u), v);
+                        v = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(y.z << 16), v);
+                        v = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(y.z & 0xFFFF0000u), v);
+                        v = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(y.w << 16), v);
+                        v = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(y.w & 0xFFFF0000u), v);
+                        acc[n] = v;
+                    }
+                }
+            }
+            float mine = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NR; ++n) {
+                const float v = bcast0(tree64(acc[n]));
+                if (lane == n) mine = v;
+            }
+            if (lane < NR) {
+                const float v = bfr(mine);
+                float r;
+                if (which) r = qsigmoid(v);
+                else r = qexp(-(qexp(bf2f(a.A_log[head])) * qsoftplus(v + bf2f(a.dt_bias[head]))));
+                a.ab_out[(size_t)(which * kMaxRows + lane) * a.ab_vh + head] = r;
+            }
+        }
+    }
     const int vi = lane / LPV;                         // the value this lane holds after the tree
     const bool holder = (lane % LPV) == 0 && vi < V;
     const int hn = (vi < V) ? vi / RPW : NR - 1, hr = (vi < V) ? vi - (vi / RPW) * RPW : 0;
@@ -288,46 +351,57 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             __builtin_amdgcn_s_waitcnt(0);
         }
     };
-    for (int j = wave; j < nrb;) {
-        unsigned jn = 0u;
-        if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const int jnext = NW + __builtin_amdgcn_readfirstlane((int)jn);
-        const bool more = valid(jnext);
-        const int rg_next = __builtin_amdgcn_readfirstlane(row_of(jnext, 0));
-        // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use; loaded
-        // (from a harmless address) also when there is none, for the reason given at ld
-        size_t ridx = 0;
-        uint32_t rw = 0u;
-        if constexpr (EPI == EPI_STORE) {
-            int row = row_of(j, hr);
-            row = row < a.rows ? row : a.rows - 1;
-            ridx = (size_t)hn * a.rstride + row;
-            rw = *(resw ? resw + (a.res_bf16 ? (ridx >> 1) : ridx) : (const uint32_t*)a.W);
+    // Conv epilogue of channel r0 (k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439): the NR raw values
+    // x_n = bf16(v_n) (v_n in lane n * LPV) follow the committed history (the record's history
+    // and the first npend pending raw inputs) in one sequence h0 h1 h2 x_0 .. x_{NR-1}; lane n
+    // convolves row n's window (the three values before x_n, then x_n: acc = s0 w0 + s1 w1 + s2 w2
+    // + x_n w3, an fmaf chain), out = bf16(SiLU(acc)), and stores it; lane 0 rewrites the record
+    // (committed history, this call's raw inputs as the new pending ones).
+    auto conv_epilogue = [&](float tv, uint32_t cvd, int r0, int ln) __attribute__((always_inline)) {
+        uint32_t dw[10];
+#pragma unroll
+        for (int i = 0; i < 10; ++i) dw[i] = (uint32_t)__builtin_amdgcn_readlane((int)cvd, i);
+        uint32_t h0 = dw[0] & 0xFFFFu, h1 = dw[0] >> 16, h2 = dw[1] & 0xFFFFu;
+#pragma unroll
+        for (int p = 0; p < kMaxRows; ++p)
+            if (p < npend_cv) { h0 = h1; h1 = h2; h2 = (dw[2 + (p >> 1)] >> (16 * (p & 1))) & 0xFFFFu; }
+        uint32_t seq[NR + 3];
+        seq[0] = h0; seq[1] = h1; seq[2] = h2;
+#pragma unroll
+        for (int n = 0; n < NR; ++n) seq[3 + n] = f2bf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(tv), n * LPV)));
+        uint32_t s0 = seq[0], s1 = seq[1], s2 = seq[2], s3 = seq[3];
+#pragma unroll
+        for (int m = 1; m < NR; ++m)
+            if (ln == m) { s0 = seq[m]; s1 = seq[m + 1]; s2 = seq[m + 2]; s3 = seq[m + 3]; }
+        const float w0 = __uint_as_float(dw[8] << 16), w1 = __uint_as_float(dw[8] & 0xFFFF0000u);
+        const float w2 = __uint_as_float(dw[9] << 16), w3 = __uint_as_float(dw[9] & 0xFFFF0000u);
+        float cacc = __uint_as_float(s0 << 16) * w0;
+        cacc = __builtin_fmaf(__uint_as_float(s1 << 16), w1, cacc);
+        cacc = __builtin_fmaf(__uint_as_float(s2 << 16), w2, cacc);
+        cacc = __builtin_fmaf(__uint_as_float(s3 << 16), w3, cacc);
+        if (ln < NR) ((uint16_t*)a.y)[(size_t)ln * a.ystride + r0] = f2bf(qsilu(cacc));
+        if (ln == 0) {
+            uint32_t rec[8] = { h0 | (h1 << 16), h2, 0u, 0u, 0u, 0u, 0u, 0u };
+#pragma unroll
+            for (int n = 0; n < NR; ++n) rec[2 + (n >> 1)] |= seq[3 + n] << (16 * (n & 1));
+            uint4* d = (uint4*)(a.conv_st + (size_t)r0 * 16);
+            d[0] = make_uint4(rec[0], rec[1], rec[2], rec[3]);
+            d[1] = make_uint4(rec[4], rec[5], rec[6], rec[7]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        float acc[P];
-#pragma unroll
-        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NSTEP; ++t) {
-            const int s = t * 64 + lane;
-#pragma unroll
-            for (int n = 0; n < NR; ++n) {
-                const uint4 xa = sx[n * SL + s];
-                const float sa = ssc[n * SL + s];
-#pragma unroll
-                for (int r = 0; r < RPW; ++r) {
-                    const int d = dot16(W[r][t], xa);
-                    acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
-                }
+    };
+    // the row group's epilogue: store (+ residual, conv) or SwiGLU accumulation
+    auto emit = [&](int j, float tv, uint32_t rw, size_t ridx, uint32_t cvd) __attribute__((always_inline)) {
+        bool conv_row = false;
+        if constexpr (CV) {
+            const int r0 = row_of(j, 0);                 // wave-uniform: one row per group
+            if (r0 < a.nconv) {
+                conv_row = true;
+                conv_epilogue(tv, cvd, r0, lane);
             }
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) ld(rg_next, r, t, more);
         }
-        const float tv = tree_t<P>(acc, lane) * a.alpha;
-        if constexpr (EPI == EPI_STORE) {
+        if constexpr (ST) {
             const int row = row_of(j, hr);
-            if (holder && row < a.rows) {
+            if (!conv_row && holder && row < a.rows) {
                 float v = tv;
                 if (resw) {
                     const float rv = a.res_bf16 ? bf2f((uint16_t)((ridx & 1) ? (rw >> 16) : (rw & 0xFFFFu)))
@@ -354,6 +428,55 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
                 finish(j);
             }
         }
+    };
+    for (int j = wave; j < nrb;) {
+        unsigned jn = 0u;
+        if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int jnext = NW + __builtin_amdgcn_readfirstlane((int)jn);
+        const bool more = valid(jnext);
+        const int rg_next = __builtin_amdgcn_readfirstlane(row_of(jnext, 0));
+        // residual: one raw dword per lane (bf16 pairs or fp32), decoded at the use; loaded
+        // (from a harmless address) also when there is none, for the reason given at ld
+        size_t ridx = 0;
+        uint32_t rw = 0u;
+        if constexpr (ST) {
+            int row = row_of(j, hr);
+            row = row < a.rows ? row : a.rows - 1;
+            ridx = (size_t)hn * a.rstride + row;
+            rw = *(resw ? resw + (a.res_bf16 ? (ridx >> 1) : ridx) : (const uint32_t*)a.W);
+        }
+        // conv channel: its record (8 dwords) and its 4 tap weights (2 dwords), one dword in each
+        // of lanes 0..9, requested with the residual word
+        uint32_t cvd = 0u;
+        if constexpr (CV) {
+            const int r0 = row_of(j, 0);
+            const int rc = r0 < a.nconv ? r0 : 0;
+            const uint32_t* rec = (const uint32_t*)a.conv_st + (size_t)rc * 8;
+            const uint32_t* cw = (const uint32_t*)a.conv_w + (size_t)rc * 2;
+            cvd = *((lane < 8) ? rec + lane : (lane < 10) ? cw + (lane - 8) : rec);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[P];
+#pragma unroll
+        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+            const int s = t * 64 + lane;
+#pragma unroll
+            for (int n = 0; n < NR; ++n) {
+                const uint4 xa = sx[n * SL + s];
+                const float sa = ssc[n * SL + s];
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const int d = dot16(W[r][t], xa);
+                    acc[n * RPW + r] = __builtin_fmaf((float)d, S[r][t] * sa, acc[n * RPW + r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) ld(rg_next, r, t, more);
+        }
+        const float tv = tree_t<P>(acc, lane) * a.alpha;
+        emit(j, tv, rw, ridx, cvd);
         j = jnext;
     }
     if constexpr (EPI == EPI_SWIGLU) {
@@ -417,6 +540,10 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
         const int nwv = ngroups < wmax ? ngroups : wmax;
         grid = (nwv + NW - 1) / NW;
     }
+    if (EPI == EPI_CONV && a.ab_vh && grid < 2 * a.ab_vh) {
+        set_error("proj: %d blocks cannot hold the %d GDN row-scalar rows", grid, 2 * a.ab_vh);
+        return Q27X_E_SHAPE;
+    }
     hipLaunchKernelGGL((k_proj<NR, NSTEP, RPW, EPI, FULL, PRE, NW>), dim3(grid), dim3(NW * 64), 0, s, a);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
@@ -445,6 +572,8 @@ static int route_k(const ProjArgs& a, hipStream_t s) {
         if (ns == 1) return run_proj<NR, 1, EPI, FULL, false>(a, s);
         if (ns == 5) return run_proj<NR, 5, EPI, FULL, false>(a, s);
         return -2;
+    } else if constexpr (EPI == EPI_CONV) {
+        return -2;                                     // prologue kernels only
     } else {
         switch (ns) {
             case 1: return run_proj<NR, 1, EPI, FULL, false>(a, s);
@@ -478,6 +607,7 @@ static int route_nr(const ProjArgs& a, int nr, hipStream_t s) {
 static int route(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     const bool full = (a.K & 1023) == 0;
     if (epi == EPI_SWIGLU) return full ? route_nr<EPI_SWIGLU, true>(a, nr, s) : -2;   // K = 1024 k only
+    if (epi == EPI_CONV) return (full && a.has_pre) ? route_nr<EPI_CONV, true>(a, nr, s) : -2;   // the GDN input
     return full ? route_nr<EPI_STORE, true>(a, nr, s) : route_nr<EPI_STORE, false>(a, nr, s);
 }
 
@@ -500,6 +630,16 @@ int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     }
     if (a.res && ((size_t)a.res & 3)) { set_error("proj: residual must be 4-byte aligned"); return Q27X_E_ARG; }
     if (epi == EPI_SWIGLU && (a.rows & 31)) { set_error("proj: SwiGLU rows %d not a multiple of 32", a.rows); return Q27X_E_SHAPE; }
+    if (epi == EPI_CONV && (!a.conv_w || !a.conv_st || !a.npend_ptr || a.nconv < 0 || a.nconv > a.rows || !a.out_bf16 ||
+                            a.res || ((size_t)a.conv_w & 7) || ((size_t)a.conv_st & 15))) {
+        set_error("proj: conv epilogue needs conv_w, conv_st, npend, bf16 out and no residual");
+        return Q27X_E_ARG;
+    }
+    if (epi == EPI_CONV && a.ab_vh && (!a.in_a || !a.in_b || !a.A_log || !a.dt_bias || !a.ab_out || a.ab_vh > 128 ||
+                                       ((size_t)a.in_a & 15) || ((size_t)a.in_b & 15))) {
+        set_error("proj: GDN row scalars need in_a, in_b, A_log, dt_bias and ab_out (ab_vh <= 128)");
+        return Q27X_E_ARG;
+    }
     int rc;
     if (epi == EPI_STORE && a.K > 8192 && nr > 4) {   // LDS stage limit: two launches of <= 4 rows
         ProjArgs b = a;

@@ -35,7 +35,7 @@ struct NormArgs {
     unsigned long long* stamp;                    // optional: block 0 stores the wall clock at its start
 };
 // ---------------------------------------------------------------- projection
-enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2 };
+enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2, EPI_CONV = 3 };
 struct ProjArgs {
     const int8_t* W; const float* WS; int rows; int K; float alpha;
     const int8_t* xq; int xst; const float* xs;
@@ -47,6 +47,20 @@ struct ProjArgs {
     // floats, kSwMaxSplit counters that start at zero and are left at zero)
     int8_t* act_q; float* act_s; int act_stride; float gscale;
     float* sw_part; unsigned* sw_cnt;
+    // EPI_CONV (the GDN in_qkv|in_z projection, bf16 out): rows < nconv are the q|k|v channels,
+    // each convolved by the wave that computes it -- causal depthwise conv of 4 taps over
+    // (committed history, the call's rows), SiLU, bf16 -- with the history's deferred commit:
+    // conv_st[row] is a 16 x bf16 record (committed history h0 h1 h2, pad, the last call's raw
+    // inputs r0..r7, pad); the first *npend_ptr of those are committed before the call's rows.
+    // Rows >= nconv are stored as EPI_STORE.
+    const uint16_t* conv_w; uint16_t* conv_st; int nconv; const int* npend_ptr;
+    // EPI_CONV also prepares the GDN row scalars: wave 0 of block b < 2 ab_vh takes, before its
+    // rows, the bf16 dot product of weight row b/2 of in_a (b even) or in_b (b odd) with each bf16
+    // normalized input row (lane-chunk order of the bf16 GEMV), rounds it to bf16 and stores
+    // decay = exp(-exp(A_log) softplus(a + dt_bias)) or beta = sigmoid(b) into
+    // ab_out [2][kMaxRows][ab_vh] (decay rows, then beta rows). ab_vh = 0: none.
+    const uint16_t* in_a; const uint16_t* in_b; const uint16_t* A_log; const uint16_t* dt_bias;
+    int ab_vh; float* ab_out;
     const int* stop;             // early exit when *stop != 0
     // norm prologue: instead of xq/xs, every block stages the RMSNorm + quantize of the raw rows
     // described by `pre` (K = pre.n); block 0 also writes pre's side outputs (hcopy, y, xq/xs)
@@ -78,13 +92,11 @@ int launch_swiglu(const float* g, const float* u, int stride, int8_t* xq, float*
 
 // ---------------------------------------------------------------- GDN
 struct GdnArgs {
-    const uint16_t* qkv; int qkv_stride;          // raw (conv_w set) or conv'd q|k|v rows (bf16)
+    const uint16_t* qkv; int qkv_stride;          // convolved q|k|v rows (bf16)
     const uint16_t* z; int z_stride;
-    const float* a; const float* b; int ab_stride; // precomputed a/b (fp32), or
-    const uint16_t* in_a; const uint16_t* in_b;  // bf16 weights [vh][H] with
-    const uint16_t* ynorm; int ystride; int H;    // the bf16 normed rows (a/b fused)
+    const float* rowsc;                            // prepared row scalars [2][kMaxRows][vh]: decay, beta; or
+    const float* a; const float* b; int ab_stride; // the a/b logits (fp32) with A_log and dt_bias
     const uint16_t* A_log; const uint16_t* dt_bias; const uint16_t* norm_w;
-    const uint16_t* conv_w; uint16_t* conv_hist;  // conv in the kernel: weights, committed-history mirror
     float* S; void* pend; const int* npend_ptr; int npend_imm;
     int kh, vh, d; float eps;
     uint16_t* out; int out_stride; int8_t* xq; float* xs;

@@ -169,20 +169,23 @@ struct PreNorm {
     // sxw: the LDS code stage as 32-bit words ([NR][SL] slabs of 4 words); ssc: [NR][SL] scales;
     // wsum: __shared__ float[RPG][GR][4]. Block 0 (writer) also stores the side outputs; the other
     // blocks run a copy without them, and the bf16 rounding of the normalized values is compiled
-    // in only where it is used (side output y or quant_bf16), about halving their instructions.
+    // in only where it is used (side output y, quant_bf16, or ylds), about halving their
+    // instructions. ylds (optional): LDS rows [NR][n] that receive the bf16 normalized values.
     __device__ __forceinline__ void finish(const NormArgs& a, uint32_t* sxw, float* ssc, int SL,
-                                           float (*wsum)[GR][4], bool writer) {
-        if (writer) {
-            if (a.quant_bf16) fin<true, true>(a, sxw, ssc, SL, wsum);
-            else fin<true, false>(a, sxw, ssc, SL, wsum);
+                                           float (*wsum)[GR][4], bool writer, uint16_t* ylds = nullptr) {
+        if (writer || ylds) {
+            if (a.quant_bf16) fin<true, true>(a, sxw, ssc, SL, wsum, writer, ylds);
+            else fin<true, false>(a, sxw, ssc, SL, wsum, writer, ylds);
         } else {
-            if (a.quant_bf16) fin<false, true>(a, sxw, ssc, SL, wsum);
-            else fin<false, false>(a, sxw, ssc, SL, wsum);
+            if (a.quant_bf16) fin<false, true>(a, sxw, ssc, SL, wsum, false, nullptr);
+            else fin<false, false>(a, sxw, ssc, SL, wsum, false, nullptr);
         }
     }
-    template <bool WR, bool QB>
+    // YB: the bf16 values are formed (the writer's side outputs, or ylds)
+    template <bool YB, bool QB>
     __device__ __forceinline__ void fin(const NormArgs& a, uint32_t* sxw, float* ssc, int SL,
-                                        float (*wsum)[GR][4]) {
+                                        float (*wsum)[GR][4], bool writer, uint16_t* ylds) {
+        constexpr bool WR = YB;
         const int t = threadIdx.x & 255, tg = threadIdx.x >> 8, lane = t & 63, wv = t >> 6;
         constexpr int n = NCH * 1024;
 #pragma unroll
@@ -193,7 +196,7 @@ struct PreNorm {
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 const float* v = xv[j][i];
-                if (WR && a.hcopy)
+                if (WR && writer && a.hcopy)
                     *(uint2*)(a.hcopy + (size_t)r * n + i * 1024 + 4 * t) =
                         make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
                                    (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
@@ -225,9 +228,12 @@ struct PreNorm {
                     q[e] = QB ? bf2f(yb[e]) : nm;
                     mx = fmaxf(mx, fabsf(q[e]));
                 }
-                if (WR && a.y)
+                if (WR && writer && a.y)
                     *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
                                                                            (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                if (WR && ylds)
+                    *(uint2*)(ylds + (size_t)r * n + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                    (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
                 mx = max_quad(mx);
                 const float s = mx * g * (1.0f / 127.0f);
                 const float qi = (s > 0.0f) ? (g / s) : 0.0f;
@@ -237,7 +243,7 @@ struct PreNorm {
                 const int slab = 64 * i + (t >> 2);
                 sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
                 if ((t & 3) == 0) ssc[r * SL + slab] = s;
-                if (WR && a.xq) {
+                if (WR && writer && a.xq) {
                     *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
                     if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
                 }

@@ -188,6 +188,9 @@ def check_round_state(eng, om, cfg, tag, gdn_layer=0):
             (tag, "MTP cache " + name)
     S_g = eng.read("S", gdn_layer, np.float32, cfg.gdn_vh * 128 * 128)
     assert np.array_equal(S_g.view(np.uint32), om.tensor("S", gdn_layer, np.float32).view(np.uint32)), (tag, "GDN S")
+    nqkv = (2 * cfg.gdn_kh + cfg.gdn_vh) * 128
+    hg = eng.read("conv_hist", gdn_layer, np.uint16, nqkv * 3)
+    assert np.array_equal(hg, om.tensor("conv_hist", gdn_layer, np.uint16)), (tag, "committed conv history")
 
 
 @pytest.mark.parametrize("k", [2, 7])
