@@ -346,7 +346,8 @@ int q27x_generate(q27x_ctx* ctx, int max_new, int spec, int32_t* out, int* n_out
 /* Exactly n speculative rounds (spec = 1) or plain steps (spec = 0) from the current state, launched
  * back to back; stats cover those n. */
 int q27x_run_rounds(q27x_ctx* ctx, int n, int spec, q27x_stats* st);
-/* Time of one verify pass (64 layers + head, nr rows) averaged over iters, device events. */
+/* Time of one verify pass (64 layers + head, nr rows) averaged over iters, device events. Clears
+ * the stop flag a finished request leaves, so the kernels do their work. */
 int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
 /* Time one projection launch of layer `layer` as the verify pass runs it (which: 0 in_qkv|in_z with
  * its input-norm prologue, 1 gate|up with its post-norm prologue and SwiGLU epilogue, 2 down +
@@ -354,7 +355,7 @@ int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
  * already-quantized rows, no prologue, for comparison) over iters launches with device
  * events on the context's stream, cycling through the layers so no launch finds its weights in the
  * Infinity Cache; reports ms per launch and its algorithmic bytes (weights + scales + input rows +
- * outputs). Overwrites the context's activation scratch. */
+ * outputs). Overwrites the context's activation scratch and clears the stop flag. */
 int q27x_bench_kernel(q27x_ctx* ctx, int layer, int which, int nr, int iters, float* ms, double* bytes);
 /* BASELINE configs 1 and 2 on the engine's own kernels: the mixer half of one layer (attn = 0:
  * GDN -- in_qkv|in_z with the input-norm prologue, the GDN kernel, out_proj + residual; attn = 1:

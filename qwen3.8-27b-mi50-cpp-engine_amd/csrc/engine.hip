@@ -1163,11 +1163,13 @@ int q27x_run_rounds(q27x_ctx* x, int n, int spec, q27x_stats* st) {
 
 int q27x_bench_verify(q27x_ctx* x, int nr, int iters, float* ms) {
     if (!x || !x->loaded || nr < 1 || nr > kMaxRows || iters < 1 || !ms) return Q27X_E_ARG;
+    // a finished request leaves the stop flag set, which would make every kernel return at once
+    int rc = set_ints(x, 1, DOFF(stop), 0);
+    if (rc) return rc;
     hipEvent_t a, b;
     Q27X_HIP(hipEventCreate(&a));
     Q27X_HIP(hipEventCreate(&b));
-    int rc = verify_pass(x, nr, 1, nullptr);
-    if (rc) return rc;
+    if ((rc = verify_pass(x, nr, 1, nullptr))) return rc;
     Q27X_HIP(hipEventRecord(a, x->stream));
     for (int i = 0; i < iters && !rc; ++i) rc = verify_pass(x, nr, 1, nullptr);
     Q27X_HIP(hipEventRecord(b, x->stream));
@@ -1252,10 +1254,12 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
         ga.pval = x->pval; ga.pidx = x->pidx; ga.pstride = x->pstride; ga.stop = &d->stop;
         b = (double)x->V * H * 2 + (double)nr * H * 2;
     } else return Q27X_E_ARG;
+    int rc = set_ints(x, 1, DOFF(stop), 0);     // (a finished request leaves it set)
+    if (rc) return rc;
     hipEvent_t e0, e1;
     Q27X_HIP(hipEventCreate(&e0));
     Q27X_HIP(hipEventCreate(&e1));
-    int rc = Q27X_OK, nb = 0;
+    int nb = 0;
     auto launch = [&](int i) {
         return which == 4 ? launch_gemv(ga, 1, nr, &nb, s) : launch_proj(ps[(size_t)i % ps.size()], epi, nr, s);
     };

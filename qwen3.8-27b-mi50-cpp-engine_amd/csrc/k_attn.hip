@@ -114,8 +114,9 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
 // Dynamic LDS: queries [nqr][128] fp32 | p [nqr][65] fp32.
 constexpr int kKStride = kHD + 4;
 constexpr int kAttnThreads = 512;
-// PREP: the block also does the prep of its rows (the grid then holds one split per block): the
-// queries of its kv head are normed and roped here instead of read back, and the split that holds
+constexpr int kSplitBlocks = 256;
+// PREP: the block also does the prep of its rows: the queries of its kv head are normed and roped
+// here (once per block) instead of read back, and the split that holds
 // the step's new positions computes their K and V, writes them to the cache and puts the
 // dequantized values straight into its tile.
 template <int NQW, int QPT, bool PREP>
@@ -142,14 +143,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
     float* wl = wm + (size_t)nr * a.nq * ms;
     bool staged_q = false;
-    for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
+    // the int8 K/V words of split s (thread: 16-byte words t and t + 512; K words 0..511, V
+    // 512..1023) and their scales; the step's new positions (PREP) are computed, not read
+    uint4 kv4[2];
+    float scl[2];
+    auto load_tile = [&](int s) __attribute__((always_inline)) {
         const int k0 = s * kSplit;
         const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
-        // keys [kn0, nk) are this step's new positions (PREP: computed below, not read)
         const int kn0 = PREP ? ((pos0 - k0 > 0) ? (pos0 - k0 < nk ? pos0 - k0 : nk) : 0) : nk;
-        // ---- loads: thread covers 16-byte words i = t and t + 512 (K words 0..511, V 512..1023)
-        uint4 kv4[2];
-        float scl[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
@@ -161,6 +162,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 scl[u] = (isv ? a.vs : a.ks)[off >> gsh];
             }
         }
+    };
+    if (blockIdx.x * kSplit < Lmax) load_tile(blockIdx.x);
+    for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
+        const int k0 = s * kSplit;
+        const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
+        // keys [kn0, nk) are this step's new positions (PREP: computed below, not read)
+        const int kn0 = PREP ? ((pos0 - k0 > 0) ? (pos0 - k0 < nk ? pos0 - k0 : nk) : 0) : nk;
         uint4 q4[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
         if (!PREP && !staged_q) {
 #pragma unroll
@@ -230,6 +238,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 *(float4*)(dst + 4 * e4) = f;
             }
         }
+        // the block's next split: its tile loads stay in flight through this split's work
+        if ((s + (int)gridDim.x) * kSplit < Lmax) load_tile(s + gridDim.x);
         if (!PREP && !staged_q) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -425,8 +435,9 @@ static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
         Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<8, 4, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
         lds_set = true;
     }
-    // one split per block (max_splits covers the whole context)
-    const dim3 grid(a.max_splits, a.nkv);
+    // at most kSplitBlocks blocks (about one per CU); a block takes splits blockIdx.x + i gridDim.x
+    const int bx = a.max_splits < kSplitBlocks / a.nkv ? a.max_splits : (kSplitBlocks / a.nkv > 0 ? kSplitBlocks / a.nkv : 1);
+    const dim3 grid(bx, a.nkv);
     if (nqr <= 8) hipLaunchKernelGGL((k_attn_split<1, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
     else if (nqr <= 16) hipLaunchKernelGGL((k_attn_split<2, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
     else if (nqr <= 24) hipLaunchKernelGGL((k_attn_split<3, 2, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);

@@ -91,8 +91,14 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
     static_assert(EPI != EPI_SWIGLU || RPW == 1, "SwiGLU deals single rows");
     static_assert(!PRE || NW == 16, "the norm prologue runs on 16-wave blocks");
+    // XR: the activation scales live in registers (each lane holds the scales of its own slabs),
+    // only the codes in LDS -- the K = 17408 stage of more than 4 rows (NR x 1088 slabs x 20 B)
+    // would not fit in 160 KB with its scales
+    constexpr bool XR = (NSTEP >= 17 && NR > 4);
+    static_assert(!XR || (!PRE && FULL && EPI == EPI_STORE), "register scales: plain full-K stage only");
     __shared__ uint4 sx[NR * SL];
-    __shared__ float ssc[NR * SL];
+    __shared__ float ssc[XR ? 1 : NR * SL];
+    float XS[XR ? NR : 1][XR ? NSTEP : 1];
     __shared__ float sacc[(EPI == EPI_SWIGLU) ? kSwRows * NR : 1];
     __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
     // EPI_CONV: the bf16 normalized input rows of the blocks that compute GDN row scalars
@@ -191,9 +197,18 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
                 const int n = i / SL, s = i - n * SL;
                 __builtin_amdgcn_global_load_lds((const void*)(a.xq + (size_t)n * a.xst + 16 * s),
                                                  (__attribute__((address_space(3))) void*)&sx[i0], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(a.xs + (size_t)n * (a.xst >> 4) + s),
-                                                 (__attribute__((address_space(3))) void*)&ssc[i0], 4, 0, 0);
+                if constexpr (!XR)
+                    __builtin_amdgcn_global_load_lds((const void*)(a.xs + (size_t)n * (a.xst >> 4) + s),
+                                                     (__attribute__((address_space(3))) void*)&ssc[i0], 4, 0, 0);
             }
+        }
+        if constexpr (XR) {
+            // (after the DMA requests and before the prefetch: the barrier's wait below counts the
+            // prefetch as the only loads still owed)
+#pragma unroll
+            for (int n = 0; n < NR; ++n)
+#pragma unroll
+                for (int t = 0; t < NSTEP; ++t) XS[n][t] = a.xs[(size_t)n * (a.xst >> 4) + t * 64 + lane];
         }
         prefetch();
         if (stopped(a.stop)) return;
@@ -465,7 +480,9 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
 #pragma unroll
             for (int n = 0; n < NR; ++n) {
                 const uint4 xa = sx[n * SL + s];
-                const float sa = ssc[n * SL + s];
+                float sa;
+                if constexpr (XR) sa = XS[n][t];
+                else sa = ssc[n * SL + s];
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
                     const int d = dot16(W[r][t], xa);
@@ -535,7 +552,11 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
         grid = nb < num_cus() ? nb : num_cus();
     } else {
         const int ngroups = (a.rows + RPW - 1) / RPW;
-        const int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
+        int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
+        // no more waves per CU than the blocks whose LDS stages fit (160 KB per CU)
+        constexpr int kStage = NR * NSTEP * 64 * ((NSTEP >= 17 && NR > 4) ? 16 : 20);
+        constexpr int kBpc = (160 * 1024) / kStage > 0 ? (160 * 1024) / kStage : 1;
+        if (wpc > kBpc * NW) wpc = kBpc * NW;
         const int wmax = num_cus() * wpc;
         const int nwv = ngroups < wmax ? ngroups : wmax;
         grid = (nwv + NW - 1) / NW;
@@ -555,8 +576,8 @@ static int run_proj(const ProjArgs& a, hipStream_t s) {
     return run_proj_rpw<NR, NSTEP, EPI, FULL, PRE, 1>(a, s);
 }
 
-// Shape router. NSTEP = ceil(K/1024); the LDS stage is NR*NSTEP*1280 B, so K = 17408 at NR > 4
-// (174 KB at NR = 8) is split by the caller into launches of <= 4 rows. The norm prologue (PRE)
+// Shape router. NSTEP = ceil(K/1024); the LDS stage is NR*NSTEP*1280 B, except K = 17408 at NR > 4
+// (174 KB at NR = 8), whose scales are held in registers (NR*NSTEP*1024 B). The norm prologue (PRE)
 // exists for the hidden sizes K = 1024 and 5120, the inputs of the layers' first projections.
 template <int NR, int EPI, bool FULL>
 static int route_k(const ProjArgs& a, hipStream_t s) {
@@ -582,7 +603,7 @@ static int route_k(const ProjArgs& a, hipStream_t s) {
             case 5: return run_proj<NR, 5, EPI, FULL, false>(a, s);
             case 6: return run_proj<NR, 6, EPI, FULL, false>(a, s);
             case 17:
-                if constexpr (NR <= 4) return run_proj<NR, 17, EPI, FULL, false>(a, s);
+                if constexpr (FULL && EPI == EPI_STORE) return run_proj<NR, 17, EPI, FULL, false>(a, s);
                 return -2;
             default: return -2;
         }
@@ -640,20 +661,7 @@ int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
         set_error("proj: GDN row scalars need in_a, in_b, A_log, dt_bias and ab_out (ab_vh <= 128)");
         return Q27X_E_ARG;
     }
-    int rc;
-    if (epi == EPI_STORE && a.K > 8192 && nr > 4) {   // LDS stage limit: two launches of <= 4 rows
-        ProjArgs b = a;
-        rc = route(b, EPI_STORE, 4, s);
-        if (rc) return rc == -2 ? (set_error("proj: no kernel for K=%d", a.K), Q27X_E_SHAPE) : rc;
-        b.xq = a.xq + (size_t)4 * a.xst;
-        b.xs = a.xs + (size_t)4 * (a.xst >> 4);
-        const size_t esz = a.out_bf16 ? 2 : 4;
-        b.y = (char*)a.y + (size_t)4 * a.ystride * esz;
-        if (a.res) b.res = (const char*)a.res + (size_t)4 * a.rstride * (a.res_bf16 ? 2 : 4);
-        rc = route(b, EPI_STORE, nr - 4, s);
-    } else {
-        rc = route(a, epi, nr, s);
-    }
+    const int rc = route(a, epi, nr, s);
     if (rc == -2) { set_error("proj: no kernel for K=%d nr=%d epi=%d", a.K, nr, epi); return Q27X_E_SHAPE; }
     return rc;
 }
@@ -800,10 +808,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, int upw) {
 // wave, no register copies). The activation rows are staged as fp32 with 16-byte loads issued
 // before the first group's weights. Same per-row arithmetic as k_gemv, so the same bits. MODE 1
 // merges the waves' running argmax in LDS and writes one partial per block.
+// More than 4 rows: rows 0..3 are staged as fp32 and rows 4.. as bf16 (widened at the read, which
+// is exact), so 8 rows of K = 5120 fit in 120 KB and the LDS reads stay below the VALU time.
 template <int NR, int NSTEP, int RPW, int MODE>
 __global__ __launch_bounds__(1024) void k_gemv_full(GemvArgs a) {
     constexpr int NW = 16, NT = NW * 64, CH = NSTEP * 64, NCK = NR * CH, SI = (NCK + NT - 1) / NT;
-    __shared__ float sxf[NR * CH * 8];
+    constexpr int NF = NR < 4 ? NR : 4;                // fp32-staged rows
+    __shared__ float sxf[NF * CH * 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sxb[(NR > NF ? NR - NF : 1) * CH * 8];
     __shared__ unsigned s_next;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K;
@@ -841,12 +853,16 @@ __global__ __launch_bounds__(1024) void k_gemv_full(GemvArgs a) {
         const int i = threadIdx.x + u * NT;
         if (i < NCK) {
             const int n = i / CH, c = i - n * CH;
-            float* d = &sxf[n * CH * 8 + 8 * c];
             const uint4 v = xv[u];
-            *(float4*)d = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
-                                      __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
-            *(float4*)(d + 4) = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
-                                            __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+            if (n < NF) {
+                float* d = &sxf[n * CH * 8 + 8 * c];
+                *(float4*)d = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                                          __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+                *(float4*)(d + 4) = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                                                __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+            } else {
+                *(uint4*)&sxb[(n - NF) * CH * 8 + 8 * c] = v;
+            }
         }
     }
     __syncthreads();
@@ -876,8 +892,17 @@ __global__ __launch_bounds__(1024) void k_gemv_full(GemvArgs a) {
                 wf[6] = __uint_as_float(w.w << 16); wf[7] = __uint_as_float(w.w & 0xFFFF0000u);
 #pragma unroll
                 for (int n = 0; n < NR; ++n) {
-                    const float4 x0 = *(const float4*)&sxf[n * CH * 8 + 8 * c];
-                    const float4 x1 = *(const float4*)&sxf[n * CH * 8 + 8 * c + 4];
+                    float4 x0, x1;
+                    if (n < NF) {
+                        x0 = *(const float4*)&sxf[n * CH * 8 + 8 * c];
+                        x1 = *(const float4*)&sxf[n * CH * 8 + 8 * c + 4];
+                    } else {
+                        const uint4 b = *(const uint4*)&sxb[(n - NF) * CH * 8 + 8 * c];
+                        x0 = make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u),
+                                         __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xFFFF0000u));
+                        x1 = make_float4(__uint_as_float(b.z << 16), __uint_as_float(b.z & 0xFFFF0000u),
+                                         __uint_as_float(b.w << 16), __uint_as_float(b.w & 0xFFFF0000u));
+                    }
                     float v = acc[r][n];
                     v = __builtin_fmaf(wf[0], x0.x, v); v = __builtin_fmaf(wf[1], x0.y, v);
                     v = __builtin_fmaf(wf[2], x0.z, v); v = __builtin_fmaf(wf[3], x0.w, v);
@@ -957,6 +982,9 @@ static int gemv_k(const GemvArgs& a, hipStream_t s, int* nb) {
         Q27X_HIP(hipGetLastError());
         return Q27X_OK;
     }
+    if constexpr (NR > 4) {
+        return -2;                                     // (the caller splits the rows)
+    } else {
     int wmax = num_cus() * 8;
     if (MODE == 1 && wmax > a.pstride) wmax = a.pstride & ~3;
     const int upw = (ngroups + wmax - 1) / wmax;
@@ -975,6 +1003,7 @@ static int gemv_k(const GemvArgs& a, hipStream_t s, int* nb) {
 #undef Q27X_G
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
+    }
 }
 
 int launch_gemv(const GemvArgs& a, int argmax_mode, int nr, int* nblocks_out, hipStream_t s) {
@@ -982,10 +1011,22 @@ int launch_gemv(const GemvArgs& a, int argmax_mode, int nr, int* nblocks_out, hi
         set_error("gemv: bad arguments (rows=%d K=%d nr=%d)", a.rows, a.K, nr);
         return Q27X_E_ARG;
     }
-    if (nr > 4) {   // instantiated for <= 4 rows (LDS stage): two launches
+    if (nr > 4) {
+        // one pass over the weights for all rows (aligned shapes); otherwise two launches of <= 4
+        // rows (the unaligned kernel's fp32 stage holds 4 rows)
+        int rc = -2;
+#define Q27X_GN(N) (argmax_mode ? gemv_k<N, 1>(a, s, nblocks_out) : gemv_k<N, 0>(a, s, nblocks_out))
+        switch (nr) {
+            case 5: rc = Q27X_GN(5); break;
+            case 6: rc = Q27X_GN(6); break;
+            case 7: rc = Q27X_GN(7); break;
+            default: rc = Q27X_GN(8); break;
+        }
+#undef Q27X_GN
+        if (rc != -2) return rc;
         GemvArgs b = a;
         int nb0 = 0, nb1 = 0;
-        int rc = launch_gemv(b, argmax_mode, 4, &nb0, s);
+        rc = launch_gemv(b, argmax_mode, 4, &nb0, s);
         if (rc) return rc;
         b.x = a.x + (size_t)4 * a.xst;
         if (argmax_mode) { b.pval = a.pval + (size_t)4 * a.pstride; b.pidx = a.pidx + (size_t)4 * a.pstride; }

@@ -133,7 +133,7 @@ def test_proj_shapes(gpu, O, rows, K, nr):
     same(f"proj {rows}x{K} nr={nr}", dy.download(np.float32, (nr, rows)), y_o)
 
 
-@pytest.mark.parametrize("nr", [1, 3])
+@pytest.mark.parametrize("nr", [1, 3, 5, 8])
 def test_bf16_gemv(gpu, O, nr):
     X = gpu
     rng = np.random.default_rng(11 + nr)
