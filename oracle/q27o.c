@@ -414,6 +414,32 @@ void q27o_rmsnorm_quant_rows(const void* x, int x_bf16, int xstride, const uint1
     free(nv);
 }
 
+/* The same norm with the normed values as fp32 (bf16-rounded when round_bf16), for the prefill's
+ * per-(token, group) quantizer (q27_red_rn_tok_b1 / q27_rmsnorm_hostss_tok_b,
+ * src/q27_main.cpp:4123-4124): identical arithmetic to q27o_rmsnorm_quant_rows up to the value
+ * it quantizes. hcopy = bf16(x), y = bf16(normed); any output may be NULL. */
+void q27o_rmsnorm_f32_rows(const void* x, int x_bf16, int xstride, const uint16_t* w, float plus,
+                           float eps, int n, uint16_t* hcopy, uint16_t* y, int ystride, float* yf,
+                           int yfstride, int round_bf16, int nr) {
+    float* xv = (float*)malloc((size_t)n * sizeof(float));
+    const float rn = 1.0f / (float)n;
+    for (int r = 0; r < nr; ++r) {
+        for (int k = 0; k < n; ++k)
+            xv[k] = x_bf16 ? q27o_bf2f(((const uint16_t*)x)[(size_t)r * xstride + k])
+                           : ((const float*)x)[(size_t)r * xstride + k];
+        const float ss = q27o_rowsumsq(xv, n);
+        const float inv = 1.0f / sqrtf(ss * rn + eps);
+        for (int k = 0; k < n; ++k) {
+            const float nm = xv[k] * inv * (plus + q27o_bf2f(w[k]));
+            const uint16_t yb = q27o_f2bf(nm);
+            if (hcopy) hcopy[(size_t)r * n + k] = q27o_f2bf(xv[k]);
+            if (y) y[(size_t)r * ystride + k] = yb;
+            if (yf) yf[(size_t)r * yfstride + k] = round_bf16 ? q27o_bf2f(yb) : nm;
+        }
+    }
+    free(xv);
+}
+
 /* ------------------------------------------------------------------ R10-R12 GDN */
 /* pend layout (per layer): khat [R][KH][D] f32 | delta [R][VH][D] f32 | decay [R][VH] f32 |
  * raw [R][NQKV] bf16, R = max rows. */

@@ -84,6 +84,10 @@ void  q27o_rmsnorm_quant_rows(const void* x, int x_bf16, int xstride, const uint
                               int ystride, int8_t* xq, float* xs, int quant_bf16,
                               float in_scale, int nr);
 
+void  q27o_rmsnorm_f32_rows(const void* x, int x_bf16, int xstride, const uint16_t* w, float plus,
+                            float eps, int n, uint16_t* hcopy, uint16_t* y, int ystride, float* yf,
+                            int yfstride, int round_bf16, int nr);
+
 /* ---- R10/R11/R12 GDN verify with deferred commit ---- */
 size_t q27o_gdn_pend_bytes(int kh, int vh, int d, int max_rows);
 void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, int z_stride,
@@ -136,6 +140,13 @@ int  q27o_model_prefill(q27o_model* m, const int32_t* ids, int n);          /* r
 int  q27o_model_decode_step(q27o_model* m);                                 /* returns token */
 int  q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced); /* ncommit */
 int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx);
+/* Layer-major prefill on the GEMM representation (chunks of `chunk` tokens): every projection as
+ * the per-(row, group) x per-(token, group) int8 GEMM (group 1024, or the whole K when 1024 does
+ * not divide it), everything else in the decode path's arithmetic; the MTP prompt pass computes
+ * only the draft KV cache (fc, input norm, k|v). Leaves the state fully committed; returns the
+ * first generated token. */
+int  q27o_model_prefill_gemm(q27o_model* m, const int32_t* ids, int n, int chunk);
+void q27o_debug_plant(int code);   /* tests only: plants a prefill composition mistake */
 /* one MTP pass (mtp_pass_nr, src/q27_main.cpp:2551-2618) over nr rows at draft positions dpos0..;
  * res [nr][H] bf16 out, logits [vocab] of head_row (may be NULL); returns the head row's argmax */
 int  q27o_model_mtp_pass(q27o_model* m, int nr, const uint16_t* hrows, const int32_t* toks, int dpos0,

@@ -56,6 +56,8 @@ _SIGS = {
     "q27o_accept": ([VP, VP, I, VP], I),
     "q27o_model_create": ([VP, U64], VP), "q27o_model_destroy": ([VP], None),
     "q27o_model_reset": ([VP], None), "q27o_model_prefill": ([VP, VP, I], I),
+    "q27o_model_prefill_gemm": ([VP, VP, I, I], I), "q27o_debug_plant": ([I], None),
+    "q27o_rmsnorm_f32_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, I, I, I], None),
     "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
     "q27o_model_verify_rows": ([VP, I, VP, VP], I),
     "q27o_model_mtp_pass": ([VP, I, VP, VP, I, I, VP, VP], I),
@@ -109,6 +111,10 @@ class Model:
         self.m = lib().q27o_model_create(ctypes.byref(self.cfg), seed)
         if not self.m:
             raise RuntimeError("q27o_model_create failed")
+
+    def prefill_gemm(self, ids, chunk=0):
+        ids = np.ascontiguousarray(ids, np.int32)
+        return lib().q27o_model_prefill_gemm(self.m, ids.ctypes.data, len(ids), chunk)
 
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

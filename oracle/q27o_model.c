@@ -423,6 +423,193 @@ int q27o_model_prefill(q27o_model* m, const int32_t* ids, int n) {
     return first;
 }
 
+/* ------------------------------------------------------------------ prefill on the GEMM path */
+/* Test knob: plants one composition mistake in the prefill restatement so the tests can show
+ * that their tolerance rejects it (0 = none; 1 = down without its residual, 2 = the MTP fc
+ * halves exchanged, 3 = the GDN scan not committing between sub-chunks, 4 = the a/b logits
+ * exchanged). Never set outside tests. */
+static int g_pf_plant = 0;
+void q27o_debug_plant(int code) { g_pf_plant = code; }
+
+/* Group size of the prefill GEMM over K (the reference's q8gs: 1024, or the whole K). */
+static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
+/* y[M][rows] = GEMM(W, act) * 1 (+ rs * res), W's per-64 mirror requantized per (row, group)
+ * (src/q27_epi.hip:14-35) and act quantized per (token, group) from fp32 values v [M][K]
+ * (src/q27_epi.hip:64-75); the GEMM and its fp32 fold follow src/q27_rb.cpp:43-55 and
+ * src/q27_epi.hip:189-243. rows0/nrows select a row range of W. */
+static void pf_proj(const i8m* W, int row0, int nrows, const float* v, int M, float* y, int ldy,
+                    const float* res, int ldr, float rs) {
+    const int K = W->K, gs = pf_gs(K), ng = K / gs;
+    int8_t* wg = (int8_t*)malloc((size_t)nrows * K);
+    float* sg = (float*)malloc((size_t)nrows * ng * 4);
+    q27o_i8g64_to_grp(W->w + (size_t)row0 * K, W->s + (size_t)row0 * (K / 64), nrows, K, gs, wg, sg);
+    int8_t* xq = (int8_t*)malloc((size_t)M * K);
+    float* xs = (float*)malloc((size_t)M * ng * 4);
+    q27o_quant_tok_groups(v, K, M, K, gs, xq, xs);
+    q27o_gemm_i8g(wg, sg, nrows, K, gs, 1.0f, xq, xs, M, y, ldy, res, ldr, rs);
+    free(wg); free(sg); free(xq); free(xs);
+}
+static void bf_to_f(const uint16_t* b, float* f, size_t n) { for (size_t i = 0; i < n; ++i) f[i] = q27o_bf2f(b[i]); }
+static void f_to_bf(const float* f, uint16_t* b, size_t n) { for (size_t i = 0; i < n; ++i) b[i] = q27o_f2bf(f[i]); }
+
+/* One chunk of C prompt rows at positions p0.. through every layer (ls_q8_layer's stage order,
+ * src/q27_main.cpp:4076-4316): input norm -> q|k|v or in_qkv|in_z GEMM -> attention over the
+ * cache / conv + GDN scan -> o / out_proj GEMM + residual -> post norm -> gate, up GEMMs ->
+ * SwiGLU -> down GEMM + residual. The mixers, norms and residual adds are the decode path's
+ * (a row's attention and recurrence are those of verify()); hall gets the rows' final residuals. */
+static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t* hall) {
+    const q27o_cfg* c = &m->c;
+    const int H = c->hidden, I = c->inter, D = c->gdn_d, VH = c->gdn_vh;
+    const int nqkv = (2 * c->gdn_kh + VH) * D, nz = VH * D;
+    const int qr = qrows_of(c), kvr = c->n_kv * c->head_dim, att = c->n_q * c->head_dim;
+    const int wq = qr + 2 * kvr, wz = nqkv + nz, wmax = wq > wz ? wq : wz, mmax = nz > att ? nz : att;
+    uint16_t* h = (uint16_t*)malloc((size_t)C * H * 2);        /* bf16 residual copy */
+    float* hf = (float*)malloc((size_t)C * H * 4);             /* the same as fp32 */
+    float* x = (float*)malloc((size_t)C * H * 4);              /* fp32 residual */
+    uint16_t* y = (uint16_t*)malloc((size_t)C * H * 2);        /* bf16 normed (a/b) */
+    float* v = (float*)malloc((size_t)C * (I > wmax ? I : wmax) * 4);   /* values to quantize / GEMM out */
+    uint16_t* pb = (uint16_t*)malloc((size_t)C * wmax * 2);
+    uint16_t* mix = (uint16_t*)malloc((size_t)C * mmax * 2);
+    uint16_t* qh = (uint16_t*)malloc((size_t)8 * att * 2);
+    float* g = (float*)malloc((size_t)C * I * 4);
+    float* u = (float*)malloc((size_t)C * I * 4);
+    float* ab = (float*)malloc((size_t)C * VH * 4 * 2);
+    float* tmp = (float*)malloc((size_t)C * VH * 4);
+    for (int r = 0; r < C; ++r) memcpy(h + (size_t)r * H, m->emb + (size_t)ids[p0 + r] * H, (size_t)H * 2);
+    for (int L = 0; L < c->n_layers; ++L) {
+        layer_t* Y = &m->L[L];
+        if (L == 0) q27o_rmsnorm_f32_rows(h, 1, H, Y->in_norm, 1.0f, c->rms_eps, H, NULL, y, H, v, H, 1, C);
+        else q27o_rmsnorm_f32_rows(x, 0, H, Y->in_norm, 1.0f, c->rms_eps, H, h, y, H, v, H, 0, C);
+        bf_to_f(h, hf, (size_t)C * H);
+        if (Y->is_attn) {
+            float* o = (float*)malloc((size_t)C * wq * 4);
+            pf_proj(&Y->qkv, 0, wq, v, C, o, wq, NULL, 0, 0.0f);
+            f_to_bf(o, pb, (size_t)C * wq);
+            free(o);
+            for (int r0 = 0; r0 < C; r0 += 8) {
+                const int cn = (C - r0 < 8) ? C - r0 : 8;
+                q27o_attn_prep_rows(pb + (size_t)r0 * wq, wq, Y->q_norm, Y->k_norm, m->rope_cos, m->rope_sin,
+                                    c->rot_dims, Y->kc, Y->ks, Y->vc, Y->vs, c->kv_group, qh, c->n_q, c->n_kv,
+                                    c->head_dim, c->attn_gate, c->rms_eps, p0 + r0, cn);
+                q27o_attn_rows(qh, pb + (size_t)r0 * wq, wq, Y->kc, Y->ks, Y->vc, Y->vs, c->kv_group, c->n_q,
+                               c->n_kv, c->head_dim, c->attn_gate, p0 + r0, cn, mix + (size_t)r0 * att, NULL, NULL);
+            }
+            bf_to_f(mix, v, (size_t)C * att);
+            pf_proj(&Y->o, 0, H, v, C, x, H, hf, H, 1.0f);
+        } else {
+            float* o = (float*)malloc((size_t)C * wz * 4);
+            pf_proj(&Y->qkvz, 0, wz, v, C, o, wz, NULL, 0, 0.0f);
+            f_to_bf(o, pb, (size_t)C * wz);
+            free(o);
+            /* a / b: the decode path's bf16 GEMV on the bf16 normed rows, bf16 outputs */
+            q27o_bf16_gemv_rows(Y->in_a, VH, H, y, H, tmp, VH, C);
+            for (int i = 0; i < C * VH; ++i) ab[i] = q27o_bf2f(q27o_f2bf(tmp[i]));
+            q27o_bf16_gemv_rows(Y->in_b, VH, H, y, H, tmp, VH, C);
+            for (int i = 0; i < C * VH; ++i) ab[C * VH + i] = q27o_bf2f(q27o_f2bf(tmp[i]));
+            /* the scan: rows in order, each committed before the next (sub-chunks of 8 rows, each
+             * call committing the previous one -- the same updates as one continuous scan) */
+            int npend = m->gdn_npend;
+            for (int r0 = 0; r0 < C; r0 += 8) {
+                const int cn = (C - r0 < 8) ? C - r0 : 8;
+                const float* la = ab + (size_t)(g_pf_plant == 4 ? C + r0 : r0) * VH;
+                const float* lb = ab + (size_t)(g_pf_plant == 4 ? r0 : C + r0) * VH;
+                q27o_gdn_verify(pb + (size_t)r0 * wz, wz, pb + (size_t)r0 * wz + nqkv, wz, la, lb, VH, Y->A_log, Y->dt_bias, Y->gdn_norm, Y->conv_w,
+                                Y->S, Y->conv_hist, Y->pend, npend, c->gdn_kh, VH, D, c->rms_eps,
+                                mix + (size_t)r0 * nz, nz, NULL, NULL, cn);
+                npend = g_pf_plant == 3 ? 0 : cn;
+            }
+            q27o_gdn_verify(NULL, 0, NULL, 0, NULL, NULL, 0, Y->A_log, Y->dt_bias, Y->gdn_norm, Y->conv_w, Y->S,
+                            Y->conv_hist, Y->pend, npend, c->gdn_kh, VH, D, c->rms_eps, NULL, 0, NULL, NULL, 0);
+            bf_to_f(mix, v, (size_t)C * nz);
+            pf_proj(&Y->out_proj, 0, H, v, C, x, H, hf, H, 1.0f);
+        }
+        q27o_rmsnorm_f32_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, v, H, 0, C);
+        bf_to_f(h, hf, (size_t)C * H);
+        pf_proj(&Y->gate, 0, I, v, C, g, I, NULL, 0, 0.0f);
+        pf_proj(&Y->up, 0, I, v, C, u, I, NULL, 0, 0.0f);
+        for (size_t i = 0; i < (size_t)C * I; ++i) {   /* q27o_swiglu_quant_rows' value, in_scale 1 */
+            const float a = g[i];
+            const float sw = a / (1.0f + q27o_exp(-a));
+            v[i] = sw * u[i] * 1.0f;
+        }
+        pf_proj(&Y->down, 0, H, v, C, x, H, hf, H, g_pf_plant == 1 ? 0.0f : 1.0f);
+    }
+    m->gdn_npend = 0;
+    for (int r = 0; r < C; ++r)
+        for (int k = 0; k < H; ++k) {
+            const float t = c->head_double_residual ? q27o_bf2f(h[(size_t)r * H + k]) + x[(size_t)r * H + k]
+                                                    : x[(size_t)r * H + k];
+            hall[(size_t)r * H + k] = q27o_f2bf(t);
+        }
+    free(h); free(hf); free(x); free(y); free(v); free(pb); free(mix); free(qh); free(g); free(u); free(ab); free(tmp);
+}
+
+/* The MTP prompt pass over positions [p0, p0 + C) (mtp_prompt_pass, src/q27_main.cpp:2647-2688):
+ * position p pairs the final residual at p with the embedding of token p+1; pre-norms (fp32
+ * values, per-(token, group) quantized), fc as two GEMMs (the embedding half first, the hidden
+ * half added in fp32), the layer's input norm, then only k|v: their rows' GEMM -> bf16 -> K/V
+ * cache (k_norm, RoPE, int8) at draft positions p. */
+static void pf_mtp(q27o_model* m, const int32_t* ids, int p0, int C, const uint16_t* hall) {
+    const q27o_cfg* c = &m->c;
+    layer_t* Y = &m->mtp;
+    const int H = c->hidden;
+    const int qr = qrows_of(c), kvr = c->n_kv * c->head_dim, att = c->n_q * c->head_dim, wq = qr + 2 * kvr;
+    const float po = c->mtp_plus_one ? 1.0f : 0.0f;
+    float* ve = (float*)malloc((size_t)C * H * 4);
+    float* vh = (float*)malloc((size_t)C * H * 4);
+    float* res = (float*)malloc((size_t)C * H * 4);
+    float* kv = (float*)malloc((size_t)C * 2 * kvr * 4);
+    uint16_t* pb = (uint16_t*)calloc((size_t)C * wq, 2);
+    uint16_t* qh = (uint16_t*)malloc((size_t)8 * att * 2);
+    uint16_t* e = (uint16_t*)malloc((size_t)C * H * 2);
+    for (int r = 0; r < C; ++r) memcpy(e + (size_t)r * H, m->emb + (size_t)ids[p0 + r + 1] * H, (size_t)H * 2);
+    q27o_rmsnorm_f32_rows(e, 1, H, m->pre_emb, po, c->rms_eps, H, NULL, NULL, H, ve, H, 0, C);
+    q27o_rmsnorm_f32_rows(hall + (size_t)p0 * H, 1, H, m->pre_hid, po, c->rms_eps, H, NULL, NULL, H, vh, H, 0, C);
+    const int sw = c->mtp_swap ^ (g_pf_plant == 2);
+    const i8m* fe = sw ? &m->fc0 : &m->fc1;   /* the half that multiplies the embedding */
+    const i8m* fh = sw ? &m->fc1 : &m->fc0;
+    pf_proj(fe, 0, H, ve, C, res, H, NULL, 0, 0.0f);
+    pf_proj(fh, 0, H, vh, C, res, H, res, H, 1.0f);
+    q27o_rmsnorm_f32_rows(res, 0, H, Y->in_norm, po, c->rms_eps, H, NULL, NULL, H, ve, H, 0, C);
+    pf_proj(&Y->qkv, qr, 2 * kvr, ve, C, kv, 2 * kvr, NULL, 0, 0.0f);
+    for (int r = 0; r < C; ++r)
+        for (int k = 0; k < 2 * kvr; ++k) pb[(size_t)r * wq + qr + k] = q27o_f2bf(kv[(size_t)r * 2 * kvr + k]);
+    for (int r0 = 0; r0 < C; r0 += 8) {
+        const int cn = (C - r0 < 8) ? C - r0 : 8;
+        q27o_attn_prep_rows(pb + (size_t)r0 * wq, wq, Y->q_norm, Y->k_norm, m->rope_cos, m->rope_sin, c->rot_dims,
+                            Y->kc, Y->ks, Y->vc, Y->vs, c->kv_group, qh, c->n_q, c->n_kv, c->head_dim, c->attn_gate,
+                            c->rms_eps, p0 + r0, cn);
+    }
+    free(ve); free(vh); free(res); free(kv); free(pb); free(qh); free(e);
+}
+
+int q27o_model_prefill_gemm(q27o_model* m, const int32_t* ids, int n, int chunk) {
+    const q27o_cfg* c = &m->c;
+    const int H = c->hidden;
+    if (chunk < 1) chunk = n;
+    q27o_model_reset(m);
+    uint16_t* hall = (uint16_t*)malloc((size_t)n * H * 2);
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int C = (n - p0 < chunk) ? n - p0 : chunk;
+        pf_chunk(m, ids, p0, C, hall + (size_t)p0 * H);
+        const int cm = (p0 + C < n) ? C : C - 1;    /* MTP positions of this chunk (p + 1 < n) */
+        if (cm > 0) pf_mtp(m, ids, p0, cm, hall);
+    }
+    /* head of the last row: final norm, lm_head, argmax */
+    uint16_t* y = (uint16_t*)malloc((size_t)H * 2);
+    float* logits = (float*)malloc((size_t)c->vocab * 4);
+    q27o_rmsnorm_quant_rows(hall + (size_t)(n - 1) * H, 1, H, m->final_norm, 1.0f, c->rms_eps, H, NULL, y, H, NULL,
+                            NULL, 1, 1.0f, 1);
+    q27o_bf16_gemv_rows(m->lm_head, c->vocab, H, y, H, logits, c->vocab, 1);
+    int32_t first = 0;
+    float val = 0.0f;
+    q27o_argmax_rows(logits, c->vocab, c->vocab, 1, &first, &val);
+    memcpy(m->hprev, hall + (size_t)(n - 1) * H, (size_t)H * 2);
+    free(y); free(logits); free(hall);
+    m->pos = n; m->tok = first; m->ncatch = 0; m->have_h = 1; m->gdn_npend = 0;
+    return first;
+}
+
 /* plain greedy step (the Q27_SPEC=0 path, src/q27_main.cpp:6396-6502) */
 int q27o_model_decode_step(q27o_model* m) {
     int32_t t = m->tok, nx;
