@@ -313,6 +313,14 @@ int q27x_reset(q27x_ctx* ctx);
 /* Ingest a prompt (positions 0..n-1), produce the first decode token, and prompt-condition the
  * MTP layer (reference: prefill sweep + mtp_prompt_pass, src/q27_main.cpp:2649-2692, 5131-5136). */
 int q27x_prefill(q27x_ctx* ctx, const int32_t* ids, int n, int32_t* first_token);
+/* The same ingest on the layer-major GEMM path (the reference's Q27_LS_Q8 prefill graph,
+ * ls_q8_layer, src/q27_main.cpp:4076-4316, and mtp_prompt_pass, 2647-2688): the prompt in chunks
+ * of up to 2048 rows (Q27X_PF_CHUNK overrides), each chunk through every layer; every projection is
+ * the int8 MFMA GEMM of per-(row, 1024) weights and per-(token, 1024) activations (whole-K groups
+ * where 1024 does not divide K); norms, GDN conv / scan, attention, SwiGLU and residual adds keep
+ * the decode path's arithmetic; the MTP prompt pass computes only the draft KV cache. Leaves the
+ * state fully committed. Its results differ from q27x_prefill's by the quantization granularity. */
+int q27x_prefill_gemm(q27x_ctx* ctx, const int32_t* ids, int n, int32_t* first_token);
 /* One plain greedy step (Q27_SPEC=0 semantics): consumes the current token, returns the next. */
 int q27x_decode_step(q27x_ctx* ctx, int32_t* out_token);
 /* One chained-MTP speculative round (spec_round, src/q27_main.cpp:2702-2958): K drafts, an

@@ -13,6 +13,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <string>
 #include <vector>
@@ -78,6 +79,25 @@ struct Mailbox { volatile int round; volatile int committed; volatile int ncommi
 
 using namespace q27x;
 
+// Buffers of the layer-major prefill (allocated on its first use, sized for a chunk of `cap` rows).
+struct PfBuf {
+    int cap = 0;
+    float* x = nullptr;          // [cap][H] fp32 residual
+    uint16_t* h = nullptr;       // [cap][H] bf16 residual copy (the next add's residual)
+    uint16_t* y = nullptr;       // [cap][H] bf16 normed rows (GDN a/b)
+    float* yf = nullptr;         // [cap][H] normed values to quantize
+    int8_t* xq = nullptr; float* xs = nullptr;     // [cap][kmax] codes, [cap][32] group scales
+    int8_t* xq2 = nullptr; float* xs2 = nullptr;   // [cap][H], [cap][32]: the MTP pass's second fc input
+    uint16_t* pb = nullptr;      // [cap][wmax] projection rows
+    uint16_t* qh = nullptr;      // [cap][att] normed, roped queries
+    float* gu = nullptr;         // [cap][2I] gate|up GEMM output
+    uint16_t* mix = nullptr;     // [cap][max(nz, att)] mixer output
+    float* rowsc = nullptr;      // [2][cap][vh] GDN decay, beta
+    int8_t* wg = nullptr; float* sg = nullptr;     // one matrix in the GEMM representation
+    float* work = nullptr;       // attention split partials of kPfAttnRows rows
+    std::vector<void*> allocs;
+};
+
 struct q27x_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -117,6 +137,7 @@ struct q27x_ctx {
     int g_spec_k = 0;
     int wclk_khz = 0;      // device wall clock (s_memrealtime) rate
     float sl2e = 0.0f;
+    PfBuf* pf = nullptr;
 };
 
 namespace q27x {
@@ -766,6 +787,10 @@ int q27x_ctx_destroy(q27x_ctx* x) {
     if (x->g_spec) (void)hipGraphExecDestroy(x->g_spec);
     if (x->g_plain) (void)hipGraphExecDestroy(x->g_plain);
     if (x->mbox) (void)hipHostFree((void*)x->mbox);
+    if (x->pf) {
+        for (void* p : x->pf->allocs) (void)hipFree(p);
+        delete x->pf;
+    }
     if (x->warena) (void)hipFree(x->warena);
     if (x->sarena) (void)hipFree(x->sarena);
     if (x->stream) (void)hipStreamDestroy(x->stream);
@@ -947,6 +972,236 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
     x->n_prompt = n;
     if (first_token) *first_token = first;
     (void)t0;
+    return Q27X_OK;
+}
+
+// ---------------------------------------------------------------- layer-major prefill (GEMM path)
+// The prompt in chunks of up to kPfChunk rows, each chunk through every layer (ls_q8_layer's
+// stage order, src/q27_main.cpp:4076-4316): every projection is the int8 MFMA GEMM of per-(row,
+// group) weights and per-(token, group) activations (group 1024, or the whole K), each matrix
+// brought to that representation from its per-64 mirror right before its GEMM; the norms, GDN
+// conv / row scalars / scan, attention, SwiGLU and residual adds keep the decode path's
+// arithmetic. The MTP prompt pass fills only the draft KV cache (src/q27_main.cpp:2647-2688).
+constexpr int kPfChunk = 2048;
+constexpr int kPfAttnRows = 128;    // query rows per attention launch (tiles of 8)
+static int env_int(const char* name, int def);
+static int pf_chunk() {   // rows per pass over the layers; Q27X_PF_CHUNK (8 .. 2048) overrides, read per call
+    const int v = env_int("Q27X_PF_CHUNK", kPfChunk);
+    return v < 8 ? 8 : (v > kPfChunk ? kPfChunk : v);
+}
+static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
+
+static int pf_alloc(q27x_ctx* x, int cap) {
+    if (x->pf && x->pf->cap >= cap) return Q27X_OK;
+    if (x->pf) {
+        Q27X_HIP(hipStreamSynchronize(x->stream));
+        for (void* p : x->pf->allocs) (void)hipFree(p);
+        delete x->pf;
+        x->pf = nullptr;
+    }
+    const q27x_config& c = x->c;
+    const int H = x->H, I = x->I;
+    const int wz = x->nqkv + x->nz, wq = x->qr + 2 * x->kvr;
+    const int kmax = std::max(std::max(H, I), std::max(x->nz, x->att));
+    const int wmax = std::max(std::max(wz, wq), H);
+    size_t wgmax = 0;
+    for (size_t r : { (size_t)2 * I * H, (size_t)H * I, (size_t)wz * H, (size_t)wq * H, (size_t)H * x->att,
+                      (size_t)H * x->nz, (size_t)H * H })
+        wgmax = std::max(wgmax, r);
+    const size_t rows_max = (size_t)std::max(std::max(2 * I, wz), std::max(wq, H));
+    PfBuf* B = new PfBuf();
+    B->cap = cap;
+    auto A = [&](void** p, size_t bytes) -> int {
+        const hipError_t e = hipMalloc(p, bytes);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc (prefill buffers)");
+        B->allocs.push_back(*p);
+        return Q27X_OK;
+    };
+    const size_t C = (size_t)cap;
+    const size_t ms = (size_t)x->max_splits;
+    int rc = 0;
+    if ((rc = A((void**)&B->x, C * H * 4)) || (rc = A((void**)&B->h, C * H * 2)) || (rc = A((void**)&B->y, C * H * 2)) ||
+        (rc = A((void**)&B->yf, C * H * 4)) || (rc = A((void**)&B->xq, C * kmax)) || (rc = A((void**)&B->xs, C * 32 * 4)) ||
+        (rc = A((void**)&B->xq2, C * H)) || (rc = A((void**)&B->xs2, C * 32 * 4)) ||
+        (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
+        (rc = A((void**)&B->gu, C * 2 * I * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
+        (rc = A((void**)&B->rowsc, 2 * C * c.gdn_vh * 4)) || (rc = A((void**)&B->wg, wgmax)) ||
+        (rc = A((void**)&B->sg, rows_max * 32 * 4)) ||
+        (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4))) {
+        for (void* p : B->allocs) (void)hipFree(p);
+        delete B;
+        return rc;
+    }
+    x->pf = B;
+    return Q27X_OK;
+}
+
+// y = GEMM(rows [r0, r0 + nrows) of W, the codes xq/xs of M rows) (+ the bf16 residual), y bf16
+// or fp32 with row stride ldy
+static int pf_gemm(q27x_ctx* x, const Mat& W, int r0, int nrows, const int8_t* xq, const float* xs, int M, void* y,
+                   int ldy, int out_bf16, const uint16_t* res_bf16) {
+    PfBuf& B = *x->pf;
+    hipStream_t s = x->stream;
+    const int K = W.K, gs = pf_gs(K);
+    int rc = q27x_i8g64_to_grp(W.w + (size_t)r0 * K, W.s + (size_t)r0 * (K / 64), nrows, K, gs, B.wg, B.sg,
+                               (q27x_stream_t)s);
+    if (rc) return rc;
+    return launch_gemm_i8g(B.wg, B.sg, nrows, K, gs, 1.0f, xq, xs, M, y, ldy, out_bf16, res_bf16, x->H, 1,
+                           res_bf16 ? 1.0f : 0.0f, s);
+}
+// norm of C rows (values to B.yf) and their per-(token, group) codes
+static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs) {
+    PfBuf& B = *x->pf;
+    n.yf = B.yf; n.yfstride = x->H;
+    int rc = launch_norm(n, C, x->stream);
+    if (rc) return rc;
+    return q27x_quant_tok_groups(B.yf, x->H, C, x->H, pf_gs(x->H), xq, xs, (q27x_stream_t)x->stream);
+}
+
+static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
+    const q27x_config& c = x->c;
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    PfBuf& B = *x->pf;
+    LayerDev& Y = x->L[l];
+    const int H = x->H, I = x->I;
+    int rc;
+    NormArgs nin;
+    if (l == 0) {
+        nin = norm_of(x, nullptr, 1, Y.in_norm, 1.0f, 1, B.h, Y.is_attn ? nullptr : B.y);
+        nin.emb = x->emb; nin.tok = x->prompt_dev + p0;
+    } else {
+        nin = norm_of(x, B.x, 0, Y.in_norm, 1.0f, 0, B.h, Y.is_attn ? nullptr : B.y);
+    }
+    if ((rc = pf_norm_quant(x, nin, C, B.xq, B.xs))) return rc;
+    if (Y.is_attn) {
+        const int wq = Y.qkv.rows;
+        if ((rc = pf_gemm(x, Y.qkv, 0, wq, B.xq, B.xs, C, B.pb, wq, 1, nullptr))) return rc;
+        AttnArgs a{};
+        a.qkv = B.pb; a.qkv_stride = wq; a.q_norm_w = Y.q_norm; a.k_norm_w = Y.k_norm;
+        a.rope_cos = x->rope_cos; a.rope_sin = x->rope_sin; a.rot = c.rot_dims;
+        a.kc = Y.kc; a.ks = Y.ks; a.vc = Y.vc; a.vs = Y.vs; a.kv_group = c.kv_group; a.qh = B.qh;
+        a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
+        a.pos0_imm = p0; a.sl2e = x->sl2e; a.stop = &d->stop;
+        if ((rc = launch_attn_prep_rows(a, C, s))) return rc;
+        for (int q0 = 0; q0 < C; q0 += kPfAttnRows) {
+            const int cq = std::min(kPfAttnRows, C - q0);
+            AttnArgs t = a;
+            t.qh = B.qh + (size_t)q0 * x->att; t.qkv = B.pb + (size_t)q0 * wq; t.pos0_imm = p0 + q0;
+            t.work = B.work; t.max_splits = (p0 + q0 + cq + kSplit - 1) / kSplit;
+            t.zrows = 8; t.ztotal = cq; t.out = B.mix + (size_t)q0 * x->att;
+            if ((rc = launch_attn(t, 8, s, false))) return rc;
+        }
+        if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(x->att), B.xq, B.xs, s))) return rc;
+        if ((rc = pf_gemm(x, Y.o, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
+    } else {
+        const int wz = Y.qkvz.rows;
+        if ((rc = pf_gemm(x, Y.qkvz, 0, wz, B.xq, B.xs, C, B.pb, wz, 1, nullptr))) return rc;
+        if ((rc = launch_pf_ab(Y.in_a, Y.in_b, Y.A_log, Y.dt_bias, B.y, H, H, c.gdn_vh, C, B.rowsc, s))) return rc;
+        if ((rc = launch_pf_conv(B.pb, wz, C, x->nqkv, Y.conv_w, Y.conv_st, 0, s))) return rc;
+        GdnArgs g{};
+        g.qkv = B.pb; g.qkv_stride = wz; g.z = B.pb + x->nqkv; g.z_stride = wz;
+        g.rowsc = B.rowsc; g.norm_w = Y.gdn_norm; g.S = Y.S;
+        g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
+        g.out = B.mix; g.out_stride = x->nz; g.stop = &d->stop;
+        if ((rc = launch_gdn_scan(g, C, s))) return rc;
+        if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), B.xq, B.xs, s))) return rc;
+        if ((rc = pf_gemm(x, Y.out_proj, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
+    }
+    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, Y.post_norm, 1.0f, 0, B.h, nullptr), C, B.xq, B.xs))) return rc;
+    if ((rc = pf_gemm(x, Y.gu, 0, 2 * I, B.xq, B.xs, C, B.gu, 2 * I, 0, nullptr))) return rc;
+    if ((rc = launch_pf_swiglu_quant(B.gu, I, pf_gs(I), 1.0f, C, B.xq, B.xs, s))) return rc;
+    return pf_gemm(x, Y.down, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h);
+}
+
+// the MTP prompt pass over draft positions p0 .. p0 + C - 1 (final residual rows hall[p], token p+1)
+static int pf_mtp(q27x_ctx* x, int p0, int C) {
+    const q27x_config& c = x->c;
+    Dctl* d = x->dctl;
+    PfBuf& B = *x->pf;
+    LayerDev& M = x->mtp;
+    const int H = x->H;
+    const float po = c.mtp_plus_one ? 1.0f : 0.0f;
+    int rc;
+    NormArgs ne = norm_of(x, nullptr, 1, x->pre_emb, po, 0, nullptr, nullptr);
+    ne.emb = x->emb; ne.tok = x->prompt_dev + p0 + 1;
+    if ((rc = pf_norm_quant(x, ne, C, B.xq, B.xs))) return rc;
+    if ((rc = pf_norm_quant(x, norm_of(x, x->hall + (size_t)p0 * H, 1, x->pre_hid, po, 0, nullptr, nullptr), C,
+                            B.xq2, B.xs2))) return rc;
+    const Mat& fe = c.mtp_swap ? x->fc0 : x->fc1;    // the half that multiplies the embedding
+    const Mat& fh = c.mtp_swap ? x->fc1 : x->fc0;
+    if ((rc = pf_gemm(x, fe, 0, H, B.xq, B.xs, C, B.x, H, 0, nullptr))) return rc;
+    // (fp32 residual: the same GEMM with res = the first half's output, read and written in place)
+    {
+        const int K = fh.K, gs = pf_gs(K);
+        if ((rc = q27x_i8g64_to_grp(fh.w, fh.s, H, K, gs, B.wg, B.sg, (q27x_stream_t)x->stream))) return rc;
+        if ((rc = launch_gemm_i8g(B.wg, B.sg, H, K, gs, 1.0f, B.xq2, B.xs2, C, B.x, H, 0, B.x, H, 0, 1.0f, x->stream)))
+            return rc;
+    }
+    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, M.in_norm, po, 0, nullptr, nullptr), C, B.xq, B.xs))) return rc;
+    const int wq = M.qkv.rows;
+    if ((rc = pf_gemm(x, M.qkv, x->qr, 2 * x->kvr, B.xq, B.xs, C, B.pb + x->qr, wq, 1, nullptr))) return rc;
+    AttnArgs a{};
+    a.qkv = B.pb; a.qkv_stride = wq; a.q_norm_w = M.q_norm; a.k_norm_w = M.k_norm;
+    a.rope_cos = x->rope_cos; a.rope_sin = x->rope_sin; a.rot = c.rot_dims;
+    a.kc = M.kc; a.ks = M.ks; a.vc = M.vc; a.vs = M.vs; a.kv_group = c.kv_group;
+    a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
+    a.pos0_imm = p0; a.prep_kv_only = 1; a.stop = &d->stop;
+    return launch_attn_prep_rows(a, C, x->stream);
+}
+
+int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
+    if (!x || !ids || n < 1) { set_error("q27x_prefill_gemm: bad arguments"); return Q27X_E_ARG; }
+    if (!x->loaded) { set_error("q27x_prefill_gemm: no weights"); return Q27X_E_STATE; }
+    if (n + x->c.spec_k + 2 > x->c.ctx || n > x->prompt_cap) {
+        set_error("q27x_prefill_gemm: prompt of %d exceeds ctx %d", n, x->c.ctx);
+        return Q27X_E_RANGE;
+    }
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= x->V) { set_error("q27x_prefill_gemm: token %d out of range", ids[i]); return Q27X_E_RANGE; }
+    int rc = q27x_reset(x);
+    if (rc) return rc;
+    const int chunk = pf_chunk();
+    if ((rc = pf_alloc(x, std::min(n, chunk)))) return rc;
+    hipStream_t s = x->stream;
+    Dctl* d = x->dctl;
+    const q27x_config& c = x->c;
+    const int H = x->H;
+    Q27X_HIP(hipMemcpyAsync(x->prompt_dev, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int C = std::min(chunk, n - p0);
+        for (int l = 0; l < c.n_layers; ++l)
+            if ((rc = pf_layer(x, l, p0, C))) return rc;
+        // the rows' final residuals: bf16(bf16(r1) + r2) (the reference's double add) or bf16(r2)
+        NormArgs hn{};
+        hn.x = x->pf->x; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->pf->h : nullptr;
+        hn.hout = x->hall + (size_t)p0 * H; hn.w = x->final_norm; hn.plus = 1.0f; hn.eps = c.rms_eps; hn.n = H;
+        hn.ystride = H; hn.in_scale = 1.0f; hn.stop = &d->stop;
+        if ((rc = launch_norm(hn, C, s))) return rc;
+        const int cm = (p0 + C < n) ? C : C - 1;     // MTP positions p with p + 1 < n
+        if (cm > 0 && (rc = pf_mtp(x, p0, cm))) return rc;
+    }
+    // head of the last row: final norm, lm_head, argmax
+    NormArgs hf = norm_of(x, x->hall + (size_t)(n - 1) * H, 1, x->final_norm, 1.0f, 1, nullptr, x->ynorm);
+    if ((rc = launch_norm(hf, 1, s))) return rc;
+    GemvArgs ga{};
+    ga.W = x->lm_head; ga.rows = x->V; ga.K = H; ga.x = x->ynorm; ga.xst = H;
+    ga.pval = x->pval; ga.pidx = x->pidx; ga.pstride = x->pstride; ga.stop = &d->stop;
+    int nb = 0;
+    if ((rc = launch_gemv(ga, 1, 1, &nb, s))) return rc;
+    if ((rc = launch_argmax_final(x->pval, x->pidx, x->pstride, nb, 1, d->nx, d->nxval, &d->stop, s))) return rc;
+    int32_t first = 0;
+    Q27X_HIP(hipMemcpyAsync(&first, &d->nx[0], 4, hipMemcpyDeviceToHost, s));
+    Q27X_HIP(hipMemcpyAsync(x->hprev, x->hall + (size_t)(n - 1) * H, (size_t)H * 2, hipMemcpyDeviceToDevice, s));
+    Q27X_HIP(hipStreamSynchronize(s));
+    if ((rc = set_ints(x, 4, DOFF(pos), n, DOFF(tok), first, DOFF(ncatch), 0, DOFF(gdn_npend), 0))) return rc;
+    if ((rc = set_ints(x, 4, DOFF(committed), 1, DOFF(rounds), 0, DOFF(stop), 0, DOFF(max_new), 0x7fffffff))) return rc;
+    Q27X_HIP(hipMemcpyAsync(x->out_ring, &first, 4, hipMemcpyHostToDevice, s));
+    Q27X_HIP(hipStreamSynchronize(s));
+    if ((rc = check_device_err(x))) return rc;
+    x->prefilled = 1;
+    x->n_prompt = n;
+    if (first_token) *first_token = first;
     return Q27X_OK;
 }
 

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
     if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
     const int pos = (a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm) + r;
     const int l = threadIdx.x;
-    const int u = blockIdx.x;
+    const int u = blockIdx.x + (a.prep_kv_only ? a.nq : 0);
     const bool isq = u < a.nq;
     const int head = isq ? u : u - a.nq;
     const int qw = a.gate ? 2 * kHD : kHD;
@@ -119,14 +119,28 @@ constexpr int kSplitBlocks = 256;
 // here (once per block) instead of read back, and the split that holds
 // the step's new positions computes their K and V, writes them to the cache and puts the
 // dequantized values straight into its tile.
+// Row tiles (a.zrows > 0, prefill): block z of grid.z works on rows z zrows .. of the query rows,
+// at their positions, with its own work region, exactly as a launch of those rows alone would.
+__device__ __forceinline__ void tile_rows(AttnArgs& a, int nr, int& pos0, int& nact) {
+    const int z = blockIdx.z;
+    const int r0 = z * a.zrows;
+    pos0 += r0;
+    nact = (a.ztotal - r0 < a.zrows) ? a.ztotal - r0 : a.zrows;
+    a.qh += (size_t)r0 * a.nq * kHD;
+    a.qkv += (size_t)r0 * a.qkv_stride;
+    a.work += (size_t)z * nr * a.nq * a.max_splits * (size_t)(kHD + 2);   // attn_work_floats of the tile
+    a.out += (size_t)r0 * a.nq * kHD;
+    if (a.xq) { a.xq += (size_t)r0 * a.nq * kHD; a.xs += (size_t)r0 * a.nq * kHD / 16; }
+}
 template <int NQW, int QPT, bool PREP>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
     warm_args(a);
     if (stopped(a.stop)) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
-    const int nact = a.nact_ptr ? ld_uniform(a.nact_ptr) : nr;
-    const int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
+    int nact = a.nact_ptr ? ld_uniform(a.nact_ptr) : nr;
+    int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
+    if (!PREP && a.zrows) tile_rows(a, nr, pos0, nact);
     const int Lmax = pos0 + nact;
     const int nqr = nact * G;                       // query vectors of this kv head
     const int kvrows = a.nkv * kHD;
@@ -352,7 +366,12 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
     if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
-    const int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
+    int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
+    if (a.zrows) {
+        int nact = 0;
+        tile_rows(a, nr, pos0, nact);
+        if (r >= nact) return;
+    }
     const int L = pos0 + r + 1;
     const int ns = (L + kSplit - 1) / kSplit;
     const int ms = a.max_splits;
@@ -420,6 +439,18 @@ int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
     return Q27X_E_SHAPE;
 }
 
+// prep of any number of rows (prefill): one wave per (head, row); K/V only when a.prep_kv_only
+int launch_attn_prep_rows(const AttnArgs& a, int nrows, hipStream_t s) {
+    if (int rc = attn_check(a, 1)) return rc;
+    if (nrows < 1 || !(a.rot == kHD || a.rot <= 64) || a.nact_ptr) {
+        set_error("attn prep: rows=%d rot=%d unsupported", nrows, a.rot);
+        return Q27X_E_SHAPE;
+    }
+    hipLaunchKernelGGL(k_attn_prep, dim3(a.prep_kv_only ? a.nkv : a.nq + a.nkv, nrows), dim3(64), 0, s, a);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
 template <bool PREP>
 static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
     const int nqr = nr * (a.nq / a.nkv);
@@ -437,7 +468,7 @@ static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
     }
     // at most kSplitBlocks blocks (about one per CU); a block takes splits blockIdx.x + i gridDim.x
     const int bx = a.max_splits < kSplitBlocks / a.nkv ? a.max_splits : (kSplitBlocks / a.nkv > 0 ? kSplitBlocks / a.nkv : 1);
-    const dim3 grid(bx, a.nkv);
+    const dim3 grid(bx, a.nkv, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u);
     if (nqr <= 8) hipLaunchKernelGGL((k_attn_split<1, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
     else if (nqr <= 16) hipLaunchKernelGGL((k_attn_split<2, 1, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
     else if (nqr <= 24) hipLaunchKernelGGL((k_attn_split<3, 2, PREP>), grid, dim3(kAttnThreads), lds, s, a, nr);
@@ -453,9 +484,14 @@ int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
     if (prep_fused && !(a.rot == kHD || a.rot <= 64)) { set_error("attn: rot=%d unsupported", a.rot); return Q27X_E_SHAPE; }
+    if (a.zrows && (prep_fused || a.zrows != nr || a.ztotal < 1 || a.nact_ptr)) {
+        set_error("attn: row tiles need separate prep, zrows == nr and no active-row count");
+        return Q27X_E_ARG;
+    }
     const int rc = prep_fused ? launch_split<true>(a, nr, s) : launch_split<false>(a, nr, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr), dim3(kHD), 0, s, a, nr);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u),
+                       dim3(kHD), 0, s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

@@ -252,6 +252,134 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
     }
 }
 
+// Prefill scan: the same per-row arithmetic as k_gdn over all nrows rows of a chunk, in blocks of
+// kMaxRows staged rows; the state stays in registers from the first row to the last, is updated
+// after every row and written back once (nothing pending afterwards). Row scalars: decay at
+// rowsc[n vh + h], beta at rowsc[(nrows + n) vh + h]. Output bf16 only (the prefill quantizes it
+// per token group afterwards).
+__global__ __launch_bounds__(kNT) void k_gdn_scan(GdnArgs a, int nrows) {
+    const int h = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int d = t & (kD - 1), g = t >> 7;
+    const int ratio = a.vh / a.kh, kk = h / ratio;
+    const int KD = a.kh * kD;
+    __shared__ float scv[kMaxRows][3 * kD];
+    __shared__ float sz[kMaxRows][kD];
+    __shared__ __attribute__((aligned(16))) float sq[kMaxRows][kD];
+    __shared__ __attribute__((aligned(16))) float sk[kMaxRows][kD];
+    __shared__ float pA[2][4][kD], pB[2][4][kD];
+    __shared__ float smix[kMaxRows][kD];
+    __shared__ float red[kMaxRows][2];
+    __shared__ float srow[kMaxRows][4];
+    float* Sp = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
+    float st[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
+    const int cl = (t < 3 * kD) ? t : 0;
+    const int ch = (cl < kD) ? kk * kD + cl : (cl < 2 * kD) ? KD + kk * kD + (cl - kD) : 2 * KD + h * kD + (cl - 2 * kD);
+    const float nw = bf2f(a.norm_w[(t & 63) + 64 * (wv & 1)]);
+    const int e = 64 * (wv & 1) + lane;
+    for (int r0 = 0; r0 < nrows; r0 += kMaxRows) {
+        const int nr = (nrows - r0 < kMaxRows) ? nrows - r0 : kMaxRows;
+        uint16_t xr[kMaxRows];
+#pragma unroll
+        for (int n = 0; n < kMaxRows; ++n)
+            xr[n] = (n < nr) ? ((t < 3 * kD) ? a.qkv[(size_t)(r0 + n) * a.qkv_stride + ch]
+                                             : a.z[(size_t)(r0 + n) * a.z_stride + (size_t)h * kD + d])
+                             : (uint16_t)0;
+        float r_a = 0.0f, r_b = 0.0f;
+        if (t < nr) {
+            r_a = a.rowsc[(size_t)(r0 + t) * a.vh + h];
+            r_b = a.rowsc[(size_t)(nrows + r0 + t) * a.vh + h];
+        }
+        __syncthreads();                            // the previous block's rows are consumed
+        if (t < nr) { srow[t][1] = r_b; srow[t][2] = r_a; }
+#pragma unroll
+        for (int n = 0; n < kMaxRows; ++n) {
+            if (n >= nr) break;
+            if (t < 3 * kD) scv[n][cl] = bf2f(xr[n]);
+            else sz[n][d] = bf2f(xr[n]);
+        }
+        __syncthreads();
+        for (int n = wv; n < nr; n += kNT / 64) {
+            const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
+            const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
+            const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
+            const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
+            const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
+            const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
+            const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
+            const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
+            const float invk = rsqrt_cr(ssk + 1e-6f);
+            sq[n][lane] = q0 * invq;
+            sq[n][64 + lane] = q1 * invq;
+            sk[n][lane] = k0 * invk;
+            sk[n][64 + lane] = k1 * invk;
+            if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
+        }
+        __syncthreads();
+        for (int n = 0; n < nr; ++n) {
+            const float kq = srow[n][0], beta = srow[n][1], decay = srow[n][2];
+            const float vv = scv[n][2 * kD + d];
+            float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < kJ; j4 += 4) {
+                const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
+                const float4 q4 = *(const float4*)&sq[n][g * kJ + j4];
+                accA = __builtin_fmaf(st[j4], k4.x, accA);
+                accB = __builtin_fmaf(st[j4], q4.x, accB);
+                accA = __builtin_fmaf(st[j4 + 1], k4.y, accA);
+                accB = __builtin_fmaf(st[j4 + 1], q4.y, accB);
+                accA = __builtin_fmaf(st[j4 + 2], k4.z, accA);
+                accB = __builtin_fmaf(st[j4 + 2], q4.z, accB);
+                accA = __builtin_fmaf(st[j4 + 3], k4.w, accA);
+                accB = __builtin_fmaf(st[j4 + 3], q4.w, accB);
+            }
+            pA[n & 1][g][d] = accA;
+            pB[n & 1][g][d] = accB;
+            __syncthreads();
+            const float A = ((pA[n & 1][0][d] + pA[n & 1][1][d]) + pA[n & 1][2][d]) + pA[n & 1][3][d];
+            const float B = ((pB[n & 1][0][d] + pB[n & 1][1][d]) + pB[n & 1][2][d]) + pB[n & 1][3][d];
+            const float delta = (vv - decay * A) * beta;
+            const float mixed = __builtin_fmaf(delta, kq, decay * B);
+#pragma unroll
+            for (int j4 = 0; j4 < kJ; j4 += 4) {
+                const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
+                st[j4] = __builtin_fmaf(k4.x, delta, decay * st[j4]);
+                st[j4 + 1] = __builtin_fmaf(k4.y, delta, decay * st[j4 + 1]);
+                st[j4 + 2] = __builtin_fmaf(k4.z, delta, decay * st[j4 + 2]);
+                st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
+            }
+            if (g == 0) smix[n][d] = mixed;
+        }
+        __syncthreads();
+        for (int n = wv >> 1; n < nr; n += 4) {
+            const float mx = smix[n][e];
+            const float r3 = tree64(mx * mx);
+            if (lane == 0) red[n][wv & 1] = r3;
+        }
+        __syncthreads();
+        for (int n = wv >> 1; n < nr; n += 4) {
+            const float mx = smix[n][e];
+            const float inv = rsqrt_cr((red[n][0] + red[n][1]) * (1.0f / (float)kD) + a.eps);
+            const float y = mx * inv * nw * qsilu(sz[n][e]);
+            a.out[(size_t)(r0 + n) * a.out_stride + (size_t)h * kD + e] = f2bf(y);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) Sp[(size_t)j * kD] = st[j];
+}
+int launch_gdn_scan(const GdnArgs& a, int nrows, hipStream_t s) {
+    if (a.d != kD || a.kh < 1 || a.vh % a.kh || nrows < 1 || !a.qkv || !a.z || !a.S || !a.rowsc || !a.out ||
+        !a.norm_w) {
+        set_error("gdn scan: unsupported shape or null argument (d=%d kh=%d vh=%d rows=%d)", a.d, a.kh, a.vh, nrows);
+        return Q27X_E_SHAPE;
+    }
+    hipLaunchKernelGGL(k_gdn_scan, dim3(a.vh), dim3(kNT), 0, s, a, nrows);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s) {
     if (a.d != kD || a.kh < 1 || a.vh % a.kh || nr < 1 || nr > kMaxRows || !a.qkv || !a.z || !a.S || !a.pend ||
         !a.out || !a.norm_w) {

@@ -48,10 +48,11 @@ struct GemmArgs {
     const float* sw;    // [N][ng]
     const int8_t* x;    // [M][K] per-(token, group) codes
     const float* sx;    // [M][ng]
-    float* y;           // [M][ldy]
-    const float* res;   // [M][ldr] or null
+    float* y;           // [M][ldy] (bf16 when out_bf16)
+    const float* res;   // [M][ldr] or null (bf16 when res_bf16)
     float alpha, rs;
     int M, N, K, gs, ng, ldy, ldr;
+    int out_bf16, res_bf16;
 };
 
 template <int BM, int NS>
@@ -195,8 +196,10 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (t < a.M) {
                     float o = facc[i][j][r] * a.alpha;
-                    if (a.res) o = o + a.rs * a.res[(size_t)t * a.ldr + n];
-                    a.y[(size_t)t * a.ldy + n] = o;
+                    if (a.res) o = o + a.rs * (a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)t * a.ldr + n])
+                                                          : a.res[(size_t)t * a.ldr + n]);
+                    if (a.out_bf16) ((uint16_t*)a.y)[(size_t)t * a.ldy + n] = f2bf(o);
+                    else a.y[(size_t)t * a.ldy + n] = o;
                 }
             }
         }
@@ -346,8 +349,10 @@ _Pragma("unroll")                                                               
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (t < a.M) {
                     float o = facc[i][j][r] * a.alpha;
-                    if (a.res) o = o + a.rs * a.res[(size_t)t * a.ldr + n];
-                    a.y[(size_t)t * a.ldy + n] = o;
+                    if (a.res) o = o + a.rs * (a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)t * a.ldr + n])
+                                                          : a.res[(size_t)t * a.ldr + n]);
+                    if (a.out_bf16) ((uint16_t*)a.y)[(size_t)t * a.ldy + n] = f2bf(o);
+                    else a.y[(size_t)t * a.ldy + n] = o;
                 }
             }
         }
@@ -447,9 +452,22 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
                   "K/gs <= %d, 16-byte aligned codes)", N, K, gs, kGK, kGK, kGMaxG);
         return Q27X_E_SHAPE;
     }
+    return launch_gemm_i8g(w, sw, N, K, gs, alpha, x, sx, M, y, ldy, 0, res, ldr, 0, rs, (hipStream_t)s);
+}
+
+namespace q27x {
+int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
+                    const float* sx, int M, void* y, int ldy, int out_bf16, const void* res, int ldr, int res_bf16,
+                    float rs, hipStream_t s) {
+    if ((N % 128) || (K % kGK) || (gs % kGK) || (K % gs) || K / gs > kGMaxG || ((uintptr_t)w & 15) ||
+        ((uintptr_t)x & 15) || M < 1 || ldy < N || (res && ldr < N)) {
+        set_error("gemm: no kernel for M %d, N %d, K %d, gs %d", M, N, K, gs);
+        return Q27X_E_SHAPE;
+    }
     GemmArgs a{};
-    a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = y; a.res = res; a.alpha = alpha; a.rs = rs;
+    a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = (float*)y; a.res = (const float*)res; a.alpha = alpha; a.rs = rs;
     a.M = M; a.N = N; a.K = K; a.gs = gs; a.ng = K / gs; a.ldy = ldy; a.ldr = ldr;
+    a.out_bf16 = out_bf16; a.res_bf16 = res_bf16;
     // Weight tiles of 128 rows (256-row tiles need 433 registers per lane, one block per CU, and
     // measured 1-8% slower). Token tiles of 256 (8 waves, one block per CU, a 5-stage ring) from
     // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
@@ -473,3 +491,4 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
+}  // namespace q27x

@@ -1,0 +1,194 @@
+// k_prefill.hip -- the element kernels of the layer-major prefill (ls_q8_layer's stages,
+// src/q27_main.cpp:4076-4316) around the int8 MFMA GEMM: the per-(token, group) quantizer of bf16
+// rows, the GDN chunk conv, the GDN row scalars and the SwiGLU quantizer. Each keeps the decode
+// path's arithmetic for its values, so a prefilled state continues exactly like a decoded one.
+#include "q27x_dev.h"
+#include "q27x_int.h"
+
+namespace q27x {
+
+// bf16 rows [M][ld] -> per-(token, group) codes [M][K] and scales [M][K / gs] (the quantizer of
+// k_quant_tok_grp on the rows' float values: sc = max|v| / 127, qi = sc > 0 ? 1/sc : 0).
+// One 256-thread block per (group, token), four values per thread per 1024 columns.
+__global__ __launch_bounds__(256) void k_pf_quant_bf16(const uint16_t* __restrict__ x, int ld, int K, int gs,
+                                                       int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = K / gs;
+    __shared__ float red[4];
+    const uint16_t* row = x + (size_t)tok * ld + (size_t)g * gs;
+    float mx = 0.0f;
+    for (int k = 4 * t; k < gs; k += 1024) {
+        const uint2 u = *(const uint2*)(row + k);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(__uint_as_float(u.x << 16)), fabsf(__uint_as_float(u.x & 0xFFFF0000u))),
+                             fmaxf(fabsf(__uint_as_float(u.y << 16)), fabsf(__uint_as_float(u.y & 0xFFFF0000u)))));
+    }
+    mx = max_xor(mx, 64);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+    if (t == 0) xs[(size_t)tok * ng + g] = sc;
+    int8_t* out = xq + (size_t)tok * K + (size_t)g * gs;
+    for (int k = 4 * t; k < gs; k += 1024) {
+        const uint2 u = *(const uint2*)(row + k);
+        const uint32_t pk = (uint32_t)(uint8_t)qcode(__uint_as_float(u.x << 16), qi) |
+                            ((uint32_t)(uint8_t)qcode(__uint_as_float(u.x & 0xFFFF0000u), qi) << 8) |
+                            ((uint32_t)(uint8_t)qcode(__uint_as_float(u.y << 16), qi) << 16) |
+                            ((uint32_t)(uint8_t)qcode(__uint_as_float(u.y & 0xFFFF0000u), qi) << 24);
+        *(uint32_t*)(out + k) = pk;
+    }
+}
+int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t* xq, float* xs, hipStream_t s) {
+    if (!x || !xq || !xs || M < 1 || K < 4 || gs < 4 || (gs & 3) || (K % gs) || ld < K || (ld & 3) || ((uintptr_t)x & 7)) {
+        set_error("prefill quant: bad arguments (M %d, K %d, gs %d, ld %d)", M, K, gs, ld);
+        return Q27X_E_ARG;
+    }
+    hipLaunchKernelGGL(k_pf_quant_bf16, dim3((unsigned)(K / gs), (unsigned)M), dim3(256), 0, s, x, ld, K, gs, xq, xs);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+// GDN conv of a chunk, in place on the q|k|v columns of the projection rows buf [C][ld]: the
+// decode path's conv (k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439: taps 0..3 over the three
+// committed inputs and the row's, the first a plain product, SiLU, bf16). One thread per channel
+// runs the rows in order from the history in the channel's 32-byte record (committed h0 h1 h2,
+// then the npend pending raw inputs of the last decode call) and leaves the committed history of
+// the chunk's last three inputs in the record, nothing pending.
+__global__ __launch_bounds__(256) void k_pf_conv(uint16_t* __restrict__ buf, int ld, int C, int nconv,
+                                                 const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ rec,
+                                                 int npend) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= nconv) return;
+    const uint4 r0 = *(const uint4*)(rec + (size_t)c * 16);
+    const uint4 r1 = *(const uint4*)(rec + (size_t)c * 16 + 8);
+    const uint32_t dw[8] = { r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w };
+    uint32_t h0 = dw[0] & 0xFFFFu, h1 = dw[0] >> 16, h2 = dw[1] & 0xFFFFu;
+    for (int p = 0; p < npend && p < kMaxRows; ++p) {
+        h0 = h1; h1 = h2; h2 = (dw[2 + (p >> 1)] >> (16 * (p & 1))) & 0xFFFFu;
+    }
+    const uint2 wv = *(const uint2*)(conv_w + (size_t)c * 4);
+    const float w0 = __uint_as_float(wv.x << 16), w1 = __uint_as_float(wv.x & 0xFFFF0000u);
+    const float w2 = __uint_as_float(wv.y << 16), w3 = __uint_as_float(wv.y & 0xFFFF0000u);
+    for (int n = 0; n < C; ++n) {
+        uint16_t* p = buf + (size_t)n * ld + c;
+        const uint32_t xr = *p;
+        float acc = __uint_as_float(h0 << 16) * w0;
+        acc = __builtin_fmaf(__uint_as_float(h1 << 16), w1, acc);
+        acc = __builtin_fmaf(__uint_as_float(h2 << 16), w2, acc);
+        acc = __builtin_fmaf(__uint_as_float(xr << 16), w3, acc);
+        *p = f2bf(qsilu(acc));
+        h0 = h1; h1 = h2; h2 = xr;
+    }
+    uint4* d = (uint4*)(rec + (size_t)c * 16);
+    d[0] = make_uint4(h0 | (h1 << 16), h2, 0u, 0u);
+    d[1] = make_uint4(0u, 0u, 0u, 0u);
+}
+int launch_pf_conv(uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
+                   hipStream_t s) {
+    if (!buf || !conv_w || !rec || C < 1 || nconv < 1 || ld < nconv || npend < 0 || npend > kMaxRows ||
+        ((uintptr_t)rec & 15) || ((uintptr_t)conv_w & 7)) {
+        set_error("prefill conv: bad arguments");
+        return Q27X_E_ARG;
+    }
+    hipLaunchKernelGGL(k_pf_conv, dim3((unsigned)((nconv + 255) / 256)), dim3(256), 0, s, buf, ld, C, nconv, conv_w,
+                       rec, npend);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+// GDN row scalars of C rows: the bf16 GEMV of in_a / in_b row h with each bf16 normed row y (the
+// decode path's order: 8-element chunk c on lane c % 64 in ascending c, fmaf per element, the
+// shfl tree, bf16 rounding; k_bf16_gemv2_tile, src/q27_util.hip:114-167), then
+// decay = exp(-exp(A_log) softplus(a + dt_bias)) and beta = sigmoid(b) (src/q27_gdn.hip:206-372)
+// into out [2][C][vh]. One wave per (weight row, row); block = 4 weight rows of one row.
+__global__ __launch_bounds__(256) void k_pf_ab(const uint16_t* __restrict__ in_a, const uint16_t* __restrict__ in_b,
+                                               const uint16_t* __restrict__ A_log,
+                                               const uint16_t* __restrict__ dt_bias, const uint16_t* __restrict__ y,
+                                               int ystride, int K, int vh, int C, float* __restrict__ out) {
+    const int tok = blockIdx.x, lane = threadIdx.x & 63;
+    const int j = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (j >= 2 * vh) return;
+    const int which = j / vh, head = j - which * vh;
+    const uint16_t* wrow = (which ? in_b : in_a) + (size_t)head * K;
+    const uint16_t* yr = y + (size_t)tok * ystride;
+    const int nch = K >> 3;
+    float acc = 0.0f;
+    for (int c = lane; c < nch; c += 64) {
+        const uint4 w = *(const uint4*)(wrow + 8 * c);
+        const uint4 x = *(const uint4*)(yr + 8 * c);
+        acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(x.x << 16), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(x.x & 0xFFFF0000u), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(x.y << 16), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(x.y & 0xFFFF0000u), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(x.z << 16), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(x.z & 0xFFFF0000u), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(x.w << 16), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(x.w & 0xFFFF0000u), acc);
+    }
+    const float v = bfr(bcast0(tree64(acc)));
+    if (lane == 0) {
+        float r;
+        if (which) r = qsigmoid(v);
+        else r = qexp(-(qexp(bf2f(A_log[head])) * qsoftplus(v + bf2f(dt_bias[head]))));
+        out[((size_t)which * C + tok) * vh + head] = r;
+    }
+}
+int launch_pf_ab(const uint16_t* in_a, const uint16_t* in_b, const uint16_t* A_log, const uint16_t* dt_bias,
+                 const uint16_t* y, int ystride, int K, int vh, int C, float* out, hipStream_t s) {
+    if (!in_a || !in_b || !A_log || !dt_bias || !y || !out || (K & 7) || K < 8 || vh < 1 || C < 1 || (ystride & 7) ||
+        ((uintptr_t)y & 15) || ((uintptr_t)in_a & 15) || ((uintptr_t)in_b & 15)) {
+        set_error("prefill a/b: bad arguments");
+        return Q27X_E_ARG;
+    }
+    hipLaunchKernelGGL(k_pf_ab, dim3((unsigned)C, (unsigned)((2 * vh + 3) / 4)), dim3(256), 0, s, in_a, in_b, A_log,
+                       dt_bias, y, ystride, K, vh, C, out);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+// SwiGLU of the fused gate|up GEMM rows gu [C][2I] (units of 32 rows: 16 gate rows, then the 16
+// matching up rows) and the per-(token, group) quantizer of its I outputs: v = silu(g) u gscale
+// with the decode path's expression (g / (1 + e^-g)), then sc = max|v| / 127 over each group of
+// gs outputs. One 256-thread block per (group, token).
+__global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict__ gu, int I, int gs, float gscale,
+                                                         int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = I / gs;
+    __shared__ float red[4];
+    const float* row = gu + (size_t)tok * 2 * I;
+    constexpr int VPT = 8;                         // values per thread held for the two passes
+    float v[VPT];
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const int i = g * gs + t + 256 * u;
+        v[u] = 0.0f;
+        if (t + 256 * u < gs) {
+            const int gr = (i >> 4) * 32 + (i & 15);
+            const float gv = row[gr], uv = row[gr + 16];
+            const float swv = gv / (1.0f + qexp(-gv));
+            v[u] = swv * uv * gscale;
+            mx = fmaxf(mx, fabsf(v[u]));
+        }
+    }
+    mx = max_xor(mx, 64);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+    if (t == 0) xs[(size_t)tok * ng + g] = sc;
+#pragma unroll
+    for (int u = 0; u < VPT; ++u)
+        if (t + 256 * u < gs) xq[(size_t)tok * I + g * gs + t + 256 * u] = qcode(v[u], qi);
+}
+int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
+                           hipStream_t s) {
+    if (!gu || !xq || !xs || C < 1 || (I & 31) || gs < 16 || gs > 2048 || (I % gs)) {
+        set_error("prefill swiglu: bad arguments (I %d, gs %d)", I, gs);
+        return Q27X_E_ARG;
+    }
+    hipLaunchKernelGGL(k_pf_swiglu_quant, dim3((unsigned)(I / gs), (unsigned)C), dim3(256), 0, s, gu, I, gs, gscale, xq,
+                       xs);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+}  // namespace q27x

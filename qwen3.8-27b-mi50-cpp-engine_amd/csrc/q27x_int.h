@@ -33,6 +33,7 @@ struct NormArgs {
     const int* stop;
     const int* row_sel;                           // optional: process only row *row_sel (into row 0)
     unsigned long long* stamp;                    // optional: block 0 stores the wall clock at its start
+    float* yf; int yfstride;                      // optional: the values xq would quantize, as fp32
 };
 // ---------------------------------------------------------------- projection
 enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2, EPI_CONV = 3 };
@@ -103,6 +104,9 @@ struct GdnArgs {
     const int* stop;
 };
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s);
+// prefill: nrows rows (any count) with the row scalars prepared in rowsc [2][nrows][vh], the state
+// committed through the last row, bf16 output only
+int launch_gdn_scan(const GdnArgs& a, int nrows, hipStream_t s);
 int gdn_set_lds_limit();
 // conv + SiLU with deferred commit as a standalone kernel (kernel-tier entry)
 int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_stride,
@@ -125,11 +129,32 @@ struct AttnArgs {
     float sl2e;                                   // (float)(log2(e) / sqrt(hd))
     uint16_t* out; int8_t* xq; float* xs;
     const int* stop;
+    // prefill: the rows come in tiles of zrows (grid.z = tile) out of ztotal rows; tile z holds rows
+    // z zrows .. at positions pos0 + z zrows .., its own work region; 0 = no tiles
+    int zrows, ztotal;
+    int prep_kv_only;                             // prep writes K/V only (the MTP prompt pass)
 };
 int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s);
+int launch_attn_prep_rows(const AttnArgs& a, int nrows, hipStream_t s);   // any row count (prefill)
 // prep_fused: the split kernel also norms/ropes the rows and writes the new K/V (no prep launch)
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused = false);
 size_t attn_work_floats(int nq, int hd, int max_splits, int nr);
+
+// ---------------------------------------------------------------- prefill GEMM (int8 MFMA)
+// y = GEMM of per-(row, group) weights and per-(token, group) activations (k_gemm.hip), y bf16 when
+// out_bf16, the residual bf16 when res_bf16
+int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
+                    const float* sx, int M, void* y, int ldy, int out_bf16, const void* res, int ldr, int res_bf16,
+                    float rs, hipStream_t s);
+
+// ---------------------------------------------------------------- prefill element kernels (k_prefill.hip)
+int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t* xq, float* xs, hipStream_t s);
+int launch_pf_conv(uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
+                   hipStream_t s);
+int launch_pf_ab(const uint16_t* in_a, const uint16_t* in_b, const uint16_t* A_log, const uint16_t* dt_bias,
+                 const uint16_t* y, int ystride, int K, int vh, int C, float* out, hipStream_t s);
+int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
+                           hipStream_t s);
 
 // ---------------------------------------------------------------- synthetic weights
 int launch_gen_i8(int8_t* W, float* WS, int rows, int K, uint64_t key, int layout_gu, int is_up,

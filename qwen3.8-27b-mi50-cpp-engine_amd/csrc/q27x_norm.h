@@ -102,6 +102,10 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int r0, int nrows, 
                 if (a.y)
                     *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
                                                                            (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                if (a.yf)
+                    *(float4*)(a.yf + (size_t)r * a.yfstride + k) =
+                        a.quant_bf16 ? make_float4(bf2f(yb[0]), bf2f(yb[1]), bf2f(yb[2]), bf2f(yb[3]))
+                                     : make_float4(nm[0], nm[1], nm[2], nm[3]);
                 if (a.xq) {
                     float q[4], mx = 0.0f;
 #pragma unroll

@@ -95,7 +95,7 @@ _SIGS = {
     "q27x_spec_config_from_env": ([VP], I),
     "q27x_ctx_create": ([I, VP, VP], I), "q27x_ctx_destroy": ([VP], I),
     "q27x_load_synthetic": ([VP, U64], I), "q27x_weight_bytes": ([VP, VP], I),
-    "q27x_reset": ([VP], I), "q27x_prefill": ([VP, VP, I, VP], I),
+    "q27x_reset": ([VP], I), "q27x_prefill": ([VP, VP, I, VP], I), "q27x_prefill_gemm": ([VP, VP, I, VP], I),
     "q27x_decode_step": ([VP, VP], I), "q27x_spec_round": ([VP, VP, VP], I),
     "q27x_set_forced_drafts": ([VP, VP, I], I),
     "q27x_mtp_draft": ([VP, VP, VP, I, I, I, VP, VP, VP], I),
@@ -216,6 +216,12 @@ class Engine:
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         t = ctypes.c_int32(0)
         call("q27x_prefill", self.ctx, ids.ctypes.data, len(ids), ctypes.byref(t))
+        return t.value
+
+    def prefill_gemm(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        t = ctypes.c_int32(0)
+        call("q27x_prefill_gemm", self.ctx, ids.ctypes.data, len(ids), ctypes.byref(t))
         return t.value
 
     def decode_step(self):

@@ -153,6 +153,28 @@ def test_full_geometry_spec_equals_plain(gpu):
     eng.close()
 
 
+
+def test_config4_k7_ctx16k_forced_equals_plain(gpu):
+    """BASELINE config 4 (64 layers, K = 7, ctx 16384): after a 16200-token prompt, forced
+    acceptance (drafts = the trunk's own greedy continuation) commits K + 1 = 8 tokens per round
+    and the stream equals plain greedy -- the 8-row verify forms (one weight pass for down and
+    lm_head), attention over ~16K positions, and the K = 7 hand-off at full geometry."""
+    X = gpu
+    cfg = X.default_config(spec_k=7, ctx=16384)
+    eng = X.Engine(cfg, SEED)
+    p = prompt_of(cfg, 16200, seed=4)
+    first = eng.prefill(p)
+    plain, _ = eng.generate(48, spec=False)
+    assert plain[0] == first
+    eng.prefill(p)
+    eng.set_forced(np.array(plain, np.int32))
+    forced, stf = eng.generate(48, spec=True)
+    assert forced == plain
+    assert stf.acc_hist[7] >= stf.rounds - 1, (stf.rounds, list(stf.acc_hist))
+    assert stf.committed >= 8 * (stf.rounds - 1)
+    eng.set_forced([])
+    eng.close()
+
 # ---------------------------------------------------------------- drafts and hand-off
 def kv_bytes(cfg):
     return cfg.ctx * cfg.n_kv * cfg.head_dim
