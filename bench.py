@@ -401,10 +401,22 @@ def main():
     prompt = np.random.default_rng(0x51E70003).integers(0, cfg.vocab, args.prompt).astype(np.int32)
 
     # ---- natural acceptance
+    # prompt ingest: the verify kernels over the prompt (q27x_prefill) and the layer-major int8-MFMA
+    # GEMM path (q27x_prefill_gemm, BASELINE config 4's prefill ingest), wall clock per call
     t = time.time()
     eng.prefill(prompt)
     prefill_s = time.time() - t
-    log(f"prefill {args.prompt} tokens: {prefill_s:.2f} s")
+    prefill = {"verify_path": {"tokens": args.prompt, "s": round(prefill_s, 4),
+                               "tok_s": round(args.prompt / prefill_s, 1)}}
+    for n_pf in sorted({args.prompt, 1024, 4096}):
+        p_pf = np.random.default_rng(0x51E70004 + n_pf).integers(0, cfg.vocab, n_pf).astype(np.int32)
+        eng.prefill_gemm(p_pf)                      # first call allocates its buffers
+        t = time.time()
+        eng.prefill_gemm(p_pf)
+        s_pf = time.time() - t
+        prefill[f"gemm_path_{n_pf}"] = {"tokens": n_pf, "s": round(s_pf, 4), "tok_s": round(n_pf / s_pf, 1)}
+    log(f"prefill: {prefill}")
+    eng.prefill_gemm(prompt)
     eng.run_rounds(args.warmup, spec=True)
     st = eng.run_rounds(args.steps, spec=True)
     nat_tps = st.committed / (st.decode_ms / 1e3)
@@ -414,7 +426,7 @@ def main():
         f"phases {phases}")
 
     # ---- plain greedy (comparator, and the forced-acceptance draft stream)
-    eng.prefill(prompt)
+    eng.prefill_gemm(prompt)
     n_plain = rounds_total * (K + 1) + 4
     t = time.time()
     plain, _ = eng.generate(n_plain, spec=False)
@@ -424,7 +436,7 @@ def main():
 
     forced = None
     if not args.no_forced:
-        eng.prefill(prompt)
+        eng.prefill_gemm(prompt)
         eng.set_forced(np.array(plain, np.int32))
         eng.run_rounds(args.warmup, spec=True)
         sf = eng.run_rounds(args.steps, spec=True)
@@ -506,6 +518,7 @@ def main():
         "configs_gpu": gpu_cfg,
         "configs_cpu": cpu_cfg,
         "prefill_s": round(prefill_s, 3),
+        "prefill": prefill,
         "prefill_gemm": pg,
         "cpu_baseline": cpu,
     }

@@ -35,7 +35,12 @@ enum {
 };
 static uint64_t tid(int code, int kind) { return ((uint64_t)code << 8) | (uint64_t)kind; }
 
-struct Mat { int8_t* w = nullptr; float* s = nullptr; int rows = 0, K = 0; };
+struct Mat {
+    int8_t* w = nullptr; float* s = nullptr; int rows = 0, K = 0;
+    // the prefill GEMM's representation of the same matrix (per-(row, group) codes and scales),
+    // made on the first GEMM prefill after a load
+    int8_t* pw = nullptr; float* ps = nullptr;
+};
 
 struct LayerDev {
     int is_attn = 0;
@@ -93,8 +98,8 @@ struct PfBuf {
     float* gu = nullptr;         // [cap][2I] gate|up GEMM output
     uint16_t* mix = nullptr;     // [cap][max(nz, att)] mixer output
     float* rowsc = nullptr;      // [2][cap][vh] GDN decay, beta
-    int8_t* wg = nullptr; float* sg = nullptr;     // one matrix in the GEMM representation
     float* work = nullptr;       // attention split partials of kPfAttnRows rows
+    uint16_t* cv = nullptr;      // [cap][nqkv] convolved q|k|v rows
     std::vector<void*> allocs;
 };
 
@@ -138,6 +143,8 @@ struct q27x_ctx {
     int wclk_khz = 0;      // device wall clock (s_memrealtime) rate
     float sl2e = 0.0f;
     PfBuf* pf = nullptr;
+    std::vector<void*> pf_walloc;   // the GEMM representations of the weights
+    int pf_wready = 0;
 };
 
 namespace q27x {
@@ -791,6 +798,7 @@ int q27x_ctx_destroy(q27x_ctx* x) {
         for (void* p : x->pf->allocs) (void)hipFree(p);
         delete x->pf;
     }
+    for (void* p : x->pf_walloc) (void)hipFree(p);
     if (x->warena) (void)hipFree(x->warena);
     if (x->sarena) (void)hipFree(x->sarena);
     if (x->stream) (void)hipStreamDestroy(x->stream);
@@ -891,6 +899,7 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
 #undef VEC
     Q27X_HIP(hipStreamSynchronize(s));
     x->loaded = 1;
+    x->pf_wready = 0;   // the GEMM representations are remade from these weights
     return q27x_reset(x);
 }
 
@@ -1004,11 +1013,6 @@ static int pf_alloc(q27x_ctx* x, int cap) {
     const int wz = x->nqkv + x->nz, wq = x->qr + 2 * x->kvr;
     const int kmax = std::max(std::max(H, I), std::max(x->nz, x->att));
     const int wmax = std::max(std::max(wz, wq), H);
-    size_t wgmax = 0;
-    for (size_t r : { (size_t)2 * I * H, (size_t)H * I, (size_t)wz * H, (size_t)wq * H, (size_t)H * x->att,
-                      (size_t)H * x->nz, (size_t)H * H })
-        wgmax = std::max(wgmax, r);
-    const size_t rows_max = (size_t)std::max(std::max(2 * I, wz), std::max(wq, H));
     PfBuf* B = new PfBuf();
     B->cap = cap;
     auto A = [&](void** p, size_t bytes) -> int {
@@ -1025,9 +1029,9 @@ static int pf_alloc(q27x_ctx* x, int cap) {
         (rc = A((void**)&B->xq2, C * H)) || (rc = A((void**)&B->xs2, C * 32 * 4)) ||
         (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
         (rc = A((void**)&B->gu, C * 2 * I * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
-        (rc = A((void**)&B->rowsc, 2 * C * c.gdn_vh * 4)) || (rc = A((void**)&B->wg, wgmax)) ||
-        (rc = A((void**)&B->sg, rows_max * 32 * 4)) ||
-        (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4))) {
+        (rc = A((void**)&B->rowsc, 2 * C * c.gdn_vh * 4)) ||
+        (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4)) ||
+        (rc = A((void**)&B->cv, C * x->nqkv * 2))) {
         for (void* p : B->allocs) (void)hipFree(p);
         delete B;
         return rc;
@@ -1039,15 +1043,36 @@ static int pf_alloc(q27x_ctx* x, int cap) {
 // y = GEMM(rows [r0, r0 + nrows) of W, the codes xq/xs of M rows) (+ the bf16 residual), y bf16
 // or fp32 with row stride ldy
 static int pf_gemm(q27x_ctx* x, const Mat& W, int r0, int nrows, const int8_t* xq, const float* xs, int M, void* y,
-                   int ldy, int out_bf16, const uint16_t* res_bf16) {
-    PfBuf& B = *x->pf;
-    hipStream_t s = x->stream;
+                   int ldy, int out_bf16, const void* res, int res_bf16 = 1) {
     const int K = W.K, gs = pf_gs(K);
-    int rc = q27x_i8g64_to_grp(W.w + (size_t)r0 * K, W.s + (size_t)r0 * (K / 64), nrows, K, gs, B.wg, B.sg,
-                               (q27x_stream_t)s);
-    if (rc) return rc;
-    return launch_gemm_i8g(B.wg, B.sg, nrows, K, gs, 1.0f, xq, xs, M, y, ldy, out_bf16, res_bf16, x->H, 1,
-                           res_bf16 ? 1.0f : 0.0f, s);
+    if (!W.pw) { set_error("prefill: no GEMM representation of a %d x %d matrix", W.rows, K); return Q27X_E_STATE; }
+    return launch_gemm_i8g(W.pw + (size_t)r0 * K, W.ps + (size_t)r0 * (K / gs), nrows, K, gs, 1.0f, xq, xs, M, y, ldy,
+                           out_bf16, res, x->H, res_bf16, res ? 1.0f : 0.0f, x->stream);
+}
+// every matrix of the model in the GEMM representation (the reference keeps such per-(row, group)
+// mirrors from load time, src/q27_epi.hip:14-35); made once per load, kept on the device
+static int pf_weights(q27x_ctx* x) {
+    if (x->pf_wready) return Q27X_OK;
+    std::vector<Mat*> ms;
+    for (LayerDev& Y : x->L) {
+        for (Mat* m : { &Y.qkvz, &Y.out_proj, &Y.qkv, &Y.o, &Y.gu, &Y.down }) if (m->w) ms.push_back(m);
+    }
+    for (Mat* m : { &x->fc0, &x->fc1, &x->mtp.qkv }) if (m->w) ms.push_back(m);
+    for (Mat* m : ms) {
+        const int K = m->K, gs = pf_gs(K);
+        if (!m->pw) {
+            hipError_t e = hipMalloc((void**)&m->pw, (size_t)m->rows * K);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc (prefill weights)");
+            x->pf_walloc.push_back(m->pw);
+            e = hipMalloc((void**)&m->ps, (size_t)m->rows * (K / gs) * 4);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc (prefill weight scales)");
+            x->pf_walloc.push_back(m->ps);
+        }
+        const int rc = q27x_i8g64_to_grp(m->w, m->s, m->rows, K, gs, m->pw, m->ps, (q27x_stream_t)x->stream);
+        if (rc) return rc;
+    }
+    x->pf_wready = 1;
+    return Q27X_OK;
 }
 // norm of C rows (values to B.yf) and their per-(token, group) codes
 static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs) {
@@ -1098,9 +1123,9 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         const int wz = Y.qkvz.rows;
         if ((rc = pf_gemm(x, Y.qkvz, 0, wz, B.xq, B.xs, C, B.pb, wz, 1, nullptr))) return rc;
         if ((rc = launch_pf_ab(Y.in_a, Y.in_b, Y.A_log, Y.dt_bias, B.y, H, H, c.gdn_vh, C, B.rowsc, s))) return rc;
-        if ((rc = launch_pf_conv(B.pb, wz, C, x->nqkv, Y.conv_w, Y.conv_st, 0, s))) return rc;
+        if ((rc = launch_pf_conv(B.pb, wz, C, x->nqkv, Y.conv_w, Y.conv_st, 0, B.cv, x->nqkv, s))) return rc;
         GdnArgs g{};
-        g.qkv = B.pb; g.qkv_stride = wz; g.z = B.pb + x->nqkv; g.z_stride = wz;
+        g.qkv = B.cv; g.qkv_stride = x->nqkv; g.z = B.pb + x->nqkv; g.z_stride = wz;
         g.rowsc = B.rowsc; g.norm_w = Y.gdn_norm; g.S = Y.S;
         g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
         g.out = B.mix; g.out_stride = x->nz; g.stop = &d->stop;
@@ -1131,13 +1156,8 @@ static int pf_mtp(q27x_ctx* x, int p0, int C) {
     const Mat& fe = c.mtp_swap ? x->fc0 : x->fc1;    // the half that multiplies the embedding
     const Mat& fh = c.mtp_swap ? x->fc1 : x->fc0;
     if ((rc = pf_gemm(x, fe, 0, H, B.xq, B.xs, C, B.x, H, 0, nullptr))) return rc;
-    // (fp32 residual: the same GEMM with res = the first half's output, read and written in place)
-    {
-        const int K = fh.K, gs = pf_gs(K);
-        if ((rc = q27x_i8g64_to_grp(fh.w, fh.s, H, K, gs, B.wg, B.sg, (q27x_stream_t)x->stream))) return rc;
-        if ((rc = launch_gemm_i8g(B.wg, B.sg, H, K, gs, 1.0f, B.xq2, B.xs2, C, B.x, H, 0, B.x, H, 0, 1.0f, x->stream)))
-            return rc;
-    }
+    // (fp32 residual: the first half's output, read and written in place)
+    if ((rc = pf_gemm(x, fh, 0, H, B.xq2, B.xs2, C, B.x, H, 0, B.x, 0))) return rc;
     if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, M.in_norm, po, 0, nullptr, nullptr), C, B.xq, B.xs))) return rc;
     const int wq = M.qkv.rows;
     if ((rc = pf_gemm(x, M.qkv, x->qr, 2 * x->kvr, B.xq, B.xs, C, B.pb + x->qr, wq, 1, nullptr))) return rc;
@@ -1163,6 +1183,7 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
     if (rc) return rc;
     const int chunk = pf_chunk();
     if ((rc = pf_alloc(x, std::min(n, chunk)))) return rc;
+    if ((rc = pf_weights(x))) return rc;
     hipStream_t s = x->stream;
     Dctl* d = x->dctl;
     const q27x_config& c = x->c;

@@ -47,50 +47,63 @@ int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t
     return Q27X_OK;
 }
 
-// GDN conv of a chunk, in place on the q|k|v columns of the projection rows buf [C][ld]: the
-// decode path's conv (k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439: taps 0..3 over the three
-// committed inputs and the row's, the first a plain product, SiLU, bf16). One thread per channel
-// runs the rows in order from the history in the channel's 32-byte record (committed h0 h1 h2,
-// then the npend pending raw inputs of the last decode call) and leaves the committed history of
-// the chunk's last three inputs in the record, nothing pending.
-__global__ __launch_bounds__(256) void k_pf_conv(uint16_t* __restrict__ buf, int ld, int C, int nconv,
-                                                 const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ rec,
-                                                 int npend) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
+// GDN conv of a chunk: the decode path's conv (k_gdn_conv_tp_tile, src/q27_gdn.hip:411-439: taps
+// 0..3 over the three inputs before the row's and the row's own, the first a plain product, SiLU,
+// bf16) of the q|k|v columns of the projection rows buf [C][ld] into out [C][ldo]. Each output
+// depends only on raw inputs, so one thread per (channel, row): the inputs before row 0 come from
+// the channel's 32-byte record (committed h0 h1 h2, then the npend pending raw inputs of the last
+// decode call). k_pf_conv_commit then leaves the chunk's last three inputs in the record as the
+// committed history, nothing pending.
+__device__ __forceinline__ uint32_t conv_hist_at(const uint16_t* rec, int c, int npend, int j) {
+    // element j (0..2) of the committed history after applying the npend pending inputs
+    const int src = j + npend;                      // index into h0 h1 h2 r0 r1 ...
+    return src < 3 ? rec[(size_t)c * 16 + src] : rec[(size_t)c * 16 + 4 + (src - 3)];
+}
+__global__ __launch_bounds__(256) void k_pf_conv(const uint16_t* __restrict__ buf, int ld, int C, int nconv,
+                                                 const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ rec,
+                                                 int npend, uint16_t* __restrict__ out, int ldo) {
+    const int c = blockIdx.x * 256 + threadIdx.x, n = blockIdx.y;
     if (c >= nconv) return;
-    const uint4 r0 = *(const uint4*)(rec + (size_t)c * 16);
-    const uint4 r1 = *(const uint4*)(rec + (size_t)c * 16 + 8);
-    const uint32_t dw[8] = { r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w };
-    uint32_t h0 = dw[0] & 0xFFFFu, h1 = dw[0] >> 16, h2 = dw[1] & 0xFFFFu;
-    for (int p = 0; p < npend && p < kMaxRows; ++p) {
-        h0 = h1; h1 = h2; h2 = (dw[2 + (p >> 1)] >> (16 * (p & 1))) & 0xFFFFu;
+    uint32_t x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = n - 3 + j;                    // row of tap j; r < 0: the history
+        x[j] = (r >= 0) ? buf[(size_t)r * ld + c] : conv_hist_at(rec, c, npend, 3 + r);
     }
     const uint2 wv = *(const uint2*)(conv_w + (size_t)c * 4);
-    const float w0 = __uint_as_float(wv.x << 16), w1 = __uint_as_float(wv.x & 0xFFFF0000u);
-    const float w2 = __uint_as_float(wv.y << 16), w3 = __uint_as_float(wv.y & 0xFFFF0000u);
-    for (int n = 0; n < C; ++n) {
-        uint16_t* p = buf + (size_t)n * ld + c;
-        const uint32_t xr = *p;
-        float acc = __uint_as_float(h0 << 16) * w0;
-        acc = __builtin_fmaf(__uint_as_float(h1 << 16), w1, acc);
-        acc = __builtin_fmaf(__uint_as_float(h2 << 16), w2, acc);
-        acc = __builtin_fmaf(__uint_as_float(xr << 16), w3, acc);
-        *p = f2bf(qsilu(acc));
-        h0 = h1; h1 = h2; h2 = xr;
+    float acc = __uint_as_float(x[0] << 16) * __uint_as_float(wv.x << 16);
+    acc = __builtin_fmaf(__uint_as_float(x[1] << 16), __uint_as_float(wv.x & 0xFFFF0000u), acc);
+    acc = __builtin_fmaf(__uint_as_float(x[2] << 16), __uint_as_float(wv.y << 16), acc);
+    acc = __builtin_fmaf(__uint_as_float(x[3] << 16), __uint_as_float(wv.y & 0xFFFF0000u), acc);
+    out[(size_t)n * ldo + c] = f2bf(qsilu(acc));
+}
+__global__ __launch_bounds__(256) void k_pf_conv_commit(const uint16_t* __restrict__ buf, int ld, int C, int nconv,
+                                                        uint16_t* __restrict__ rec, int npend) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= nconv) return;
+    uint32_t h[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int r = C - 3 + j;
+        h[j] = (r >= 0) ? buf[(size_t)r * ld + c] : conv_hist_at(rec, c, npend, 3 + r);
     }
     uint4* d = (uint4*)(rec + (size_t)c * 16);
-    d[0] = make_uint4(h0 | (h1 << 16), h2, 0u, 0u);
+    d[0] = make_uint4(h[0] | (h[1] << 16), h[2], 0u, 0u);
     d[1] = make_uint4(0u, 0u, 0u, 0u);
 }
-int launch_pf_conv(uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
-                   hipStream_t s) {
-    if (!buf || !conv_w || !rec || C < 1 || nconv < 1 || ld < nconv || npend < 0 || npend > kMaxRows ||
-        ((uintptr_t)rec & 15) || ((uintptr_t)conv_w & 7)) {
+int launch_pf_conv(const uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
+                   uint16_t* out, int ldo, hipStream_t s) {
+    if (!buf || !conv_w || !rec || !out || C < 1 || nconv < 1 || ld < nconv || ldo < nconv || npend < 0 ||
+        npend > kMaxRows || ((uintptr_t)rec & 15) || ((uintptr_t)conv_w & 7)) {
         set_error("prefill conv: bad arguments");
         return Q27X_E_ARG;
     }
-    hipLaunchKernelGGL(k_pf_conv, dim3((unsigned)((nconv + 255) / 256)), dim3(256), 0, s, buf, ld, C, nconv, conv_w,
-                       rec, npend);
+    const unsigned gx = (unsigned)((nconv + 255) / 256);
+    hipLaunchKernelGGL(k_pf_conv, dim3(gx, (unsigned)C), dim3(256), 0, s, buf, ld, C, nconv, conv_w, rec, npend, out,
+                       ldo);
+    Q27X_HIP(hipGetLastError());
+    // (after every row has read the record)
+    hipLaunchKernelGGL(k_pf_conv_commit, dim3(gx), dim3(256), 0, s, buf, ld, C, nconv, rec, npend);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

@@ -149,8 +149,8 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
 
 // ---------------------------------------------------------------- prefill element kernels (k_prefill.hip)
 int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t* xq, float* xs, hipStream_t s);
-int launch_pf_conv(uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
-                   hipStream_t s);
+int launch_pf_conv(const uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
+                   uint16_t* out, int ldo, hipStream_t s);
 int launch_pf_ab(const uint16_t* in_a, const uint16_t* in_b, const uint16_t* A_log, const uint16_t* dt_bias,
                  const uint16_t* y, int ystride, int K, int vh, int C, float* out, hipStream_t s);
 int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
