@@ -38,6 +38,9 @@ typedef void* q27x_stream_t; /* hipStream_t; NULL = the null stream */
 #define Q27X_E_STATE  -5   /* call out of order (no weights, no prefill, ...)   */
 #define Q27X_E_RANGE  -6   /* position / context / row count out of range        */
 #define Q27X_E_DEVICE -7   /* a kernel raised its device-side error flag         */
+#define Q27X_E_IO     -8   /* checkpoint open / stat / mmap failed               */
+#define Q27X_E_FORMAT -9   /* checkpoint header malformed or census mismatch     */
+#define Q27X_E_MISSING -10 /* a tensor the plan needs is absent                  */
 
 /* Last error message of the calling thread (never NULL). */
 const char* q27x_last_error(void);
@@ -302,10 +305,54 @@ int q27x_spec_config_from_env(q27x_config* c);
 
 int q27x_ctx_create(int device, const q27x_config* c, q27x_ctx** out);
 int q27x_ctx_destroy(q27x_ctx* ctx);
+/* ---- checkpoint catalog (q27_open / q27_close / q27_host_ptr / q27_catalog_*,
+ * include/q27_load.h:146-165; src/q27_load.cpp:428-494). Host only: nothing touches the GPU.
+ * The shards model-XXXXX-of-NNNNN.safetensors (numbered from 0 or 1) are mapped read-only; every
+ * tensor needs a known dtype, offsets inside its shard's payload, a byte count equal to its
+ * shape's and a unique name, and the census (tensor count, payload bytes) must match: any
+ * mismatch returns NULL with the reason in err (Q27X_E_IO / _FORMAT / _SHAPE). */
+#define Q27X_CKPT_SHARDS         3              /* the reference checkpoint (include/q27_load.h:52-54) */
+#define Q27X_CKPT_TENSORS        2194
+#define Q27X_CKPT_PAYLOAD_BYTES  21921428072LL
+#define Q27X_MAX_DIMS            8
+enum {                                          /* dtype codes, include/q27_load.h:60-66 */
+    Q27X_DT_UNKNOWN = 0,
+    Q27X_DT_BF16, Q27X_DT_F16, Q27X_DT_F32, Q27X_DT_F64,
+    Q27X_DT_F8_E4M3, Q27X_DT_F8_E5M2,
+    Q27X_DT_U8, Q27X_DT_I8, Q27X_DT_U16, Q27X_DT_I16,
+    Q27X_DT_U32, Q27X_DT_I32, Q27X_DT_U64, Q27X_DT_I64, Q27X_DT_BOOL
+};
+typedef struct q27x_ckpt q27x_ckpt;
+/* the reference checkpoint's census (3 shards, 2194 tensors, 21,921,428,072 payload bytes) */
+q27x_ckpt* q27x_ckpt_open(const char* dir, char* err, size_t errcap);
+/* any other census; a negative expectation is not checked */
+q27x_ckpt* q27x_ckpt_open_census(const char* dir, int nshards, long long expect_tensors,
+                                 long long expect_bytes, char* err, size_t errcap);
+void        q27x_ckpt_close(q27x_ckpt* ck);
+int         q27x_ckpt_tensor_count(const q27x_ckpt* ck);
+long long   q27x_ckpt_payload_bytes(const q27x_ckpt* ck);
+/* host pointer into the mapping for a named tensor, or NULL; shape has room for Q27X_MAX_DIMS */
+const void* q27x_ckpt_host_ptr(const q27x_ckpt* ck, const char* name, size_t* nbytes, int* dtype,
+                               int* ndim, long long* shape);
+const char* q27x_ckpt_name(const q27x_ckpt* ck, int i);
+int         q27x_ckpt_info(const q27x_ckpt* ck, int i, int* shard, int* dtype, long long* offset,
+                           size_t* nbytes, int* ndim, long long* shape);
+
 /* Seeded random-init weights (replaces q27_open + q27_upload_*, include/q27_load.h:146-243,
  * for a synthetic checkpoint): int8 per-64 projections from N(0, 0.02) draws, bf16 lm_head,
  * embeddings, norms and GDN parameters; deterministic in (seed, tensor, index). */
 int q27x_load_synthetic(q27x_ctx* ctx, uint64_t seed);
+/* The checkpoint's tensors against this geometry's plan (names, dtypes, shapes, scales), host
+ * only: Q27X_E_MISSING / Q27X_E_SHAPE with the first problem in err. */
+int q27x_ckpt_check(const q27x_ckpt* ck, const q27x_config* cfg, char* err, size_t errcap);
+/* Upload a checkpoint in the reference's naming and formats (replaces q27_upload_*,
+ * include/q27_load.h:167-243; tensor plan src/q27_load.cpp:1139-1235, MTP head
+ * src/q27_main.cpp:7134-7152): fp8 and NVFP4 matrices become int8 per 64 by the reference's
+ * mirror rule (src/q27_nvfp4.hip:4166-4311) with alpha = input_scale x weight_scale applied per
+ * output and each projection's input quantized with its input_scale; lm_head becomes bf16
+ * (e2m1 x e4m3 x weight_scale_2); the bf16 MTP head is quantized per 64 from its values (alpha 1,
+ * input_scale 1). Checks the plan first (q27x_ckpt_check); then resets the state. */
+int q27x_load_checkpoint(q27x_ctx* ctx, const q27x_ckpt* ck, char* err, size_t errcap);
 /* Bytes of weights resident on the device. */
 int q27x_weight_bytes(q27x_ctx* ctx, size_t* bytes);
 /* Reset positions, KV, recurrent state and speculation state (a new request). */

@@ -440,6 +440,89 @@ void q27o_rmsnorm_f32_rows(const void* x, int x_bf16, int xstride, const uint16_
     free(xv);
 }
 
+/* Per-(token, group) quantizer with g = 1/in_scale (the prefill's norm / mixer quantizers):
+ * sc = mx g / 127, inv = sc > 0 ? g / sc : 0. g = 1 gives q27o_quant_tok_groups' bits. */
+void q27o_quant_tok_groups_g(const float* x, int xstride, int M, int K, int gs, float g, int8_t* xq, float* xs) {
+    for (int t = 0; t < M; ++t)
+        for (int g0 = 0; g0 < K; g0 += gs) {
+            const float* v = x + (size_t)t * xstride + g0;
+            float mx = 0.0f;
+            for (int j = 0; j < gs; ++j) mx = fmaxf(mx, fabsf(v[j]));
+            const float sc = mx * g * (1.0f / 127.0f);
+            const float inv = (sc > 0.0f) ? (g / sc) : 0.0f;
+            xs[(size_t)t * (K / gs) + g0 / gs] = sc;
+            for (int j = 0; j < gs; ++j) xq[(size_t)t * K + g0 + j] = q_code(v[j], inv);
+        }
+}
+
+/* ------------------------------------------------------------------ checkpoint formats */
+/* E4M3 byte (include/q27.h:95-114): sign bit 7, exponent bits 6-3 (bias 7), mantissa bits 2-0;
+ * exponent 0 is subnormal (m 2^-9); exponent 15 with mantissa 7 decodes as infinity (the
+ * reference's choice for the code the OCP format calls NaN). */
+float q27o_e4m3(uint8_t b) {
+    const unsigned e = (b >> 3) & 15u, m = b & 7u;
+    float v;
+    if (e == 0) v = (float)m * 0x1p-9f;
+    else if (e == 15 && m == 7) v = INFINITY;
+    else { const uint32_t u = ((e + 120u) << 23) | (m << 20); memcpy(&v, &u, 4); }
+    return (b & 0x80u) ? -v : v;
+}
+/* E2M1 nibble (sign bit 3, exponent bits 2-1 with bias 1, mantissa bit 0) */
+static float e2m1(unsigned nib) {
+    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    return mag[nib & 7u] * ((nib & 8u) ? -1.0f : 1.0f);
+}
+static void i8g64_of(const float* v, int n64, int8_t* w8, float* s64) {
+    for (int g = 0; g < n64; ++g) {
+        float mx = 0.0f;
+        for (int j = 0; j < 64; ++j) mx = fmaxf(mx, fabsf(v[g * 64 + j]));
+        const float sc = mx * (1.0f / 127.0f);
+        const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        s64[g] = sc;
+        for (int j = 0; j < 64; ++j) w8[g * 64 + j] = q_code(v[g * 64 + j], inv);
+    }
+}
+/* fp8 E4M3 [rows][ld] -> int8 per 64 (q27_k_fp8_to_i8g64, src/q27_nvfp4.hip:4259-4289) */
+void q27o_fp8_to_i8g64(const uint8_t* f8, int rows, int K, int ld, int8_t* w8, float* s64) {
+    float* v = (float*)malloc((size_t)K * 4);
+    for (int r = 0; r < rows; ++r) {
+        for (int k = 0; k < K; ++k) v[k] = q27o_e4m3(f8[(size_t)r * ld + k]);
+        i8g64_of(v, K / 64, w8 + (size_t)r * K, s64 + (size_t)r * (K / 64));
+    }
+    free(v);
+}
+/* NVFP4 [rows][K/2] (element 2j in the low nibble) with E4M3 per-16 scales [rows][K/16]
+ * -> int8 per 64 (q27_k_nvfp4_to_i8g64, src/q27_nvfp4.hip:4166-4208): v = e2m1 x e4m3(scale) */
+void q27o_nvfp4_to_i8g64(const uint8_t* w, const uint8_t* gs, int rows, int K, int8_t* w8, float* s64) {
+    float* v = (float*)malloc((size_t)K * 4);
+    for (int r = 0; r < rows; ++r) {
+        for (int k = 0; k < K; ++k) {
+            const unsigned b = w[(size_t)r * (K / 2) + k / 2];
+            v[k] = e2m1((k & 1) ? (b >> 4) : (b & 15u)) * q27o_e4m3(gs[(size_t)r * (K / 16) + k / 16] & 0x7Fu);
+        }
+        i8g64_of(v, K / 64, w8 + (size_t)r * K, s64 + (size_t)r * (K / 64));
+    }
+    free(v);
+}
+/* NVFP4 -> bf16 values bf16((e2m1 x e4m3(scale)) x weight_scale_2) (the engine's bf16 lm_head) */
+void q27o_nvfp4_to_bf16(const uint8_t* w, const uint8_t* gs, float ws2, int rows, int K, uint16_t* out) {
+    for (int r = 0; r < rows; ++r)
+        for (int k = 0; k < K; ++k) {
+            const unsigned b = w[(size_t)r * (K / 2) + k / 2];
+            const float v = e2m1((k & 1) ? (b >> 4) : (b & 15u)) * q27o_e4m3(gs[(size_t)r * (K / 16) + k / 16] & 0x7Fu);
+            out[(size_t)r * K + k] = q27o_f2bf(v * ws2);
+        }
+}
+/* bf16 [rows][ld] columns 0..K-1 -> int8 per 64 (the MTP head, quantized from its values) */
+void q27o_bf16_to_i8g64(const uint16_t* x, int rows, int K, int ld, int8_t* w8, float* s64) {
+    float* v = (float*)malloc((size_t)K * 4);
+    for (int r = 0; r < rows; ++r) {
+        for (int k = 0; k < K; ++k) v[k] = q27o_bf2f(x[(size_t)r * ld + k]);
+        i8g64_of(v, K / 64, w8 + (size_t)r * K, s64 + (size_t)r * (K / 64));
+    }
+    free(v);
+}
+
 /* ------------------------------------------------------------------ R10-R12 GDN */
 /* pend layout (per layer): khat [R][KH][D] f32 | delta [R][VH][D] f32 | decay [R][VH] f32 |
  * raw [R][NQKV] bf16, R = max rows. */

@@ -88,6 +88,16 @@ void  q27o_rmsnorm_f32_rows(const void* x, int x_bf16, int xstride, const uint16
                             float eps, int n, uint16_t* hcopy, uint16_t* y, int ystride, float* yf,
                             int yfstride, int round_bf16, int nr);
 
+void  q27o_quant_tok_groups_g(const float* x, int xstride, int M, int K, int gs, float g, int8_t* xq,
+                              float* xs);
+
+/* ---- checkpoint formats (src/q27_nvfp4.hip:4166-4311; include/q27.h:95-114) ---- */
+float q27o_e4m3(uint8_t b);
+void  q27o_fp8_to_i8g64(const uint8_t* f8, int rows, int K, int ld, int8_t* w8, float* s64);
+void  q27o_nvfp4_to_i8g64(const uint8_t* w, const uint8_t* gs, int rows, int K, int8_t* w8, float* s64);
+void  q27o_nvfp4_to_bf16(const uint8_t* w, const uint8_t* gs, float ws2, int rows, int K, uint16_t* out);
+void  q27o_bf16_to_i8g64(const uint16_t* x, int rows, int K, int ld, int8_t* w8, float* s64);
+
 /* ---- R10/R11/R12 GDN verify with deferred commit ---- */
 size_t q27o_gdn_pend_bytes(int kh, int vh, int d, int max_rows);
 void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z, int z_stride,
@@ -147,6 +157,9 @@ int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t*
  * first generated token. */
 int  q27o_model_prefill_gemm(q27o_model* m, const int32_t* ids, int n, int chunk);
 void q27o_debug_plant(int code);   /* tests only: plants a prefill composition mistake */
+/* A layer's checkpoint scales (all 1 after create): v = { alpha of q|in_qkv, k|in_z, v, o|out_proj,
+ * gate, up, down; input_scale of the input norm, post norm, SwiGLU output, mixer output } */
+void q27o_model_set_scales(q27o_model* m, int layer, const float* v);
 /* one MTP pass (mtp_pass_nr, src/q27_main.cpp:2551-2618) over nr rows at draft positions dpos0..;
  * res [nr][H] bf16 out, logits [vocab] of head_row (may be NULL); returns the head row's argmax */
 int  q27o_model_mtp_pass(q27o_model* m, int nr, const uint16_t* hrows, const int32_t* toks, int dpos0,

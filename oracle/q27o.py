@@ -57,6 +57,13 @@ _SIGS = {
     "q27o_model_create": ([VP, U64], VP), "q27o_model_destroy": ([VP], None),
     "q27o_model_reset": ([VP], None), "q27o_model_prefill": ([VP, VP, I], I),
     "q27o_model_prefill_gemm": ([VP, VP, I, I], I), "q27o_debug_plant": ([I], None),
+    "q27o_model_set_scales": ([VP, I, VP], None),
+    "q27o_quant_tok_groups_g": ([VP, I, I, I, I, F, VP, VP], None),
+    "q27o_e4m3": ([ctypes.c_uint8], F),
+    "q27o_fp8_to_i8g64": ([VP, I, I, I, VP, VP], None),
+    "q27o_nvfp4_to_i8g64": ([VP, VP, I, I, VP, VP], None),
+    "q27o_nvfp4_to_bf16": ([VP, VP, F, I, I, VP], None),
+    "q27o_bf16_to_i8g64": ([VP, I, I, I, VP, VP], None),
     "q27o_rmsnorm_f32_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, I, I, I], None),
     "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
     "q27o_model_verify_rows": ([VP, I, VP, VP], I),
@@ -154,6 +161,22 @@ class Model:
             raise KeyError(name)
         n = nb.value // np.dtype(dtype).itemsize
         return np.ctypeslib.as_array((ctypes.c_byte * nb.value).from_address(p)).view(dtype)[:n].copy()
+
+    def set_tensor(self, name, layer, arr):
+        """Overwrite a named tensor (weights loaded from a checkpoint); the byte count must match."""
+        nb = ctypes.c_size_t(0)
+        p = lib().q27o_model_tensor(self.m, name.encode(), layer, ctypes.byref(nb))
+        if not p:
+            raise KeyError(name)
+        a = np.ascontiguousarray(arr)
+        if a.nbytes != nb.value:
+            raise ValueError(f"{name}: {a.nbytes} bytes for a {nb.value}-byte tensor")
+        ctypes.memmove(p, a.ctypes.data, a.nbytes)
+
+    def set_scales(self, layer, v):
+        a = np.ascontiguousarray(v, np.float32)
+        assert a.size == 11
+        lib().q27o_model_set_scales(self.m, layer, a.ctypes.data)
 
     def close(self):
         if self.m:

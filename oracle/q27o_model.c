@@ -40,6 +40,11 @@ typedef struct {
     /* state */
     int8_t *kc, *vc; float *ks, *vs;
     float* S; uint16_t* conv_hist; void* pend;
+    /* checkpoint scales (1 for generated weights): alpha per source tensor of the stacked
+     * projections (q, k, v or in_qkv, in_z), o / out_proj, gate, up, down; input_scale of the input
+     * norm, the post norm, the SwiGLU output and the mixer output */
+    float al_qkv[3], al_o, al_gate, al_up, al_down;
+    float is_in, is_post, is_down, is_out;
 } layer_t;
 
 struct q27o_model {
@@ -186,6 +191,12 @@ q27o_model* q27o_model_create(const q27o_cfg* c, uint64_t seed) {
     m->hfinal = (uint16_t*)calloc((size_t)8 * H, 2);
     m->hchain = (uint16_t*)calloc(H, 2);
     q27o_model_reset(m);
+    for (int L = -1; L < c->n_layers; ++L) {
+        layer_t* Y = (L < 0) ? &m->mtp : &m->L[L];
+        Y->al_qkv[0] = Y->al_qkv[1] = Y->al_qkv[2] = 1.0f;
+        Y->al_o = Y->al_gate = Y->al_up = Y->al_down = 1.0f;
+        Y->is_in = Y->is_post = Y->is_down = Y->is_out = 1.0f;
+    }
     return m;
 }
 
@@ -235,6 +246,23 @@ void q27o_model_reset(q27o_model* m) {
 
 double q27o_model_weight_bytes(const q27o_model* m) { return m->wbytes; }
 
+/* A stacked projection with one alpha per source tensor: rows [r[i], r[i+1]) take al[i]
+ * (bf16 out at y + r[i], row stride ld; the decode path's projection). */
+static void proj_stacked(const i8m* W, int nparts, const int* r, const float* al, const int8_t* xq,
+                         const float* xs, uint16_t* y, int ld, int nr) {
+    const int K = W->K;
+    for (int i = 0; i < nparts; ++i)
+        q27o_proj_rows_epi(W->w + (size_t)r[i] * K, W->s + (size_t)r[i] * (K / 64), al[i], r[i + 1] - r[i], K, xq, K,
+                           xs, y + r[i], ld, 1, NULL, 0, 0, 0.0f, nr);
+}
+
+void q27o_model_set_scales(q27o_model* m, int layer, const float* v) {
+    layer_t* Y = (layer >= 0 && layer < m->c.n_layers) ? &m->L[layer] : &m->mtp;
+    Y->al_qkv[0] = v[0]; Y->al_qkv[1] = v[1]; Y->al_qkv[2] = v[2]; Y->al_o = v[3];
+    Y->al_gate = v[4]; Y->al_up = v[5]; Y->al_down = v[6];
+    Y->is_in = v[7]; Y->is_post = v[8]; Y->is_down = v[9]; Y->is_out = v[10];
+}
+
 /* ------------------------------------------------------------------ one verify pass */
 /* run_layer_tp_nr (src/q27_main.cpp:2271-2489) on one card: residual share rs = 1. Rows are
  * tokens toks[0..nr-1] at positions m->pos .. m->pos+nr-1. Leaves the final residual rows in
@@ -262,20 +290,23 @@ static void verify(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
         layer_t* Y = &m->L[L];
         /* input norm: layer 0 from the bf16 embedding rows (q27_rmsnorm_quant_fp8), later layers
          * from the fp32 residual r2 (q27_rmsnorm_hostss_fp8_b) */
-        if (L == 0) q27o_rmsnorm_quant_rows(h, 1, H, Y->in_norm, 1.0f, c->rms_eps, H, NULL, y, H, xq, xs, 1, 1.0f, nr);
-        else q27o_rmsnorm_quant_rows(x, 0, H, Y->in_norm, 1.0f, c->rms_eps, H, h, y, H, xq, xs, 0, 1.0f, nr);
+        if (L == 0) q27o_rmsnorm_quant_rows(h, 1, H, Y->in_norm, 1.0f, c->rms_eps, H, NULL, y, H, xq, xs, 1, Y->is_in, nr);
+        else q27o_rmsnorm_quant_rows(x, 0, H, Y->in_norm, 1.0f, c->rms_eps, H, h, y, H, xq, xs, 0, Y->is_in, nr);
         if (Y->is_attn) {
-            q27o_proj_rows_epi(Y->qkv.w, Y->qkv.s, 1.0f, qr + 2 * kvr, H, xq, H, xs, pb, qr + 2 * kvr, 1, NULL, 0, 0, 0.0f, nr);
+            const int rr[4] = { 0, qr, qr + kvr, qr + 2 * kvr };
+            proj_stacked(&Y->qkv, 3, rr, Y->al_qkv, xq, xs, pb, qr + 2 * kvr, nr);
             q27o_attn_prep_rows(pb, qr + 2 * kvr, Y->q_norm, Y->k_norm, m->rope_cos, m->rope_sin, c->rot_dims,
                                 Y->kc, Y->ks, Y->vc, Y->vs, c->kv_group, mix, c->n_q, c->n_kv, c->head_dim,
                                 c->attn_gate, c->rms_eps, pos0, nr);
             uint16_t* ao = (uint16_t*)malloc((size_t)nr * att * 2);
             q27o_attn_rows(mix, pb, qr + 2 * kvr, Y->kc, Y->ks, Y->vc, Y->vs, c->kv_group, c->n_q, c->n_kv,
-                           c->head_dim, c->attn_gate, pos0, nr, ao, xq, xs);
+                           c->head_dim, c->attn_gate, pos0, nr, ao, NULL, NULL);
+            q27o_quant_rows(ao, att, xq, att, xs, att / 16, att, Y->is_out, nr);   /* o_proj's input_scale */
             free(ao);
-            q27o_proj_rows_epi(Y->o.w, Y->o.s, 1.0f, H, att, xq, att, xs, x, H, 0, h, 1, H, 1.0f, nr);
+            q27o_proj_rows_epi(Y->o.w, Y->o.s, Y->al_o, H, att, xq, att, xs, x, H, 0, h, 1, H, 1.0f, nr);
         } else {
-            q27o_proj_rows_epi(Y->qkvz.w, Y->qkvz.s, 1.0f, nqkv + nz, H, xq, H, xs, pb, nqkv + nz, 1, NULL, 0, 0, 0.0f, nr);
+            const int rr[3] = { 0, nqkv, nqkv + nz };
+            proj_stacked(&Y->qkvz, 2, rr, Y->al_qkv, xq, xs, pb, nqkv + nz, nr);
             /* a / b: bf16 GEMV on the bf16 normed rows, bf16 outputs (src/q27_util.hip:158-162) */
             q27o_bf16_gemv_rows(Y->in_a, c->gdn_vh, H, y, H, tmp, c->gdn_vh, nr);
             for (int i = 0; i < nr * c->gdn_vh; ++i) ab[i] = q27o_bf2f(q27o_f2bf(tmp[i]));
@@ -283,15 +314,16 @@ static void verify(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
             for (int i = 0; i < nr * c->gdn_vh; ++i) ab[nr * c->gdn_vh + i] = q27o_bf2f(q27o_f2bf(tmp[i]));
             q27o_gdn_verify(pb, nqkv + nz, pb + nqkv, nqkv + nz, ab, ab + nr * c->gdn_vh, c->gdn_vh,
                             Y->A_log, Y->dt_bias, Y->gdn_norm, Y->conv_w, Y->S, Y->conv_hist, Y->pend,
-                            m->gdn_npend, c->gdn_kh, c->gdn_vh, D, c->rms_eps, mix, nz, xq, xs, nr);
-            q27o_proj_rows_epi(Y->out_proj.w, Y->out_proj.s, 1.0f, H, nz, xq, nz, xs, x, H, 0, h, 1, H, 1.0f, nr);
+                            m->gdn_npend, c->gdn_kh, c->gdn_vh, D, c->rms_eps, mix, nz, NULL, NULL, nr);
+            q27o_quant_rows(mix, nz, xq, nz, xs, nz / 16, nz, Y->is_out, nr);       /* out_proj's input_scale */
+            q27o_proj_rows_epi(Y->out_proj.w, Y->out_proj.s, Y->al_o, H, nz, xq, nz, xs, x, H, 0, h, 1, H, 1.0f, nr);
         }
         /* post norm (q27_rmsnorm_hostss_perm_b, natural order here): h = bf16(r1) */
-        q27o_rmsnorm_quant_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, xq, xs, 0, 1.0f, nr);
-        q27o_proj_rows(Y->gate.w, Y->gate.s, 1.0f, I, H, xq, H, xs, g, I, nr);
-        q27o_proj_rows(Y->up.w, Y->up.s, 1.0f, I, H, xq, H, xs, u, I, nr);
-        q27o_swiglu_quant_rows(g, u, I, xq, xs, I, 1.0f, nr);
-        q27o_proj_rows_epi(Y->down.w, Y->down.s, 1.0f, H, I, xq, I, xs, x, H, 0, h, 1, H, 1.0f, nr);
+        q27o_rmsnorm_quant_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, xq, xs, 0, Y->is_post, nr);
+        q27o_proj_rows(Y->gate.w, Y->gate.s, Y->al_gate, I, H, xq, H, xs, g, I, nr);
+        q27o_proj_rows(Y->up.w, Y->up.s, Y->al_up, I, H, xq, H, xs, u, I, nr);
+        q27o_swiglu_quant_rows(g, u, I, xq, xs, I, Y->is_down, nr);
+        q27o_proj_rows_epi(Y->down.w, Y->down.s, Y->al_down, H, I, xq, I, xs, x, H, 0, h, 1, H, 1.0f, nr);
     }
     /* head (src/q27_main.cpp:2457-2481): hid = bf16(bf16(r1) + r2) -- the residual the reference
      * adds twice -- or bf16(r2); final norm; lm_head; argmax */
@@ -438,15 +470,15 @@ static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
  * (src/q27_epi.hip:64-75); the GEMM and its fp32 fold follow src/q27_rb.cpp:43-55 and
  * src/q27_epi.hip:189-243. rows0/nrows select a row range of W. */
 static void pf_proj(const i8m* W, int row0, int nrows, const float* v, int M, float* y, int ldy,
-                    const float* res, int ldr, float rs) {
+                    const float* res, int ldr, float rs, float alpha, float in_scale) {
     const int K = W->K, gs = pf_gs(K), ng = K / gs;
     int8_t* wg = (int8_t*)malloc((size_t)nrows * K);
     float* sg = (float*)malloc((size_t)nrows * ng * 4);
     q27o_i8g64_to_grp(W->w + (size_t)row0 * K, W->s + (size_t)row0 * (K / 64), nrows, K, gs, wg, sg);
     int8_t* xq = (int8_t*)malloc((size_t)M * K);
     float* xs = (float*)malloc((size_t)M * ng * 4);
-    q27o_quant_tok_groups(v, K, M, K, gs, xq, xs);
-    q27o_gemm_i8g(wg, sg, nrows, K, gs, 1.0f, xq, xs, M, y, ldy, res, ldr, rs);
+    q27o_quant_tok_groups_g(v, K, M, K, gs, 1.0f / in_scale, xq, xs);
+    q27o_gemm_i8g(wg, sg, nrows, K, gs, alpha, xq, xs, M, y, ldy, res, ldr, rs);
     free(wg); free(sg); free(xq); free(xs);
 }
 static void bf_to_f(const uint16_t* b, float* f, size_t n) { for (size_t i = 0; i < n; ++i) f[i] = q27o_bf2f(b[i]); }
@@ -483,7 +515,9 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
         bf_to_f(h, hf, (size_t)C * H);
         if (Y->is_attn) {
             float* o = (float*)malloc((size_t)C * wq * 4);
-            pf_proj(&Y->qkv, 0, wq, v, C, o, wq, NULL, 0, 0.0f);
+            const int rq[4] = { 0, qr, qr + kvr, wq };
+            for (int i = 0; i < 3; ++i)
+                pf_proj(&Y->qkv, rq[i], rq[i + 1] - rq[i], v, C, o + rq[i], wq, NULL, 0, 0.0f, Y->al_qkv[i], Y->is_in);
             f_to_bf(o, pb, (size_t)C * wq);
             free(o);
             for (int r0 = 0; r0 < C; r0 += 8) {
@@ -495,10 +529,11 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
                                c->n_kv, c->head_dim, c->attn_gate, p0 + r0, cn, mix + (size_t)r0 * att, NULL, NULL);
             }
             bf_to_f(mix, v, (size_t)C * att);
-            pf_proj(&Y->o, 0, H, v, C, x, H, hf, H, 1.0f);
+            pf_proj(&Y->o, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out);
         } else {
             float* o = (float*)malloc((size_t)C * wz * 4);
-            pf_proj(&Y->qkvz, 0, wz, v, C, o, wz, NULL, 0, 0.0f);
+            pf_proj(&Y->qkvz, 0, nqkv, v, C, o, wz, NULL, 0, 0.0f, Y->al_qkv[0], Y->is_in);
+            pf_proj(&Y->qkvz, nqkv, nz, v, C, o + nqkv, wz, NULL, 0, 0.0f, Y->al_qkv[1], Y->is_in);
             f_to_bf(o, pb, (size_t)C * wz);
             free(o);
             /* a / b: the decode path's bf16 GEMV on the bf16 normed rows, bf16 outputs */
@@ -521,18 +556,19 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
             q27o_gdn_verify(NULL, 0, NULL, 0, NULL, NULL, 0, Y->A_log, Y->dt_bias, Y->gdn_norm, Y->conv_w, Y->S,
                             Y->conv_hist, Y->pend, npend, c->gdn_kh, VH, D, c->rms_eps, NULL, 0, NULL, NULL, 0);
             bf_to_f(mix, v, (size_t)C * nz);
-            pf_proj(&Y->out_proj, 0, H, v, C, x, H, hf, H, 1.0f);
+            pf_proj(&Y->out_proj, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out);
         }
         q27o_rmsnorm_f32_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, v, H, 0, C);
         bf_to_f(h, hf, (size_t)C * H);
-        pf_proj(&Y->gate, 0, I, v, C, g, I, NULL, 0, 0.0f);
-        pf_proj(&Y->up, 0, I, v, C, u, I, NULL, 0, 0.0f);
-        for (size_t i = 0; i < (size_t)C * I; ++i) {   /* q27o_swiglu_quant_rows' value, in_scale 1 */
+        pf_proj(&Y->gate, 0, I, v, C, g, I, NULL, 0, 0.0f, Y->al_gate, Y->is_post);
+        pf_proj(&Y->up, 0, I, v, C, u, I, NULL, 0, 0.0f, Y->al_up, Y->is_post);
+        const float gsc = 1.0f / Y->is_down;
+        for (size_t i = 0; i < (size_t)C * I; ++i) {   /* q27o_swiglu_quant_rows' value */
             const float a = g[i];
             const float sw = a / (1.0f + q27o_exp(-a));
-            v[i] = sw * u[i] * 1.0f;
+            v[i] = sw * u[i] * gsc;
         }
-        pf_proj(&Y->down, 0, H, v, C, x, H, hf, H, g_pf_plant == 1 ? 0.0f : 1.0f);
+        pf_proj(&Y->down, 0, H, v, C, x, H, hf, H, g_pf_plant == 1 ? 0.0f : 1.0f, Y->al_down, 1.0f);
     }
     m->gdn_npend = 0;
     for (int r = 0; r < C; ++r)
@@ -568,10 +604,10 @@ static void pf_mtp(q27o_model* m, const int32_t* ids, int p0, int C, const uint1
     const int sw = c->mtp_swap ^ (g_pf_plant == 2);
     const i8m* fe = sw ? &m->fc0 : &m->fc1;   /* the half that multiplies the embedding */
     const i8m* fh = sw ? &m->fc1 : &m->fc0;
-    pf_proj(fe, 0, H, ve, C, res, H, NULL, 0, 0.0f);
-    pf_proj(fh, 0, H, vh, C, res, H, res, H, 1.0f);
+    pf_proj(fe, 0, H, ve, C, res, H, NULL, 0, 0.0f, 1.0f, 1.0f);
+    pf_proj(fh, 0, H, vh, C, res, H, res, H, 1.0f, 1.0f, 1.0f);
     q27o_rmsnorm_f32_rows(res, 0, H, Y->in_norm, po, c->rms_eps, H, NULL, NULL, H, ve, H, 0, C);
-    pf_proj(&Y->qkv, qr, 2 * kvr, ve, C, kv, 2 * kvr, NULL, 0, 0.0f);
+    pf_proj(&Y->qkv, qr, 2 * kvr, ve, C, kv, 2 * kvr, NULL, 0, 0.0f, 1.0f, 1.0f);
     for (int r = 0; r < C; ++r)
         for (int k = 0; k < 2 * kvr; ++k) pb[(size_t)r * wq + qr + k] = q27o_f2bf(kv[(size_t)r * 2 * kvr + k]);
     for (int r0 = 0; r0 < C; r0 += 8) {
@@ -746,6 +782,16 @@ void* q27o_model_tensor(q27o_model* m, const char* name, int layer, size_t* byte
     else if (!strcmp(name, "pre_hid")) { p = m->pre_hid; b = (size_t)H * 2; }
     else if (!strcmp(name, "mtp_norm")) { p = m->mtp_norm; b = (size_t)H * 2; }
     else if (!strcmp(name, "final_norm")) { p = m->final_norm; b = (size_t)H * 2; }
+    else if (!strcmp(name, "gate_s")) { p = Y->gate.s; b = (size_t)c->inter * (H / 64) * 4; }
+    else if (!strcmp(name, "qkvz_w") && !Y->is_attn && Y->qkvz.w) { p = Y->qkvz.w; b = (size_t)Y->qkvz.rows * H; }
+    else if (!strcmp(name, "qkvz_s") && !Y->is_attn && Y->qkvz.s) { p = Y->qkvz.s; b = (size_t)Y->qkvz.rows * (H / 64) * 4; }
+    else if (!strcmp(name, "out_w") && !Y->is_attn && Y->out_proj.w) { p = Y->out_proj.w; b = (size_t)H * Y->out_proj.K; }
+    else if (!strcmp(name, "out_s") && !Y->is_attn && Y->out_proj.s) { p = Y->out_proj.s; b = (size_t)H * (Y->out_proj.K / 64) * 4; }
+    else if (!strcmp(name, "in_a") && !Y->is_attn && Y->in_a) { p = Y->in_a; b = (size_t)c->gdn_vh * H * 2; }
+    else if (!strcmp(name, "in_b") && !Y->is_attn && Y->in_b) { p = Y->in_b; b = (size_t)c->gdn_vh * H * 2; }
+    else if (!strcmp(name, "A_log") && !Y->is_attn && Y->A_log) { p = Y->A_log; b = (size_t)c->gdn_vh * 2; }
+    else if (!strcmp(name, "dt_bias") && !Y->is_attn && Y->dt_bias) { p = Y->dt_bias; b = (size_t)c->gdn_vh * 2; }
+    else if (!strcmp(name, "gdn_norm") && !Y->is_attn && Y->gdn_norm) { p = Y->gdn_norm; b = (size_t)D * 2; }
     if (bytes) *bytes = b;
     return p;
 }

@@ -1,0 +1,425 @@
+// ckpt.hip -- the checkpoint catalog (safetensors shards, mmap, fail-closed census) and the
+// load-time converters of its weight formats into the engine's representations.
+//
+// Catalog (reference interface: q27_open / q27_close / q27_host_ptr / q27_catalog_*,
+// include/q27_load.h:146-165, src/q27_load.cpp:428-494): the shards model-XXXXX-of-NNNNN.safetensors
+// (numbered from 0 or from 1) are mapped read-only; each starts with an 8-byte little-endian header
+// length and a JSON header {name: {dtype, shape, data_offsets}, "__metadata__": {...}} followed by
+// the payload. Every tensor must have a known dtype, offsets inside its shard's payload, a byte
+// count equal to its shape's, and a unique name; the census (tensor count and payload bytes over
+// all shards) must equal the expected numbers. Any mismatch closes the catalog with an error.
+// Nothing here touches the GPU.
+//
+// Converters (the reference's load-time mirrors, src/q27_nvfp4.hip:4166-4311): fp8 E4M3 [R][K]
+// and NVFP4 (E2M1 nibbles [R][K/2] + E4M3 per-16 scales [R][K/16]) to int8 codes with one fp32
+// scale per 64 weights (sc = max|v| / 127, inv = sc > 0 ? 1/sc : 0, code = clamp(rint(v inv),
+// +-127)); bf16 to the same per-64 form (the MTP weights); NVFP4 to bf16 values
+// e2m1 x e4m3 x weight_scale_2 (the bf16 lm_head). One wave per 64-weight group, lane = element.
+#include <errno.h>
+#include <fcntl.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "q27x_dev.h"
+#include "q27x_int.h"
+
+struct q27x_ckpt {
+    struct Shard { int fd = -1; unsigned char* map = nullptr; size_t len = 0; size_t payload = 0; };
+    struct T { std::string name; int dtype = 0, ndim = 0, shard = 0; long long shape[Q27X_MAX_DIMS] = {}; long long off = 0; size_t nbytes = 0; };
+    std::vector<Shard> sh;
+    std::vector<T> t;
+    std::unordered_map<std::string, int> idx;
+    long long payload_total = 0;
+};
+
+namespace q27x {
+namespace {
+
+int ck_fail(char* err, size_t cap, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (err && cap) { strncpy(err, buf, cap - 1); err[cap - 1] = 0; }
+    set_error("%s", buf);
+    return code;
+}
+
+struct DtInfo { const char* name; int code; int size; };
+const DtInfo kDt[] = {
+    {"BF16", Q27X_DT_BF16, 2}, {"F16", Q27X_DT_F16, 2}, {"F32", Q27X_DT_F32, 4}, {"F64", Q27X_DT_F64, 8},
+    {"F8_E4M3", Q27X_DT_F8_E4M3, 1}, {"F8_E5M2", Q27X_DT_F8_E5M2, 1}, {"U8", Q27X_DT_U8, 1}, {"I8", Q27X_DT_I8, 1},
+    {"U16", Q27X_DT_U16, 2}, {"I16", Q27X_DT_I16, 2}, {"U32", Q27X_DT_U32, 4}, {"I32", Q27X_DT_I32, 4},
+    {"U64", Q27X_DT_U64, 8}, {"I64", Q27X_DT_I64, 8}, {"BOOL", Q27X_DT_BOOL, 1},
+};
+
+// A JSON reader for the header's subset: objects, arrays, strings, integers, and skipping of any
+// other value (numbers, true/false/null, nested values of __metadata__).
+struct Json {
+    const char* p; const char* e;
+    void ws() { while (p < e && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p; }
+    bool eat(char c) { ws(); if (p < e && *p == c) { ++p; return true; } return false; }
+    bool str(std::string& out) {
+        ws();
+        if (p >= e || *p != '"') return false;
+        ++p;
+        out.clear();
+        while (p < e && *p != '"') {
+            if (*p == '\\') {
+                if (++p >= e) return false;
+                switch (*p) {
+                    case '"': case '\\': case '/': out += *p; break;
+                    case 'b': out += '\b'; break;
+                    case 'f': out += '\f'; break;
+                    case 'n': out += '\n'; break;
+                    case 'r': out += '\r'; break;
+                    case 't': out += '\t'; break;
+                    case 'u': {
+                        if (e - p < 5) return false;
+                        unsigned v = 0;
+                        for (int i = 1; i <= 4; ++i) {
+                            const char c = p[i];
+                            const int d = (c >= '0' && c <= '9') ? c - '0' : (c >= 'a' && c <= 'f') ? c - 'a' + 10
+                                        : (c >= 'A' && c <= 'F') ? c - 'A' + 10 : -1;
+                            if (d < 0) return false;
+                            v = v * 16 + (unsigned)d;
+                        }
+                        if (v < 0x80) out += (char)v;
+                        else if (v < 0x800) { out += (char)(0xC0 | (v >> 6)); out += (char)(0x80 | (v & 63)); }
+                        else { out += (char)(0xE0 | (v >> 12)); out += (char)(0x80 | ((v >> 6) & 63)); out += (char)(0x80 | (v & 63)); }
+                        p += 4;
+                        break;
+                    }
+                    default: return false;
+                }
+                ++p;
+            } else {
+                out += *p++;
+            }
+        }
+        if (p >= e) return false;
+        ++p;
+        return true;
+    }
+    bool integer(long long& v) {
+        ws();
+        if (p >= e || *p < '0' || *p > '9') return false;
+        v = 0;
+        while (p < e && *p >= '0' && *p <= '9') {
+            if (v > (0x7fffffffffffffffLL - 9) / 10) return false;
+            v = v * 10 + (*p++ - '0');
+        }
+        return true;
+    }
+    bool skip(int depth = 0) {
+        ws();
+        if (p >= e || depth > 64) return false;
+        if (*p == '"') { std::string s; return str(s); }
+        if (*p == '{' || *p == '[') {
+            const char close = (*p == '{') ? '}' : ']';
+            const bool obj = (*p == '{');
+            ++p;
+            if (eat(close)) return true;
+            for (;;) {
+                if (obj) { std::string k; if (!str(k) || !eat(':')) return false; }
+                if (!skip(depth + 1)) return false;
+                if (eat(',')) continue;
+                return eat(close);
+            }
+        }
+        const char* s0 = p;
+        while (p < e && *p != ',' && *p != '}' && *p != ']' && *p != ' ' && *p != '\n' && *p != '\r' && *p != '\t') ++p;
+        return p > s0;
+    }
+};
+
+int parse_header(q27x_ckpt* M, int shard, const char* h, size_t hl, char* err, size_t cap) {
+    Json j{h, h + hl};
+    const long long payload = (long long)(M->sh[shard].len - M->sh[shard].payload);   // payload bytes
+    if (!j.eat('{')) return ck_fail(err, cap, Q27X_E_FORMAT, "shard %d: header is not a JSON object", shard);
+    if (j.eat('}')) return Q27X_OK;
+    for (;;) {
+        std::string name;
+        if (!j.str(name) || !j.eat(':')) return ck_fail(err, cap, Q27X_E_FORMAT, "shard %d: bad tensor name", shard);
+        if (name == "__metadata__") {
+            if (!j.skip()) return ck_fail(err, cap, Q27X_E_FORMAT, "shard %d: bad __metadata__", shard);
+        } else {
+            q27x_ckpt::T T;
+            T.name = name;
+            T.shard = shard;
+            std::string dts;
+            long long a = -1, b = -1;
+            bool have_dt = false, have_shape = false, have_off = false;
+            if (!j.eat('{')) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': entry is not an object", name.c_str());
+            if (!j.eat('}')) {
+                for (;;) {
+                    std::string field;
+                    if (!j.str(field) || !j.eat(':')) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad field", name.c_str());
+                    if (field == "dtype") {
+                        if (!j.str(dts)) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad dtype", name.c_str());
+                        have_dt = true;
+                    } else if (field == "shape") {
+                        if (!j.eat('[')) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad shape", name.c_str());
+                        if (!j.eat(']')) {
+                            for (;;) {
+                                long long v;
+                                if (T.ndim >= Q27X_MAX_DIMS || !j.integer(v))
+                                    return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad shape", name.c_str());
+                                T.shape[T.ndim++] = v;
+                                if (j.eat(',')) continue;
+                                if (!j.eat(']')) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad shape", name.c_str());
+                                break;
+                            }
+                        }
+                        have_shape = true;
+                    } else if (field == "data_offsets") {
+                        if (!j.eat('[') || !j.integer(a) || !j.eat(',') || !j.integer(b) || !j.eat(']'))
+                            return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad data_offsets", name.c_str());
+                        have_off = true;
+                    } else if (!j.skip()) {
+                        return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': bad value of '%s'", name.c_str(), field.c_str());
+                    }
+                    if (j.eat(',')) continue;
+                    if (!j.eat('}')) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': unterminated entry", name.c_str());
+                    break;
+                }
+            }
+            if (!have_dt || !have_shape || !have_off)
+                return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': dtype, shape and data_offsets are required", name.c_str());
+            int esz = 0;
+            for (const DtInfo& d : kDt)
+                if (dts == d.name) { T.dtype = d.code; esz = d.size; }
+            if (!esz) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': unknown dtype '%s'", name.c_str(), dts.c_str());
+            if (a < 0 || b < a || b > payload)
+                return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': data_offsets [%lld, %lld) outside the %lld-byte payload",
+                               name.c_str(), a, b, payload);
+            long long n = 1;
+            for (int i = 0; i < T.ndim; ++i) {
+                if (T.shape[i] < 0 || (T.shape[i] && n > (1LL << 50) / T.shape[i]))
+                    return ck_fail(err, cap, Q27X_E_SHAPE, "'%s': bad shape", name.c_str());
+                n *= T.shape[i];
+            }
+            if (n * esz != b - a)
+                return ck_fail(err, cap, Q27X_E_SHAPE, "'%s': %s shape needs %lld B, the offsets give %lld B", name.c_str(),
+                               dts.c_str(), n * esz, b - a);
+            T.off = a;
+            T.nbytes = (size_t)(b - a);
+            if (M->idx.count(name)) return ck_fail(err, cap, Q27X_E_FORMAT, "'%s': duplicate tensor name", name.c_str());
+            M->idx[name] = (int)M->t.size();
+            M->t.push_back(T);
+        }
+        if (j.eat(',')) continue;
+        if (!j.eat('}')) return ck_fail(err, cap, Q27X_E_FORMAT, "shard %d: unterminated header", shard);
+        j.ws();
+        if (j.p != j.e) return ck_fail(err, cap, Q27X_E_FORMAT, "shard %d: bytes after the header object", shard);
+        return Q27X_OK;
+    }
+}
+
+// ---------------------------------------------------------------- converters
+// E4M3 (sign bit 7, exponent bits 6-3 with bias 7, mantissa bits 2-0): exponent 0 is subnormal
+// (m x 2^-9); the all-ones code (exponent 15, mantissa 7) decodes as infinity, as the reference's
+// decoders do (include/q27.h:98-114). The group scales carry no sign bit.
+__device__ __forceinline__ float e4m3_mag(uint32_t b) {
+    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    if (e == 0) return (float)m * 0x1p-9f;
+    if (e == 15 && m == 7) return __builtin_huge_valf();
+    return __uint_as_float(((e + 120u) << 23) | (m << 20));
+}
+__device__ __forceinline__ float e2m1_val(uint32_t nib) {
+    const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    return mag[nib & 7u] * ((nib & 8u) ? -1.0f : 1.0f);
+}
+__device__ __forceinline__ int dst_row(int r, int row_mode) {
+    // 0: r; 1 / 2: gate / up row r into the 32-row units of the fused gate|up matrix
+    if (row_mode == 0) return r;
+    return (r >> 4) * 32 + (row_mode == 2 ? 16 : 0) + (r & 15);
+}
+
+// kind: 0 fp8 E4M3 [R][K]; 1 NVFP4 ([R][K/2] nibbles, low nibble first, + [R][K/16] E4M3 scales);
+// 2 bf16 [R][K]. Block = 4 waves = 4 groups of 64; lane = element.
+__global__ __launch_bounds__(256) void k_to_i8g64(int kind, const uint8_t* __restrict__ src,
+                                                  const uint8_t* __restrict__ gsc, int rows, int K, int src_ld,
+                                                  int8_t* __restrict__ w8, float* __restrict__ s64, int row_mode) {
+    const int ng = K >> 6;
+    const long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= (long long)rows * ng) return;
+    const int lane = threadIdx.x & 63;
+    const int r = (int)(g / ng), gr = (int)(g - (long long)r * ng);
+    const int e = gr * 64 + lane;
+    float v;
+    if (kind == 0) {
+        const uint32_t b = src[(size_t)r * src_ld + e];
+        v = e4m3_mag(b) * ((b & 0x80u) ? -1.0f : 1.0f);
+    } else if (kind == 1) {
+        const uint32_t b = src[(size_t)r * src_ld + (e >> 1)];
+        const uint32_t nib = (e & 1) ? (b >> 4) : (b & 15u);
+        v = e2m1_val(nib) * e4m3_mag(gsc[(size_t)r * (K >> 4) + (e >> 4)]);
+    } else {
+        v = bf2f(((const uint16_t*)src)[(size_t)r * src_ld + e]);
+    }
+    const float mx = max_xor(fabsf(v), 64);
+    const float sc = mx * (1.0f / 127.0f);
+    const float inv = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+    const int dr = dst_row(r, row_mode);
+    w8[(size_t)dr * K + e] = qcode(v, inv);
+    if (lane == 0) s64[(size_t)dr * ng + gr] = sc;
+}
+__global__ __launch_bounds__(256) void k_nvfp4_to_bf16(const uint8_t* __restrict__ src, const uint8_t* __restrict__ gsc,
+                                                       float ws2, int rows, int K, uint16_t* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)rows * K) return;
+    const int r = (int)(i / K), e = (int)(i - (long long)r * K);
+    const uint32_t b = src[(size_t)r * (K >> 1) + (e >> 1)];
+    const uint32_t nib = (e & 1) ? (b >> 4) : (b & 15u);
+    out[i] = f2bf((e2m1_val(nib) * e4m3_mag(gsc[(size_t)r * (K >> 4) + (e >> 4)])) * ws2);
+}
+
+}  // namespace
+
+int launch_to_i8g64(int kind, const void* src, const void* gsc, int rows, int K, int src_ld, int8_t* w8, float* s64,
+                    int row_mode, hipStream_t s) {
+    if (!src || !w8 || !s64 || rows < 1 || K < 64 || (K & 63) || (kind == 1 && !gsc) || kind < 0 || kind > 2 ||
+        row_mode < 0 || row_mode > 2) {
+        set_error("checkpoint convert: bad arguments");
+        return Q27X_E_ARG;
+    }
+    const long long groups = (long long)rows * (K >> 6);
+    hipLaunchKernelGGL(k_to_i8g64, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, s, kind, (const uint8_t*)src,
+                       (const uint8_t*)gsc, rows, K, src_ld, w8, s64, row_mode);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+int launch_nvfp4_to_bf16(const void* src, const void* gsc, float ws2, int rows, int K, uint16_t* out, hipStream_t s) {
+    if (!src || !gsc || !out || rows < 1 || K < 16 || (K & 15)) {
+        set_error("checkpoint convert: bad arguments");
+        return Q27X_E_ARG;
+    }
+    const long long n = (long long)rows * K;
+    hipLaunchKernelGGL(k_nvfp4_to_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)src,
+                       (const uint8_t*)gsc, ws2, rows, K, out);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+int ckpt_get(const q27x_ckpt* M, const char* name, CkTensor* out) {
+    if (!M || !name) return Q27X_E_ARG;
+    auto it = M->idx.find(name);
+    if (it == M->idx.end()) return Q27X_E_MISSING;
+    const q27x_ckpt::T& T = M->t[(size_t)it->second];
+    if (out) {
+        out->dtype = T.dtype; out->ndim = T.ndim;
+        for (int i = 0; i < Q27X_MAX_DIMS; ++i) out->shape[i] = T.shape[i];
+        out->host = M->sh[(size_t)T.shard].map + M->sh[(size_t)T.shard].payload + T.off;
+        out->nbytes = T.nbytes;
+    }
+    return Q27X_OK;
+}
+
+}  // namespace q27x
+
+using namespace q27x;
+
+extern "C" void q27x_ckpt_close(q27x_ckpt* m) {
+    if (!m) return;
+    for (auto& s : m->sh) {
+        if (s.map) munmap(s.map, s.len);
+        if (s.fd >= 0) close(s.fd);
+    }
+    delete m;
+}
+
+extern "C" q27x_ckpt* q27x_ckpt_open_census(const char* dir, int nshards, long long expect_tensors,
+                                            long long expect_bytes, char* err, size_t errcap) {
+    if (!dir || nshards < 1 || nshards > 99999) {
+        ck_fail(err, errcap, Q27X_E_ARG, "q27x_ckpt_open: bad arguments");
+        return nullptr;
+    }
+    q27x_ckpt* M = new q27x_ckpt();
+    char path[4096];
+    // shard numbering starts at 0 (a merged requant) or 1 (the Hugging Face convention)
+    int base = 0;
+    snprintf(path, sizeof path, "%s/model-%05d-of-%05d.safetensors", dir, 0, nshards);
+    if (access(path, R_OK) != 0) {
+        snprintf(path, sizeof path, "%s/model-%05d-of-%05d.safetensors", dir, 1, nshards);
+        if (access(path, R_OK) == 0) base = 1;
+    }
+    M->sh.resize((size_t)nshards);
+    for (int s = 0; s < nshards; ++s) {
+        snprintf(path, sizeof path, "%s/model-%05d-of-%05d.safetensors", dir, s + base, nshards);
+        q27x_ckpt::Shard& S = M->sh[(size_t)s];
+        S.fd = open(path, O_RDONLY);
+        if (S.fd < 0) { ck_fail(err, errcap, Q27X_E_IO, "open('%s'): %s", path, strerror(errno)); q27x_ckpt_close(M); return nullptr; }
+        struct stat st;
+        if (fstat(S.fd, &st) != 0) { ck_fail(err, errcap, Q27X_E_IO, "fstat('%s'): %s", path, strerror(errno)); q27x_ckpt_close(M); return nullptr; }
+        S.len = (size_t)st.st_size;
+        if (S.len < 8) { ck_fail(err, errcap, Q27X_E_FORMAT, "'%s': %zu bytes, no header", path, S.len); q27x_ckpt_close(M); return nullptr; }
+        void* mp = mmap(nullptr, S.len, PROT_READ, MAP_PRIVATE, S.fd, 0);
+        if (mp == MAP_FAILED) { S.len = 0; ck_fail(err, errcap, Q27X_E_IO, "mmap('%s'): %s", path, strerror(errno)); q27x_ckpt_close(M); return nullptr; }
+        S.map = (unsigned char*)mp;
+        unsigned long long hl = 0;
+        for (int k = 7; k >= 0; --k) hl = (hl << 8) | S.map[k];   // little endian, host order irrelevant
+        if (hl == 0 || hl > S.len - 8) {
+            ck_fail(err, errcap, Q27X_E_FORMAT, "'%s': header length %llu does not fit in %zu bytes", path, hl, S.len);
+            q27x_ckpt_close(M); return nullptr;
+        }
+        S.payload = (size_t)(8 + hl);
+        M->payload_total += (long long)(S.len - S.payload);
+        const int rc = parse_header(M, s, (const char*)S.map + 8, (size_t)hl, err, errcap);
+        if (rc) { q27x_ckpt_close(M); return nullptr; }
+    }
+    if (expect_tensors >= 0 && (long long)M->t.size() != expect_tensors) {
+        ck_fail(err, errcap, Q27X_E_FORMAT, "census: %zu tensors, expected %lld", M->t.size(), expect_tensors);
+        q27x_ckpt_close(M); return nullptr;
+    }
+    if (expect_bytes >= 0 && M->payload_total != expect_bytes) {
+        ck_fail(err, errcap, Q27X_E_FORMAT, "census: %lld payload bytes, expected %lld", M->payload_total, expect_bytes);
+        q27x_ckpt_close(M); return nullptr;
+    }
+    return M;
+}
+
+extern "C" q27x_ckpt* q27x_ckpt_open(const char* dir, char* err, size_t errcap) {
+    return q27x_ckpt_open_census(dir, Q27X_CKPT_SHARDS, Q27X_CKPT_TENSORS, Q27X_CKPT_PAYLOAD_BYTES, err, errcap);
+}
+
+extern "C" int q27x_ckpt_tensor_count(const q27x_ckpt* m) { return m ? (int)m->t.size() : -1; }
+extern "C" long long q27x_ckpt_payload_bytes(const q27x_ckpt* m) { return m ? m->payload_total : -1; }
+
+extern "C" const void* q27x_ckpt_host_ptr(const q27x_ckpt* m, const char* name, size_t* nbytes, int* dtype, int* ndim,
+                                          long long* shape) {
+    CkTensor T;
+    if (ckpt_get(m, name, &T)) return nullptr;
+    if (nbytes) *nbytes = T.nbytes;
+    if (dtype) *dtype = T.dtype;
+    if (ndim) *ndim = T.ndim;
+    if (shape) for (int i = 0; i < Q27X_MAX_DIMS; ++i) shape[i] = T.shape[i];
+    return T.host;
+}
+
+extern "C" const char* q27x_ckpt_name(const q27x_ckpt* m, int i) {
+    if (!m || i < 0 || i >= (int)m->t.size()) return nullptr;
+    return m->t[(size_t)i].name.c_str();
+}
+
+extern "C" int q27x_ckpt_info(const q27x_ckpt* m, int i, int* shard, int* dtype, long long* offset, size_t* nbytes,
+                              int* ndim, long long* shape) {
+    if (!m || i < 0 || i >= (int)m->t.size()) return Q27X_E_ARG;
+    const q27x_ckpt::T& T = m->t[(size_t)i];
+    if (shard) *shard = T.shard;
+    if (dtype) *dtype = T.dtype;
+    if (offset) *offset = T.off;
+    if (nbytes) *nbytes = T.nbytes;
+    if (ndim) *ndim = T.ndim;
+    if (shape) for (int k = 0; k < Q27X_MAX_DIMS; ++k) shape[k] = T.shape[k];
+    return Q27X_OK;
+}

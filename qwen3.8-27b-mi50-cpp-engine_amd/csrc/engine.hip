@@ -9,6 +9,7 @@
 //   * rollback is the GDN kernel's deferred commit (no snapshot banks); KV needs none (R13);
 //   * only the round's (ncommit, tokens) reach the host, through a pinned mailbox.
 #include <math.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -37,6 +38,9 @@ static uint64_t tid(int code, int kind) { return ((uint64_t)code << 8) | (uint64
 
 struct Mat {
     int8_t* w = nullptr; float* s = nullptr; int rows = 0, K = 0;
+    // per-output scale of the stacked source tensors (alpha = input_scale x weight_scale; 1 for
+    // weights made from their values, as the synthetic ones)
+    float alpha = 1.0f; AlphaSel asel{};
     // the prefill GEMM's representation of the same matrix (per-(row, group) codes and scales),
     // made on the first GEMM prefill after a load
     int8_t* pw = nullptr; float* ps = nullptr;
@@ -53,6 +57,10 @@ struct LayerDev {
     int8_t *kc = nullptr, *vc = nullptr; float *ks = nullptr, *vs = nullptr;
     float* S = nullptr; void* pend = nullptr;
     uint16_t* conv_st = nullptr;   // per q|k|v channel: committed conv history + pending raw inputs (16 bf16)
+    // input_scale of the quantized activations each projection consumes (the input norm's for
+    // in_qkv / q_proj, the post norm's for gate|up, the SwiGLU output's for down, the mixer
+    // output's for out_proj / o_proj)
+    float in_s_in = 1.0f, in_s_post = 1.0f, in_s_down = 1.0f, in_s_out = 1.0f;
 };
 
 // device control block (the Dev NR fields of src/q27_main.cpp:360-379 plus the round's tokens)
@@ -365,12 +373,13 @@ static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
         } else {
             nin = norm_of(x, x->xres, 0, Y.in_norm, 1.0f, 0, x->hid, nullptr);
         }
+        nin.in_scale = Y.in_s_in;
         ProjArgs o{};
-        o.alpha = 1.0f; o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
+        o.y = x->xres; o.ystride = H; o.out_bf16 = 0;
         o.res = x->hid; o.res_bf16 = 1; o.rstride = H; o.rs = 1.0f; o.stop = &d->stop;
         if (Y.is_attn) {
             ProjArgs p{};
-            p.alpha = 1.0f; p.stop = &d->stop;
+            p.alpha = Y.qkv.alpha; p.asel = Y.qkv.asel; p.stop = &d->stop;
             p.W = Y.qkv.w; p.WS = Y.qkv.s; p.rows = Y.qkv.rows; p.K = H;
             p.y = x->pb; p.ystride = Y.qkv.rows; p.out_bf16 = 1;
             set_pre(p, nin);
@@ -381,16 +390,17 @@ static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
             a.kc = Y.kc; a.ks = Y.ks; a.vc = Y.vc; a.vs = Y.vs; a.kv_group = c.kv_group; a.qh = x->qh;
             a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
             a.pos0_ptr = &d->pos; a.work = x->attn_work; a.max_splits = x->max_splits; a.sl2e = x->sl2e;
-            a.out = x->ao; a.xq = xa; a.xs = sa; a.stop = &d->stop;
+            a.out = x->ao; a.xq = xa; a.xs = sa; a.stop = &d->stop; a.in_scale = Y.in_s_out;
             if ((rc = launch_attn(a, nr, s, true))) return rc;
             o.W = Y.o.w; o.WS = Y.o.s; o.rows = H; o.K = x->att; o.xq = xa; o.xst = x->att; o.xs = sa;
+            o.alpha = Y.o.alpha; o.asel = Y.o.asel;
         } else {
             // in_qkv | in_z (raw bf16 rows; the conv runs inside the GDN kernel)
             const int rows = Y.qkvz.rows;
             // the q|k|v channels are convolved in the projection's epilogue (with the deferred
             // commit of their history), the z rows stored raw
             ProjArgs p{};
-            p.alpha = 1.0f; p.stop = &d->stop;
+            p.alpha = Y.qkvz.alpha; p.asel = Y.qkvz.asel; p.stop = &d->stop;
             p.W = Y.qkvz.w; p.WS = Y.qkvz.s; p.rows = rows; p.K = H;
             p.y = x->pb; p.ystride = rows; p.out_bf16 = 1;
             p.conv_w = Y.conv_w; p.conv_st = Y.conv_st; p.nconv = x->nqkv; p.npend_ptr = &d->gdn_npend;
@@ -404,21 +414,24 @@ static int layer_pass(q27x_ctx* x, int l, int nr, int mlp) {
             g.rowsc = x->gab; g.norm_w = Y.gdn_norm;
             g.S = Y.S; g.pend = Y.pend; g.npend_ptr = &d->gdn_npend;
             g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
-            g.out = x->gout; g.out_stride = x->nz; g.xq = xa; g.xs = sa; g.stop = &d->stop;
+            g.out = x->gout; g.out_stride = x->nz; g.xq = xa; g.xs = sa; g.stop = &d->stop; g.in_scale = Y.in_s_out;
             if ((rc = launch_gdn(g, nr, s))) return rc;
             o.W = Y.out_proj.w; o.WS = Y.out_proj.s; o.rows = H; o.K = x->nz; o.xq = xa; o.xst = x->nz; o.xs = sa;
+            o.alpha = Y.out_proj.alpha; o.asel = Y.out_proj.asel;
         }
         if ((rc = launch_proj(o, EPI_STORE, nr, s))) return rc;
         if (!mlp) return Q27X_OK;
         // post norm of r1 (fp32, quantize the fp32 normed rows, h = bf16(r1)): gate|up prologue
         ProjArgs gu{};
-        gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = 1.0f;
-        gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f; gu.stop = &d->stop;
+        gu.W = Y.gu.w; gu.WS = Y.gu.s; gu.rows = 2 * I; gu.K = H; gu.alpha = Y.gu.alpha; gu.asel = Y.gu.asel;
+        gu.act_q = xact; gu.act_s = sact; gu.act_stride = I; gu.gscale = 1.0f / Y.in_s_down; gu.stop = &d->stop;
         gu.sw_part = x->sw_part; gu.sw_cnt = x->sw_cnt;
-        set_pre(gu, norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr));
+        NormArgs npost = norm_of(x, x->xres, 0, Y.post_norm, 1.0f, 0, x->hid, nullptr);
+        npost.in_scale = Y.in_s_post;
+        set_pre(gu, npost);
         if ((rc = launch_proj(gu, EPI_SWIGLU, nr, s))) return rc;
         ProjArgs dn{};
-        dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = 1.0f;
+        dn.W = Y.down.w; dn.WS = Y.down.s; dn.rows = H; dn.K = I; dn.alpha = Y.down.alpha; dn.asel = Y.down.asel;
         dn.xq = xact; dn.xst = I; dn.xs = sact;
         dn.y = x->xres; dn.ystride = H; dn.out_bf16 = 0;
         dn.res = x->hid; dn.res_bf16 = 1; dn.rstride = H; dn.rs = 1.0f; dn.stop = &d->stop;
@@ -828,6 +841,14 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     const int H = x->H, I = x->I;
     hipStream_t s = x->stream;
     x->woff = 0; x->weight_bytes = 0;
+    // (a checkpoint loaded before may have left per-tensor scales: generated weights have none)
+    for (LayerDev& Y : x->L) {
+        Y.qkvz = Y.out_proj = Y.qkv = Y.o = Y.gu = Y.down = Mat{};
+        Y.in_s_in = Y.in_s_post = Y.in_s_down = Y.in_s_out = 1.0f;
+    }
+    x->mtp.qkv = x->mtp.o = x->mtp.gu = Mat{};
+    for (Mat& m : x->mtp.down4) m = Mat{};
+    x->fc0 = x->fc1 = Mat{};
     int rc;
 #define GEN(m, rows, K) if ((rc = gen_i8m(x, m, rows, K))) return rc
 #define VEC(dst, t, n, sd, mn, uni) if (!((dst) = gen_vec(x, seed, t, n, sd, mn, uni))) { set_error("weight generation"); return Q27X_E_NOMEM; }
@@ -900,6 +921,280 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     Q27X_HIP(hipStreamSynchronize(s));
     x->loaded = 1;
     x->pf_wready = 0;   // the GEMM representations are remade from these weights
+    return q27x_reset(x);
+}
+
+// ---------------------------------------------------------------- checkpoint plan and upload
+// The tensors of a checkpoint in the reference's naming and formats (tp_plan / the group
+// loaders, src/q27_load.cpp:690-815; the MTP head, src/q27_main.cpp:7134-7152) for this context's
+// geometry. Trunk: MLP NVFP4 (weight U8 [R][K/2], weight_scale E4M3 [R][K/16], weight_scale_2,
+// input_scale F32 scalars), attention and GDN projections fp8 E4M3 [R][K] with weight_scale and
+// input_scale, norms / a / b / conv1d / A_log / dt_bias bf16; lm_head NVFP4; the MTP head bf16.
+// Every matrix becomes the engine's int8 per-64 form (the reference's load-time mirror rule) with
+// alpha = input_scale x weight_scale per source tensor; each projection's input is quantized with
+// its input_scale; lm_head becomes bf16 (e2m1 x e4m3 x weight_scale_2), the MTP weights are
+// quantized from their bf16 values (alpha 1, input_scale 1). Fail closed: a missing tensor is
+// Q27X_E_MISSING, a wrong dtype or shape, a non-positive scale or gate/up (q/k/v) input scales
+// that differ are Q27X_E_SHAPE.
+namespace {
+struct CkPlan {
+    q27x_ctx* x;                  // null: check only
+    const q27x_ckpt* ck;
+    const q27x_config& c;
+    char* err; size_t cap;
+    int rc = Q27X_OK;
+    void* stage = nullptr; size_t stage_cap = 0;
+    int fail(int code, const char* fmt, ...) {
+        if (rc) return rc;
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        if (err && cap) { strncpy(err, buf, cap - 1); err[cap - 1] = 0; }
+        set_error("%s", buf);
+        rc = code;
+        return rc;
+    }
+    // the tensor, checked for dtype and element count (shape product; dims as given)
+    bool get(const char* name, int dtype, long long n0, long long n1, CkTensor& T) {
+        if (rc) return false;
+        if (ckpt_get(ck, name, &T)) { fail(Q27X_E_MISSING, "checkpoint: '%s' missing", name); return false; }
+        long long n = 1;
+        for (int i = 0; i < T.ndim; ++i) n *= T.shape[i];
+        const bool shape_ok = (n1 < 0) ? (n == n0) : (T.ndim == 2 && T.shape[0] == n0 && T.shape[1] == n1);
+        if (T.dtype != dtype || !shape_ok) {
+            fail(Q27X_E_SHAPE, "checkpoint: '%s' has dtype %d and %d dims (%lld x %lld), expected dtype %d, %lld x %lld",
+                 name, T.dtype, T.ndim, T.ndim > 0 ? T.shape[0] : 0, T.ndim > 1 ? T.shape[1] : 0, dtype, n0, n1);
+            return false;
+        }
+        return true;
+    }
+    float scalar(const char* name) {
+        CkTensor T;
+        if (!get(name, Q27X_DT_F32, 1, -1, T)) return 0.0f;
+        float v;
+        memcpy(&v, T.host, 4);
+        if (!(v > 0.0f) || !(v < 1e30f)) { fail(Q27X_E_SHAPE, "checkpoint: '%s' = %g is not a positive scale", name, (double)v); return 0.0f; }
+        return v;
+    }
+    void* staged(const CkTensor& T) {      // a device copy of the tensor's bytes (upload mode)
+        if (!staged_resize(T.nbytes)) return nullptr;
+        const hipError_t e = hipMemcpy(stage, T.host, T.nbytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { rc = hip_fail(e, "hipMemcpy (checkpoint)"); return nullptr; }
+        return stage;
+    }
+    // bf16 vector / matrix of n elements into the weight arena
+    void vec(const char* name, long long n, uint16_t** dst) {
+        CkTensor T;
+        if (!get(name, Q27X_DT_BF16, n, -1, T) || !x) return;
+        *dst = (uint16_t*)walloc(x, (size_t)n * 2);
+        if (!*dst) { fail(Q27X_E_NOMEM, "weight arena sizing"); return; }
+        x->weight_bytes += (size_t)n * 2;
+        const hipError_t e = hipMemcpy(*dst, T.host, (size_t)n * 2, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = hip_fail(e, "hipMemcpy (checkpoint)");
+    }
+    bool mat_alloc(Mat& m, int rows, int K) {
+        if (!x || rc) return false;
+        if (!m.w) {
+            m.rows = rows; m.K = K;
+            m.w = (int8_t*)walloc(x, (size_t)rows * K);
+            m.s = (float*)walloc(x, (size_t)rows * (K / 64) * 4);
+            if (!m.s) { fail(Q27X_E_NOMEM, "weight arena sizing"); return false; }
+            x->weight_bytes += (size_t)rows * K + (size_t)rows * (K / 64) * 4;
+        }
+        return true;
+    }
+    // fp8 projection base.{weight, weight_scale, input_scale} [rows][K] -> rows row0.. of m;
+    // returns alpha = input_scale x weight_scale
+    float fp8(const char* base, int rows, int K, Mat& m, int mrows, int row0, float* in_scale) {
+        char n[256];
+        CkTensor T;
+        snprintf(n, sizeof n, "%s.weight", base);
+        const bool ok = get(n, Q27X_DT_F8_E4M3, rows, K, T);
+        snprintf(n, sizeof n, "%s.weight_scale", base);
+        const float ws = scalar(n);
+        snprintf(n, sizeof n, "%s.input_scale", base);
+        const float is = scalar(n);
+        if (in_scale) *in_scale = is;
+        if (ok && mat_alloc(m, mrows, K)) {
+            const void* d = staged(T);
+            if (d && !rc)
+                rc = launch_to_i8g64(0, d, nullptr, rows, K, K, m.w + (size_t)row0 * K, m.s + (size_t)row0 * (K / 64), 0,
+                                     x->stream);
+            if (!rc) { const hipError_t e = hipStreamSynchronize(x->stream); if (e != hipSuccess) rc = hip_fail(e, "convert"); }
+        }
+        return is * ws;
+    }
+    // NVFP4 matrix base.{weight, weight_scale, weight_scale_2, input_scale} -> m (row_mode: 0 rows
+    // 0.., 1 / 2 gate / up rows of the fused gate|up layout); returns alpha
+    float nvfp4(const char* base, int rows, int K, Mat& m, int mrows, int row_mode, float* in_scale) {
+        char n[256];
+        CkTensor T, G;
+        snprintf(n, sizeof n, "%s.weight", base);
+        const bool ok = get(n, Q27X_DT_U8, rows, K / 2, T);
+        snprintf(n, sizeof n, "%s.weight_scale", base);
+        const bool okg = get(n, Q27X_DT_F8_E4M3, rows, K / 16, G);
+        snprintf(n, sizeof n, "%s.weight_scale_2", base);
+        const float ws2 = scalar(n);
+        snprintf(n, sizeof n, "%s.input_scale", base);
+        const float is = scalar(n);
+        if (in_scale) *in_scale = is;
+        if (ok && okg && mat_alloc(m, mrows, K)) {
+            // (weights and group scales staged together)
+            if (!staged_resize(T.nbytes + G.nbytes)) return 0.0f;
+            hipError_t e = hipMemcpy(stage, T.host, T.nbytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy((char*)stage + T.nbytes, G.host, G.nbytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) { rc = hip_fail(e, "hipMemcpy (checkpoint)"); return 0.0f; }
+            rc = launch_to_i8g64(1, stage, (char*)stage + T.nbytes, rows, K, K / 2, m.w, m.s, row_mode, x->stream);
+            if (!rc) { e = hipStreamSynchronize(x->stream); if (e != hipSuccess) rc = hip_fail(e, "convert"); }
+        }
+        return is * ws2;
+    }
+    bool staged_resize(size_t bytes) {
+        if (bytes <= stage_cap) return true;
+        if (stage) (void)hipFree(stage);
+        stage = nullptr; stage_cap = 0;
+        const hipError_t e = hipMalloc(&stage, bytes);
+        if (e != hipSuccess) { rc = hip_fail(e, "hipMalloc (checkpoint staging)"); return false; }
+        stage_cap = bytes;
+        return true;
+    }
+    // bf16 matrix [rows][ld] columns col0 .. col0+K -> rows row0.. of m, quantized per 64
+    void bf16m(const char* name, int rows, int ld, int col0, int K, Mat& m, int mrows, int row0, int row_mode) {
+        CkTensor T;
+        if (!get(name, Q27X_DT_BF16, rows, ld, T) || !mat_alloc(m, mrows, K)) return;
+        const void* d = staged(T);
+        if (!d || rc) return;
+        rc = launch_to_i8g64(2, (const uint16_t*)d + col0, nullptr, rows, K, ld,
+                             row_mode ? m.w : m.w + (size_t)row0 * K, row_mode ? m.s : m.s + (size_t)row0 * (K / 64),
+                             row_mode, x->stream);
+        if (!rc) { const hipError_t e = hipStreamSynchronize(x->stream); if (e != hipSuccess) rc = hip_fail(e, "convert"); }
+    }
+};
+
+int ckpt_plan(CkPlan& P) {
+    q27x_ctx* x = P.x;
+    const q27x_config& c = P.c;
+    const int H = c.hidden, I = c.inter, hd = c.head_dim, D = c.gdn_d;
+    const int qr = c.n_q * (c.attn_gate ? 2 * hd : hd), kvr = c.n_kv * hd, att = c.n_q * hd;
+    const int nqkv = (2 * c.gdn_kh + c.gdn_vh) * D, nz = c.gdn_vh * D;
+    static Mat scratch_m;                       // (check mode: no allocation)
+    LayerDev dummy;
+    char n[256], b[256];
+    for (int l = 0; l < c.n_layers && !P.rc; ++l) {
+        LayerDev& Y = x ? x->L[l] : dummy;
+        const bool is_attn = is_attn_layer(c, l);
+        snprintf(b, sizeof b, "model.language_model.layers.%d", l);
+        snprintf(n, sizeof n, "%s.input_layernorm.weight", b); P.vec(n, H, &Y.in_norm);
+        snprintf(n, sizeof n, "%s.post_attention_layernorm.weight", b); P.vec(n, H, &Y.post_norm);
+        float gi = 0, ui = 0, di = 0;
+        snprintf(n, sizeof n, "%s.mlp.gate_proj", b); const float ag = P.nvfp4(n, I, H, x ? Y.gu : scratch_m, 2 * I, 1, &gi);
+        snprintf(n, sizeof n, "%s.mlp.up_proj", b); const float au = P.nvfp4(n, I, H, x ? Y.gu : scratch_m, 2 * I, 2, &ui);
+        snprintf(n, sizeof n, "%s.mlp.down_proj", b); const float ad = P.nvfp4(n, H, I, x ? Y.down : scratch_m, H, 0, &di);
+        if (!P.rc && gi != ui) return P.fail(Q27X_E_SHAPE, "layer %d: mlp gate input_scale %g != up input_scale %g", l, (double)gi, (double)ui);
+        Y.gu.alpha = ag; Y.gu.asel = AlphaSel{}; Y.gu.asel.alpha_gu = 1; Y.gu.asel.alpha_b = au;
+        Y.down.alpha = ad; Y.in_s_post = gi; Y.in_s_down = di;
+        if (is_attn) {
+            float qi = 0, ki = 0, vi = 0, oi = 0;
+            snprintf(n, sizeof n, "%s.self_attn.q_proj", b); const float aq = P.fp8(n, qr, H, x ? Y.qkv : scratch_m, qr + 2 * kvr, 0, &qi);
+            snprintf(n, sizeof n, "%s.self_attn.k_proj", b); const float ak = P.fp8(n, kvr, H, x ? Y.qkv : scratch_m, qr + 2 * kvr, qr, &ki);
+            snprintf(n, sizeof n, "%s.self_attn.v_proj", b); const float av = P.fp8(n, kvr, H, x ? Y.qkv : scratch_m, qr + 2 * kvr, qr + kvr, &vi);
+            snprintf(n, sizeof n, "%s.self_attn.o_proj", b); const float ao = P.fp8(n, H, att, x ? Y.o : scratch_m, H, 0, &oi);
+            if (!P.rc && !(qi == ki && ki == vi))
+                return P.fail(Q27X_E_SHAPE, "layer %d: q/k/v input_scale differ (%g / %g / %g)", l, (double)qi, (double)ki, (double)vi);
+            Y.qkv.alpha = aq; Y.qkv.asel = AlphaSel{}; Y.qkv.asel.split_b = qr; Y.qkv.asel.alpha_b = ak;
+            Y.qkv.asel.split_c = qr + kvr; Y.qkv.asel.alpha_c = av;
+            Y.o.alpha = ao; Y.in_s_in = qi; Y.in_s_out = oi;
+            snprintf(n, sizeof n, "%s.self_attn.q_norm.weight", b); P.vec(n, hd, &Y.q_norm);
+            snprintf(n, sizeof n, "%s.self_attn.k_norm.weight", b); P.vec(n, hd, &Y.k_norm);
+        } else {
+            float qi = 0, zi = 0, oi = 0;
+            snprintf(n, sizeof n, "%s.linear_attn.in_proj_qkv", b); const float aq = P.fp8(n, nqkv, H, x ? Y.qkvz : scratch_m, nqkv + nz, 0, &qi);
+            snprintf(n, sizeof n, "%s.linear_attn.in_proj_z", b); const float az = P.fp8(n, nz, H, x ? Y.qkvz : scratch_m, nqkv + nz, nqkv, &zi);
+            snprintf(n, sizeof n, "%s.linear_attn.out_proj", b); const float ao = P.fp8(n, H, nz, x ? Y.out_proj : scratch_m, H, 0, &oi);
+            Y.qkvz.alpha = aq; Y.qkvz.asel = AlphaSel{}; Y.qkvz.asel.split_b = nqkv; Y.qkvz.asel.alpha_b = az;
+            Y.out_proj.alpha = ao; Y.in_s_in = qi; Y.in_s_out = oi;
+            snprintf(n, sizeof n, "%s.linear_attn.in_proj_a.weight", b); P.vec(n, (long long)c.gdn_vh * H, &Y.in_a);
+            snprintf(n, sizeof n, "%s.linear_attn.in_proj_b.weight", b); P.vec(n, (long long)c.gdn_vh * H, &Y.in_b);
+            snprintf(n, sizeof n, "%s.linear_attn.conv1d.weight", b); P.vec(n, (long long)nqkv * 4, &Y.conv_w);
+            snprintf(n, sizeof n, "%s.linear_attn.A_log", b); P.vec(n, c.gdn_vh, &Y.A_log);
+            snprintf(n, sizeof n, "%s.linear_attn.dt_bias", b); P.vec(n, c.gdn_vh, &Y.dt_bias);
+            snprintf(n, sizeof n, "%s.linear_attn.norm.weight", b); P.vec(n, D, &Y.gdn_norm);
+        }
+    }
+    if (P.rc) return P.rc;
+    // globals
+    uint16_t* dummy16 = nullptr;
+    P.vec("model.language_model.embed_tokens.weight", (long long)c.vocab * H, x ? &x->emb : &dummy16);
+    P.vec("model.language_model.norm.weight", H, x ? &x->final_norm : &dummy16);
+    {
+        CkTensor T, G;
+        const bool ok = P.get("lm_head.weight", Q27X_DT_U8, c.vocab, H / 2, T);
+        const bool okg = P.get("lm_head.weight_scale", Q27X_DT_F8_E4M3, c.vocab, H / 16, G);
+        const float ws2 = P.scalar("lm_head.weight_scale_2");
+        if (ok && okg && x && !P.rc) {
+            x->lm_head = (uint16_t*)walloc(x, (size_t)c.vocab * H * 2);
+            if (!x->lm_head) return P.fail(Q27X_E_NOMEM, "weight arena sizing");
+            x->weight_bytes += (size_t)c.vocab * H * 2;
+            if (!P.staged_resize(T.nbytes + G.nbytes)) return P.rc;
+            hipError_t e = hipMemcpy(P.stage, T.host, T.nbytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy((char*)P.stage + T.nbytes, G.host, G.nbytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) return P.rc = hip_fail(e, "hipMemcpy (checkpoint)");
+            if ((P.rc = launch_nvfp4_to_bf16(P.stage, (char*)P.stage + T.nbytes, ws2, c.vocab, H, x->lm_head, x->stream)))
+                return P.rc;
+            if ((e = hipStreamSynchronize(x->stream)) != hipSuccess) return P.rc = hip_fail(e, "convert");
+        }
+    }
+    if (P.rc) return P.rc;
+    // the MTP head (bf16; quantized per 64 from its values)
+    LayerDev& M = x ? x->mtp : dummy;
+    const char* B = "mtp.layers.0";
+    snprintf(n, sizeof n, "%s.self_attn.q_proj.weight", B); P.bf16m(n, qr, H, 0, H, x ? M.qkv : scratch_m, qr + 2 * kvr, 0, 0);
+    snprintf(n, sizeof n, "%s.self_attn.k_proj.weight", B); P.bf16m(n, kvr, H, 0, H, x ? M.qkv : scratch_m, qr + 2 * kvr, qr, 0);
+    snprintf(n, sizeof n, "%s.self_attn.v_proj.weight", B); P.bf16m(n, kvr, H, 0, H, x ? M.qkv : scratch_m, qr + 2 * kvr, qr + kvr, 0);
+    snprintf(n, sizeof n, "%s.self_attn.o_proj.weight", B); P.bf16m(n, H, att, 0, att, x ? M.o : scratch_m, H, 0, 0);
+    snprintf(n, sizeof n, "%s.mlp.gate_proj.weight", B); P.bf16m(n, I, H, 0, H, x ? M.gu : scratch_m, 2 * I, 0, 1);
+    snprintf(n, sizeof n, "%s.mlp.up_proj.weight", B); P.bf16m(n, I, H, 0, H, x ? M.gu : scratch_m, 2 * I, 0, 2);
+    snprintf(n, sizeof n, "%s.mlp.down_proj.weight", B);
+    for (int j = 0; j < 4; ++j) P.bf16m(n, H, I, j * (I / 4), I / 4, x ? M.down4[j] : scratch_m, H, 0, 0);
+    P.bf16m("mtp.fc.weight", H, 2 * H, 0, H, x ? x->fc0 : scratch_m, H, 0, 0);
+    P.bf16m("mtp.fc.weight", H, 2 * H, H, H, x ? x->fc1 : scratch_m, H, 0, 0);
+    snprintf(n, sizeof n, "%s.input_layernorm.weight", B); P.vec(n, H, &M.in_norm);
+    snprintf(n, sizeof n, "%s.post_attention_layernorm.weight", B); P.vec(n, H, &M.post_norm);
+    snprintf(n, sizeof n, "%s.self_attn.q_norm.weight", B); P.vec(n, hd, &M.q_norm);
+    snprintf(n, sizeof n, "%s.self_attn.k_norm.weight", B); P.vec(n, hd, &M.k_norm);
+    P.vec("mtp.norm.weight", H, x ? &x->mtp_norm : &dummy16);
+    P.vec("mtp.pre_fc_norm_embedding.weight", H, x ? &x->pre_emb : &dummy16);
+    P.vec("mtp.pre_fc_norm_hidden.weight", H, x ? &x->pre_hid : &dummy16);
+    return P.rc;
+}
+}  // namespace
+
+int q27x_ckpt_check(const q27x_ckpt* ck, const q27x_config* cfg, char* err, size_t errcap) {
+    if (!ck || !cfg) { set_error("q27x_ckpt_check: null argument"); return Q27X_E_ARG; }
+    CkPlan P{nullptr, ck, *cfg, err, errcap};
+    return ckpt_plan(P);
+}
+
+int q27x_load_checkpoint(q27x_ctx* x, const q27x_ckpt* ck, char* err, size_t errcap) {
+    if (!x || !ck) { set_error("q27x_load_checkpoint: null argument"); return Q27X_E_ARG; }
+    int rc = q27x_ckpt_check(ck, &x->c, err, errcap);
+    if (rc) return rc;
+    x->loaded = 0;
+    x->woff = 0; x->weight_bytes = 0;
+    for (LayerDev& Y : x->L) { Y.qkvz = Y.out_proj = Y.qkv = Y.o = Y.gu = Y.down = Mat{}; }
+    x->mtp.qkv = x->mtp.o = x->mtp.gu = Mat{};
+    for (Mat& m : x->mtp.down4) m = Mat{};
+    x->fc0 = x->fc1 = Mat{};
+    Q27X_HIP(hipSetDevice(x->device));
+    CkPlan P{x, ck, x->c, err, errcap};
+    rc = ckpt_plan(P);
+    if (P.stage) (void)hipFree(P.stage);
+    if (rc) return rc;
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    x->loaded = 1;
+    x->pf_wready = 0;
     return q27x_reset(x);
 }
 
@@ -1046,8 +1341,17 @@ static int pf_gemm(q27x_ctx* x, const Mat& W, int r0, int nrows, const int8_t* x
                    int ldy, int out_bf16, const void* res, int res_bf16 = 1) {
     const int K = W.K, gs = pf_gs(K);
     if (!W.pw) { set_error("prefill: no GEMM representation of a %d x %d matrix", W.rows, K); return Q27X_E_STATE; }
-    return launch_gemm_i8g(W.pw + (size_t)r0 * K, W.ps + (size_t)r0 * (K / gs), nrows, K, gs, 1.0f, xq, xs, M, y, ldy,
-                           out_bf16, res, x->H, res_bf16, res ? 1.0f : 0.0f, x->stream);
+    // the stacked tensors' scales, for rows counted from r0
+    AlphaSel as = W.asel;
+    float a0 = W.alpha;
+    if (r0 > 0 && !as.alpha_gu) {
+        a0 = alpha_of(W.alpha, W.asel, r0);
+        as.split_b = as.split_b > r0 ? as.split_b - r0 : 0;
+        as.split_c = as.split_c > r0 ? as.split_c - r0 : 0;
+        if (as.split_b == 0 && as.split_c > 0) { as.split_b = as.split_c; as.alpha_b = as.alpha_c; as.split_c = 0; }
+    }
+    return launch_gemm_i8g(W.pw + (size_t)r0 * K, W.ps + (size_t)r0 * (K / gs), nrows, K, gs, a0, xq, xs, M, y, ldy,
+                           out_bf16, res, x->H, res_bf16, res ? 1.0f : 0.0f, x->stream, &as);
 }
 // every matrix of the model in the GEMM representation (the reference keeps such per-(row, group)
 // mirrors from load time, src/q27_epi.hip:14-35); made once per load, kept on the device
@@ -1075,12 +1379,12 @@ static int pf_weights(q27x_ctx* x) {
     return Q27X_OK;
 }
 // norm of C rows (values to B.yf) and their per-(token, group) codes
-static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs) {
+static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs, float in_scale = 1.0f) {
     PfBuf& B = *x->pf;
     n.yf = B.yf; n.yfstride = x->H;
     int rc = launch_norm(n, C, x->stream);
     if (rc) return rc;
-    return q27x_quant_tok_groups(B.yf, x->H, C, x->H, pf_gs(x->H), xq, xs, (q27x_stream_t)x->stream);
+    return launch_quant_tok_grp(B.yf, x->H, C, x->H, pf_gs(x->H), in_scale, xq, xs, x->stream);
 }
 
 static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
@@ -1098,7 +1402,7 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
     } else {
         nin = norm_of(x, B.x, 0, Y.in_norm, 1.0f, 0, B.h, Y.is_attn ? nullptr : B.y);
     }
-    if ((rc = pf_norm_quant(x, nin, C, B.xq, B.xs))) return rc;
+    if ((rc = pf_norm_quant(x, nin, C, B.xq, B.xs, Y.in_s_in))) return rc;
     if (Y.is_attn) {
         const int wq = Y.qkv.rows;
         if ((rc = pf_gemm(x, Y.qkv, 0, wq, B.xq, B.xs, C, B.pb, wq, 1, nullptr))) return rc;
@@ -1117,7 +1421,7 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
             t.zrows = 8; t.ztotal = cq; t.out = B.mix + (size_t)q0 * x->att;
             if ((rc = launch_attn(t, 8, s, false))) return rc;
         }
-        if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(x->att), B.xq, B.xs, s))) return rc;
+        if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(x->att), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.o, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     } else {
         const int wz = Y.qkvz.rows;
@@ -1130,12 +1434,13 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
         g.out = B.mix; g.out_stride = x->nz; g.stop = &d->stop;
         if ((rc = launch_gdn_scan(g, C, s))) return rc;
-        if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), B.xq, B.xs, s))) return rc;
+        if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.out_proj, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     }
-    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, Y.post_norm, 1.0f, 0, B.h, nullptr), C, B.xq, B.xs))) return rc;
+    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, Y.post_norm, 1.0f, 0, B.h, nullptr), C, B.xq, B.xs, Y.in_s_post)))
+        return rc;
     if ((rc = pf_gemm(x, Y.gu, 0, 2 * I, B.xq, B.xs, C, B.gu, 2 * I, 0, nullptr))) return rc;
-    if ((rc = launch_pf_swiglu_quant(B.gu, I, pf_gs(I), 1.0f, C, B.xq, B.xs, s))) return rc;
+    if ((rc = launch_pf_swiglu_quant(B.gu, I, pf_gs(I), 1.0f / Y.in_s_down, C, B.xq, B.xs, s))) return rc;
     return pf_gemm(x, Y.down, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h);
 }
 

@@ -408,11 +408,12 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     const uint16_t vb = f2bf(v);
     const size_t k = (size_t)r * a.nq * kHD + (size_t)hq * kHD + t;
     a.out[k] = vb;
-    if (a.xq) {
+    if (a.xq) {   // the per-16 quantizer with g = 1/in_scale (s = mx g / 127, 1/s -> g / s)
+        const float g = (a.in_scale > 0.0f) ? 1.0f / a.in_scale : 1.0f;
         const float yv = bf2f(vb);
         const float m16 = max_xor(fabsf(yv), 16);
-        const float sc = m16 * (1.0f / 127.0f);
-        const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        const float sc = m16 * g * (1.0f / 127.0f);
+        const float qi = (sc > 0.0f) ? (g / sc) : 0.0f;
         a.xq[k] = qcode(yv, qi);
         if ((t & 15) == 0) a.xs[k >> 4] = sc;
     }

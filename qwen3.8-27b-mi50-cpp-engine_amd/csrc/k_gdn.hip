@@ -241,11 +241,12 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
         const uint16_t yb = f2bf(y);
         const size_t k = (size_t)n * a.out_stride + (size_t)h * kD + e;
         a.out[k] = yb;
-        if (a.xq) {
+        if (a.xq) {   // the per-16 quantizer with g = 1/in_scale (s = mx g / 127, 1/s -> g / s)
+            const float g = (a.in_scale > 0.0f) ? 1.0f / a.in_scale : 1.0f;
             const float yv = bf2f(yb);
             const float m16 = max_xor(fabsf(yv), 16);
-            const float sc = m16 * (1.0f / 127.0f);
-            const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+            const float sc = m16 * g * (1.0f / 127.0f);
+            const float qi = (sc > 0.0f) ? (g / sc) : 0.0f;
             a.xq[k] = qcode(yv, qi);
             if ((e & 15) == 0) a.xs[k >> 4] = sc;
         }

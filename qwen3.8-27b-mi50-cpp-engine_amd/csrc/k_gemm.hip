@@ -53,6 +53,7 @@ struct GemmArgs {
     float alpha, rs;
     int M, N, K, gs, ng, ldy, ldr;
     int out_bf16, res_bf16;
+    AlphaSel asel;
 };
 
 template <int BM, int NS>
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
             for (int r = 0; r < 16; ++r) {
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (t < a.M) {
-                    float o = facc[i][j][r] * a.alpha;
+                    float o = facc[i][j][r] * alpha_of(a.alpha, a.asel, n);
                     if (a.res) o = o + a.rs * (a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)t * a.ldr + n])
                                                           : a.res[(size_t)t * a.ldr + n]);
                     if (a.out_bf16) ((uint16_t*)a.y)[(size_t)t * a.ldy + n] = f2bf(o);
@@ -348,7 +349,7 @@ _Pragma("unroll")                                                               
             for (int r = 0; r < 16; ++r) {
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (t < a.M) {
-                    float o = facc[i][j][r] * a.alpha;
+                    float o = facc[i][j][r] * alpha_of(a.alpha, a.asel, n);
                     if (a.res) o = o + a.rs * (a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)t * a.ldr + n])
                                                           : a.res[(size_t)t * a.ldr + n]);
                     if (a.out_bf16) ((uint16_t*)a.y)[(size_t)t * a.ldy + n] = f2bf(o);
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(256) void k_i8g64_to_grp(const int8_t* w, const flo
 // Activations: fp32 rows -> per-(token, group) codes and scales; one 256-thread block per
 // (group, token), four values per thread per 1024 columns.
 __global__ __launch_bounds__(256) void k_quant_tok_grp(const float* x, int xstride, int K, int gs, int8_t* xq,
-                                                       float* xs) {
+                                                       float* xs, float gq) {
     const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = K / gs;
     __shared__ float red[4];
     const float* row = x + (size_t)tok * xstride + (size_t)g * gs;
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(256) void k_quant_tok_grp(const float* x, int xstri
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
     const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+    const float sc = m * gq * (1.0f / 127.0f), qi = (sc > 0.0f) ? gq / sc : 0.0f;   // gq = 1/in_scale
     if (t == 0) xs[(size_t)tok * ng + g] = sc;
     int8_t* out = xq + (size_t)tok * K + (size_t)g * gs;
     for (int k = 4 * t; k < gs; k += 1024) {
@@ -434,7 +435,7 @@ extern "C" int q27x_quant_tok_groups(const float* x, int xstride, int M, int K, 
         return Q27X_E_ARG;
     }
     hipLaunchKernelGGL(k_quant_tok_grp, dim3((unsigned)(K / gs), (unsigned)M), dim3(256), 0, (hipStream_t)s, x,
-                       xstride, K, gs, xq, xs);
+                       xstride, K, gs, xq, xs, 1.0f);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
@@ -458,7 +459,7 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
 namespace q27x {
 int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
                     const float* sx, int M, void* y, int ldy, int out_bf16, const void* res, int ldr, int res_bf16,
-                    float rs, hipStream_t s) {
+                    float rs, hipStream_t s, const AlphaSel* asel) {
     if ((N % 128) || (K % kGK) || (gs % kGK) || (K % gs) || K / gs > kGMaxG || ((uintptr_t)w & 15) ||
         ((uintptr_t)x & 15) || M < 1 || ldy < N || (res && ldr < N)) {
         set_error("gemm: no kernel for M %d, N %d, K %d, gs %d", M, N, K, gs);
@@ -468,6 +469,7 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
     a.w = w; a.sw = sw; a.x = x; a.sx = sx; a.y = (float*)y; a.res = (const float*)res; a.alpha = alpha; a.rs = rs;
     a.M = M; a.N = N; a.K = K; a.gs = gs; a.ng = K / gs; a.ldy = ldy; a.ldr = ldr;
     a.out_bf16 = out_bf16; a.res_bf16 = res_bf16;
+    if (asel) a.asel = *asel;
     // Weight tiles of 128 rows (256-row tiles need 433 registers per lane, one block per CU, and
     // measured 1-8% slower). Token tiles of 256 (8 waves, one block per CU, a 5-stage ring) from
     // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
@@ -491,4 +493,18 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
+// the per-(token, group) quantizer with g = 1/in_scale (s = mx g / 127, qi = g / s)
+int launch_quant_tok_grp(const float* x, int xstride, int M, int K, int gs, float in_scale, int8_t* xq, float* xs,
+                         hipStream_t s) {
+    if (!x || !xq || !xs || M < 1 || K < 4 || gs < 4 || (gs & 3) || (K % gs) || xstride < K || (xstride & 3) ||
+        ((uintptr_t)x & 15) || !(in_scale > 0.0f)) {
+        set_error("quant tok groups: bad arguments (M %d, K %d, gs %d)", M, K, gs);
+        return Q27X_E_ARG;
+    }
+    hipLaunchKernelGGL(k_quant_tok_grp, dim3((unsigned)(K / gs), (unsigned)M), dim3(256), 0, s, x, xstride, K, gs, xq,
+                       xs, 1.0f / in_scale);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
 }  // namespace q27x

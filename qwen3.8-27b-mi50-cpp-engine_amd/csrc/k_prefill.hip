@@ -8,10 +8,11 @@
 namespace q27x {
 
 // bf16 rows [M][ld] -> per-(token, group) codes [M][K] and scales [M][K / gs] (the quantizer of
-// k_quant_tok_grp on the rows' float values: sc = max|v| / 127, qi = sc > 0 ? 1/sc : 0).
+// k_quant_tok_grp on the rows' float values with gq = 1/in_scale: sc = max|v| gq / 127,
+// qi = sc > 0 ? gq / sc : 0).
 // One 256-thread block per (group, token), four values per thread per 1024 columns.
 __global__ __launch_bounds__(256) void k_pf_quant_bf16(const uint16_t* __restrict__ x, int ld, int K, int gs,
-                                                       int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                       int8_t* __restrict__ xq, float* __restrict__ xs, float gq) {
     const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = K / gs;
     __shared__ float red[4];
     const uint16_t* row = x + (size_t)tok * ld + (size_t)g * gs;
@@ -25,7 +26,7 @@ __global__ __launch_bounds__(256) void k_pf_quant_bf16(const uint16_t* __restric
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
     const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+    const float sc = m * gq * (1.0f / 127.0f), qi = (sc > 0.0f) ? gq / sc : 0.0f;
     if (t == 0) xs[(size_t)tok * ng + g] = sc;
     int8_t* out = xq + (size_t)tok * K + (size_t)g * gs;
     for (int k = 4 * t; k < gs; k += 1024) {
@@ -37,12 +38,15 @@ __global__ __launch_bounds__(256) void k_pf_quant_bf16(const uint16_t* __restric
         *(uint32_t*)(out + k) = pk;
     }
 }
-int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t* xq, float* xs, hipStream_t s) {
-    if (!x || !xq || !xs || M < 1 || K < 4 || gs < 4 || (gs & 3) || (K % gs) || ld < K || (ld & 3) || ((uintptr_t)x & 7)) {
+int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, float in_scale, int8_t* xq, float* xs,
+                         hipStream_t s) {
+    if (!x || !xq || !xs || M < 1 || K < 4 || gs < 4 || (gs & 3) || (K % gs) || ld < K || (ld & 3) || ((uintptr_t)x & 7) ||
+        !(in_scale > 0.0f)) {
         set_error("prefill quant: bad arguments (M %d, K %d, gs %d, ld %d)", M, K, gs, ld);
         return Q27X_E_ARG;
     }
-    hipLaunchKernelGGL(k_pf_quant_bf16, dim3((unsigned)(K / gs), (unsigned)M), dim3(256), 0, s, x, ld, K, gs, xq, xs);
+    hipLaunchKernelGGL(k_pf_quant_bf16, dim3((unsigned)(K / gs), (unsigned)M), dim3(256), 0, s, x, ld, K, gs, xq, xs,
+                       1.0f / in_scale);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

@@ -444,7 +444,12 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
         }
     };
+    // the per-output scale of the group's row (one weight row per group), selected from the
+    // group's first row, which the loop carries from one group to the next
+    int rg_cur = __builtin_amdgcn_readfirstlane(row_of(wave, 0));
     for (int j = wave; j < nrb;) {
+        float al = a.alpha;
+        if constexpr (RPW == 1) al = alpha_of(a.alpha, a.asel, rg_cur);
         unsigned jn = 0u;
         if (lane == 0) jn = __hip_atomic_fetch_add(&s_next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const int jnext = NW + __builtin_amdgcn_readfirstlane((int)jn);
@@ -492,9 +497,10 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
 #pragma unroll
             for (int r = 0; r < RPW; ++r) ld(rg_next, r, t, more);
         }
-        const float tv = tree_t<P>(acc, lane) * a.alpha;
+        const float tv = tree_t<P>(acc, lane) * al;
         emit(j, tv, rw, ridx, cvd);
         j = jnext;
+        rg_cur = rg_next;
     }
     if constexpr (EPI == EPI_SWIGLU) {
         // the whole units' codes and scales, quantized in the loop, written out together

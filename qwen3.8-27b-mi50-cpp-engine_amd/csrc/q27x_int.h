@@ -37,8 +37,22 @@ struct NormArgs {
 };
 // ---------------------------------------------------------------- projection
 enum ProjEpi { EPI_STORE = 0, EPI_SWIGLU = 2, EPI_CONV = 3 };
+// Per-output scale of a stacked matrix (the reference's alpha = input_scale x weight_scale, applied
+// once per output, one per source tensor): rows [0, split_b) take alpha, [split_b, split_c) alpha_b,
+// [split_c, rows) alpha_c (a split <= 0 is absent); alpha_gu: the SwiGLU layout of 32-row units,
+// gate rows (row & 16 == 0) alpha, up rows alpha_b.
+struct AlphaSel {
+    float alpha_b, alpha_c; int split_b, split_c, alpha_gu;
+};
+__host__ __device__ inline float alpha_of(float alpha, const AlphaSel& s, int row) {
+    if (s.alpha_gu) return (row & 16) ? s.alpha_b : alpha;
+    float a = alpha;
+    if (s.split_b > 0 && row >= s.split_b) a = s.alpha_b;
+    if (s.split_c > 0 && row >= s.split_c) a = s.alpha_c;
+    return a;
+}
 struct ProjArgs {
-    const int8_t* W; const float* WS; int rows; int K; float alpha;
+    const int8_t* W; const float* WS; int rows; int K; float alpha; AlphaSel asel;
     const int8_t* xq; int xst; const float* xs;
     // EPI_STORE: y = v (+ rs*res); res_round rounds v through bf16 before the add
     void* y; int ystride; int out_bf16;
@@ -102,6 +116,7 @@ struct GdnArgs {
     int kh, vh, d; float eps;
     uint16_t* out; int out_stride; int8_t* xq; float* xs;
     const int* stop;
+    float in_scale;                                // the quantized output's input_scale (0 = 1)
 };
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s);
 // prefill: nrows rows (any count) with the row scalars prepared in rowsc [2][nrows][vh], the state
@@ -133,6 +148,7 @@ struct AttnArgs {
     // z zrows .. at positions pos0 + z zrows .., its own work region; 0 = no tiles
     int zrows, ztotal;
     int prep_kv_only;                             // prep writes K/V only (the MTP prompt pass)
+    float in_scale;                               // the quantized output's input_scale (0 = 1)
 };
 int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s);
 int launch_attn_prep_rows(const AttnArgs& a, int nrows, hipStream_t s);   // any row count (prefill)
@@ -145,16 +161,28 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr);
 // out_bf16, the residual bf16 when res_bf16
 int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
                     const float* sx, int M, void* y, int ldy, int out_bf16, const void* res, int ldr, int res_bf16,
-                    float rs, hipStream_t s);
+                    float rs, hipStream_t s, const AlphaSel* asel = nullptr);
 
 // ---------------------------------------------------------------- prefill element kernels (k_prefill.hip)
-int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, int8_t* xq, float* xs, hipStream_t s);
+int launch_pf_quant_bf16(const uint16_t* x, int ld, int M, int K, int gs, float in_scale, int8_t* xq, float* xs,
+                         hipStream_t s);
+int launch_quant_tok_grp(const float* x, int xstride, int M, int K, int gs, float in_scale, int8_t* xq, float* xs,
+                         hipStream_t s);
 int launch_pf_conv(const uint16_t* buf, int ld, int C, int nconv, const uint16_t* conv_w, uint16_t* rec, int npend,
                    uint16_t* out, int ldo, hipStream_t s);
 int launch_pf_ab(const uint16_t* in_a, const uint16_t* in_b, const uint16_t* A_log, const uint16_t* dt_bias,
                  const uint16_t* y, int ystride, int K, int vh, int C, float* out, hipStream_t s);
 int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
                            hipStream_t s);
+
+// ---------------------------------------------------------------- checkpoint (ckpt.hip)
+struct CkTensor { int dtype, ndim; long long shape[Q27X_MAX_DIMS]; const void* host; size_t nbytes; };
+int ckpt_get(const q27x_ckpt* ck, const char* name, CkTensor* out);   // Q27X_E_MISSING if absent
+// kind 0 fp8 E4M3, 1 NVFP4 (gsc = its E4M3 per-16 scales), 2 bf16 -> int8 per-64 (row_mode 1 / 2:
+// gate / up rows into the fused gate|up layout)
+int launch_to_i8g64(int kind, const void* src, const void* gsc, int rows, int K, int src_ld, int8_t* w8, float* s64,
+                    int row_mode, hipStream_t s);
+int launch_nvfp4_to_bf16(const void* src, const void* gsc, float ws2, int rows, int K, uint16_t* out, hipStream_t s);
 
 // ---------------------------------------------------------------- synthetic weights
 int launch_gen_i8(int8_t* W, float* WS, int rows, int K, uint64_t key, int layout_gu, int is_up,

@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libq27x.so")
 
 Q27X_OK = 0
-ERRORS = {-1: "ARG", -2: "SHAPE", -3: "HIP", -4: "NOMEM", -5: "STATE", -6: "RANGE", -7: "DEVICE"}
+ERRORS = {-1: "ARG", -2: "SHAPE", -3: "HIP", -4: "NOMEM", -5: "STATE", -6: "RANGE", -7: "DEVICE", -8: "IO",
+          -9: "FORMAT", -10: "MISSING"}
 
 
 class Q27XError(RuntimeError):
@@ -107,6 +108,15 @@ _SIGS = {
     "q27x_bench_mixer": ([VP, I, I, I, I, VP, VP], I),
     "q27x_debug_read": ([VP, ctypes.c_char_p, I, VP, SZ], I),
     "q27x_bench_stream": ([I, SZ, I, I, I, VP], I),
+    # checkpoint catalog and upload
+    "q27x_ckpt_open": ([ctypes.c_char_p, VP, SZ], VP),
+    "q27x_ckpt_open_census": ([ctypes.c_char_p, I, ctypes.c_longlong, ctypes.c_longlong, VP, SZ], VP),
+    "q27x_ckpt_close": ([VP], None), "q27x_ckpt_tensor_count": ([VP], I),
+    "q27x_ckpt_payload_bytes": ([VP], ctypes.c_longlong),
+    "q27x_ckpt_host_ptr": ([VP, ctypes.c_char_p, VP, VP, VP, VP], VP),
+    "q27x_ckpt_name": ([VP, I], ctypes.c_char_p),
+    "q27x_ckpt_info": ([VP, I, VP, VP, VP, VP, VP, VP], I),
+    "q27x_ckpt_check": ([VP, VP, VP, SZ], I), "q27x_load_checkpoint": ([VP, VP, VP, SZ], I),
 }
 
 
@@ -197,6 +207,37 @@ def tiny_config(**kw):
     return c
 
 
+class Checkpoint:
+    """A mapped checkpoint catalog (q27x_ckpt_open_census); raises Q27XError with the reason."""
+
+    def __init__(self, path, nshards=3, tensors=-1, payload_bytes=-1):
+        err = ctypes.create_string_buffer(512)
+        p = lib().q27x_ckpt_open_census(str(path).encode(), nshards, tensors, payload_bytes, err, len(err))
+        if not p:
+            msg = err.value.decode()
+            raise Q27XError(-8 if msg.startswith(("open(", "fstat(", "mmap(")) else -9, msg)
+        self.ck = p
+
+    def tensor_count(self):
+        return lib().q27x_ckpt_tensor_count(self.ck)
+
+    def payload_bytes(self):
+        return lib().q27x_ckpt_payload_bytes(self.ck)
+
+    def names(self):
+        return [lib().q27x_ckpt_name(self.ck, i).decode() for i in range(self.tensor_count())]
+
+    def check(self, cfg):
+        err = ctypes.create_string_buffer(512)
+        rc = lib().q27x_ckpt_check(self.ck, ctypes.byref(cfg), err, len(err))
+        return rc, err.value.decode()
+
+    def close(self):
+        if self.ck:
+            lib().q27x_ckpt_close(self.ck)
+            self.ck = None
+
+
 class Engine:
     """Owns one q27x context (weights, KV, GDN state, scratch) on one device."""
 
@@ -206,6 +247,12 @@ class Engine:
         call("q27x_ctx_create", device, ctypes.byref(cfg), ctypes.byref(p))
         self.ctx = p.value
         call("q27x_load_synthetic", self.ctx, seed)
+
+    def load_checkpoint(self, ck):
+        err = ctypes.create_string_buffer(512)
+        rc = lib().q27x_load_checkpoint(self.ctx, ck.ck, err, len(err))
+        if rc != Q27X_OK:
+            raise Q27XError(rc, err.value.decode())
 
     def weight_bytes(self):
         b = ctypes.c_size_t(0)

@@ -164,11 +164,15 @@ def test_config4_k7_ctx16k_forced_equals_plain(gpu):
     eng = X.Engine(cfg, SEED)
     p = prompt_of(cfg, 16200, seed=4)
     first = eng.prefill(p)
+    print("config 4: prompt ingested", flush=True)
     plain, _ = eng.generate(48, spec=False)
     assert plain[0] == first
+    print("config 4: plain stream done", flush=True)
     eng.prefill(p)
+    print("config 4: prompt ingested again", flush=True)
     eng.set_forced(np.array(plain, np.int32))
     forced, stf = eng.generate(48, spec=True)
+    print("config 4: forced rounds done", flush=True)
     assert forced == plain
     assert stf.acc_hist[7] >= stf.rounds - 1, (stf.rounds, list(stf.acc_hist))
     assert stf.committed >= 8 * (stf.rounds - 1)
