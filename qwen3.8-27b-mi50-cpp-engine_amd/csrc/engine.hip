@@ -103,7 +103,7 @@ struct PfBuf {
     int8_t* xq2 = nullptr; float* xs2 = nullptr;   // [cap][H], [cap][32]: the MTP pass's second fc input
     uint16_t* pb = nullptr;      // [cap][wmax] projection rows
     uint16_t* qh = nullptr;      // [cap][att] normed, roped queries
-    float* gu = nullptr;         // [cap][2I] gate|up GEMM output
+    float* gu = nullptr;         // [cap][max(2I, nz)] gate|up GEMM output (GDN scan's mixed rows before)
     uint16_t* mix = nullptr;     // [cap][max(nz, att)] mixer output
     float* rowsc = nullptr;      // [2][cap][vh] GDN decay, beta
     float* work = nullptr;       // attention split partials of kPfAttnRows rows
@@ -1323,7 +1323,7 @@ static int pf_alloc(q27x_ctx* x, int cap) {
         (rc = A((void**)&B->yf, C * H * 4)) || (rc = A((void**)&B->xq, C * kmax)) || (rc = A((void**)&B->xs, C * 32 * 4)) ||
         (rc = A((void**)&B->xq2, C * H)) || (rc = A((void**)&B->xs2, C * 32 * 4)) ||
         (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
-        (rc = A((void**)&B->gu, C * 2 * I * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
+        (rc = A((void**)&B->gu, C * std::max(2 * I, x->nz) * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
         (rc = A((void**)&B->rowsc, 2 * C * c.gdn_vh * 4)) ||
         (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4)) ||
         (rc = A((void**)&B->cv, C * x->nqkv * 2))) {
@@ -1433,7 +1433,7 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         g.rowsc = B.rowsc; g.norm_w = Y.gdn_norm; g.S = Y.S;
         g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
         g.out = B.mix; g.out_stride = x->nz; g.stop = &d->stop;
-        if ((rc = launch_gdn_scan(g, C, s))) return rc;
+        if ((rc = launch_gdn_scan(g, C, B.gu, s))) return rc;      // gate|up output is free until the MLP
         if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.out_proj, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     }

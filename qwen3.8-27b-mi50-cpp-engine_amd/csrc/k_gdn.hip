@@ -86,33 +86,35 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
     float st[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
+    // Every load below is unconditional (indices past the valid rows repeat a valid one, the values
+    // are not used): a load under a condition is followed by its own wait, which serialises the
+    // loads behind it into separate memory round trips.
     // (b) pending update vectors: thread t covers rows p = t/128 and p + 4
     float pk[2], pd[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int p = g + 4 * u;
-        pk[u] = (p < npend) ? P.khat[((size_t)p * a.vh + h) * kD + d] : 0.0f;
-        pd[u] = (p < npend) ? P.delta[((size_t)p * a.vh + h) * kD + d] : 0.0f;
+        const int p = g + 4 * u;                    // < kMaxRows: inside the pend area
+        pk[u] = P.khat[((size_t)p * a.vh + h) * kD + d];
+        pd[u] = P.delta[((size_t)p * a.vh + h) * kD + d];
     }
-    const float pdc = (t < npend) ? P.decay[(size_t)t * a.vh + h] : 0.0f;
+    const float pdc = P.decay[(size_t)(t & (kMaxRows - 1)) * a.vh + h];
     // (c) channel t < 384 of this head: q (key head kk), k (kk), v (h); threads 384..511 the gate z
     const int cl = (t < 3 * kD) ? t : 0;
     const int ch = (cl < kD) ? kk * kD + cl : (cl < 2 * kD) ? KD + kk * kD + (cl - kD) : 2 * KD + h * kD + (cl - 2 * kD);
+    const uint16_t* xsrc = (t < 3 * kD) ? a.qkv + ch : a.z + (size_t)h * kD + d;
+    const size_t xstride = (t < 3 * kD) ? (size_t)a.qkv_stride : (size_t)a.z_stride;
     uint16_t xr[kMaxRows];
 #pragma unroll
-    for (int n = 0; n < kMaxRows; ++n)
-        xr[n] = (n < nr) ? ((t < 3 * kD) ? a.qkv[(size_t)n * a.qkv_stride + ch] : a.z[(size_t)n * a.z_stride + (size_t)h * kD + d])
-                         : (uint16_t)0;
+    for (int n = 0; n < kMaxRows; ++n) xr[n] = xsrc[(size_t)((n < nr) ? n : nr - 1) * xstride];
     // (d) the row scalars: prepared (decay, beta), or the a/b logits
-    float r_a = 0.0f, r_b = 0.0f;
-    if (t < nr) {
-        if (a.rowsc) {
-            r_a = a.rowsc[(size_t)t * a.vh + h];                           // decay
-            r_b = a.rowsc[(size_t)(kMaxRows + t) * a.vh + h];              // beta
-        } else {
-            r_a = a.a[(size_t)t * a.ab_stride + h];
-            r_b = a.b[(size_t)t * a.ab_stride + h];
-        }
+    const int tr = (t < nr) ? t : nr - 1;
+    float r_a, r_b;
+    if (a.rowsc) {
+        r_a = a.rowsc[(size_t)tr * a.vh + h];                              // decay
+        r_b = a.rowsc[(size_t)(kMaxRows + tr) * a.vh + h];                 // beta
+    } else {
+        r_a = a.a[(size_t)tr * a.ab_stride + h];
+        r_b = a.b[(size_t)tr * a.ab_stride + h];
     }
     const float Aexp = a.rowsc ? 0.0f : qexp(bf2f(a.A_log[h]));
     const float dtb = a.rowsc ? 0.0f : bf2f(a.dt_bias[h]);
@@ -135,9 +137,10 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
             srow[t][2] = qexp(-(Aexp * qsoftplus(r_a + dtb)));
         }
     }
+    // every staged row is written (rows past nr hold copies of row nr - 1 and are not read): an
+    // exit at nr would index the register array dynamically (a select chain per element)
 #pragma unroll
     for (int n = 0; n < kMaxRows; ++n) {
-        if (n >= nr) break;
         if (t < 3 * kD) scv[n][cl] = bf2f(xr[n]);
         else sz[n][d] = bf2f(xr[n]);
     }
@@ -253,56 +256,102 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
     }
 }
 
-// Prefill scan: the same per-row arithmetic as k_gdn over all nrows rows of a chunk, in blocks of
-// kMaxRows staged rows; the state stays in registers from the first row to the last, is updated
-// after every row and written back once (nothing pending afterwards). Row scalars: decay at
-// rowsc[n vh + h], beta at rowsc[(nrows + n) vh + h]. Output bf16 only (the prefill quantizes it
-// per token group afterwards).
-__global__ __launch_bounds__(kNT) void k_gdn_scan(GdnArgs a, int nrows) {
-    const int h = blockIdx.x;
+// Prefill scan: the same per-row arithmetic as k_gdn over all nrows rows of a chunk, with the
+// value columns spread over waves instead of the key rows over a block. Value columns of the
+// delta rule are independent given the row's (k^, q^, beta, decay), so a wave owns 16 of them:
+// lane 16 g + c holds key rows 32g..32g+31 of column c, and the four key groups' partial sums
+// S^T k, S^T q meet by lane swaps in the order ((p0 + p1) + p2) + p3, which is k_gdn's order. No
+// barrier per row: a block (WPB waves, 16 WPB columns of one head) only synchronises per batch
+// of staged rows, to share the q/k norms. The state stays in registers from the first row to the
+// last and is written back once. Each row's mixed values go to `mix` [nrows][vh*128] fp32;
+// k_gdn_gnorm applies the gated RMSNorm afterwards (it needs the head's 128 columns, which live in
+// several blocks). Row scalars: decay at rowsc[n vh + h], beta at rowsc[(nrows + n) vh + h].
+#ifndef Q27X_SCAN_WPB
+#define Q27X_SCAN_WPB 4
+#endif
+constexpr int kScanWPB = Q27X_SCAN_WPB;  // waves per block
+// ((p0 + p1) + p2) + p3 over the lanes c, 16 + c, 32 + c, 48 + c (p_g in lane 16 g + c), exact in
+// the lanes of group 0 (the other lanes hold partial values). The gfx950 lane swaps exchange
+// 16-lane rows 0<->1, 2<->3 and the 32-lane halves; the second result holds the partner's value
+// in the even rows / lower half.
+__device__ __forceinline__ float key_group_sum_g0(float x) {
+    const float a = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+    const float b = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+    const float c = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(b), __float_as_uint(b), false, false)[1]);
+    return ((x + a) + b) + c;      // group 0: a = p1, b = p2, c = p3 (row 1's b is row 3's x)
+}
+// group 0's value in every lane of its column: row 0 -> row 1 by a 16-lane swap, rows 0, 1 -> rows
+// 2, 3 by a 32-lane swap (the first result holds the partner's value in the odd rows / upper half)
+__device__ __forceinline__ float from_group0(float s) {
+    const int g = (threadIdx.x >> 4) & 3;
+    const float t = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false)[0]);
+    const float u = (g == 1) ? t : s;
+    const float w = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(u), false, false)[0]);
+    return (g >= 2) ? w : u;
+}
+template <int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, float* __restrict__ mix, int nrows) {
+    constexpr int NT = 64 * WPB, NC = 16 * WPB;          // threads, value columns of the block
+    constexpr int R = 8 * WPB;                           // rows staged per batch
+    constexpr int CPT = 2 * kD / NT;                     // q|k channels loaded per thread
+    constexpr int BPH = kD / NC;                         // blocks per head
+    const int h = blockIdx.x / BPH, part = blockIdx.x % BPH;
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int d = t & (kD - 1), g = t >> 7;
+    const int g = lane >> 4, cw = 16 * wv + (lane & 15);      // column within the block's NC
+    const int col = NC * part + cw;
     const int ratio = a.vh / a.kh, kk = h / ratio;
     const int KD = a.kh * kD;
-    __shared__ float scv[kMaxRows][3 * kD];
-    __shared__ float sz[kMaxRows][kD];
-    __shared__ __attribute__((aligned(16))) float sq[kMaxRows][kD];
-    __shared__ __attribute__((aligned(16))) float sk[kMaxRows][kD];
-    __shared__ float pA[2][4][kD], pB[2][4][kD];
-    __shared__ float smix[kMaxRows][kD];
-    __shared__ float red[kMaxRows][2];
-    __shared__ float srow[kMaxRows][4];
-    float* Sp = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + d;
+    const size_t mstride = (size_t)a.vh * kD;
+    __shared__ float scv[R][2 * kD];             // raw q | k of the key head (bf16 values)
+    __shared__ float sv[R][NC];                  // v of the block's columns
+    __shared__ __attribute__((aligned(16))) float sq[R][kD];
+    __shared__ __attribute__((aligned(16))) float sk[R][kD];
+    __shared__ float srow[R][4];                 // per row: kq, beta, decay
+    __shared__ float smix[R][NC];
+    float* Sp = a.S + (size_t)h * kD * kD + (size_t)(g * kJ) * kD + col;
     float st[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
-    const int cl = (t < 3 * kD) ? t : 0;
-    const int ch = (cl < kD) ? kk * kD + cl : (cl < 2 * kD) ? KD + kk * kD + (cl - kD) : 2 * KD + h * kD + (cl - 2 * kD);
-    const float nw = bf2f(a.norm_w[(t & 63) + 64 * (wv & 1)]);
-    const int e = 64 * (wv & 1) + lane;
-    for (int r0 = 0; r0 < nrows; r0 += kMaxRows) {
-        const int nr = (nrows - r0 < kMaxRows) ? nrows - r0 : kMaxRows;
-        uint16_t xr[kMaxRows];
+    // thread t loads q|k channels t + NT i (< 128: q, else k) and v column NC part + t % NC
+    size_t chq[CPT];
 #pragma unroll
-        for (int n = 0; n < kMaxRows; ++n)
-            xr[n] = (n < nr) ? ((t < 3 * kD) ? a.qkv[(size_t)(r0 + n) * a.qkv_stride + ch]
-                                             : a.z[(size_t)(r0 + n) * a.z_stride + (size_t)h * kD + d])
-                             : (uint16_t)0;
-        float r_a = 0.0f, r_b = 0.0f;
-        if (t < nr) {
-            r_a = a.rowsc[(size_t)(r0 + t) * a.vh + h];
-            r_b = a.rowsc[(size_t)(nrows + r0 + t) * a.vh + h];
+    for (int i = 0; i < CPT; ++i) {
+        const int c = t + NT * i;
+        chq[i] = (c < kD) ? (size_t)kk * kD + c : (size_t)KD + kk * kD + (c - kD);
+    }
+    const size_t chv = (size_t)2 * KD + (size_t)h * kD + NC * part + (t % NC);
+    uint16_t xr[R][CPT], xv[R];
+    float r_a = 0.0f, r_b = 0.0f;
+    // unconditional loads (rows past the last repeat it; every thread loads a v column): a load
+    // under a condition is followed by its own wait, which would serialise the batch's loads
+    auto load = [&](int r0) {
+#pragma unroll
+        for (int n = 0; n < R; ++n) {
+            const size_t row = (size_t)((r0 + n < nrows) ? r0 + n : nrows - 1) * a.qkv_stride;
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) xr[n][i] = a.qkv[row + chq[i]];
+            xv[n] = a.qkv[row + chv];
         }
-        __syncthreads();                            // the previous block's rows are consumed
+        const int rt = (r0 + (t % R) < nrows) ? r0 + (t % R) : nrows - 1;
+        r_a = a.rowsc[(size_t)rt * a.vh + h];
+        r_b = a.rowsc[(size_t)(nrows + rt) * a.vh + h];
+    };
+    load(0);
+    for (int r0 = 0; r0 < nrows; r0 += R) {
+        const int nr = (nrows - r0 < R) ? nrows - r0 : R;
+        __syncthreads();                            // the previous batch is written out
         if (t < nr) { srow[t][1] = r_b; srow[t][2] = r_a; }
+        // every staged row is written (rows past nr hold copies of the last row and are not read):
+        // an exit at nr would index the register arrays dynamically (a select chain per element)
 #pragma unroll
-        for (int n = 0; n < kMaxRows; ++n) {
-            if (n >= nr) break;
-            if (t < 3 * kD) scv[n][cl] = bf2f(xr[n]);
-            else sz[n][d] = bf2f(xr[n]);
+        for (int n = 0; n < R; ++n) {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) scv[n][t + NT * i] = bf2f(xr[n][i]);
+            if (t < NC) sv[n][t] = bf2f(xv[n]);
         }
+        if (r0 + R < nrows) load(r0 + R);            // next batch in flight during this one
         __syncthreads();
-        for (int n = wv; n < nr; n += kNT / 64) {
+        for (int n = wv; n < nr; n += WPB) {        // q/k norms (k_gdn's arithmetic)
             const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
             const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
             const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
@@ -319,64 +368,81 @@ __global__ __launch_bounds__(kNT) void k_gdn_scan(GdnArgs a, int nrows) {
             if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
         }
         __syncthreads();
-        for (int n = 0; n < nr; ++n) {
-            const float kq = srow[n][0], beta = srow[n][1], decay = srow[n][2];
-            const float vv = scv[n][2 * kD + d];
-            float accA = 0.0f, accB = 0.0f;
+        // rows in pairs: everything a row reads from LDS is requested while the row before it
+        // computes (a row's own reads would make every wait cover the prefetch behind them)
+        struct RowIn { float k[kJ], q[kJ]; float kq, beta, decay, v; };
+        auto lds_row = [&](int n, RowIn& r) {
 #pragma unroll
             for (int j4 = 0; j4 < kJ; j4 += 4) {
                 const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
                 const float4 q4 = *(const float4*)&sq[n][g * kJ + j4];
-                accA = __builtin_fmaf(st[j4], k4.x, accA);
-                accB = __builtin_fmaf(st[j4], q4.x, accB);
-                accA = __builtin_fmaf(st[j4 + 1], k4.y, accA);
-                accB = __builtin_fmaf(st[j4 + 1], q4.y, accB);
-                accA = __builtin_fmaf(st[j4 + 2], k4.z, accA);
-                accB = __builtin_fmaf(st[j4 + 2], q4.z, accB);
-                accA = __builtin_fmaf(st[j4 + 3], k4.w, accA);
-                accB = __builtin_fmaf(st[j4 + 3], q4.w, accB);
+                r.k[j4] = k4.x; r.k[j4 + 1] = k4.y; r.k[j4 + 2] = k4.z; r.k[j4 + 3] = k4.w;
+                r.q[j4] = q4.x; r.q[j4 + 1] = q4.y; r.q[j4 + 2] = q4.z; r.q[j4 + 3] = q4.w;
             }
-            pA[n & 1][g][d] = accA;
-            pB[n & 1][g][d] = accB;
-            __syncthreads();
-            const float A = ((pA[n & 1][0][d] + pA[n & 1][1][d]) + pA[n & 1][2][d]) + pA[n & 1][3][d];
-            const float B = ((pB[n & 1][0][d] + pB[n & 1][1][d]) + pB[n & 1][2][d]) + pB[n & 1][3][d];
-            const float delta = (vv - decay * A) * beta;
-            const float mixed = __builtin_fmaf(delta, kq, decay * B);
+            r.kq = srow[n][0]; r.beta = srow[n][1]; r.decay = srow[n][2];
+            r.v = sv[n][cw];
+        };
+        auto do_row = [&](int n, const RowIn& r) {
+            float accA = 0.0f, accB = 0.0f;
 #pragma unroll
-            for (int j4 = 0; j4 < kJ; j4 += 4) {
-                const float4 k4 = *(const float4*)&sk[n][g * kJ + j4];
-                st[j4] = __builtin_fmaf(k4.x, delta, decay * st[j4]);
-                st[j4 + 1] = __builtin_fmaf(k4.y, delta, decay * st[j4 + 1]);
-                st[j4 + 2] = __builtin_fmaf(k4.z, delta, decay * st[j4 + 2]);
-                st[j4 + 3] = __builtin_fmaf(k4.w, delta, decay * st[j4 + 3]);
+            for (int j = 0; j < kJ; ++j) {
+                accA = __builtin_fmaf(st[j], r.k[j], accA);
+                accB = __builtin_fmaf(st[j], r.q[j], accB);
             }
-            if (g == 0) smix[n][d] = mixed;
+            const float A = from_group0(key_group_sum_g0(accA));
+            const float delta = (r.v - r.decay * A) * r.beta;
+#pragma unroll
+            for (int j = 0; j < kJ; ++j) st[j] = __builtin_fmaf(r.k[j], delta, r.decay * st[j]);
+            const float B = key_group_sum_g0(accB);                 // needed in group 0 only
+            const float mixed = __builtin_fmaf(delta, r.kq, r.decay * B);
+            if (g == 0) smix[n][cw] = mixed;
+        };
+        // (the prefetches are unconditional, of row min(n, nr - 1), so that every path through the
+        // loop has the same reads in flight and the waits count only the reads a row needs)
+        RowIn ra, rb;
+        lds_row(0, ra);
+        for (int n = 0; n < nr; n += 2) {
+            lds_row((n + 1 < nr) ? n + 1 : nr - 1, rb);
+            do_row(n, ra);
+            lds_row((n + 2 < nr) ? n + 2 : nr - 1, ra);
+            if (n + 1 < nr) do_row(n + 1, rb);
         }
         __syncthreads();
-        for (int n = wv >> 1; n < nr; n += 4) {
-            const float mx = smix[n][e];
-            const float r3 = tree64(mx * mx);
-            if (lane == 0) red[n][wv & 1] = r3;
-        }
-        __syncthreads();
-        for (int n = wv >> 1; n < nr; n += 4) {
-            const float mx = smix[n][e];
-            const float inv = rsqrt_cr((red[n][0] + red[n][1]) * (1.0f / (float)kD) + a.eps);
-            const float y = mx * inv * nw * qsilu(sz[n][e]);
-            a.out[(size_t)(r0 + n) * a.out_stride + (size_t)h * kD + e] = f2bf(y);
+        for (int i = t; i < nr * NC; i += NT) {
+            const int n = i / NC, c = i % NC;
+            mix[(size_t)(r0 + n) * mstride + (size_t)h * kD + NC * part + c] = smix[n][c];
         }
     }
 #pragma unroll
     for (int j = 0; j < kJ; ++j) Sp[(size_t)j * kD] = st[j];
 }
-int launch_gdn_scan(const GdnArgs& a, int nrows, hipStream_t s) {
+// gated RMSNorm of the scan's rows (k_gdn's arithmetic: two 64-lane trees of mixed^2, their sum
+// over 128, rsqrt; y = mixed inv norm_w SiLU(z) -> bf16). One 128-thread block per (head, row).
+__global__ __launch_bounds__(kD) void k_gdn_gnorm(const float* __restrict__ mix, const uint16_t* __restrict__ z,
+                                                  int z_stride, const uint16_t* __restrict__ norm_w, float eps,
+                                                  int vh, uint16_t* __restrict__ out, int out_stride) {
+    const int h = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    __shared__ float red[2];
+    const float mx = mix[(size_t)row * vh * kD + (size_t)h * kD + t];
+    const float zz = bf2f(z[(size_t)row * z_stride + (size_t)h * kD + t]);
+    const float nw = bf2f(norm_w[t]);
+    const float r3 = tree64(mx * mx);
+    if (lane == 0) red[w] = r3;
+    __syncthreads();
+    const float inv = rsqrt_cr((red[0] + red[1]) * (1.0f / (float)kD) + eps);
+    out[(size_t)row * out_stride + (size_t)h * kD + t] = f2bf(mx * inv * nw * qsilu(zz));
+}
+int launch_gdn_scan(const GdnArgs& a, int nrows, float* mix, hipStream_t s) {
     if (a.d != kD || a.kh < 1 || a.vh % a.kh || nrows < 1 || !a.qkv || !a.z || !a.S || !a.rowsc || !a.out ||
-        !a.norm_w) {
+        !a.norm_w || !mix || nrows > 65535) {
         set_error("gdn scan: unsupported shape or null argument (d=%d kh=%d vh=%d rows=%d)", a.d, a.kh, a.vh, nrows);
         return Q27X_E_SHAPE;
     }
-    hipLaunchKernelGGL(k_gdn_scan, dim3(a.vh), dim3(kNT), 0, s, a, nrows);
+    hipLaunchKernelGGL(k_gdn_scan<kScanWPB>, dim3(a.vh * (kD / (16 * kScanWPB))), dim3(64 * kScanWPB), 0, s, a, mix,
+                       nrows);
+    Q27X_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.vh, nrows), dim3(kD), 0, s, (const float*)mix, a.z, a.z_stride, a.norm_w,
+                       a.eps, a.vh, a.out, a.out_stride);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
