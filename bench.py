@@ -371,6 +371,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="eager launches (profilers that cannot follow graphs)")
     ap.add_argument("--prefill-gemm-only", action="store_true",
                     help="only the int8-MFMA prefill GEMM leg (for rocprofv3 passes on it)")
+    ap.add_argument("--rounds-only", action="store_true",
+                    help="only the prompt ingest (GEMM path) and the natural-acceptance rounds (for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate|up) and the calibration copy, for rocprofv3 --pmc passes")
     args = ap.parse_args()
@@ -399,6 +401,15 @@ def main():
     eng = q27x.Engine(cfg, SEED)
     log(f"engine: {eng.weight_bytes() / 1e9:.2f} GB weights resident, {time.time() - t0:.1f} s")
     prompt = np.random.default_rng(0x51E70003).integers(0, cfg.vocab, args.prompt).astype(np.int32)
+    if args.rounds_only:
+        eng.prefill_gemm(prompt)
+        eng.run_rounds(args.warmup, spec=True)
+        st = eng.run_rounds(args.steps, spec=True)
+        print(json.dumps({"rounds_only": {"spec_k": K, "prompt": args.prompt, "rounds": st.rounds,
+                                          "committed": st.committed,
+                                          "ms_per_round": round(st.decode_ms / st.rounds, 4)}}), flush=True)
+        eng.close()
+        return 0
 
     # ---- natural acceptance
     # prompt ingest: the verify kernels over the prompt (q27x_prefill) and the layer-major int8-MFMA

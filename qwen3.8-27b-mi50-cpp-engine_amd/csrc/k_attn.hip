@@ -112,7 +112,11 @@ size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
 //   P.V: thread = (4 dims, queries t/32 + 16 u, u < QPT), o = fmaf(p_k, v_k, o) over the valid keys
 //        in order.
 // Dynamic LDS: queries [nqr][128] fp32 | p [nqr][65] fp32.
-constexpr int kKStride = kHD + 4;
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kKStride = kHD + 4;     // LDS row strides chosen so the MFMA operand reads of 64
+constexpr int kQStride = kHD + 4;     // lanes (16 rows x 4 columns) hit every bank twice
+constexpr int kVStride = kHD + 16;
+constexpr int kSpStride = kSplit + 4;
 constexpr int kAttnThreads = 512;
 constexpr int kSplitBlocks = 256;
 // PREP: the block also does the prep of its rows: the queries of its kv head are normed and roped
@@ -147,10 +151,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     const int ms = a.max_splits;
     const int gsh = __builtin_ctz(a.kv_group);      // kv_group is a power of two
     __shared__ float kd[kSplit * kKStride];
-    __shared__ float vd[kSplit * kHD];
+    __shared__ float vd[kSplit * kVStride];
     extern __shared__ float dyn[];
-    float* qf = dyn;                                // [nqr_max][kHD]
-    float* sp = dyn + (size_t)nr * G * kHD;         // [nqr_max][kSplit + 1]
+    float* qf = dyn;                                // [nqr_max][kQStride]
+    float* sp = dyn + (size_t)nr * G * kQStride;    // [nqr_max][kSpStride]: scores, then p
     const int t = threadIdx.x, lane = t & 63;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     float* wo = a.work;
@@ -214,11 +218,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             for (int i = 0; i < NQW; ++i) {
                 const int qi = wv + (kAttnThreads / 64) * i;
                 if (qi < nqr) {
-                    qf[qi * kHD + lane] = bfr(qy[i][0]);
-                    qf[qi * kHD + 64 + lane] = bfr(qy[i][1]);
+                    qf[qi * kQStride + lane] = bfr(qy[i][0]);
+                    qf[qi * kQStride + 64 + lane] = bfr(qy[i][1]);
                 }
             }
-            // new positions of this split: one wave per key
+        }
+        // new positions of this split (in whichever of the block's splits holds them): one wave
+        // per key. In the block's first split this runs before the barrier below (nothing to
+        // overwrite yet, and its loads overlap the tile's); in a later split only after it, when
+        // the previous split's tiles are consumed.
+        auto new_keys = [&]() __attribute__((always_inline)) {
+            const int qw = a.gate ? 2 * kHD : kHD;
             const int qrows = a.nq * qw;
             for (int k = kn0 + wv; k < nk; k += kAttnThreads / 64) {
                 const int pos = k0 + k, r = pos - pos0;
@@ -231,17 +241,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                          lane, deq);
                 kd[k * kKStride + lane] = deq[0];
                 kd[k * kKStride + 64 + lane] = deq[1];
-                vd[k * kHD + lane] = deq[2];
-                vd[k * kHD + 64 + lane] = deq[3];
+                vd[k * kVStride + lane] = deq[2];
+                vd[k * kVStride + 64 + lane] = deq[3];
             }
-        }
+        };
+        if (PREP && !staged_q && kn0 < nk) new_keys();
         __syncthreads();                           // the previous split's tiles are consumed
+        if (PREP && staged_q && kn0 < nk) new_keys();
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
             if (k >= kn0 && k < nk) continue;      // a new position (PREP)
             const uint32_t w4[4] = {kv4[u].x, kv4[u].y, kv4[u].z, kv4[u].w};
-            float* dst = isv ? &vd[k * kHD + 16 * c] : &kd[k * kKStride + 16 * c];
+            float* dst = isv ? &vd[k * kVStride + 16 * c] : &kd[k * kKStride + 16 * c];
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {
                 float4 f;
@@ -260,7 +272,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 const int i = t + kAttnThreads * u;
                 const int qi = i >> 4, c = i & 15;
                 if (qi < nqr) {
-                    float4* d = (float4*)&qf[qi * kHD + 8 * c];
+                    float4* d = (float4*)&qf[qi * kQStride + 8 * c];
                     d[0] = make_float4(__uint_as_float(q4[u].x << 16), __uint_as_float(q4[u].x & 0xFFFF0000u),
                                        __uint_as_float(q4[u].y << 16), __uint_as_float(q4[u].y & 0xFFFF0000u));
                     d[1] = make_float4(__uint_as_float(q4[u].z << 16), __uint_as_float(q4[u].z & 0xFFFF0000u),
@@ -270,89 +282,75 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
         }
         staged_q = true;
         __syncthreads();
-        // ---- scores + split softmax: lane = key, this wave's queries wv + 8 i
-        {
-            const int k = lane;
-            float acc[NQW];
+        // ---- scores on the matrix cores: query tile qt (16 queries) x key tile kt (16 keys) per
+        // wave, v_mfma_f32_16x16x4f32 over the head dims in order. Each instruction adds its four
+        // products one after another with fused multiply-adds (k = 0..3), so the chain of 32
+        // instructions is exactly the oracle's fmaf loop over dims 0..127.
+        // Operand lanes: lane 16 g + j gives A[j][g] = q(16 qt + j)[4 s + g] and
+        // B[g][j] = k(16 kt + j)[4 s + g]; result r of lane 16 g + j is score(query 4 g + r, key j).
+        constexpr int QT = (8 * NQW + 15) / 16;   // query tiles of the kernel's capacity
+        const int g4 = lane >> 4, j16 = lane & 15;
+        for (int ti = wv; ti < 4 * QT; ti += kAttnThreads / 64) {
+            const int qt = ti >> 2, kt = ti & 3;
+            const int qa = (16 * qt + j16 < nqr) ? 16 * qt + j16 : 0;     // rows past nqr: discarded
+            const float* qrow = qf + (size_t)qa * kQStride + g4;
+            const float* krow = kd + (size_t)(16 * kt + j16) * kKStride + g4;
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+            for (int st4 = 0; st4 < kHD / 4; ++st4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[4 * st4], krow[4 * st4], acc, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < NQW; ++i) acc[i] = 0.0f;
-            const float* kr = &kd[k * kKStride];
-            // a wave with fewer than NQW queries computes its missing ones on query 0 (discarded
-            // below): no branch inside the loop, so the LDS reads of several steps are in flight
-            // together instead of one read and one wait per step
-            int qrow[NQW];
-#pragma unroll
-            for (int i = 0; i < NQW; ++i) qrow[i] = (wv + 8 * i < nqr) ? (wv + 8 * i) * kHD : 0;
-#pragma unroll 4
-            for (int c = 0; c < kHD / 4; ++c) {
-                const float4 kv = *(const float4*)(kr + 4 * c);
-#pragma unroll
-                for (int i = 0; i < NQW; ++i) {
-                    const float4 q = *(const float4*)&qf[qrow[i] + 4 * c];
-                    float v = acc[i];
-                    v = __builtin_fmaf(q.x, kv.x, v);
-                    v = __builtin_fmaf(q.y, kv.y, v);
-                    v = __builtin_fmaf(q.z, kv.z, v);
-                    v = __builtin_fmaf(q.w, kv.w, v);
-                    acc[i] = v;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < NQW; ++i) {
-                const int qi = wv + 8 * i;
-                if (qi >= nqr) break;             // wave-uniform
-                const int r = qi / G, g = qi - r * G;
-                const int L = pos0 + r + 1;
-                const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
-                const bool valid = k < nv;
-                const float x = acc[i] * a.sl2e;
-                float m = valid ? x : -__builtin_huge_valf();
-                m = max_xor(m, 64);
-                const float p = valid ? qexp2(x - m) : 0.0f;
-                sp[qi * (kSplit + 1) + k] = p;
-                const float l = tree64(p);
-                if (lane == 0 && nv > 0) {
-                    const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
-                    wm[mi] = m;
-                    wl[mi] = l;
-                }
+            for (int r = 0; r < 4; ++r) {
+                const int qi = 16 * qt + 4 * g4 + r;
+                if (qi < nqr) sp[qi * kSpStride + 16 * kt + j16] = acc[r];
             }
         }
         __syncthreads();
-        // ---- o = sum_k p_k v_k in key order
-        {
-            const int d4 = 4 * (t & 31), qs = t >> 5;
-            float o[QPT][4];
-            int nvq[QPT];
-            int kmax = 0;
+        // ---- split softmax: lane = key, this wave's queries wv + 8 i (p replaces the score)
 #pragma unroll
-            for (int u = 0; u < QPT; ++u) {
-                const int qi = qs + 16 * u;
-                const int L = pos0 + qi / G + 1;
-                nvq[u] = (qi < nqr) ? ((L - k0 < nk) ? (L - k0) : nk) : 0;
-                kmax = nvq[u] > kmax ? nvq[u] : kmax;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[u][e] = 0.0f;
+        for (int i = 0; i < NQW; ++i) {
+            const int qi = wv + 8 * i;
+            if (qi >= nqr) break;                 // wave-uniform
+            const int k = lane;
+            const int r = qi / G, g = qi - r * G;
+            const int L = pos0 + r + 1;
+            const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
+            const bool valid = k < nv;
+            const float x = sp[qi * kSpStride + k] * a.sl2e;
+            float m = valid ? x : -__builtin_huge_valf();
+            m = max_xor(m, 64);
+            const float p = valid ? qexp2(x - m) : 0.0f;
+            sp[qi * kSpStride + k] = p;
+            const float l = tree64(p);
+            if (lane == 0 && nv > 0) {
+                const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
+                wm[mi] = m;
+                wl[mi] = l;
             }
-            for (int k = 0; k < kmax; ++k) {
-                const float4 v = *(const float4*)&vd[k * kHD + d4];
+        }
+        __syncthreads();
+        // ---- o = sum_k p_k v_k in key order, on the matrix cores: query tile qt x dim tile dt
+        // per wave, 16 instructions over keys 0..63 in order (p = 0 for the keys a row does not
+        // see, whose V rows are finite: fma(0, v, o) leaves o unchanged).
+        // A[j][g] = p(16 qt + j)[4 s + g], B[g][j] = v[4 s + g][16 dt + j]; result r of lane
+        // 16 g + j is o(query 16 qt + 4 g + r)[16 dt + j].
+        for (int ti = wv; ti < 8 * QT; ti += kAttnThreads / 64) {
+            const int qt = ti >> 3, dt = ti & 7;
+            const int qa = (16 * qt + j16 < nqr) ? 16 * qt + j16 : 0;
+            const float* prow = sp + (size_t)qa * kSpStride + g4;
+            const float* vcol = vd + (size_t)g4 * kVStride + 16 * dt + j16;
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int u = 0; u < QPT; ++u) {
-                    if (k < nvq[u]) {
-                        const float p = sp[(qs + 16 * u) * (kSplit + 1) + k];
-                        o[u][0] = __builtin_fmaf(p, v.x, o[u][0]);
-                        o[u][1] = __builtin_fmaf(p, v.y, o[u][1]);
-                        o[u][2] = __builtin_fmaf(p, v.z, o[u][2]);
-                        o[u][3] = __builtin_fmaf(p, v.w, o[u][3]);
-                    }
-                }
-            }
+            for (int st4 = 0; st4 < kSplit / 4; ++st4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[4 * st4], vcol[4 * st4 * kVStride], acc, 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < QPT; ++u) {
-                if (nvq[u] <= 0) continue;
-                const int qi = qs + 16 * u, r = qi / G, g = qi - r * G;
-                float* dst = &wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + d4];
-                *(float4*)dst = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+            for (int r = 0; r < 4; ++r) {
+                const int qi = 16 * qt + 4 * g4 + r;
+                if (qi >= nqr) continue;
+                const int rr = qi / G, g = qi - rr * G;
+                const int L = pos0 + rr + 1;
+                if (L - k0 <= 0) continue;        // no key of this split is visible to the row
+                wo[(((size_t)rr * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + 16 * dt + j16] = acc[r];
             }
         }
     }
@@ -455,10 +453,10 @@ int launch_attn_prep_rows(const AttnArgs& a, int nrows, hipStream_t s) {
 template <bool PREP>
 static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
     const int nqr = nr * (a.nq / a.nkv);
-    const size_t lds = (size_t)nqr * (kHD + kSplit + 1) * 4;
-    static bool lds_set = false;                  // queries + p of up to 64 query vectors: 49 KiB
+    const size_t lds = (size_t)nqr * (kQStride + kSpStride) * 4;
+    static bool lds_set = false;                  // queries + p of up to 64 query vectors: 50 KiB
     if (!lds_set) {
-        const int mx = 64 * (kHD + kSplit + 1) * 4;
+        const int mx = 64 * (kQStride + kSpStride) * 4;
         Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<1, 1, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
         Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<2, 1, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
         Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_split<3, 2, PREP>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));

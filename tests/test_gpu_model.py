@@ -153,6 +153,29 @@ def test_full_geometry_spec_equals_plain(gpu):
     eng.close()
 
 
+@pytest.mark.parametrize("k", [2, 7])
+def test_long_context_spec_equals_plain(gpu, k):
+    """Past 2048 positions each attention block takes several 64-key splits in turn, so the step's
+    new positions (normed, roped, written to the cache inside the split kernel) can fall in a later
+    split of a block. After a 2400-token prompt: spec == plain greedy, and forced acceptance
+    commits K + 1 tokens per round."""
+    X = gpu
+    cfg = X.default_config(spec_k=k, ctx=2560)
+    eng = X.Engine(cfg, SEED)
+    p = prompt_of(cfg, 2400, seed=5)
+    eng.prefill_gemm(p)
+    plain, _ = eng.generate(40, spec=False)
+    eng.prefill_gemm(p)
+    spec, _ = eng.generate(40, spec=True)
+    assert spec == plain
+    eng.prefill_gemm(p)
+    eng.set_forced(np.array(plain, np.int32))
+    forced, stf = eng.generate(40, spec=True)
+    assert forced == plain
+    assert stf.acc_hist[k] >= stf.rounds - 1, (stf.rounds, list(stf.acc_hist))
+    eng.set_forced([])
+    eng.close()
+
 
 def test_config4_k7_ctx16k_forced_equals_plain(gpu):
     """BASELINE config 4 (64 layers, K = 7, ctx 16384): after a 16200-token prompt, forced
@@ -163,12 +186,12 @@ def test_config4_k7_ctx16k_forced_equals_plain(gpu):
     cfg = X.default_config(spec_k=7, ctx=16384)
     eng = X.Engine(cfg, SEED)
     p = prompt_of(cfg, 16200, seed=4)
-    first = eng.prefill(p)
+    first = eng.prefill_gemm(p)
     print("config 4: prompt ingested", flush=True)
     plain, _ = eng.generate(48, spec=False)
     assert plain[0] == first
     print("config 4: plain stream done", flush=True)
-    eng.prefill(p)
+    eng.prefill_gemm(p)
     print("config 4: prompt ingested again", flush=True)
     eng.set_forced(np.array(plain, np.int32))
     forced, stf = eng.generate(48, spec=True)
