@@ -371,6 +371,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="eager launches (profilers that cannot follow graphs)")
     ap.add_argument("--prefill-gemm-only", action="store_true",
                     help="only the int8-MFMA prefill GEMM leg (for rocprofv3 passes on it)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the GEMM-path prompt ingest of --prompt tokens, twice (for kernel traces)")
     ap.add_argument("--rounds-only", action="store_true",
                     help="only the prompt ingest (GEMM path) and the natural-acceptance rounds (for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
@@ -401,6 +403,16 @@ def main():
     eng = q27x.Engine(cfg, SEED)
     log(f"engine: {eng.weight_bytes() / 1e9:.2f} GB weights resident, {time.time() - t0:.1f} s")
     prompt = np.random.default_rng(0x51E70003).integers(0, cfg.vocab, args.prompt).astype(np.int32)
+    if args.prefill_only:
+        ts = []
+        for _ in range(2):
+            t = time.time()
+            eng.prefill_gemm(prompt)
+            ts.append(time.time() - t)
+        print(json.dumps({"prefill_only": {"tokens": args.prompt, "s": [round(x, 4) for x in ts],
+                                           "tok_s": round(args.prompt / ts[-1], 1)}}), flush=True)
+        eng.close()
+        return 0
     if args.rounds_only:
         eng.prefill_gemm(prompt)
         eng.run_rounds(args.warmup, spec=True)

@@ -5,6 +5,12 @@
       Per-round kernel breakdown of a --kernel-trace run (rocpd SQLite output): the dispatches after
       one marker kernel (default k_accept, the last kernel of a speculative round) up to and
       including the next; the median-span round of the second half of the trace is printed.
+  prefill <run_results.db>
+      Per-kernel totals of the last prompt ingest in a --kernel-trace run of
+      `bench.py --prefill-only` (the dispatches after the next-to-last k_argmax_final, which ends
+      an ingest, up to the last one).
+  counters <dir> [<dir> ...]
+      Mean per dispatch of every counter of every kernel in --pmc output directories.
   traffic <fetch_dir> <write_dir> <kernel-substring> <copy_bytes> <out.json>
       HBM bytes per launch of one kernel from two --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB
       per dispatch), each scaled by the same counter's reading for the calibration copy kernel
@@ -41,6 +47,34 @@ def rounds(db, marker="k_accept"):
     print(f"round: {len(seg)} kernels, span {span:.1f} us, busy {busy:.1f} us, gaps {span - busy:.1f} us")
     for n, (k, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         print(f"{t:10.1f} us {k:5d} x {t / k:8.2f} us  {n[:100]}")
+
+
+def prefill(db):
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, start, end from kernels order by start").fetchall()
+    idx = [i for i, r in enumerate(rows) if "k_argmax_final" in r[0]]
+    seg = rows[idx[-2] + 1:idx[-1] + 1] if len(idx) >= 2 else rows
+    agg = collections.OrderedDict()
+    for n, s, e in seg:
+        t = agg.setdefault(n.split("(")[0], [0, 0.0])
+        t[0] += 1
+        t[1] += (e - s) / 1e3
+    busy = sum(t for _, t in agg.values())
+    span = (seg[-1][2] - seg[0][1]) / 1e3
+    print(f"ingest: {len(seg)} kernels, span {span / 1e3:.2f} ms, busy {busy / 1e3:.2f} ms")
+    for n, (k, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"{t / 1e3:9.2f} ms {100 * t / busy:5.1f}% {k:5d} x {t / k:9.1f} us  {n[:80]}")
+
+
+def counters(dirs):
+    out = collections.OrderedDict()
+    for d in dirs:
+        for n, cn, v in _counter_rows(d):
+            out.setdefault(n.split("(")[0], collections.OrderedDict()).setdefault(cn, []).append(v)
+    for n, cs in out.items():
+        print(n[:80])
+        for cn, v in cs.items():
+            print(f"    {cn:28s} {sum(v) / len(v):16.1f}   ({len(v)} dispatches)")
 
 
 def _counter_rows(d):
@@ -87,6 +121,10 @@ def traffic(fetch_dir, write_dir, kernel, copy_bytes, out):
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "rounds":
         rounds(sys.argv[2], *(sys.argv[3:4]))
+    elif len(sys.argv) == 3 and sys.argv[1] == "prefill":
+        prefill(sys.argv[2])
+    elif len(sys.argv) >= 3 and sys.argv[1] == "counters":
+        counters(sys.argv[2:])
     elif len(sys.argv) == 7 and sys.argv[1] == "traffic":
         traffic(sys.argv[2], sys.argv[3], sys.argv[4], int(sys.argv[5]), sys.argv[6])
     else:
