@@ -723,18 +723,25 @@ void q27o_attn_prep_rows(const uint16_t* qkv, int qkv_stride, const uint16_t* q_
     }
 }
 
-/* score: fmaf over the head dims in order */
-static float score_seq(const float* q, const float* k, int hd) {
-    float a = 0.0f;
-    for (int i = 0; i < hd; ++i) a = fmaf(q[i], k[i], a);
-    return a;
+/* score: four fmaf chains over the head dims in order, chain c over dims [c hd/4, (c+1) hd/4),
+ * summed ((c0 + c1) + c2) + c3 (the GPU's matrix-core tiles run the four chains side by side) */
+static float score_4chain(const float* q, const float* k, int hd) {
+    float c[4];
+    const int w = hd / 4;
+    for (int j = 0; j < 4; ++j) {
+        float a = 0.0f;
+        for (int i = j * w; i < (j + 1) * w; ++i) a = fmaf(q[i], k[i], a);
+        c[j] = a;
+    }
+    return ((c[0] + c[1]) + c[2]) + c[3];
 }
 
 #define Q27O_SPLIT 64
 /* src/q27_attn.hip:258-463 semantics (GQA, causal over pos0+r, log2-domain softmax, split
- * combine, sigmoid output gate); this build's order: fixed 64-key splits, scores summed over the
- * head dims in order, per split m = max, p = 2^(x - m), l = shfl_down tree over the split's 64
- * lanes, o = fmaf over the keys in ascending order; splits combined in ascending order. */
+ * combine, sigmoid output gate); this build's order: fixed 64-key splits, scores as four fmaf
+ * chains over the head dims (score_4chain), per split m = max, p = 2^(x - m), l = shfl_down tree
+ * over the split's 64 lanes, o = four fmaf chains over the split's 16-key blocks in ascending key
+ * order, summed ((o0 + o1) + o2) + o3; splits combined in ascending order. */
 void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride,
                     const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
                     int kv_group, int nq, int nkv, int hd, int gate, int pos0, int nr,
@@ -763,20 +770,24 @@ void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride
                 for (int k = k0; k < k1; ++k) {
                     const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
                     for (int i = 0; i < hd; ++i) kd[i] = (float)kc[off + i] * ks[(off + i) / kv_group];
-                    const float x = score_seq(q, kd, hd) * sl2e;
+                    const float x = score_4chain(q, kd, hd) * sl2e;
                     xsc[k - k0] = x;
                     m = fmaxf(m, x);
                 }
                 /* l: the 64 keys' p (0 past the valid ones) summed by the shfl_down tree */
                 float pl[Q27O_SPLIT];
                 for (int i = 0; i < Q27O_SPLIT; ++i) pl[i] = 0.0f;
-                for (int i = 0; i < hd; ++i) os[i] = 0.0f;
+                float oc[4][256];
+                for (int j = 0; j < 4; ++j)
+                    for (int i = 0; i < hd; ++i) oc[j][i] = 0.0f;
                 for (int k = k0; k < k1; ++k) {
                     const float p = q27o_exp2(xsc[k - k0] - m);
                     pl[k - k0] = p;
                     const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
-                    for (int i = 0; i < hd; ++i) os[i] = fmaf(p, (float)vc[off + i] * vs[(off + i) / kv_group], os[i]);
+                    float* oj = oc[(k - k0) / (Q27O_SPLIT / 4)];
+                    for (int i = 0; i < hd; ++i) oj[i] = fmaf(p, (float)vc[off + i] * vs[(off + i) / kv_group], oj[i]);
                 }
+                for (int i = 0; i < hd; ++i) os[i] = ((oc[0][i] + oc[1][i]) + oc[2][i]) + oc[3][i];
                 const float l = tree64(pl);
                 ms[s] = m; ls[s] = l;
                 memcpy(ob + (size_t)s * hd, os, (size_t)hd * sizeof(float));

@@ -284,8 +284,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
         __syncthreads();
         // ---- scores on the matrix cores: query tile qt (16 queries) x key tile kt (16 keys) per
         // wave, v_mfma_f32_16x16x4f32 over the head dims in order. Each instruction adds its four
-        // products one after another with fused multiply-adds (k = 0..3), so the chain of 32
-        // instructions is exactly the oracle's fmaf loop over dims 0..127.
+        // products one after another with fused multiply-adds (k = 0..3), so a chain of 8
+        // instructions is exactly an fmaf loop over 32 dims; four such chains (dims 32c..32c+31)
+        // run side by side and are summed ((c0 + c1) + c2) + c3, the oracle's score order.
         // Operand lanes: lane 16 g + j gives A[j][g] = q(16 qt + j)[4 s + g] and
         // B[g][j] = k(16 kt + j)[4 s + g]; result r of lane 16 g + j is score(query 4 g + r, key j).
         constexpr int QT = (8 * NQW + 15) / 16;   // query tiles of the kernel's capacity
@@ -295,43 +296,61 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             const int qa = (16 * qt + j16 < nqr) ? 16 * qt + j16 : 0;     // rows past nqr: discarded
             const float* qrow = qf + (size_t)qa * kQStride + g4;
             const float* krow = kd + (size_t)(16 * kt + j16) * kKStride + g4;
-            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-            for (int st4 = 0; st4 < kHD / 4; ++st4)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[4 * st4], krow[4 * st4], acc, 0, 0, 0);
+            v4f c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0, c3 = c0;
+#pragma unroll
+            for (int st4 = 0; st4 < kHD / 16; ++st4) {
+                c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[4 * st4], krow[4 * st4], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[32 + 4 * st4], krow[32 + 4 * st4], c1, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[64 + 4 * st4], krow[64 + 4 * st4], c2, 0, 0, 0);
+                c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(qrow[96 + 4 * st4], krow[96 + 4 * st4], c3, 0, 0, 0);
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int qi = 16 * qt + 4 * g4 + r;
-                if (qi < nqr) sp[qi * kSpStride + 16 * kt + j16] = acc[r];
+                if (qi < nqr) sp[qi * kSpStride + 16 * kt + j16] = ((c0[r] + c1[r]) + c2[r]) + c3[r];
             }
         }
         __syncthreads();
         // ---- split softmax: lane = key, this wave's queries wv + 8 i (p replaces the score)
+        // (every one of the wave's NQW queries is computed, on a clamped row past nqr, and only
+        // the real ones are stored: no exit inside the loop, so the independent reductions run
+        // side by side)
+        {
+            float pv[NQW], mv[NQW];
 #pragma unroll
-        for (int i = 0; i < NQW; ++i) {
-            const int qi = wv + 8 * i;
-            if (qi >= nqr) break;                 // wave-uniform
-            const int k = lane;
-            const int r = qi / G, g = qi - r * G;
-            const int L = pos0 + r + 1;
-            const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
-            const bool valid = k < nv;
-            const float x = sp[qi * kSpStride + k] * a.sl2e;
-            float m = valid ? x : -__builtin_huge_valf();
-            m = max_xor(m, 64);
-            const float p = valid ? qexp2(x - m) : 0.0f;
-            sp[qi * kSpStride + k] = p;
-            const float l = tree64(p);
-            if (lane == 0 && nv > 0) {
-                const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
-                wm[mi] = m;
-                wl[mi] = l;
+            for (int i = 0; i < NQW; ++i) {
+                const int qi = wv + 8 * i, qc = qi < nqr ? qi : nqr - 1;
+                const int r = qc / G;
+                const int L = pos0 + r + 1;
+                const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
+                const bool valid = lane < nv;
+                const float x = sp[qc * kSpStride + lane] * a.sl2e;
+                float m = valid ? x : -__builtin_huge_valf();
+                m = max_xor(m, 64);
+                pv[i] = valid ? qexp2(x - m) : 0.0f;
+                mv[i] = m;
+            }
+#pragma unroll
+            for (int i = 0; i < NQW; ++i) {
+                const int qi = wv + 8 * i;
+                const float l = tree64(pv[i]);
+                if (qi < nqr) {
+                    sp[qi * kSpStride + lane] = pv[i];
+                    const int r = qi / G, g = qi - r * G;
+                    const int L = pos0 + r + 1;
+                    if (lane == 0 && L - k0 > 0) {
+                        const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
+                        wm[mi] = mv[i];
+                        wl[mi] = l;
+                    }
+                }
             }
         }
         __syncthreads();
-        // ---- o = sum_k p_k v_k in key order, on the matrix cores: query tile qt x dim tile dt
-        // per wave, 16 instructions over keys 0..63 in order (p = 0 for the keys a row does not
-        // see, whose V rows are finite: fma(0, v, o) leaves o unchanged).
+        // ---- o = sum_k p_k v_k on the matrix cores: query tile qt x dim tile dt per wave; four
+        // chains of 4 instructions over the 16-key blocks of the split in key order, summed
+        // ((o0 + o1) + o2) + o3 (p = 0 for the keys a row does not see, whose V rows are finite:
+        // fma(0, v, o) leaves o unchanged).
         // A[j][g] = p(16 qt + j)[4 s + g], B[g][j] = v[4 s + g][16 dt + j]; result r of lane
         // 16 g + j is o(query 16 qt + 4 g + r)[16 dt + j].
         for (int ti = wv; ti < 8 * QT; ti += kAttnThreads / 64) {
@@ -339,10 +358,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             const int qa = (16 * qt + j16 < nqr) ? 16 * qt + j16 : 0;
             const float* prow = sp + (size_t)qa * kSpStride + g4;
             const float* vcol = vd + (size_t)g4 * kVStride + 16 * dt + j16;
-            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = o0, o2 = o0, o3 = o0;
 #pragma unroll
-            for (int st4 = 0; st4 < kSplit / 4; ++st4)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[4 * st4], vcol[4 * st4 * kVStride], acc, 0, 0, 0);
+            for (int st4 = 0; st4 < kSplit / 16; ++st4) {
+                o0 = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[4 * st4], vcol[4 * st4 * kVStride], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[16 + 4 * st4], vcol[(16 + 4 * st4) * kVStride], o1, 0, 0, 0);
+                o2 = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[32 + 4 * st4], vcol[(32 + 4 * st4) * kVStride], o2, 0, 0, 0);
+                o3 = __builtin_amdgcn_mfma_f32_16x16x4f32(prow[48 + 4 * st4], vcol[(48 + 4 * st4) * kVStride], o3, 0, 0, 0);
+            }
+            v4f acc;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = ((o0[r] + o1[r]) + o2[r]) + o3[r];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int qi = 16 * qt + 4 * g4 + r;
