@@ -163,8 +163,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     bool staged_q = false;
     // the int8 K/V words of split s (thread: 16-byte words t and t + 512; K words 0..511, V
     // 512..1023) and their scales; the step's new positions (PREP) are computed, not read
+    // (every thread loads its two words unconditionally, keys past the cached ones from key 0 of
+    // the split, and the dequantization below zeroes them; the load addresses stay live until
+    // then, so the matrix-core work in between never reuses their registers, which would make it
+    // wait for the prefetch)
     uint4 kv4[2];
     float scl[2];
+    const int8_t* lp[2];
+    const float* lsp[2];
     auto load_tile = [&](int s) __attribute__((always_inline)) {
         const int k0 = s * kSplit;
         const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
@@ -172,13 +178,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
-            kv4[u] = make_uint4(0u, 0u, 0u, 0u);
-            scl[u] = 0.0f;
-            if (k < kn0) {
-                const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * kHD + 16 * c;
-                kv4[u] = *(const uint4*)((isv ? a.vc : a.kc) + off);
-                scl[u] = (isv ? a.vs : a.ks)[off >> gsh];
-            }
+            const size_t off = (size_t)(k0 + (k < kn0 ? k : 0)) * kvrows + (size_t)kvh * kHD + 16 * c;
+            lp[u] = (isv ? a.vc : a.kc) + off;
+            lsp[u] = (isv ? a.vs : a.ks) + (off >> gsh);
+            kv4[u] = *(const uint4*)lp[u];
+            scl[u] = *lsp[u];
         }
     };
     if (blockIdx.x * kSplit < Lmax) load_tile(blockIdx.x);
@@ -222,6 +226,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                     qf[qi * kQStride + 64 + lane] = bfr(qy[i][1]);
                 }
             }
+            __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0): as at the end of new_keys below
         }
         // new positions of this split (in whichever of the block's splits holds them): one wave
         // per key. In the block's first split this runs before the barrier below (nothing to
@@ -244,14 +249,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 vd[k * kVStride + lane] = deq[2];
                 vd[k * kVStride + 64 + lane] = deq[3];
             }
+            // the cache stores retire here: left in flight, their data registers would be
+            // protected at the next register reuse (the score tiles) by a wait for every vector
+            // memory operation, the tile prefetch included, in every split
+            __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
         };
         if (PREP && !staged_q && kn0 < nk) new_keys();
         __syncthreads();                           // the previous split's tiles are consumed
         if (PREP && staged_q && kn0 < nk) new_keys();
+        asm volatile("" :: "v"(lp[0]), "v"(lp[1]), "v"(lsp[0]), "v"(lsp[1]));
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = t + kAttnThreads * u, isv = i >> 9, j = i & 511, k = j >> 3, c = j & 7;
             if (k >= kn0 && k < nk) continue;      // a new position (PREP)
+            if (k >= kn0) { kv4[u] = make_uint4(0u, 0u, 0u, 0u); scl[u] = 0.0f; }   // past the split's keys
             const uint32_t w4[4] = {kv4[u].x, kv4[u].y, kv4[u].z, kv4[u].w};
             float* dst = isv ? &vd[k * kVStride + 16 * c] : &kd[k * kKStride + 16 * c];
 #pragma unroll
