@@ -116,48 +116,85 @@ int launch_pf_conv(const uint16_t* buf, int ld, int C, int nconv, const uint16_t
 // decode path's order: 8-element chunk c on lane c % 64 in ascending c, fmaf per element, the
 // shfl tree, bf16 rounding; k_bf16_gemv2_tile, src/q27_util.hip:114-167), then
 // decay = exp(-exp(A_log) softplus(a + dt_bias)) and beta = sigmoid(b) (src/q27_gdn.hip:206-372)
-// into out [2][C][vh]. One wave per (weight row, row); block = 4 weight rows of one row.
-__global__ __launch_bounds__(256) void k_pf_ab(const uint16_t* __restrict__ in_a, const uint16_t* __restrict__ in_b,
-                                               const uint16_t* __restrict__ A_log,
-                                               const uint16_t* __restrict__ dt_bias, const uint16_t* __restrict__ y,
-                                               int ystride, int K, int vh, int C, float* __restrict__ out) {
-    const int tok = blockIdx.x, lane = threadIdx.x & 63;
-    const int j = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (j >= 2 * vh) return;
-    const int which = j / vh, head = j - which * vh;
-    const uint16_t* wrow = (which ? in_b : in_a) + (size_t)head * K;
-    const uint16_t* yr = y + (size_t)tok * ystride;
+// into out [2][C][vh]. A block stages kAbTok rows y in LDS; each wave holds one weight row's
+// chunks in registers (lane l: chunks l, l + 64, ...) and runs it against every staged row.
+constexpr int kAbTok = 8;            // rows per block
+constexpr int kAbChunks = 10;        // weight chunks per lane at most (K <= 5120)
+// KC: chunks per lane (every lane runs KC of them; chunks past K / 8 have zero weights, and
+// fma(0, x, acc) = acc for the finite normed rows, so they change nothing)
+template <int KC>
+__global__ __launch_bounds__(1024) void k_pf_ab(const uint16_t* __restrict__ in_a, const uint16_t* __restrict__ in_b,
+                                                const uint16_t* __restrict__ A_log,
+                                                const uint16_t* __restrict__ dt_bias, const uint16_t* __restrict__ y,
+                                                int ystride, int K, int vh, int C, float* __restrict__ out) {
+    extern __shared__ uint4 sy[];                 // [kAbTok][K / 8] chunks
+    const int t0 = blockIdx.x * kAbTok, nt = (C - t0 < kAbTok) ? C - t0 : kAbTok;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nch = K >> 3;
-    float acc = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-        const uint4 w = *(const uint4*)(wrow + 8 * c);
-        const uint4 x = *(const uint4*)(yr + 8 * c);
-        acc = __builtin_fmaf(__uint_as_float(w.x << 16), __uint_as_float(x.x << 16), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(x.x & 0xFFFF0000u), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.y << 16), __uint_as_float(x.y << 16), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), __uint_as_float(x.y & 0xFFFF0000u), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.z << 16), __uint_as_float(x.z << 16), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), __uint_as_float(x.z & 0xFFFF0000u), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.w << 16), __uint_as_float(x.w << 16), acc);
-        acc = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), __uint_as_float(x.w & 0xFFFF0000u), acc);
+    for (int i = threadIdx.x; i < nt * nch; i += 1024) {
+        const int n = i / nch, c = i - n * nch;
+        sy[i] = *(const uint4*)(y + (size_t)(t0 + n) * ystride + 8 * c);
     }
-    const float v = bfr(bcast0(tree64(acc)));
-    if (lane == 0) {
-        float r;
-        if (which) r = qsigmoid(v);
-        else r = qexp(-(qexp(bf2f(A_log[head])) * qsoftplus(v + bf2f(dt_bias[head]))));
-        out[((size_t)which * C + tok) * vh + head] = r;
+    __syncthreads();
+    for (int j = wv; j < 2 * vh; j += 16) {
+        const int which = j / vh, head = j - which * vh;
+        const uint16_t* wrow = (which ? in_b : in_a) + (size_t)head * K;
+        uint4 w[KC];
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            const int c = lane + 64 * i;
+            w[i] = *(const uint4*)(wrow + 8 * (c < nch ? c : 0));
+            if (c >= nch) w[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        const float Aexp = which ? 0.0f : qexp(bf2f(A_log[head]));
+        const float dtb = which ? 0.0f : bf2f(dt_bias[head]);
+        for (int n = 0; n < nt; ++n) {
+            const uint4* yr = sy + (size_t)n * nch;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KC; ++i) {
+                const int c = lane + 64 * i;
+                const uint4 x = yr[c < nch ? c : 0];
+                acc = __builtin_fmaf(__uint_as_float(w[i].x << 16), __uint_as_float(x.x << 16), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].x & 0xFFFF0000u), __uint_as_float(x.x & 0xFFFF0000u), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].y << 16), __uint_as_float(x.y << 16), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].y & 0xFFFF0000u), __uint_as_float(x.y & 0xFFFF0000u), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].z << 16), __uint_as_float(x.z << 16), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].z & 0xFFFF0000u), __uint_as_float(x.z & 0xFFFF0000u), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].w << 16), __uint_as_float(x.w << 16), acc);
+                acc = __builtin_fmaf(__uint_as_float(w[i].w & 0xFFFF0000u), __uint_as_float(x.w & 0xFFFF0000u), acc);
+            }
+            const float v = bfr(bcast0(tree64(acc)));
+            if (lane == 0) {
+                const float r = which ? qsigmoid(v) : qexp(-(Aexp * qsoftplus(v + dtb)));
+                out[((size_t)which * C + t0 + n) * vh + head] = r;
+            }
+        }
     }
 }
 int launch_pf_ab(const uint16_t* in_a, const uint16_t* in_b, const uint16_t* A_log, const uint16_t* dt_bias,
                  const uint16_t* y, int ystride, int K, int vh, int C, float* out, hipStream_t s) {
-    if (!in_a || !in_b || !A_log || !dt_bias || !y || !out || (K & 7) || K < 8 || vh < 1 || C < 1 || (ystride & 7) ||
-        ((uintptr_t)y & 15) || ((uintptr_t)in_a & 15) || ((uintptr_t)in_b & 15)) {
+    if (!in_a || !in_b || !A_log || !dt_bias || !y || !out || (K & 7) || K < 8 || K > 8 * 64 * kAbChunks || vh < 1 ||
+        C < 1 || (ystride & 7) || ((uintptr_t)y & 15) || ((uintptr_t)in_a & 15) || ((uintptr_t)in_b & 15)) {
         set_error("prefill a/b: bad arguments");
         return Q27X_E_ARG;
     }
-    hipLaunchKernelGGL(k_pf_ab, dim3((unsigned)C, (unsigned)((2 * vh + 3) / 4)), dim3(256), 0, s, in_a, in_b, A_log,
-                       dt_bias, y, ystride, K, vh, C, out);
+    const size_t lds = (size_t)kAbTok * (K / 8) * 16;
+    static bool lds_set = false;
+    const int mx = kAbTok * 64 * kAbChunks * 16;
+    if (!lds_set) {
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_pf_ab<2>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_pf_ab<4>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_pf_ab<8>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_pf_ab<10>, hipFuncAttributeMaxDynamicSharedMemorySize, mx));
+        lds_set = true;
+    }
+    const int kc = (K / 8 + 63) / 64;
+    const dim3 grid((unsigned)((C + kAbTok - 1) / kAbTok));
+    if (kc <= 2) hipLaunchKernelGGL(k_pf_ab<2>, grid, dim3(1024), lds, s, in_a, in_b, A_log, dt_bias, y, ystride, K, vh, C, out);
+    else if (kc <= 4) hipLaunchKernelGGL(k_pf_ab<4>, grid, dim3(1024), lds, s, in_a, in_b, A_log, dt_bias, y, ystride, K, vh, C, out);
+    else if (kc <= 8) hipLaunchKernelGGL(k_pf_ab<8>, grid, dim3(1024), lds, s, in_a, in_b, A_log, dt_bias, y, ystride, K, vh, C, out);
+    else hipLaunchKernelGGL(k_pf_ab<10>, grid, dim3(1024), lds, s, in_a, in_b, A_log, dt_bias, y, ystride, K, vh, C, out);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
