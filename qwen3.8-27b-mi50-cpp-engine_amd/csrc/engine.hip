@@ -98,14 +98,14 @@ struct PfBuf {
     float* x = nullptr;          // [cap][H] fp32 residual
     uint16_t* h = nullptr;       // [cap][H] bf16 residual copy (the next add's residual)
     uint16_t* y = nullptr;       // [cap][H] bf16 normed rows (GDN a/b)
-    float* yf = nullptr;         // [cap][H] normed values to quantize
+    float* yf = nullptr;         // [cap][H] normed values to quantize; the GDN scan's q^|k^ ([cap][kh][256])
     int8_t* xq = nullptr; float* xs = nullptr;     // [cap][kmax] codes, [cap][32] group scales
     int8_t* xq2 = nullptr; float* xs2 = nullptr;   // [cap][H], [cap][32]: the MTP pass's second fc input
     uint16_t* pb = nullptr;      // [cap][wmax] projection rows
     uint16_t* qh = nullptr;      // [cap][att] normed, roped queries
     float* gu = nullptr;         // [cap][max(2I, nz)] gate|up GEMM output (GDN scan's mixed rows before)
     uint16_t* mix = nullptr;     // [cap][max(nz, att)] mixer output
-    float* rowsc = nullptr;      // [2][cap][vh] GDN decay, beta
+    float* rowsc = nullptr;      // [3][cap][vh] GDN decay, beta; the scan's k^.q^ ([cap][kh])
     float* work = nullptr;       // attention split partials of kPfAttnRows rows
     uint16_t* cv = nullptr;      // [cap][nqkv] convolved q|k|v rows
     std::vector<void*> allocs;
@@ -1320,11 +1320,11 @@ static int pf_alloc(q27x_ctx* x, int cap) {
     const size_t ms = (size_t)x->max_splits;
     int rc = 0;
     if ((rc = A((void**)&B->x, C * H * 4)) || (rc = A((void**)&B->h, C * H * 2)) || (rc = A((void**)&B->y, C * H * 2)) ||
-        (rc = A((void**)&B->yf, C * H * 4)) || (rc = A((void**)&B->xq, C * kmax)) || (rc = A((void**)&B->xs, C * 32 * 4)) ||
+        (rc = A((void**)&B->yf, C * std::max(H, 2 * c.gdn_kh * x->D) * 4)) || (rc = A((void**)&B->xq, C * kmax)) || (rc = A((void**)&B->xs, C * 32 * 4)) ||
         (rc = A((void**)&B->xq2, C * H)) || (rc = A((void**)&B->xs2, C * 32 * 4)) ||
         (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
         (rc = A((void**)&B->gu, C * std::max(2 * I, x->nz) * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
-        (rc = A((void**)&B->rowsc, 2 * C * c.gdn_vh * 4)) ||
+        (rc = A((void**)&B->rowsc, 3 * C * c.gdn_vh * 4)) ||
         (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4)) ||
         (rc = A((void**)&B->cv, C * x->nqkv * 2))) {
         for (void* p : B->allocs) (void)hipFree(p);
@@ -1433,7 +1433,9 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         g.rowsc = B.rowsc; g.norm_w = Y.gdn_norm; g.S = Y.S;
         g.kh = c.gdn_kh; g.vh = c.gdn_vh; g.d = x->D; g.eps = c.rms_eps;
         g.out = B.mix; g.out_stride = x->nz; g.stop = &d->stop;
-        if ((rc = launch_gdn_scan(g, C, B.gu, s))) return rc;      // gate|up output is free until the MLP
+        // scratch: yf (free after the in_qkv|in_z GEMM's quantizer) for q^|k^, the third rowsc
+        // slab for k^.q^, the gate|up output (free until the MLP) for the mixed rows
+        if ((rc = launch_gdn_scan(g, C, B.yf, B.rowsc + (size_t)2 * B.cap * c.gdn_vh, B.gu, s))) return rc;
         if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.out_proj, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     }

@@ -266,6 +266,33 @@ __global__ __launch_bounds__(kNT) void k_gdn(GdnArgs a, int nr) {
 // last and is written back once. Each row's mixed values go to `mix` [nrows][vh*128] fp32;
 // k_gdn_gnorm applies the gated RMSNorm afterwards (it needs the head's 128 columns, which live in
 // several blocks). Row scalars: decay at rowsc[n vh + h], beta at rowsc[(nrows + n) vh + h].
+// q/k norms of the scan's rows, outside the scan (they do not depend on the state): one wave per
+// (row, key head), k_gdn's arithmetic (two 64-lane trees per sum, first half + second half).
+// qk [nrows][kh][256]: q^ (128) then k^ (128); kq [nrows][kh]: k^.q^.
+__global__ __launch_bounds__(256) void k_gdn_qknorm(const uint16_t* __restrict__ qkv, int qkv_stride, int kh,
+                                                    int nrows, float* __restrict__ qk, float* __restrict__ kq) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);     // (row, key head) pair
+    if (u >= nrows * kh) return;
+    const int row = u / kh, kk = u - row * kh;
+    const uint16_t* src = qkv + (size_t)row * qkv_stride;
+    const int KD = kh * kD;
+    const float q0 = bf2f(src[kk * kD + lane]), q1 = bf2f(src[kk * kD + 64 + lane]);
+    const float k0 = bf2f(src[KD + kk * kD + lane]), k1 = bf2f(src[KD + kk * kD + 64 + lane]);
+    const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
+    const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
+    const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
+    const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
+    const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
+    const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
+    const float invk = rsqrt_cr(ssk + 1e-6f);
+    float* d = qk + (size_t)u * 2 * kD;
+    d[lane] = q0 * invq;
+    d[64 + lane] = q1 * invq;
+    d[kD + lane] = k0 * invk;
+    d[kD + 64 + lane] = k1 * invk;
+    if (lane == 0) kq[u] = ((sx0 + sx1) * invq) * invk;
+}
 #ifndef Q27X_SCAN_WPB
 #define Q27X_SCAN_WPB 4
 #endif
@@ -290,7 +317,9 @@ __device__ __forceinline__ float from_group0(float s) {
     return (g >= 2) ? w : u;
 }
 template <int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, float* __restrict__ mix, int nrows) {
+__global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, const float* __restrict__ qk,
+                                                      const float* __restrict__ kqv, float* __restrict__ mix,
+                                                      int nrows) {
     constexpr int NT = 64 * WPB, NC = 16 * WPB;          // threads, value columns of the block
     constexpr int R = 8 * WPB;                           // rows staged per batch
     constexpr int CPT = 2 * kD / NT;                     // q|k channels loaded per thread
@@ -302,7 +331,6 @@ __global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, float* __restr
     const int ratio = a.vh / a.kh, kk = h / ratio;
     const int KD = a.kh * kD;
     const size_t mstride = (size_t)a.vh * kD;
-    __shared__ float scv[R][2 * kD];             // raw q | k of the key head (bf16 values)
     __shared__ float sv[R][NC];                  // v of the block's columns
     __shared__ __attribute__((aligned(16))) float sq[R][kD];
     __shared__ __attribute__((aligned(16))) float sk[R][kD];
@@ -312,61 +340,45 @@ __global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, float* __restr
     float st[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) st[j] = Sp[(size_t)j * kD];
-    // thread t loads q|k channels t + NT i (< 128: q, else k) and v column NC part + t % NC
-    size_t chq[CPT];
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        const int c = t + NT * i;
-        chq[i] = (c < kD) ? (size_t)kk * kD + c : (size_t)KD + kk * kD + (c - kD);
-    }
+    // thread t loads the normed q^|k^ values t + NT i of the key head (< 128: q^, else k^) and v
+    // column NC part + t % NC
     const size_t chv = (size_t)2 * KD + (size_t)h * kD + NC * part + (t % NC);
-    uint16_t xr[R][CPT], xv[R];
-    float r_a = 0.0f, r_b = 0.0f;
+    float xr[R][CPT];
+    uint16_t xv[R];
+    float r_a = 0.0f, r_b = 0.0f, r_kq = 0.0f;
     // unconditional loads (rows past the last repeat it; every thread loads a v column): a load
     // under a condition is followed by its own wait, which would serialise the batch's loads
     auto load = [&](int r0) {
 #pragma unroll
         for (int n = 0; n < R; ++n) {
-            const size_t row = (size_t)((r0 + n < nrows) ? r0 + n : nrows - 1) * a.qkv_stride;
+            const int rn = (r0 + n < nrows) ? r0 + n : nrows - 1;
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) xr[n][i] = a.qkv[row + chq[i]];
-            xv[n] = a.qkv[row + chv];
+            for (int i = 0; i < CPT; ++i) xr[n][i] = qk[((size_t)rn * a.kh + kk) * 2 * kD + t + NT * i];
+            xv[n] = a.qkv[(size_t)rn * a.qkv_stride + chv];
         }
         const int rt = (r0 + (t % R) < nrows) ? r0 + (t % R) : nrows - 1;
         r_a = a.rowsc[(size_t)rt * a.vh + h];
         r_b = a.rowsc[(size_t)(nrows + rt) * a.vh + h];
+        r_kq = kqv[(size_t)rt * a.kh + kk];
     };
     load(0);
     for (int r0 = 0; r0 < nrows; r0 += R) {
         const int nr = (nrows - r0 < R) ? nrows - r0 : R;
         __syncthreads();                            // the previous batch is written out
-        if (t < nr) { srow[t][1] = r_b; srow[t][2] = r_a; }
+        if (t < nr) { srow[t][0] = r_kq; srow[t][1] = r_b; srow[t][2] = r_a; }
         // every staged row is written (rows past nr hold copies of the last row and are not read):
         // an exit at nr would index the register arrays dynamically (a select chain per element)
 #pragma unroll
         for (int n = 0; n < R; ++n) {
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) scv[n][t + NT * i] = bf2f(xr[n][i]);
+            for (int i = 0; i < CPT; ++i) {
+                const int c = t + NT * i;
+                if (c < kD) sq[n][c] = xr[n][i];
+                else sk[n][c - kD] = xr[n][i];
+            }
             if (t < NC) sv[n][t] = bf2f(xv[n]);
         }
         if (r0 + R < nrows) load(r0 + R);            // next batch in flight during this one
-        __syncthreads();
-        for (int n = wv; n < nr; n += WPB) {        // q/k norms (k_gdn's arithmetic)
-            const float q0 = scv[n][lane], q1 = scv[n][64 + lane];
-            const float k0 = scv[n][kD + lane], k1 = scv[n][kD + 64 + lane];
-            const float sq0 = tree64(q0 * q0), sq1 = tree64(q1 * q1);
-            const float sk0 = tree64(k0 * k0), sk1 = tree64(k1 * k1);
-            const float sx0 = tree64(q0 * k0), sx1 = tree64(q1 * k1);
-            const float ssq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq0 + sq1)));
-            const float ssk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sk0 + sk1)));
-            const float invq = rsqrt_cr(ssq + 1e-6f) * 0.0883883476f;
-            const float invk = rsqrt_cr(ssk + 1e-6f);
-            sq[n][lane] = q0 * invq;
-            sq[n][64 + lane] = q1 * invq;
-            sk[n][lane] = k0 * invk;
-            sk[n][64 + lane] = k1 * invk;
-            if (lane == 0) srow[n][0] = ((sx0 + sx1) * invq) * invk;
-        }
         __syncthreads();
         // rows in pairs: everything a row reads from LDS is requested while the row before it
         // computes (a row's own reads would make every wait cover the prefetch behind them)
@@ -432,14 +444,17 @@ __global__ __launch_bounds__(kD) void k_gdn_gnorm(const float* __restrict__ mix,
     const float inv = rsqrt_cr((red[0] + red[1]) * (1.0f / (float)kD) + eps);
     out[(size_t)row * out_stride + (size_t)h * kD + t] = f2bf(mx * inv * nw * qsilu(zz));
 }
-int launch_gdn_scan(const GdnArgs& a, int nrows, float* mix, hipStream_t s) {
+int launch_gdn_scan(const GdnArgs& a, int nrows, float* qk, float* kq, float* mix, hipStream_t s) {
     if (a.d != kD || a.kh < 1 || a.vh % a.kh || nrows < 1 || !a.qkv || !a.z || !a.S || !a.rowsc || !a.out ||
-        !a.norm_w || !mix || nrows > 65535) {
+        !a.norm_w || !mix || !qk || !kq || nrows > 65535) {
         set_error("gdn scan: unsupported shape or null argument (d=%d kh=%d vh=%d rows=%d)", a.d, a.kh, a.vh, nrows);
         return Q27X_E_SHAPE;
     }
-    hipLaunchKernelGGL(k_gdn_scan<kScanWPB>, dim3(a.vh * (kD / (16 * kScanWPB))), dim3(64 * kScanWPB), 0, s, a, mix,
-                       nrows);
+    hipLaunchKernelGGL(k_gdn_qknorm, dim3((unsigned)((nrows * a.kh + 3) / 4)), dim3(256), 0, s, a.qkv, a.qkv_stride,
+                       a.kh, nrows, qk, kq);
+    Q27X_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_gdn_scan<kScanWPB>, dim3(a.vh * (kD / (16 * kScanWPB))), dim3(64 * kScanWPB), 0, s, a,
+                       (const float*)qk, (const float*)kq, mix, nrows);
     Q27X_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.vh, nrows), dim3(kD), 0, s, (const float*)mix, a.z, a.z_stride, a.norm_w,
                        a.eps, a.vh, a.out, a.out_stride);

@@ -120,8 +120,9 @@ struct GdnArgs {
 };
 int launch_gdn(const GdnArgs& a, int nr, hipStream_t s);
 // prefill: nrows rows (any count) with the row scalars prepared in rowsc [2][nrows][vh], the state
-// committed through the last row, bf16 output only; mix: [nrows][vh*128] fp32 scratch
-int launch_gdn_scan(const GdnArgs& a, int nrows, float* mix, hipStream_t s);
+// committed through the last row, bf16 output only; scratch: qk [nrows][kh][256] and kq
+// [nrows][kh] (the rows' normed q^|k^ and k^.q^), mix [nrows][vh*128], all fp32
+int launch_gdn_scan(const GdnArgs& a, int nrows, float* qk, float* kq, float* mix, hipStream_t s);
 int gdn_set_lds_limit();
 // conv + SiLU with deferred commit as a standalone kernel (kernel-tier entry)
 int launch_gdn_conv(const uint16_t* raw, int raw_stride, uint16_t* out, int out_stride,
