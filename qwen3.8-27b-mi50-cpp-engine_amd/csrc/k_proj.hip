@@ -91,14 +91,16 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
     static_assert(EPI != EPI_SWIGLU || RPW == 1, "SwiGLU deals single rows");
     static_assert(!PRE || NW == 16, "the norm prologue runs on 16-wave blocks");
-    // XR: the activation scales live in registers (each lane holds the scales of its own slabs),
-    // only the codes in LDS -- the K = 17408 stage of more than 4 rows (NR x 1088 slabs x 20 B)
-    // would not fit in 160 KB with its scales
+    // XR: the K = 17408 stage of more than 4 rows (NR x 1088 slabs x 20 B) does not fit in 160 KB
+    // with all its scales: rows 0..3 keep their scales in LDS, the rows after them in registers
+    // (each lane holds the scales of its own slabs). With every row's scales in registers the
+    // kernel ran out of them and waited for each LDS code read on its own.
     constexpr bool XR = (NSTEP >= 17 && NR > 4);
+    constexpr int XL = XR ? 4 : NR;                    // rows whose scales are staged in LDS
     static_assert(!XR || (!PRE && FULL && EPI == EPI_STORE), "register scales: plain full-K stage only");
     __shared__ uint4 sx[NR * SL];
-    __shared__ float ssc[XR ? 1 : NR * SL];
-    float XS[XR ? NR : 1][XR ? NSTEP : 1];
+    __shared__ float ssc[XL * SL];
+    float XS[XR ? NR - XL : 1][XR ? NSTEP : 1];
     __shared__ float sacc[(EPI == EPI_SWIGLU) ? kSwRows * NR : 1];
     __shared__ float wsum[PRE ? PreNorm<NSTEP, NR>::RPG : 1][4][4];
     // EPI_CONV: the bf16 normalized input rows of the blocks that compute GDN row scalars
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
                 const int n = i / SL, s = i - n * SL;
                 __builtin_amdgcn_global_load_lds((const void*)(a.xq + (size_t)n * a.xst + 16 * s),
                                                  (__attribute__((address_space(3))) void*)&sx[i0], 16, 0, 0);
-                if constexpr (!XR)
+                if (i0 / SL < XL)                       // (the wave's row: SL is a multiple of 64)
                     __builtin_amdgcn_global_load_lds((const void*)(a.xs + (size_t)n * (a.xst >> 4) + s),
                                                      (__attribute__((address_space(3))) void*)&ssc[i0], 4, 0, 0);
             }
@@ -206,9 +208,9 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             // (after the DMA requests and before the prefetch: the barrier's wait below counts the
             // prefetch as the only loads still owed)
 #pragma unroll
-            for (int n = 0; n < NR; ++n)
+            for (int n = XL; n < NR; ++n)
 #pragma unroll
-                for (int t = 0; t < NSTEP; ++t) XS[n][t] = a.xs[(size_t)n * (a.xst >> 4) + t * 64 + lane];
+                for (int t = 0; t < NSTEP; ++t) XS[n - XL][t] = a.xs[(size_t)n * (a.xst >> 4) + t * 64 + lane];
         }
         prefetch();
         if (stopped(a.stop)) return;
@@ -482,12 +484,24 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
 #pragma unroll
         for (int t = 0; t < NSTEP; ++t) {
             const int s = t * 64 + lane;
+            // XR: the step's code reads are requested together ahead of its arithmetic (left to
+            // itself at this register pressure the compiler waits for each read before the next)
+            uint4 xb[XR ? NR : 1];
+            float sb[XR ? XL : 1];
+            if constexpr (XR) {
+#pragma unroll
+                for (int n = 0; n < NR; ++n) {
+                    xb[n] = sx[n * SL + s];
+                    if (n < XL) sb[n < XL ? n : 0] = ssc[n * SL + s];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int n = 0; n < NR; ++n) {
-                const uint4 xa = sx[n * SL + s];
+                const uint4 xa = XR ? xb[XR ? n : 0] : sx[n * SL + s];
                 float sa;
-                if constexpr (XR) sa = XS[n][t];
-                else sa = ssc[n * SL + s];
+                if (n >= XL) sa = XS[n >= XL ? n - XL : 0][t];
+                else sa = XR ? sb[XR && n < XL ? n : 0] : ssc[n * SL + s];
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
                     const int d = dot16(W[r][t], xa);
@@ -560,7 +574,7 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
         const int ngroups = (a.rows + RPW - 1) / RPW;
         int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
         // no more waves per CU than the blocks whose LDS stages fit (160 KB per CU)
-        constexpr int kStage = NR * NSTEP * 64 * ((NSTEP >= 17 && NR > 4) ? 16 : 20);
+        constexpr int kStage = NR * NSTEP * 64 * 16 + ((NSTEP >= 17 && NR > 4) ? 4 : NR) * NSTEP * 64 * 4;
         constexpr int kBpc = (160 * 1024) / kStage > 0 ? (160 * 1024) / kStage : 1;
         if (wpc > kBpc * NW) wpc = kBpc * NW;
         const int wmax = num_cus() * wpc;

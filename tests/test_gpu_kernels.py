@@ -112,8 +112,8 @@ def test_proj_config0(gpu, O, nr):
     same("bf16 projection + bf16 residual", dy.download(np.uint16, (nr, rows)), yb_o)
 
 
-@pytest.mark.parametrize("rows,K,nr", [(5120, 6144, 3), (5120, 17408, 3), (5120, 17408, 8), (10240, 5120, 8),
-                                       (5120, 4096, 2), (1000, 1024, 5)])
+@pytest.mark.parametrize("rows,K,nr", [(5120, 6144, 3), (5120, 17408, 3), (5120, 17408, 8), (5120, 17408, 5),
+                                       (1000, 17408, 7), (10240, 5120, 8), (5120, 4096, 2), (1000, 1024, 5)])
 def test_proj_shapes(gpu, O, rows, K, nr):
     X = gpu
     rng = np.random.default_rng(rows * 7 + K + nr)
