@@ -142,6 +142,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     if (stopped(a.stop)) return;
     const int kvh = blockIdx.y;
     const int G = a.nq / a.nkv;
+    const int gsq = __builtin_ctz(G);               // G is a power of two: query i = (row i >> gsq, head i & (G - 1))
     int nact = a.nact_ptr ? ld_uniform(a.nact_ptr) : nr;
     int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
     if (!PREP && a.zrows) tile_rows(a, nr, pos0, nact);
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 const int i = t + kAttnThreads * u;   // query vector i/16, 8 dims (i%16)*8
                 const int qi = i >> 4, c = i & 15;
                 if (qi < nqr) {
-                    const int r = qi / G, g = qi - r * G;
+                    const int r = qi >> gsq, g = qi & (G - 1);
                     q4[u] = *(const uint4*)(a.qh + (size_t)r * a.nq * kHD + (size_t)(kvh * G + g) * kHD + 8 * c);
                 }
             }
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 #pragma unroll
             for (int i = 0; i < NQW; ++i) {
                 const int qi = wv + (kAttnThreads / 64) * i, qc = qi < nqr ? qi : nqr - 1;
-                const int r = qc / G, g = qc - r * G;
+                const int r = qc >> gsq, g = qc & (G - 1);
                 const uint16_t* src = a.qkv + (size_t)r * a.qkv_stride + (size_t)(kvh * G + g) * qw;
                 norm_rope(a, src, a.q_norm_w, pos0 + r, lane, qy[i][0], qy[i][1]);
             }
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 #pragma unroll
             for (int i = 0; i < NQW; ++i) {
                 const int qi = wv + 8 * i, qc = qi < nqr ? qi : nqr - 1;
-                const int r = qc / G;
+                const int r = qc >> gsq;
                 const int L = pos0 + r + 1;
                 const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
                 const bool valid = lane < nv;
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
                 const float l = tree64(pv[i]);
                 if (qi < nqr) {
                     sp[qi * kSpStride + lane] = pv[i];
-                    const int r = qi / G, g = qi - r * G;
+                    const int r = qi >> gsq, g = qi & (G - 1);
                     const int L = pos0 + r + 1;
                     if (lane == 0 && L - k0 > 0) {
                         const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             for (int r = 0; r < 4; ++r) {
                 const int qi = 16 * qt + 4 * g4 + r;
                 if (qi >= nqr) continue;
-                const int rr = qi / G, g = qi - rr * G;
+                const int rr = qi >> gsq, g = qi & (G - 1);
                 const int L = pos0 + rr + 1;
                 if (L - k0 <= 0) continue;        // no key of this split is visible to the row
                 wo[(((size_t)rr * a.nq + (size_t)(kvh * G + g)) * ms + s) * kHD + 16 * dt + j16] = acc[r];
@@ -455,9 +456,11 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
 }
 
 static int attn_check(const AttnArgs& a, int nr) {
-    if (a.hd != kHD || a.nkv < 1 || a.nq % a.nkv || nr < 1 || nr > kMaxRows || nr * (a.nq / a.nkv) > kMaxQ ||
+    if (a.hd != kHD || a.nkv < 1 || a.nq % a.nkv || ((a.nq / a.nkv) & (a.nq / a.nkv - 1)) || nr < 1 ||
+        nr > kMaxRows || nr * (a.nq / a.nkv) > kMaxQ ||
         (a.kv_group != 16 && a.kv_group != 32 && a.kv_group != 64) || a.rot < 2 || a.rot > kHD || (a.rot & (a.rot - 1))) {
-        set_error("attn: unsupported shape (nq=%d nkv=%d hd=%d nr=%d kv_group=%d rot=%d)", a.nq, a.nkv, a.hd, nr,
+        set_error("attn: unsupported shape (nq=%d nkv=%d: the GQA group must be a power of two; hd=%d nr=%d "
+                  "kv_group=%d rot=%d)", a.nq, a.nkv, a.hd, nr,
                   a.kv_group, a.rot);
         return Q27X_E_SHAPE;
     }

@@ -28,10 +28,10 @@ __device__ __forceinline__ float scale2(float p, int n) {
     return p * __uint_as_float((uint32_t)(n + 127) << 23);
 }
 // e^x: Cody-Waite reduction with ln2 split in hi/lo, degree-7 Taylor polynomial (Horner, fmaf).
-__device__ __forceinline__ float qexp(float x) {
-    if (x != x) return x;
-    if (x > 88.7228393555f) return __builtin_huge_valf();
-    if (x < -103.972084045f) return 0.0f;
+// Branch-free: the polynomial runs on x clamped to the finite range (x itself wherever the
+// result is finite) and the special cases are selected at the end.
+__device__ __forceinline__ float qexp(float xin) {
+    const float x = fminf(fmaxf(xin, -103.972084045f), 88.7228393555f);
     const float kf = rintf(x * 1.44269502163f);
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
     r = __builtin_fmaf(kf, -1.42860682e-06f, r);
@@ -43,13 +43,12 @@ __device__ __forceinline__ float qexp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return scale2(p, (int)kf);
+    const float v = scale2(p, (int)kf);
+    return (xin != xin) ? xin : (xin > 88.7228393555f) ? __builtin_huge_valf() : (xin < -103.972084045f) ? 0.0f : v;
 }
-// 2^x = 2^k * e^(r ln2), x = k + r exactly.
-__device__ __forceinline__ float qexp2(float x) {
-    if (x != x) return x;
-    if (x >= 128.0f) return __builtin_huge_valf();
-    if (x < -150.0f) return 0.0f;
+// 2^x = 2^k * e^(r ln2), x = k + r exactly. Branch-free as qexp.
+__device__ __forceinline__ float qexp2(float xin) {
+    const float x = fminf(fmaxf(xin, -150.0f), 128.0f);
     const float kf = rintf(x);
     const float r = x - kf;
     float p = 1.52527336e-5f;
@@ -60,7 +59,8 @@ __device__ __forceinline__ float qexp2(float x) {
     p = __builtin_fmaf(p, r, 2.40226507e-1f);
     p = __builtin_fmaf(p, r, 6.93147182e-1f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return scale2(p, (int)kf);
+    const float v = scale2(p, (int)kf);
+    return (xin != xin) ? xin : (xin >= 128.0f) ? __builtin_huge_valf() : (xin < -150.0f) ? 0.0f : v;
 }
 // log(u), finite normal u > 0: u = m 2^e, s = (m-1)/(m+1), log m = 2 atanh(s) to s^9.
 __device__ __forceinline__ float qlog_pos(float u) {
