@@ -394,10 +394,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
     }
 }
 
-// Merge the splits of one (row, query head): M = max m_s; w_s = 2^(m_s - M) computed once per
-// split in LDS; den and o accumulated over splits in order (fmaf), o's split values staged 32 at a
-// time with coalesced loads; x sigmoid(gate) -> bf16 -> per-16 quantize.
-constexpr int kCombChunk = 32;
+// Merge the splits of one (row, query head): M = max m_s; w_s = 2^(m_s - M); den and o accumulated
+// over the splits in order (fmaf); x sigmoid(gate) -> bf16 -> per-16 quantize. Thread t owns dim
+// t. The split outputs of up to kCombWin splits go to LDS at once by LDS DMA (each wave moves its
+// 64 dims of every split: ~150 KiB per block in flight; staged 32 splits at a time, each chunk
+// waited a full memory round trip), requested right after the m_s / l_s loads, so waiting for
+// those leaves the transfers in flight. Each thread then reads only the column its own wave
+// moved, so only the shared weights need a barrier. Longer contexts take further windows.
+constexpr int kCombWin = 296;                    // splits per LDS window (18,944 positions)
+constexpr int kCombLds = (kCombWin * kHD + 2 * kCombWin) * 4;
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
@@ -411,30 +416,54 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     const int L = pos0 + r + 1;
     const int ns = (L + kSplit - 1) / kSplit;
     const int ms = a.max_splits;
-    const int t = threadIdx.x, lane = t & 63;
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const float* wo = a.work;
     const float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
     const float* wl = wm + (size_t)nr * a.nq * ms;
     const size_t base = ((size_t)r * a.nq + hq) * ms;
     __shared__ float smax[2];
-    __shared__ float sw[kCombChunk], sl[kCombChunk];
-    __shared__ float so[kCombChunk][kHD];
+    extern __shared__ float cwin[];                 // [kCombWin][128] outputs | [kCombWin] w | [kCombWin] l
+    float* so = cwin;
+    float* cw = cwin + kCombWin * kHD;
+    float* cl = cw + kCombWin;
+    // this wave's 64 dims of splits w0 .. w0 + wn - 1 into LDS (lane l -> dim 64 wv + l)
+    auto dma = [&](int w0, int wn) __attribute__((always_inline)) {
+        for (int j = 0; j < wn; ++j)
+            __builtin_amdgcn_global_load_lds((const void*)(wo + (base + w0 + j) * kHD + 64 * wv + lane),
+                                             (__attribute__((address_space(3))) void*)&so[j * kHD + 64 * wv], 4, 0, 0);
+    };
+    // M over all splits: loads 4 splits per thread per batch, all issued before the first use
+    // (the first batch and the first window's transfers are issued by every thread: a transfer
+    // moves the lanes that execute it)
     float M = -__builtin_huge_valf();
-    for (int s = t; s < ns; s += kHD) M = fmaxf(M, wm[base + s]);
+    const int wn0 = ns < kCombWin ? ns : kCombWin;
+    for (int s0 = t; s0 - t < ns; s0 += 4 * kHD) {
+        float mv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) mv[u] = wm[base + ((s0 + u * kHD < ns) ? s0 + u * kHD : ns - 1)];
+        if (s0 == t) dma(0, wn0);                   // the first window's transfers, behind the first batch
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (s0 + u * kHD < ns) M = fmaxf(M, mv[u]);
+    }
     M = max_xor(M, 64);
     if (lane == 0) smax[t >> 6] = M;
     __syncthreads();
     M = fmaxf(smax[0], smax[1]);
     float den = 0.0f, o = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += kCombChunk) {
-        const int cn = (ns - s0 < kCombChunk) ? ns - s0 : kCombChunk;
-        __syncthreads();
-        if (t < cn) { sw[t] = qexp2(wm[base + s0 + t] - M); sl[t] = wl[base + s0 + t]; }
-        for (int j = 0; j < cn; ++j) so[j][t] = wo[(base + s0 + j) * kHD + t];
-        __syncthreads();
-        for (int j = 0; j < cn; ++j) {
-            den = __builtin_fmaf(sl[j], sw[j], den);
-            o = __builtin_fmaf(so[j][t], sw[j], o);
+    for (int w0 = 0; w0 < ns; w0 += kCombWin) {
+        const int wn = (ns - w0 < kCombWin) ? ns - w0 : kCombWin;
+        if (w0 > 0) {
+            __syncthreads();                        // the previous window is consumed
+            dma(w0, wn);
+        }
+        for (int j = t; j < wn; j += kHD) { cw[j] = qexp2(wm[base + w0 + j] - M); cl[j] = wl[base + w0 + j]; }
+        __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's transfers have landed
+        __syncthreads();                            // every thread's weights are in LDS
+        for (int j = 0; j < wn; ++j) {
+            const float w = cw[j];
+            den = __builtin_fmaf(cl[j], w, den);
+            o = __builtin_fmaf(so[j * kHD + t], w, o);
         }
     }
     const float inv = 1.0f / den;
@@ -522,6 +551,11 @@ static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
+    static bool comb_lds = false;
+    if (!comb_lds) {
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_combine, hipFuncAttributeMaxDynamicSharedMemorySize, kCombLds));
+        comb_lds = true;
+    }
     if (prep_fused && !(a.rot == kHD || a.rot <= 64)) { set_error("attn: rot=%d unsupported", a.rot); return Q27X_E_SHAPE; }
     if (a.zrows && (prep_fused || a.zrows != nr || a.ztotal < 1 || a.nact_ptr)) {
         set_error("attn: row tiles need separate prep, zrows == nr and no active-row count");
@@ -530,7 +564,7 @@ int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     const int rc = prep_fused ? launch_split<true>(a, nr, s) : launch_split<false>(a, nr, s);
     if (rc) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u),
-                       dim3(kHD), 0, s, a, nr);
+                       dim3(kHD), (size_t)kCombLds, s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
