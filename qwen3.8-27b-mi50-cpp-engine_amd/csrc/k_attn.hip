@@ -323,36 +323,44 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
             }
         }
         __syncthreads();
-        // ---- split softmax: lane = key, this wave's queries wv + 8 i (p replaces the score)
-        // (every one of the wave's NQW queries is computed, on a clamped row past nqr, and only
-        // the real ones are stored: no exit inside the loop, so the independent reductions run
-        // side by side)
+        // ---- split softmax, p replacing the score: this wave's queries wv + 8 i, four at a time,
+        // query i of a pass in lane row i (lanes 16 i .. 16 i + 15), lane 16 i + c holding keys c,
+        // c + 16, c + 32, c + 48. The 64-lane shfl_down tree for l pairs key c with c + 32, then
+        // c with c + 16: those two levels are this lane's ((p_c + p_c+32) + (p_c+16 + p_c+48)),
+        // and the levels 8, 4, 2, 1 run in every row at once (DPP row shifts), l landing in lane
+        // 16 i; the max is exact in any order. (Query rows past the wave's NQW run on a clamped
+        // query and are discarded.)
         {
-            float pv[NQW], mv[NQW];
+            const int qrow = lane >> 4, c = lane & 15;
 #pragma unroll
-            for (int i = 0; i < NQW; ++i) {
-                const int qi = wv + 8 * i, qc = qi < nqr ? qi : nqr - 1;
+            for (int pass = 0; pass < (NQW + 3) / 4; ++pass) {
+                const int iq = 4 * pass + qrow;
+                const int qi = wv + 8 * iq, qc = (qi < nqr && iq < NQW) ? qi : nqr - 1;
                 const int r = qc >> gsq;
                 const int L = pos0 + r + 1;
                 const int nv = (L - k0 < nk) ? (L - k0) : nk;   // valid keys of this row in the split
-                const bool valid = lane < nv;
-                const float x = sp[qc * kSpStride + lane] * a.sl2e;
-                float m = valid ? x : -__builtin_huge_valf();
-                m = max_xor(m, 64);
-                pv[i] = valid ? qexp2(x - m) : 0.0f;
-                mv[i] = m;
-            }
+                float x[4], p[4];
+                float m = -__builtin_huge_valf();
 #pragma unroll
-            for (int i = 0; i < NQW; ++i) {
-                const int qi = wv + 8 * i;
-                const float l = tree64(pv[i]);
-                if (qi < nqr) {
-                    sp[qi * kSpStride + lane] = pv[i];
-                    const int r = qi >> gsq, g = qi & (G - 1);
-                    const int L = pos0 + r + 1;
-                    if (lane == 0 && L - k0 > 0) {
+                for (int e = 0; e < 4; ++e) {
+                    x[e] = sp[qc * kSpStride + c + 16 * e] * a.sl2e;
+                    if (c + 16 * e < nv) m = fmaxf(m, x[e]);
+                }
+                m = max_xor(m, 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[e] = (c + 16 * e < nv) ? qexp2(x[e] - m) : 0.0f;
+                float l = (p[0] + p[2]) + (p[1] + p[3]);
+                l = down_add<8>(l);
+                l = down_add<4>(l);
+                l = down_add<2>(l);
+                l = down_add<1>(l);
+                if (qi < nqr && iq < NQW) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sp[qi * kSpStride + c + 16 * e] = p[e];
+                    const int g = qi & (G - 1);
+                    if (c == 0 && L - k0 > 0) {
                         const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
-                        wm[mi] = mv[i];
+                        wm[mi] = m;
                         wl[mi] = l;
                     }
                 }
