@@ -409,8 +409,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 // waited a full memory round trip), requested right after the m_s / l_s loads, so waiting for
 // those leaves the transfers in flight. Each thread then reads only the column its own wave
 // moved, so only the shared weights need a barrier. Longer contexts take further windows.
-constexpr int kCombWin = 296;                    // splits per LDS window (18,944 positions)
-constexpr int kCombLds = (kCombWin * kHD + 2 * kCombWin) * 4;
+constexpr int kCombWin = 296;                    // splits per LDS window at most (18,944 positions)
+// the window of a launch: its split count, capped (short contexts keep several blocks per CU)
+__host__ __device__ inline int comb_win(int max_splits) { return max_splits < kCombWin ? max_splits : kCombWin; }
+__host__ __device__ inline size_t comb_lds(int max_splits) { return (size_t)comb_win(max_splits) * (kHD + 2) * 4; }
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
@@ -430,10 +432,11 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     const float* wl = wm + (size_t)nr * a.nq * ms;
     const size_t base = ((size_t)r * a.nq + hq) * ms;
     __shared__ float smax[2];
-    extern __shared__ float cwin[];                 // [kCombWin][128] outputs | [kCombWin] w | [kCombWin] l
+    extern __shared__ float cwin[];                 // [W][128] outputs | [W] w | [W] l
+    const int W = comb_win(ms);
     float* so = cwin;
-    float* cw = cwin + kCombWin * kHD;
-    float* cl = cw + kCombWin;
+    float* cw = cwin + (size_t)W * kHD;
+    float* cl = cw + W;
     // this wave's 64 dims of splits w0 .. w0 + wn - 1 into LDS (lane l -> dim 64 wv + l)
     auto dma = [&](int w0, int wn) __attribute__((always_inline)) {
         for (int j = 0; j < wn; ++j)
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     // (the first batch and the first window's transfers are issued by every thread: a transfer
     // moves the lanes that execute it)
     float M = -__builtin_huge_valf();
-    const int wn0 = ns < kCombWin ? ns : kCombWin;
+    const int wn0 = ns < W ? ns : W;
     for (int s0 = t; s0 - t < ns; s0 += 4 * kHD) {
         float mv[4];
 #pragma unroll
@@ -459,8 +462,8 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     __syncthreads();
     M = fmaxf(smax[0], smax[1]);
     float den = 0.0f, o = 0.0f;
-    for (int w0 = 0; w0 < ns; w0 += kCombWin) {
-        const int wn = (ns - w0 < kCombWin) ? ns - w0 : kCombWin;
+    for (int w0 = 0; w0 < ns; w0 += W) {
+        const int wn = (ns - w0 < W) ? ns - w0 : W;
         if (w0 > 0) {
             __syncthreads();                        // the previous window is consumed
             dma(w0, wn);
@@ -559,10 +562,11 @@ static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
-    static bool comb_lds = false;
-    if (!comb_lds) {
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_combine, hipFuncAttributeMaxDynamicSharedMemorySize, kCombLds));
-        comb_lds = true;
+    static bool comb_attr = false;
+    if (!comb_attr) {
+        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_combine, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)comb_lds(kCombWin)));
+        comb_attr = true;
     }
     if (prep_fused && !(a.rot == kHD || a.rot <= 64)) { set_error("attn: rot=%d unsupported", a.rot); return Q27X_E_SHAPE; }
     if (a.zrows && (prep_fused || a.zrows != nr || a.ztotal < 1 || a.nact_ptr)) {
@@ -572,7 +576,7 @@ int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     const int rc = prep_fused ? launch_split<true>(a, nr, s) : launch_split<false>(a, nr, s);
     if (rc) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u),
-                       dim3(kHD), (size_t)kCombLds, s, a, nr);
+                       dim3(kHD), comb_lds(a.max_splits), s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
