@@ -294,9 +294,10 @@ def fill_kv(rng, O, L, nkv, hd, group, ctx):
     return kc, ks, vc, vs
 
 
-@pytest.mark.parametrize("L0", [1024, 4096, 16384])
+@pytest.mark.parametrize("L0", [1024, 4096, 16384, 20000])
 def test_attention_config2(gpu, O, L0):
-    """GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows."""
+    """GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows.
+    (20000 positions: 313 splits, past one LDS window of the combine, which then takes two.)"""
     X = gpu
     rng = np.random.default_rng(0x51E70002 + L0)
     nq, nkv, hd, rot, group, nr, gate = 32, 8, 128, 32, 32, 3, 1
