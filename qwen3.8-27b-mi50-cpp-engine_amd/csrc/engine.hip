@@ -1286,10 +1286,10 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
 // brought to that representation from its per-64 mirror right before its GEMM; the norms, GDN
 // conv / row scalars / scan, attention, SwiGLU and residual adds keep the decode path's
 // arithmetic. The MTP prompt pass fills only the draft KV cache (src/q27_main.cpp:2647-2688).
-constexpr int kPfChunk = 2048;
+constexpr int kPfChunk = 4096;
 constexpr int kPfAttnRows = 128;    // query rows per attention launch (tiles of 8)
 static int env_int(const char* name, int def);
-static int pf_chunk() {   // rows per pass over the layers; Q27X_PF_CHUNK (8 .. 2048) overrides, read per call
+static int pf_chunk() {   // rows per pass over the layers; Q27X_PF_CHUNK (8 .. 4096) overrides, read per call
     const int v = env_int("Q27X_PF_CHUNK", kPfChunk);
     return v < 8 ? 8 : (v > kPfChunk ? kPfChunk : v);
 }
