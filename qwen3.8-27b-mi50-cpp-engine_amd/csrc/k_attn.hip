@@ -405,10 +405,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 // Merge the splits of one (row, query head): M = max m_s; w_s = 2^(m_s - M); den and o accumulated
 // over the splits in order (fmaf); x sigmoid(gate) -> bf16 -> per-16 quantize. Thread t owns dim
 // t. The split outputs of up to kCombWin splits go to LDS at once by LDS DMA (each wave moves its
-// 64 dims of every split: ~150 KiB per block in flight; staged 32 splits at a time, each chunk
-// waited a full memory round trip), requested right after the m_s / l_s loads, so waiting for
-// those leaves the transfers in flight. Each thread then reads only the column its own wave
-// moved, so only the shared weights need a barrier. Longer contexts take further windows.
+// 64 dims of every split: up to ~150 KiB per block in flight; staged 32 splits at a time, each
+// chunk waited a full memory round trip), requested right behind the first batch of m_s loads.
+// The waits after that cover every transfer (their count is a run-time loop, so the compiler's
+// waits count all of them): one round trip for the whole window. Each thread then reads only the
+// column its own wave moved, so only the shared weights need a barrier. Longer contexts take
+// further windows.
 constexpr int kCombWin = 296;                    // splits per LDS window at most (18,944 positions)
 // the window of a launch: its split count, capped (short contexts keep several blocks per CU)
 __host__ __device__ inline int comb_win(int max_splits) { return max_splits < kCombWin ? max_splits : kCombWin; }
