@@ -153,6 +153,13 @@ struct q27x_ctx {
     PfBuf* pf = nullptr;
     std::vector<void*> pf_walloc;   // the GEMM representations of the weights
     int pf_wready = 0;
+    // two-chunk pipeline of the prefill: the second chunk buffer set, its stream, and per buffer
+    // set one event per layer (+ the MTP pass, + the chunk's end)
+    PfBuf* pf2 = nullptr;
+    hipStream_t pf_stream = nullptr;
+    std::vector<hipEvent_t> pf_ev;
+    PfBuf* pfc = nullptr;         // the chunk being enqueued: its buffers and stream
+    hipStream_t pfs = nullptr;
 };
 
 namespace q27x {
@@ -807,10 +814,13 @@ int q27x_ctx_destroy(q27x_ctx* x) {
     if (x->g_spec) (void)hipGraphExecDestroy(x->g_spec);
     if (x->g_plain) (void)hipGraphExecDestroy(x->g_plain);
     if (x->mbox) (void)hipHostFree((void*)x->mbox);
-    if (x->pf) {
-        for (void* p : x->pf->allocs) (void)hipFree(p);
-        delete x->pf;
-    }
+    for (PfBuf* b : { x->pf, x->pf2 })
+        if (b) {
+            for (void* p : b->allocs) (void)hipFree(p);
+            delete b;
+        }
+    for (hipEvent_t e : x->pf_ev) (void)hipEventDestroy(e);
+    if (x->pf_stream) (void)hipStreamDestroy(x->pf_stream);
     for (void* p : x->pf_walloc) (void)hipFree(p);
     if (x->warena) (void)hipFree(x->warena);
     if (x->sarena) (void)hipFree(x->sarena);
@@ -1286,22 +1296,26 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
 // brought to that representation from its per-64 mirror right before its GEMM; the norms, GDN
 // conv / row scalars / scan, attention, SwiGLU and residual adds keep the decode path's
 // arithmetic. The MTP prompt pass fills only the draft KV cache (src/q27_main.cpp:2647-2688).
-constexpr int kPfChunk = 4096;
+constexpr int kPfChunk = 2048;
 constexpr int kPfAttnRows = 128;    // query rows per attention launch (tiles of 8)
 static int env_int(const char* name, int def);
 static int pf_chunk() {   // rows per pass over the layers; Q27X_PF_CHUNK (8 .. 4096) overrides, read per call
     const int v = env_int("Q27X_PF_CHUNK", kPfChunk);
-    return v < 8 ? 8 : (v > kPfChunk ? kPfChunk : v);
+    return v < 8 ? 8 : (v > 4096 ? 4096 : v);
 }
+// successive chunks on two streams, chunk c + 1's layer l behind chunk c's layer l (Q27X_PF_PIPE=0: one
+// stream)
+static int pf_pipe() { return env_int("Q27X_PF_PIPE", 1) != 0; }
 static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
 
-static int pf_alloc(q27x_ctx* x, int cap) {
-    if (x->pf && x->pf->cap >= cap) return Q27X_OK;
-    if (x->pf) {
+static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
+    if (*slot && (*slot)->cap >= cap) return Q27X_OK;
+    if (*slot) {
         Q27X_HIP(hipStreamSynchronize(x->stream));
-        for (void* p : x->pf->allocs) (void)hipFree(p);
-        delete x->pf;
-        x->pf = nullptr;
+        if (x->pf_stream) Q27X_HIP(hipStreamSynchronize(x->pf_stream));
+        for (void* p : (*slot)->allocs) (void)hipFree(p);
+        delete *slot;
+        *slot = nullptr;
     }
     const q27x_config& c = x->c;
     const int H = x->H, I = x->I;
@@ -1331,7 +1345,7 @@ static int pf_alloc(q27x_ctx* x, int cap) {
         delete B;
         return rc;
     }
-    x->pf = B;
+    *slot = B;
     return Q27X_OK;
 }
 
@@ -1351,7 +1365,7 @@ static int pf_gemm(q27x_ctx* x, const Mat& W, int r0, int nrows, const int8_t* x
         if (as.split_b == 0 && as.split_c > 0) { as.split_b = as.split_c; as.alpha_b = as.alpha_c; as.split_c = 0; }
     }
     return launch_gemm_i8g(W.pw + (size_t)r0 * K, W.ps + (size_t)r0 * (K / gs), nrows, K, gs, a0, xq, xs, M, y, ldy,
-                           out_bf16, res, x->H, res_bf16, res ? 1.0f : 0.0f, x->stream, &as);
+                           out_bf16, res, x->H, res_bf16, res ? 1.0f : 0.0f, x->pfs, &as);
 }
 // every matrix of the model in the GEMM representation (the reference keeps such per-(row, group)
 // mirrors from load time, src/q27_epi.hip:14-35); made once per load, kept on the device
@@ -1380,18 +1394,18 @@ static int pf_weights(q27x_ctx* x) {
 }
 // norm of C rows (values to B.yf) and their per-(token, group) codes
 static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs, float in_scale = 1.0f) {
-    PfBuf& B = *x->pf;
+    PfBuf& B = *x->pfc;
     n.yf = B.yf; n.yfstride = x->H;
-    int rc = launch_norm(n, C, x->stream);
+    int rc = launch_norm(n, C, x->pfs);
     if (rc) return rc;
-    return launch_quant_tok_grp(B.yf, x->H, C, x->H, pf_gs(x->H), in_scale, xq, xs, x->stream);
+    return launch_quant_tok_grp(B.yf, x->H, C, x->H, pf_gs(x->H), in_scale, xq, xs, x->pfs);
 }
 
 static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
     const q27x_config& c = x->c;
-    hipStream_t s = x->stream;
+    hipStream_t s = x->pfs;
     Dctl* d = x->dctl;
-    PfBuf& B = *x->pf;
+    PfBuf& B = *x->pfc;
     LayerDev& Y = x->L[l];
     const int H = x->H, I = x->I;
     int rc;
@@ -1450,7 +1464,7 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
 static int pf_mtp(q27x_ctx* x, int p0, int C) {
     const q27x_config& c = x->c;
     Dctl* d = x->dctl;
-    PfBuf& B = *x->pf;
+    PfBuf& B = *x->pfc;
     LayerDev& M = x->mtp;
     const int H = x->H;
     const float po = c.mtp_plus_one ? 1.0f : 0.0f;
@@ -1474,7 +1488,7 @@ static int pf_mtp(q27x_ctx* x, int p0, int C) {
     a.kc = M.kc; a.ks = M.ks; a.vc = M.vc; a.vs = M.vs; a.kv_group = c.kv_group;
     a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
     a.pos0_imm = p0; a.prep_kv_only = 1; a.stop = &d->stop;
-    return launch_attn_prep_rows(a, C, x->stream);
+    return launch_attn_prep_rows(a, C, x->pfs);
 }
 
 int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
@@ -1489,26 +1503,65 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
     int rc = q27x_reset(x);
     if (rc) return rc;
     const int chunk = pf_chunk();
-    if ((rc = pf_alloc(x, std::min(n, chunk)))) return rc;
+    const bool pipe = pf_pipe() && n > chunk;
+    if ((rc = pf_alloc(x, std::min(n, chunk), &x->pf))) return rc;
+    if (pipe && (rc = pf_alloc(x, chunk, &x->pf2))) return rc;
     if ((rc = pf_weights(x))) return rc;
     hipStream_t s = x->stream;
     Dctl* d = x->dctl;
     const q27x_config& c = x->c;
     const int H = x->H;
+    const int NE = c.n_layers + 2;                 // per buffer set: one event per layer, the MTP pass, the end
+    if (pipe) {
+        if (!x->pf_stream) {
+            const hipError_t e = hipStreamCreateWithFlags(&x->pf_stream, hipStreamNonBlocking);
+            if (e != hipSuccess) return hip_fail(e, "hipStreamCreate (prefill)");
+        }
+        while ((int)x->pf_ev.size() < 2 * NE + 1) {
+            hipEvent_t ev;
+            const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+            if (e != hipSuccess) return hip_fail(e, "hipEventCreate (prefill)");
+            x->pf_ev.push_back(ev);
+        }
+    }
     Q27X_HIP(hipMemcpyAsync(x->prompt_dev, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
-    for (int p0 = 0; p0 < n; p0 += chunk) {
+    if (pipe) {                                     // the second stream starts behind the upload and the weights
+        Q27X_HIP(hipEventRecord(x->pf_ev[2 * NE], s));
+        Q27X_HIP(hipStreamWaitEvent(x->pf_stream, x->pf_ev[2 * NE], 0));
+    }
+    // Chunk i runs on buffer set and stream i % 2. Its layer l waits for chunk i - 1's layer l (the
+    // GDN state and conv records, the KV cache rows before its own), its MTP pass for chunk i - 1's
+    // (the draft KV); its buffers were last used by chunk i - 2 on the same stream.
+    int ci = 0;
+    for (int p0 = 0; p0 < n; p0 += chunk, ++ci) {
         const int C = std::min(chunk, n - p0);
-        for (int l = 0; l < c.n_layers; ++l)
+        const int sl = pipe ? (ci & 1) : 0;
+        x->pfc = sl ? x->pf2 : x->pf;
+        x->pfs = sl ? x->pf_stream : s;
+        hipEvent_t* ev = pipe ? &x->pf_ev[(size_t)sl * NE] : nullptr;
+        hipEvent_t* evp = pipe ? &x->pf_ev[(size_t)(sl ^ 1) * NE] : nullptr;
+        for (int l = 0; l < c.n_layers; ++l) {
+            if (pipe && ci > 0) Q27X_HIP(hipStreamWaitEvent(x->pfs, evp[l], 0));
             if ((rc = pf_layer(x, l, p0, C))) return rc;
+            if (pipe) Q27X_HIP(hipEventRecord(ev[l], x->pfs));
+        }
         // the rows' final residuals: bf16(bf16(r1) + r2) (the reference's double add) or bf16(r2)
         NormArgs hn{};
-        hn.x = x->pf->x; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->pf->h : nullptr;
+        hn.x = x->pfc->x; hn.x_bf16 = 0; hn.xstride = H; hn.hadd = c.head_double_residual ? x->pfc->h : nullptr;
         hn.hout = x->hall + (size_t)p0 * H; hn.w = x->final_norm; hn.plus = 1.0f; hn.eps = c.rms_eps; hn.n = H;
         hn.ystride = H; hn.in_scale = 1.0f; hn.stop = &d->stop;
-        if ((rc = launch_norm(hn, C, s))) return rc;
+        if ((rc = launch_norm(hn, C, x->pfs))) return rc;
         const int cm = (p0 + C < n) ? C : C - 1;     // MTP positions p with p + 1 < n
+        if (pipe && ci > 0) Q27X_HIP(hipStreamWaitEvent(x->pfs, evp[c.n_layers], 0));
         if (cm > 0 && (rc = pf_mtp(x, p0, cm))) return rc;
+        if (pipe) {
+            Q27X_HIP(hipEventRecord(ev[c.n_layers], x->pfs));
+            Q27X_HIP(hipEventRecord(ev[c.n_layers + 1], x->pfs));
+        }
     }
+    if (pipe && ci > 1) Q27X_HIP(hipStreamWaitEvent(s, x->pf_ev[(size_t)((ci - 1) & 1) * NE + c.n_layers + 1], 0));
+    x->pfc = x->pf;
+    x->pfs = s;
     // head of the last row: final norm, lm_head, argmax
     NormArgs hf = norm_of(x, x->hall + (size_t)(n - 1) * H, 1, x->final_norm, 1.0f, 1, nullptr, x->ynorm);
     if ((rc = launch_norm(hf, 1, s))) return rc;
