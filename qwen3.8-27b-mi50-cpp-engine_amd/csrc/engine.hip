@@ -1290,17 +1290,20 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
 }
 
 // ---------------------------------------------------------------- layer-major prefill (GEMM path)
-// The prompt in chunks of up to kPfChunk rows, each chunk through every layer (ls_q8_layer's
+// The prompt in chunks (pf_chunk), each chunk through every layer (ls_q8_layer's
 // stage order, src/q27_main.cpp:4076-4316): every projection is the int8 MFMA GEMM of per-(row,
 // group) weights and per-(token, group) activations (group 1024, or the whole K), each matrix
 // brought to that representation from its per-64 mirror right before its GEMM; the norms, GDN
 // conv / row scalars / scan, attention, SwiGLU and residual adds keep the decode path's
 // arithmetic. The MTP prompt pass fills only the draft KV cache (src/q27_main.cpp:2647-2688).
-constexpr int kPfChunk = 2048;
 constexpr int kPfAttnRows = 128;    // query rows per attention launch (tiles of 8)
 static int env_int(const char* name, int def);
-static int pf_chunk() {   // rows per pass over the layers; Q27X_PF_CHUNK (8 .. 4096) overrides, read per call
-    const int v = env_int("Q27X_PF_CHUNK", kPfChunk);
+// Rows per pass over the layers for an n-token prompt: 1024 from 2048 tokens on, else 512 (with the two
+// streams below, smaller chunks overlap more: at 4096 tokens 1024-row chunks measured 15.1K tok/s
+// against 14.0K with 2048 and 11.3K with one stream; 512 and 768 were slower). Q27X_PF_CHUNK
+// (8 .. 4096) overrides, read per call.
+static int pf_chunk(int n) {
+    const int v = env_int("Q27X_PF_CHUNK", n >= 2048 ? 1024 : 512);
     return v < 8 ? 8 : (v > 4096 ? 4096 : v);
 }
 // successive chunks on two streams, chunk c + 1's layer l behind chunk c's layer l (Q27X_PF_PIPE=0: one
@@ -1502,7 +1505,7 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
         if (ids[i] < 0 || ids[i] >= x->V) { set_error("q27x_prefill_gemm: token %d out of range", ids[i]); return Q27X_E_RANGE; }
     int rc = q27x_reset(x);
     if (rc) return rc;
-    const int chunk = pf_chunk();
+    const int chunk = pf_chunk(n);
     const bool pipe = pf_pipe() && n > chunk;
     if ((rc = pf_alloc(x, std::min(n, chunk), &x->pf))) return rc;
     if (pipe && (rc = pf_alloc(x, chunk, &x->pf2))) return rc;
