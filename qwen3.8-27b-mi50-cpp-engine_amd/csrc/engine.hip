@@ -153,10 +153,10 @@ struct q27x_ctx {
     PfBuf* pf = nullptr;
     std::vector<void*> pf_walloc;   // the GEMM representations of the weights
     int pf_wready = 0;
-    // two-chunk pipeline of the prefill: the second chunk buffer set, its stream, and per buffer
-    // set one event per layer (+ the MTP pass, + the chunk's end)
-    PfBuf* pf2 = nullptr;
-    hipStream_t pf_stream = nullptr;
+    // chunk pipeline of the prefill: the further chunk buffer sets and their streams (set 0 is pf
+    // on the context's stream), and per buffer set one event per layer (+ the MTP pass, + the end)
+    PfBuf* pfx[2] = { nullptr, nullptr };
+    hipStream_t pf_stream[2] = { nullptr, nullptr };
     std::vector<hipEvent_t> pf_ev;
     PfBuf* pfc = nullptr;         // the chunk being enqueued: its buffers and stream
     hipStream_t pfs = nullptr;
@@ -814,13 +814,13 @@ int q27x_ctx_destroy(q27x_ctx* x) {
     if (x->g_spec) (void)hipGraphExecDestroy(x->g_spec);
     if (x->g_plain) (void)hipGraphExecDestroy(x->g_plain);
     if (x->mbox) (void)hipHostFree((void*)x->mbox);
-    for (PfBuf* b : { x->pf, x->pf2 })
+    for (PfBuf* b : { x->pf, x->pfx[0], x->pfx[1] })
         if (b) {
             for (void* p : b->allocs) (void)hipFree(p);
             delete b;
         }
     for (hipEvent_t e : x->pf_ev) (void)hipEventDestroy(e);
-    if (x->pf_stream) (void)hipStreamDestroy(x->pf_stream);
+    for (hipStream_t ps : x->pf_stream) if (ps) (void)hipStreamDestroy(ps);
     for (void* p : x->pf_walloc) (void)hipFree(p);
     if (x->warena) (void)hipFree(x->warena);
     if (x->sarena) (void)hipFree(x->sarena);
@@ -1308,14 +1308,17 @@ static int pf_chunk(int n) {
 }
 // successive chunks on two streams, chunk c + 1's layer l behind chunk c's layer l (Q27X_PF_PIPE=0: one
 // stream)
-static int pf_pipe() { return env_int("Q27X_PF_PIPE", 1) != 0; }
+static int pf_streams() {   // chunks in flight: Q27X_PF_STREAMS (1 .. 3), default 2
+    const int v = env_int("Q27X_PF_STREAMS", 2);
+    return v < 1 ? 1 : (v > 3 ? 3 : v);
+}
 static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
 
 static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
     if (*slot && (*slot)->cap >= cap) return Q27X_OK;
     if (*slot) {
         Q27X_HIP(hipStreamSynchronize(x->stream));
-        if (x->pf_stream) Q27X_HIP(hipStreamSynchronize(x->pf_stream));
+        for (hipStream_t ps : x->pf_stream) if (ps) Q27X_HIP(hipStreamSynchronize(ps));
         for (void* p : (*slot)->allocs) (void)hipFree(p);
         delete *slot;
         *slot = nullptr;
@@ -1506,9 +1509,11 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
     int rc = q27x_reset(x);
     if (rc) return rc;
     const int chunk = pf_chunk(n);
-    const bool pipe = pf_pipe() && n > chunk;
+    const int NS = (n > chunk) ? std::min(pf_streams(), (n + chunk - 1) / chunk) : 1;
+    const bool pipe = NS > 1;
     if ((rc = pf_alloc(x, std::min(n, chunk), &x->pf))) return rc;
-    if (pipe && (rc = pf_alloc(x, chunk, &x->pf2))) return rc;
+    for (int k = 1; k < NS; ++k)
+        if ((rc = pf_alloc(x, chunk, &x->pfx[k - 1]))) return rc;
     if ((rc = pf_weights(x))) return rc;
     hipStream_t s = x->stream;
     Dctl* d = x->dctl;
@@ -1516,11 +1521,12 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
     const int H = x->H;
     const int NE = c.n_layers + 2;                 // per buffer set: one event per layer, the MTP pass, the end
     if (pipe) {
-        if (!x->pf_stream) {
-            const hipError_t e = hipStreamCreateWithFlags(&x->pf_stream, hipStreamNonBlocking);
-            if (e != hipSuccess) return hip_fail(e, "hipStreamCreate (prefill)");
-        }
-        while ((int)x->pf_ev.size() < 2 * NE + 1) {
+        for (int k = 1; k < NS; ++k)
+            if (!x->pf_stream[k - 1]) {
+                const hipError_t e = hipStreamCreateWithFlags(&x->pf_stream[k - 1], hipStreamNonBlocking);
+                if (e != hipSuccess) return hip_fail(e, "hipStreamCreate (prefill)");
+            }
+        while ((int)x->pf_ev.size() < 3 * NE + 1) {
             hipEvent_t ev;
             const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
             if (e != hipSuccess) return hip_fail(e, "hipEventCreate (prefill)");
@@ -1528,21 +1534,21 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
         }
     }
     Q27X_HIP(hipMemcpyAsync(x->prompt_dev, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
-    if (pipe) {                                     // the second stream starts behind the upload and the weights
-        Q27X_HIP(hipEventRecord(x->pf_ev[2 * NE], s));
-        Q27X_HIP(hipStreamWaitEvent(x->pf_stream, x->pf_ev[2 * NE], 0));
+    if (pipe) {                                     // the other streams start behind the upload and the weights
+        Q27X_HIP(hipEventRecord(x->pf_ev[3 * NE], s));
+        for (int k = 1; k < NS; ++k) Q27X_HIP(hipStreamWaitEvent(x->pf_stream[k - 1], x->pf_ev[3 * NE], 0));
     }
-    // Chunk i runs on buffer set and stream i % 2. Its layer l waits for chunk i - 1's layer l (the
+    // Chunk i runs on buffer set and stream i % NS. Its layer l waits for chunk i - 1's layer l (the
     // GDN state and conv records, the KV cache rows before its own), its MTP pass for chunk i - 1's
-    // (the draft KV); its buffers were last used by chunk i - 2 on the same stream.
+    // (the draft KV); its buffers were last used by chunk i - NS on the same stream.
     int ci = 0;
     for (int p0 = 0; p0 < n; p0 += chunk, ++ci) {
         const int C = std::min(chunk, n - p0);
-        const int sl = pipe ? (ci & 1) : 0;
-        x->pfc = sl ? x->pf2 : x->pf;
-        x->pfs = sl ? x->pf_stream : s;
+        const int sl = ci % NS, sp = (ci + NS - 1) % NS;
+        x->pfc = sl ? x->pfx[sl - 1] : x->pf;
+        x->pfs = sl ? x->pf_stream[sl - 1] : s;
         hipEvent_t* ev = pipe ? &x->pf_ev[(size_t)sl * NE] : nullptr;
-        hipEvent_t* evp = pipe ? &x->pf_ev[(size_t)(sl ^ 1) * NE] : nullptr;
+        hipEvent_t* evp = pipe ? &x->pf_ev[(size_t)sp * NE] : nullptr;
         for (int l = 0; l < c.n_layers; ++l) {
             if (pipe && ci > 0) Q27X_HIP(hipStreamWaitEvent(x->pfs, evp[l], 0));
             if ((rc = pf_layer(x, l, p0, C))) return rc;
@@ -1562,7 +1568,7 @@ int q27x_prefill_gemm(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_tok
             Q27X_HIP(hipEventRecord(ev[c.n_layers + 1], x->pfs));
         }
     }
-    if (pipe && ci > 1) Q27X_HIP(hipStreamWaitEvent(s, x->pf_ev[(size_t)((ci - 1) & 1) * NE + c.n_layers + 1], 0));
+    if (pipe) Q27X_HIP(hipStreamWaitEvent(s, x->pf_ev[(size_t)((ci - 1) % NS) * NE + c.n_layers + 1], 0));
     x->pfc = x->pf;
     x->pfs = s;
     // head of the last row: final norm, lm_head, argmax
