@@ -71,10 +71,12 @@ def test_tiny_k7_prefill_gemm_matches_oracle(gpu, O):
     run_case(gpu, O, gpu.tiny_config(spec_k=7), 45, 2, 16)
 
 
-def test_full_width_prefill_gemm_matches_oracle(gpu, O):
+@pytest.mark.parametrize("n,chunk", [(64, None), (96, 32)])
+def test_full_width_prefill_gemm_matches_oracle(gpu, O, n, chunk):
     """BASELINE widths at 4 layers (3 GDN + 1 attention): the 16384-row in_qkv|in_z, 34816-row
-    gate|up and K = 17408 down GEMMs, 32q/8kv attention, the 62080-row head."""
-    run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=512), 64, 2)
+    gate|up and K = 17408 down GEMMs, 32q/8kv attention, the 62080-row head. (96 tokens in 32-row
+    chunks: three chunks on alternating streams, each layer behind the previous chunk's.)"""
+    run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=512), n, 2, chunk)
 
 
 def test_full_model_spec_equals_plain_after_prefill_gemm(gpu):
