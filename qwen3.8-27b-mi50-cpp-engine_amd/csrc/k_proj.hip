@@ -158,8 +158,12 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
         row = row < a.rows ? row : a.rows - 1;
         const int s = t * 64 + lane;
         if (FULL || s < nslab) {
-            W[r][t] = ld_nt16(ok ? a.W + (size_t)row * K + 16 * s : a.W);
-            S[r][t] = *(ok ? a.WS + (size_t)row * ng64 + (s >> 2) : a.WS);
+            // (the row base is selected per wave, the lane's slab added after: a group past the
+            // wave's last reads the first row's slabs)
+            const int8_t* wrow = ok ? a.W + (size_t)row * K : a.W;
+            const float* srow = ok ? a.WS + (size_t)row * ng64 : a.WS;
+            W[r][t] = ld_nt16(wrow + 16 * s);
+            S[r][t] = srow[s >> 2];
         } else {
             W[r][t] = make_uint4(0u, 0u, 0u, 0u);
             S[r][t] = 0.0f;

@@ -207,7 +207,10 @@ __device__ __forceinline__ float max_quad(float x) {
 
 // ---------------------------------------------------------------- int8
 __device__ __forceinline__ int dot16(const uint4 w, const uint4 x) {
-    int d = __builtin_amdgcn_sdot4((int)w.x, (int)x.x, 0, false);
+    // (the first product with the clamp bit, which four int8 products can never reach: that form
+    // takes the zero accumulator as an inline constant, where the unclamped one becomes the
+    // two-operand instruction and needs a register cleared for every chain)
+    int d = __builtin_amdgcn_sdot4((int)w.x, (int)x.x, 0, true);
     d = __builtin_amdgcn_sdot4((int)w.y, (int)x.y, d, false);
     d = __builtin_amdgcn_sdot4((int)w.z, (int)x.z, d, false);
     d = __builtin_amdgcn_sdot4((int)w.w, (int)x.w, d, false);
