@@ -40,8 +40,21 @@ __device__ __forceinline__ float down_tree(float y) {
 // P - 1 + log2(64 / P) shuffles instead of 6 P.
 template <int P>
 __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
+    // levels 32 and 16: one lane-half (row) swap of the pair (v, v + h) puts value v's partners
+    // side by side in the lower half (rows 0, 2) and value v + h's in the upper half (rows 1, 3),
+    // the same pairs the exchange below forms
+    int h = P / 2, o = 32;
 #pragma unroll
-    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
+    for (; h >= 1 && o >= 16; h >>= 1, o >>= 1) {
+#pragma unroll
+        for (int v = 0; v < h; ++v) {
+            const auto r = (o == 32) ? __builtin_amdgcn_permlane32_swap(__float_as_uint(x[v]), __float_as_uint(x[v + h]), false, false)
+                                     : __builtin_amdgcn_permlane16_swap(__float_as_uint(x[v]), __float_as_uint(x[v + h]), false, false);
+            x[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    }
+#pragma unroll
+    for (; h >= 1; h >>= 1, o >>= 1) {
         // bitwise selects: a select between two array elements would become a select of
         // addresses and push the array out of registers
         const uint32_t up = (lane & o) ? 0xFFFFFFFFu : 0u;
