@@ -74,6 +74,24 @@ def test_tiny_k7_rounds_match_oracle(gpu, O):
     om.close()
 
 
+@pytest.mark.parametrize("k", [1, 3, 4, 5, 6])
+def test_tiny_rounds_every_k_match_oracle(gpu, O, k):
+    """K = 1 and 3..6 (2 and 4..7 verify rows: the projection, norm-prologue, SwiGLU, conv and
+    attention instances between the 3-row and 8-row ones), round by round with everything each
+    round leaves behind compared with the oracle."""
+    X = gpu
+    cfg = tiny(X, spec_k=k)
+    eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
+    p = prompt_of(cfg, 29, seed=13 + k)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(4):
+        a, b = eng.spec_round(), om.spec_round()
+        assert a == b, (k, r, a, b)
+        check_round_state(eng, om, cfg, f"K={k} round {r}")
+    eng.close()
+    om.close()
+
+
 @pytest.mark.parametrize("inter", [5120, 6144])
 def test_tiny_split_swiglu_units_match_oracle(gpu, O, inter):
     """gate|up with more 32-row SwiGLU units than blocks (one block per CU): 320 units leave 64
