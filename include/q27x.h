@@ -425,7 +425,9 @@ int q27x_bench_mixer(q27x_ctx* ctx, int attn, int pos, int nr, int iters, float*
  * thread. Reports ms per launch over iters launches (device events, null stream). Allocates and
  * frees its own buffers. */
 int q27x_bench_stream(int mode, size_t bytes, int blocks_per_cu, int unroll, int iters, float* ms);
-/* Raw access for tests: copy a device tensor of the context to the host by name. */
+/* Raw access for tests: copy a device tensor of the context to the host by name. The name
+ * "pf_allocs" instead gives (int32) the number of device allocations held for the prefill GEMM's
+ * weight copies, which a weight reload releases. */
 int q27x_debug_read(q27x_ctx* ctx, const char* name, int layer, void* dst, size_t bytes);
 
 #ifdef __cplusplus

@@ -837,6 +837,23 @@ static int gen_i8m(q27x_ctx* x, Mat& m, int rows, int K) {
     x->weight_bytes += (size_t)rows * K + (size_t)rows * (K / 64) * 4;
     return Q27X_OK;
 }
+// Everything made from the current weights that a reload must not reuse: the captured round and
+// plain-step graphs (their kernel arguments hold weight pointers, alphas, alpha selectors and input
+// scales by value) and the prefill GEMM copies of the matrices. Both loaders call this before
+// they touch the weight arena; nothing may still be running on the context's streams.
+static int drop_weight_derived(q27x_ctx* x) {
+    Q27X_HIP(hipSetDevice(x->device));
+    Q27X_HIP(hipStreamSynchronize(x->stream));
+    for (hipStream_t ps : x->pf_stream) if (ps) Q27X_HIP(hipStreamSynchronize(ps));
+    if (x->g_spec) (void)hipGraphExecDestroy(x->g_spec);
+    if (x->g_plain) (void)hipGraphExecDestroy(x->g_plain);
+    x->g_spec = x->g_plain = nullptr;
+    x->g_spec_k = 0;
+    for (void* p : x->pf_walloc) (void)hipFree(p);
+    x->pf_walloc.clear();
+    x->pf_wready = 0;
+    return Q27X_OK;
+}
 static uint16_t* gen_vec(q27x_ctx* x, uint64_t seed, uint64_t t, size_t n, float stdv, float mean, int uni) {
     uint16_t* p = (uint16_t*)walloc(x, n * 2);
     if (!p) return nullptr;
@@ -850,6 +867,9 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     const q27x_config& c = x->c;
     const int H = x->H, I = x->I;
     hipStream_t s = x->stream;
+    int rc = drop_weight_derived(x);
+    if (rc) return rc;
+    x->loaded = 0;
     x->woff = 0; x->weight_bytes = 0;
     // (a checkpoint loaded before may have left per-tensor scales: generated weights have none)
     for (LayerDev& Y : x->L) {
@@ -859,7 +879,6 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
     x->mtp.qkv = x->mtp.o = x->mtp.gu = Mat{};
     for (Mat& m : x->mtp.down4) m = Mat{};
     x->fc0 = x->fc1 = Mat{};
-    int rc;
 #define GEN(m, rows, K) if ((rc = gen_i8m(x, m, rows, K))) return rc
 #define VEC(dst, t, n, sd, mn, uni) if (!((dst) = gen_vec(x, seed, t, n, sd, mn, uni))) { set_error("weight generation"); return Q27X_E_NOMEM; }
     // slices: 0 = one down matrix (trunk layers), 4 = four [H][I/4] column slices (the MTP layer)
@@ -1191,6 +1210,7 @@ int q27x_load_checkpoint(q27x_ctx* x, const q27x_ckpt* ck, char* err, size_t err
     if (!x || !ck) { set_error("q27x_load_checkpoint: null argument"); return Q27X_E_ARG; }
     int rc = q27x_ckpt_check(ck, &x->c, err, errcap);
     if (rc) return rc;
+    if ((rc = drop_weight_derived(x))) return rc;
     x->loaded = 0;
     x->woff = 0; x->weight_bytes = 0;
     for (LayerDev& Y : x->L) { Y.qkvz = Y.out_proj = Y.qkv = Y.o = Y.gu = Y.down = Mat{}; }
@@ -1976,6 +1996,12 @@ int q27x_bench_mixer(q27x_ctx* x, int attn, int pos, int nr, int iters, float* m
 
 int q27x_debug_read(q27x_ctx* x, const char* name, int layer, void* dst, size_t bytes) {
     if (!x || !name || !dst) return Q27X_E_ARG;
+    if (!strcmp(name, "pf_allocs")) {   // device allocations held for the prefill GEMM's weight copies
+        const int32_t cnt = (int32_t)x->pf_walloc.size();
+        if (bytes < 4) return Q27X_E_ARG;
+        memcpy(dst, &cnt, 4);
+        return Q27X_OK;
+    }
     const void* src = nullptr;
     size_t n = 0;
     const LayerDev* Y = (layer >= 0 && layer < x->c.n_layers) ? &x->L[layer] : &x->mtp;

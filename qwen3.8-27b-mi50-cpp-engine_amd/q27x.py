@@ -248,6 +248,9 @@ class Engine:
         self.ctx = p.value
         call("q27x_load_synthetic", self.ctx, seed)
 
+    def load_synthetic(self, seed):
+        call("q27x_load_synthetic", self.ctx, seed)
+
     def load_checkpoint(self, ck):
         err = ctypes.create_string_buffer(512)
         rc = lib().q27x_load_checkpoint(self.ctx, ck.ck, err, len(err))

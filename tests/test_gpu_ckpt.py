@@ -67,3 +67,52 @@ def test_checkpoint_shape_mismatch_is_refused(gpu, tmp_path):
     assert eng.prefill(prompt_of(eng.cfg, 9)) == first       # still the generated weights
     eng.close()
     ck.close()
+
+
+def test_reload_after_rounds_matches_oracle(gpu, O, tmp_path):
+    """New weights on a context that already ran with other ones: the captured round and plain-step
+    graphs hold weight pointers, alphas and input scales, and the GEMM prefill holds its own copy of
+    every matrix. After load_checkpoint (and back to generated weights with load_synthetic) the
+    prefill, the rounds and the GEMM prefill follow the new weights, bit for bit against the oracle,
+    and the old GEMM copies are released instead of piling up."""
+    X = gpu
+    cfg = X.tiny_config(spec_k=2, n_layers=4)
+    eng = X.Engine(cfg, SEED)                         # generated weights
+    p = prompt_of(cfg, 29, seed=12)
+    eng.prefill_gemm(p)                               # GEMM copies of the generated weights
+    eng.spec_round()                                  # round graph captured on them
+    eng.decode_step()                                 # plain-step graph too
+    held = int(eng.read("pf_allocs", -1, np.int32, 1)[0])
+    assert held > 0
+    syn = CS.Synth(cfg, seed=11)
+    n, b = CS.write(syn.t, tmp_path)
+    ck = X.Checkpoint(tmp_path, 3, n, b)
+    eng.load_checkpoint(ck)
+    assert int(eng.read("pf_allocs", -1, np.int32, 1)[0]) == 0
+    om = O.Model(cfg, SEED)
+    CS.install_into_oracle(O, om, syn)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(3):
+        a, b_ = eng.spec_round(), om.spec_round()
+        assert a == b_, (r, a, b_)
+        check_round_state(eng, om, cfg, f"reloaded round {r}")
+    assert eng.decode_step() == om.decode_step()
+    assert eng.prefill_gemm(p) == om.prefill_gemm(p, 0)
+    check_prefill_state(eng, om, cfg, "reloaded GEMM prefill")
+    assert int(eng.read("pf_allocs", -1, np.int32, 1)[0]) == held
+    a, b_ = eng.spec_round(), om.spec_round()
+    assert a == b_
+    om.close()
+    # and back to generated weights
+    eng.load_synthetic(SEED)
+    assert int(eng.read("pf_allocs", -1, np.int32, 1)[0]) == 0
+    om2 = O.Model(cfg, SEED)
+    assert eng.prefill(p) == om2.prefill(p)
+    for r in range(2):
+        a, b_ = eng.spec_round(), om2.spec_round()
+        assert a == b_, (r, a, b_)
+        check_round_state(eng, om2, cfg, f"generated again, round {r}")
+    assert eng.decode_step() == om2.decode_step()
+    om2.close()
+    eng.close()
+    ck.close()
