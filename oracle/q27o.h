@@ -25,7 +25,14 @@
  * own KV cache, the four bf16-rounded down slices, mtp.norm + lm_head) is pinned against a float64
  * forward written from its definition, with planted composition mistakes shown to fail
  * (tests/test_oracle_mtp.py); the draft hand-off by spec == plain greedy under forced drafts with
- * planted wrong tokens (tests/test_oracle_model.py).
+ * planted wrong tokens (tests/test_oracle_model.py). The trunk's composition (verify(); the
+ * reference's run_layer_tp_nr, src/q27_main.cpp:2271-2489, head 2457-2481: input norm, mixer,
+ * out_proj / o_proj + residual, post norm from the fp32 r1, MLP + residual on bf16(r1), the head's
+ * bf16(bf16(r1) + r2), final norm, lm_head) is pinned against float64 forwards written from its
+ * definition: the ideal forward end to end within the quantization error, and a storage-faithful
+ * forward stage by stage from the oracle's own traced inputs (r1, the post-norm codes, r2, the
+ * final residual bits, the logits); planted composition and storage-point mistakes fail both
+ * (tests/test_oracle_trunk.py).
  */
 #ifndef Q27O_H
 #define Q27O_H
@@ -150,6 +157,11 @@ int  q27o_model_prefill(q27o_model* m, const int32_t* ids, int n);          /* r
 int  q27o_model_decode_step(q27o_model* m);                                 /* returns token */
 int  q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced); /* ncommit */
 int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx);
+int  q27o_model_verify_logits(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance);
+/* The same pass recording, per layer, r1 and r2 (fp32 [n_layers][nr][H]) and the post norm's codes
+ * and per-16 scales ([n_layers][nr][H], [n_layers][nr][H/16]); any of them may be NULL. */
+int  q27o_model_verify_trace(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance,
+                             float* r1, float* r2, int8_t* pq, float* ps);
 /* Layer-major prefill on the GEMM representation (chunks of `chunk` tokens): every projection as
  * the per-(row, group) x per-(token, group) int8 GEMM (group 1024, or the whole K when 1024 does
  * not divide it), everything else in the decode path's arithmetic; the MTP prompt pass computes

@@ -67,6 +67,8 @@ _SIGS = {
     "q27o_rmsnorm_f32_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, I, I, I], None),
     "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
     "q27o_model_verify_rows": ([VP, I, VP, VP], I),
+    "q27o_model_verify_logits": ([VP, I, VP, VP, VP, I], I),
+    "q27o_model_verify_trace": ([VP, I, VP, VP, VP, I, VP, VP, VP, VP], I),
     "q27o_model_mtp_pass": ([VP, I, VP, VP, I, I, VP, VP], I),
     "q27o_model_weight_bytes": ([VP], D),
     "q27o_model_tensor": ([VP, ctypes.c_char_p, I, VP], VP),
@@ -141,6 +143,37 @@ class Model:
         nx = np.zeros(8, np.int32)
         lib().q27o_model_verify_rows(self.m, len(toks), toks.ctypes.data, nx.ctypes.data)
         return nx[: len(toks)].tolist()
+
+    def verify_logits(self, toks, advance=True):
+        """One verify pass over toks at the current position: (argmax per row, logits [nr][vocab],
+        final residual rows [nr][H] bf16 bits); advance commits the rows (pos += nr)."""
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        nr = len(toks)
+        nx = np.zeros(8, np.int32)
+        lg = np.zeros((nr, self.cfg.vocab), np.float32)
+        rc = lib().q27o_model_verify_logits(self.m, nr, toks.ctypes.data, nx.ctypes.data, lg.ctypes.data,
+                                             1 if advance else 0)
+        if rc:
+            raise ValueError("verify_logits: bad row count or position")
+        hf = self.tensor("hfinal", -1, np.uint16)[: nr * self.cfg.hidden].reshape(nr, self.cfg.hidden)
+        return nx[:nr].tolist(), lg, hf
+
+    def verify_trace(self, toks, advance=True):
+        """verify_logits plus, per layer, r1 and r2 (fp32 [n_layers][nr][H]) and the post norm's
+        codes [n_layers][nr][H] and per-16 scales [n_layers][nr][H/16]."""
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        nr, nl, H = len(toks), self.cfg.n_layers, self.cfg.hidden
+        nx = np.zeros(8, np.int32)
+        lg = np.zeros((nr, self.cfg.vocab), np.float32)
+        r1, r2 = np.zeros((nl, nr, H), np.float32), np.zeros((nl, nr, H), np.float32)
+        pq, ps = np.zeros((nl, nr, H), np.int8), np.zeros((nl, nr, H // 16), np.float32)
+        rc = lib().q27o_model_verify_trace(self.m, nr, toks.ctypes.data, nx.ctypes.data, lg.ctypes.data,
+                                            1 if advance else 0, r1.ctypes.data, r2.ctypes.data, pq.ctypes.data,
+                                            ps.ctypes.data)
+        if rc:
+            raise ValueError("verify_trace: bad row count or position")
+        hf = self.tensor("hfinal", -1, np.uint16)[: nr * H].reshape(nr, H)
+        return dict(nx=nx[:nr].tolist(), logits=lg, hfinal=hf, r1=r1, r2=r2, pq=pq, ps=ps)
 
     def mtp_pass(self, hrows, toks, dpos0, head_row):
         """One MTP pass over rows (hrows [nr][H] bf16 bits, toks [nr]) at draft positions

@@ -67,6 +67,11 @@ struct q27o_model {
     int32_t dt[8], dt_raw[8], nx[8];
     int nacc_last;
     double wbytes;
+    float* vlogits;               /* when set, the next verify's logits [rows][vocab] go here */
+    /* when set, the next verify records per layer L (each [n_layers][rows][...]): the fp32
+     * residual after the mixer r1 and after the MLP r2, and the post norm's int8 codes and per-16
+     * scales (the MLP's input) */
+    float *tr_r1, *tr_r2, *tr_ps; int8_t* tr_pq;
 };
 
 /* ------------------------------------------------------------------ generation */
@@ -318,12 +323,18 @@ static void verify(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
             q27o_quant_rows(mix, nz, xq, nz, xs, nz / 16, nz, Y->is_out, nr);       /* out_proj's input_scale */
             q27o_proj_rows_epi(Y->out_proj.w, Y->out_proj.s, Y->al_o, H, nz, xq, nz, xs, x, H, 0, h, 1, H, 1.0f, nr);
         }
+        if (m->tr_r1) memcpy(m->tr_r1 + (size_t)L * nr * H, x, (size_t)nr * H * 4);
         /* post norm (q27_rmsnorm_hostss_perm_b, natural order here): h = bf16(r1) */
         q27o_rmsnorm_quant_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, xq, xs, 0, Y->is_post, nr);
+        if (m->tr_pq) {
+            memcpy(m->tr_pq + (size_t)L * nr * H, xq, (size_t)nr * H);
+            memcpy(m->tr_ps + (size_t)L * nr * (H / 16), xs, (size_t)nr * (H / 16) * 4);
+        }
         q27o_proj_rows(Y->gate.w, Y->gate.s, Y->al_gate, I, H, xq, H, xs, g, I, nr);
         q27o_proj_rows(Y->up.w, Y->up.s, Y->al_up, I, H, xq, H, xs, u, I, nr);
         q27o_swiglu_quant_rows(g, u, I, xq, xs, I, Y->is_down, nr);
         q27o_proj_rows_epi(Y->down.w, Y->down.s, Y->al_down, H, I, xq, I, xs, x, H, 0, h, 1, H, 1.0f, nr);
+        if (m->tr_r2) memcpy(m->tr_r2 + (size_t)L * nr * H, x, (size_t)nr * H * 4);
     }
     /* head (src/q27_main.cpp:2457-2481): hid = bf16(bf16(r1) + r2) -- the residual the reference
      * adds twice -- or bf16(r2); final norm; lm_head; argmax */
@@ -339,6 +350,7 @@ static void verify(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
         q27o_bf16_gemv_rows(m->lm_head, c->vocab, H, y, H, logits, c->vocab, nr);
         float val[8];
         q27o_argmax_rows(logits, c->vocab, c->vocab, nr, nx, val);
+        if (m->vlogits) memcpy(m->vlogits, logits, (size_t)nr * c->vocab * 4);
         free(logits);
     }
     m->gdn_npend = nr;   /* default: every row committed (plain step / prefill); spec overrides */
@@ -671,6 +683,23 @@ int q27o_model_mtp_pass(q27o_model* m, int nr, const uint16_t* hrows, const int3
 
 int q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx) {
     verify(m, nr, toks, nx);
+    return 0;
+}
+
+/* One verify pass at the current position with its logits [nr][vocab] (for the float64 pin of the
+ * trunk composition). advance != 0 commits the rows as a prompt chunk does: pos += nr. */
+int q27o_model_verify_logits(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance) {
+    return q27o_model_verify_trace(m, nr, toks, nx, logits, advance, NULL, NULL, NULL, NULL);
+}
+int q27o_model_verify_trace(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance,
+                            float* r1, float* r2, int8_t* pq, float* ps) {
+    if (nr < 1 || nr > 8 || m->pos + nr > m->c.ctx || (pq && !ps)) return -1;
+    m->vlogits = logits;
+    m->tr_r1 = r1; m->tr_r2 = r2; m->tr_pq = pq; m->tr_ps = ps;
+    verify(m, nr, toks, nx);
+    m->vlogits = NULL;
+    m->tr_r1 = m->tr_r2 = m->tr_ps = NULL; m->tr_pq = NULL;
+    if (advance) m->pos += nr;
     return 0;
 }
 

@@ -223,3 +223,188 @@ def mtp_forward(W, c, hrows, toks, pos0, swap_halves=False, plus_one=None, drop_
     xn = rmsnorm(res, bf2f(W["mtp_norm"]), 1.0, eps)
     logits = xn @ bf2f(W["lm_head"]).reshape(-1, H).astype(np.float64).T
     return res, logits
+
+
+def absmax_codes(v, group):
+    """int8 absmax codes per `group` of the last axis, decided in float32 as the reference's
+    quantizer does (src/q27_fp8.hip:373-425 with in_scale 1: s = mx (1/127), inv = 1/s,
+    q = clamp(rintf(v inv), -127, 127)). Returns (codes [..., n] int8, scales [..., n/group] float32)."""
+    v = np.asarray(v, np.float64).astype(np.float32)
+    g = v.reshape(v.shape[:-1] + (v.shape[-1] // group, group))
+    s = (np.abs(g).max(axis=-1, keepdims=True) * np.float32(1.0 / 127.0)).astype(np.float32)
+    inv = np.where(s > 0, np.float32(1.0) / np.where(s > 0, s, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    q = np.clip(np.rint((g * inv).astype(np.float32)), -127, 127).astype(np.int8)
+    return q.reshape(v.shape), s[..., 0]
+
+
+def trunk_forward(W, c, toks, faithful=False, plant=None, trace=None, force=None):
+    """The verify trunk (run_layer_tp_nr, src/q27_main.cpp:2271-2489, and its head 2457-2481) in
+    float64, written from the layer definition, for tokens toks at positions 0..n-1 from an empty
+    state. Per layer L (attention when L % attn_period == attn_period - 1, else Gated DeltaNet):
+      n   = rmsnorm(x_L) (1 + w_in)                  x_0 = emb[tok]; x_L = r2 of layer L-1
+      r1  = x_L + out_proj(mixer(n))                 (o_proj for attention)
+      r2  = r1 + down(silu(gate(m)) * up(m)),  m = rmsnorm(r1) (1 + w_post)
+    head: hfin = r1 + r2 of the last layer (the reference adds the residual twice, 2471), then
+    logits = lm_head rmsnorm(hfin) (1 + w_final).
+    GDN mixer: causal depthwise conv4 + SiLU over the q|k|v channels; per value head h (key head
+    h // (vh/kh)) q^ = q/||q||/sqrt(d), k^ = k/||k||, beta = sigmoid(b), decay = exp(-exp(A_log)
+    softplus(a + dt_bias)), S <- decay S + k^ (beta (v - decay S^T k^))^T, o = S^T q^,
+    y = o / rms(o) * w_norm * silu(z); a, b = in_a n, in_b n.
+    Attention mixer: per head RMSNorm (1 + w), rotate-half RoPE on the first rot dims, causal GQA
+    softmax attention, output * sigmoid(gate) (gate rows follow each head's q rows in q_proj).
+
+    faithful=False: every value float64, no rounding or quantization (the "ideal" model).
+    faithful=True: the reference's storage points applied, every sum still float64: bf16 where it
+    stores bf16 (the residual copy x_L and r1, projection outputs, the normed rows, conv and mixer
+    outputs, the final residual and its norm), int8 absmax codes per 16 of every projection input
+    (layer 0 codes the bf16 normed rows, later layers the unrounded ones), the fp32 residual r1 / r2
+    unrounded, K and V as int8 per kv_group.
+    plant names one composition mistake, to show that a comparison rejects it:
+      "drop_out_residual"   r1 = out_proj(...) in the GDN layers (residual not added)
+      "single_head_residual" hfin = r2 (no double count)
+      "post_norm_bf16"      the post norm reads bf16(r1) instead of r1
+      "zgate_before_norm"   y = rmsnorm(o * silu(z)) * w_norm (gate applied before the norm)
+      "attn_gate_dropped"   attention output without the sigmoid gate
+    W: {"layers": [per-layer dicts], "emb", "final_norm", "lm_head"} of the oracle's weights.
+    trace: an optional dict that receives the intermediate values, keyed (layer, stage): "r1"
+    (before any forcing), "a2" (the post norm's int8 codes, faithful mode), "r2".
+    force: optional values that replace the forward's own at a stage boundary (teacher forcing,
+    so that a comparison of one stage does not inherit rounding flips of earlier ones): (L, "x")
+    the input rows of layer L >= 1 (r2 of layer L-1), (L, "r1") the residual after layer L's mixer,
+    ("head", "r2") the last layer's r2.
+    Returns (hfin [n][H], logits [n][vocab]) float64."""
+    force = force or {}
+    H, eps = c["hidden"], c["rms_eps"]
+    D, kh, vh = c["gdn_d"], c["gdn_kh"], c["gdn_vh"]
+    hd, nq, nkv = c["head_dim"], c["n_q"], c["n_kv"]
+    toks = np.asarray(toks)
+    n = len(toks)
+
+    def R(v):
+        v = np.asarray(v, np.float64)
+        return bf2f(bf16_rne(v.astype(np.float32))).astype(np.float64).reshape(v.shape) if faithful else v
+
+    def Q(v, group=16):
+        v = np.asarray(v, np.float64)
+        if not faithful:
+            return v
+        q, s = absmax_codes(v, group)
+        return (q.astype(np.float64) * np.repeat(s.astype(np.float64), group, axis=-1)).reshape(v.shape)
+
+    def wmat(Wl, name):
+        return dequant_rows(Wl[name + "_w"], Wl[name + "_s"])
+
+    def norm(x, w, plus=1.0):
+        return rmsnorm(x, bf2f(w), plus, eps)
+
+    emb = bf2f(W["emb"]).reshape(-1, H).astype(np.float64)
+    x = emb[toks]
+    h = x.copy()                 # the residual operand of the layer (bf16 copy of x_L)
+    r1 = r2 = None
+    for L, Wl in enumerate(W["layers"]):
+        is_attn = (L % c["attn_period"]) == c["attn_period"] - 1
+        if L == 0:
+            nn_ = norm(x, Wl["in_norm"])
+            y = R(nn_)
+            a_in = Q(y)
+        else:
+            r2 = np.asarray(force.get((L, "x"), r2), np.float64)
+            nn_ = norm(r2, Wl["in_norm"])
+            h = R(r2)
+            y = R(nn_)
+            a_in = Q(nn_)
+        if is_attn:
+            qkv = R(a_in @ wmat(Wl, "qkv").T)
+            if trace is not None:
+                trace[(L, "a_in")], trace[(L, "qkv")] = a_in, qkv
+            qw = 2 * hd if c["attn_gate"] else hd
+            qrows = nq * qw
+            qn, kn = bf2f(Wl["q_norm"]).astype(np.float64), bf2f(Wl["k_norm"]).astype(np.float64)
+            Qh = np.zeros((n, nq, hd)); Gt = np.zeros((n, nq, hd))
+            Kh = np.zeros((n, nkv, hd)); Vh = np.zeros((n, nkv, hd))
+            for r in range(n):
+                for hh in range(nq):
+                    q = qkv[r, hh * qw: hh * qw + hd]
+                    q = q / np.sqrt((q * q).mean() + eps) * (1.0 + qn)
+                    Qh[r, hh] = R(rope_rotate(q, r, c["rot_dims"], c["rope_theta"]))
+                    if c["attn_gate"]:
+                        Gt[r, hh] = qkv[r, hh * qw + hd: hh * qw + 2 * hd]
+                for kv in range(nkv):
+                    k = qkv[r, qrows + kv * hd: qrows + (kv + 1) * hd]
+                    k = k / np.sqrt((k * k).mean() + eps) * (1.0 + kn)
+                    Kh[r, kv] = Q(rope_rotate(k, r, c["rot_dims"], c["rope_theta"]), c["kv_group"])
+                    Vh[r, kv] = Q(qkv[r, qrows + nkv * hd + kv * hd: qrows + nkv * hd + (kv + 1) * hd], c["kv_group"])
+            att = np.zeros((n, nq * hd))
+            grp = nq // nkv
+            for r in range(n):
+                for hh in range(nq):
+                    kv = hh // grp
+                    sc = Kh[: r + 1, kv] @ Qh[r, hh] / np.sqrt(hd)
+                    p = np.exp(sc - sc.max())
+                    o = (p @ Vh[: r + 1, kv]) / p.sum()
+                    if c["attn_gate"] and plant != "attn_gate_dropped":
+                        o = o * sigmoid(Gt[r, hh])
+                    att[r, hh * hd:(hh + 1) * hd] = R(o)
+            if trace is not None:
+                trace[(L, "q")], trace[(L, "k")], trace[(L, "v")], trace[(L, "att")] = Qh, Kh, Vh, att
+            r1 = h + Q(att) @ wmat(Wl, "o").T
+        else:
+            nqkv = (2 * kh + vh) * D
+            qkvz = R(a_in @ wmat(Wl, "qkvz").T)
+            qkv_raw, z = qkvz[:, :nqkv], qkvz[:, nqkv:]
+            ab_a = R(y @ bf2f(Wl["in_a"]).reshape(vh, H).astype(np.float64).T)
+            ab_b = R(y @ bf2f(Wl["in_b"]).reshape(vh, H).astype(np.float64).T)
+            cw = bf2f(Wl["conv_w"]).astype(np.float64).reshape(nqkv, 4)
+            A_log = bf2f(Wl["A_log"]).astype(np.float64)
+            dt_bias = bf2f(Wl["dt_bias"]).astype(np.float64)
+            w_norm = bf2f(Wl["gdn_norm"]).astype(np.float64)
+            hist = np.zeros((nqkv, 3))
+            S = np.zeros((vh, D, D))
+            ratio = vh // kh
+            mix = np.zeros((n, vh * D))
+            for t in range(n):
+                win = np.concatenate([hist, qkv_raw[t][:, None]], axis=1)
+                cv = R(silu((win * cw).sum(axis=1)))
+                hist = win[:, 1:]
+                for hh in range(vh):
+                    kk = hh // ratio
+                    q = cv[kk * D:(kk + 1) * D]
+                    k = cv[kh * D + kk * D: kh * D + (kk + 1) * D]
+                    v = cv[2 * kh * D + hh * D: 2 * kh * D + (hh + 1) * D]
+                    qh_ = q / np.sqrt((q * q).sum() + 1e-6) / np.sqrt(D)
+                    kh_ = k / np.sqrt((k * k).sum() + 1e-6)
+                    beta = sigmoid(ab_b[t, hh])
+                    decay = np.exp(-np.exp(A_log[hh]) * softplus(ab_a[t, hh] + dt_bias[hh]))
+                    delta = beta * (v - decay * (S[hh].T @ kh_))
+                    S[hh] = decay * S[hh] + np.outer(kh_, delta)
+                    o = S[hh].T @ qh_
+                    g = silu(z[t, hh * D:(hh + 1) * D])
+                    if plant == "zgate_before_norm":
+                        og = o * g
+                        yv = og / np.sqrt((og * og).mean() + eps) * w_norm
+                    else:
+                        yv = o / np.sqrt((o * o).mean() + eps) * w_norm * g
+                    mix[t, hh * D:(hh + 1) * D] = R(yv)
+            if trace is not None:
+                trace[(L, "qkvz")], trace[(L, "a")], trace[(L, "b")], trace[(L, "mix")] = qkvz, ab_a, ab_b, mix
+            proj = Q(mix) @ wmat(Wl, "out").T
+            r1 = proj if plant == "drop_out_residual" else h + proj
+        if trace is not None:
+            trace[(L, "r1")] = r1
+        r1 = np.asarray(force.get((L, "r1"), r1), np.float64)
+        m = norm(R(r1) if plant == "post_norm_bf16" else r1, Wl["post_norm"])
+        h = R(r1)
+        a2 = Q(m)
+        g = a2 @ wmat(Wl, "gate").T
+        u = a2 @ wmat(Wl, "up").T
+        r2 = h + Q(silu(g) * u) @ wmat(Wl, "down").T
+        if trace is not None:
+            trace[(L, "a2")], trace[(L, "r2")] = absmax_codes(m, 16)[0] if faithful else None, r2
+    r2 = np.asarray(force.get(("head", "r2"), r2), np.float64)
+    if c["head_double_residual"] and plant != "single_head_residual":
+        hfin = R(R(r1) + r2)
+    else:
+        hfin = R(r2)
+    nf = R(norm(hfin, W["final_norm"]))
+    logits = nf @ bf2f(W["lm_head"]).reshape(-1, H).astype(np.float64).T
+    return hfin, logits
