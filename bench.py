@@ -81,25 +81,41 @@ def best_of(fn, reps):
     return min(ts), float(np.median(ts))
 
 
-def cpu_baseline(cfg_dict, q27o, k):
-    """The oracle's integer path (int8 x int8 -> int32 per 16, fp32 scaling, OpenMP over output rows)
-    on a bounded sample of one round: the (k+1)-row verify of a 4-layer full-width slice (3 GDN + 1
-    attention) with the lm_head, the lm_head alone, and one single-row MTP draft pass with its head.
-    A round is 16 x (slice - lm_head) + lm_head + k drafts (one token per round at natural
-    acceptance on random weights)."""
+def cpu_baseline(cfg_dict, q27o, k, pos):
+    """The oracle's integer path (int8 x int8 -> int32 per 16, fp32 scaling; OpenMP over output rows,
+    attention (row, head) pairs and GDN value heads) on a bounded sample of one round at the GPU
+    line's context: the (k+1)-row verify of a 4-layer full-width slice (3 GDN + 1 attention) at
+    positions pos.. with the lm_head, the lm_head alone, and one single-row MTP draft pass with its
+    head at draft position pos - 1. The attention layer's and the MTP layer's KV caches hold pos
+    positions of seeded random int8 codes and scales (the cost of a verify depends on the cache
+    length, not on how the cache was filled). A round is 16 x (slice - lm_head) + lm_head + k drafts
+    (one token per round at natural acceptance on random weights)."""
     d = dict(cfg_dict)
     d["n_layers"] = 4
-    d["ctx"] = 256
+    d["ctx"] = pos + 64
     t0 = time.time()
     m = q27o.Model(d, SEED)
     gen_s = time.time() - t0
     lib = q27o.lib()
     H, V = d["hidden"], d["vocab"]
-    prompt = np.random.default_rng(1).integers(0, V, 8).astype(np.int32)
-    m.prefill(prompt)
+    rng = np.random.default_rng(3)
+    kvr = d["n_kv"] * d["head_dim"]
+    for layer in (3, -1):
+        for name in ("kc", "vc"):
+            codes = np.zeros((d["ctx"], kvr), np.int8)
+            codes[:pos] = rng.integers(-127, 128, (pos, kvr), dtype=np.int8)
+            m.set_tensor(name, layer, codes)
+        for name in ("ks", "vs"):
+            sc = np.zeros((d["ctx"], kvr // d["kv_group"]), np.float32)
+            sc[:pos] = rng.uniform(1e-3, 2e-2, (pos, kvr // d["kv_group"]))
+            m.set_tensor(name, layer, sc)
     toks = np.arange(1, k + 2, dtype=np.int32)
     nx = np.zeros(8, np.int32)
-    t_slice, _ = best_of(lambda: lib.q27o_model_verify_rows(m.m, k + 1, toks.ctypes.data, nx.ctypes.data), 3)
+
+    def slice_verify():
+        lib.q27o_model_set_pos(m.m, pos)
+        lib.q27o_model_verify_rows(m.m, k + 1, toks.ctypes.data, nx.ctypes.data)
+    t_slice, _ = best_of(slice_verify, 3)
     lm = m.tensor("lm_head", -1, np.uint16)
     y = q27o.f2bf(np.random.default_rng(2).standard_normal((k + 1, H)).astype(np.float32))
     logits = np.empty((k + 1, V), np.float32)
@@ -111,17 +127,18 @@ def cpu_baseline(cfg_dict, q27o, k):
     t_head, _ = best_of(head, 3)
     del lm
     hrow = y[:1].copy()
-    t_draft, _ = best_of(lambda: m.mtp_pass(hrow, toks[:1], 8, 0), 3)
+    t_draft, _ = best_of(lambda: m.mtp_pass(hrow, toks[:1], pos - 1, 0), 3)
     m.close()
     scale = cfg_dict["n_layers"] / 4.0
     round_s = scale * max(t_slice - t_head, 0.0) + t_head + k * t_draft
     info = host_info()
     return {"value": round(1.0 / round_s, 4), "unit": "committed tok/s", "cores": info["omp_threads"],
             "kind": "port", **info,
-            "sample": f"best of 3: {k + 1}-row verify of a 4-layer full-width slice (3 GDN + 1 attention) + "
-                      f"lm_head {t_slice:.3f} s, lm_head alone {t_head:.3f} s, one MTP draft pass {t_draft:.3f} s; "
-                      f"round = {scale:.0f} x (slice - lm_head) + lm_head + {k} drafts = {round_s:.2f} s at one "
-                      f"token per round; weight generation {gen_s:.1f} s not timed"}
+            "sample": f"best of 3 at context {pos}: {k + 1}-row verify of a 4-layer full-width slice (3 GDN + "
+                      f"1 attention) + lm_head {t_slice:.3f} s, lm_head alone {t_head:.3f} s, one MTP draft pass "
+                      f"{t_draft:.3f} s; round = {scale:.0f} x (slice - lm_head) + lm_head + {k} drafts = "
+                      f"{round_s:.2f} s at one token per round; KV caches of {pos} positions filled with seeded "
+                      f"random codes; weight generation {gen_s:.1f} s not timed"}
 
 
 # ---------------------------------------------------------------- BASELINE configs 0-2
@@ -153,8 +170,9 @@ def cpu_configs(q27o, attn_ctx, reps=5):
     tmin, tmed = best_of(lambda: L.q27o_proj_rows(W.ctypes.data, WS.ctypes.data, 1.0, I, H, xq.ctypes.data, H,
                                                   xs.ctypes.data, y.ctypes.data, I, nr), reps)
     b0 = I * H * i8 + nr * H * (1 + 4.0 / 16) + nr * I * 4
+    threads = host_info()["omp_threads"]
     out["config0_projection"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3),
-                                 "bytes": b0, "GB_s": round(b0 / tmin / 1e9, 2)}
+                                 "bytes": b0, "GB_s": round(b0 / tmin / 1e9, 2), "threads": threads}
     del W, WS
     # shared: the layer input (fp32 residual rows), its norm + quantize
     xres = rng.standard_normal((nr, H)).astype(np.float32)
@@ -203,7 +221,7 @@ def cpu_configs(q27o, attn_ctx, reps=5):
     b1 = ((nqkv + nz) * H * i8 + nr * H * 4 + nr * (nqkv + nz) * 2 + 2.0 * VH * H * 2 + nqkv * 4 * 2 +
           2.0 * VH * D * D * 4 + H * nz * i8 + nr * H * 6)
     out["config1_gdn_layer"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3), "bytes": b1,
-                                "GB_s": round(b1 / tmin / 1e9, 2)}
+                                "GB_s": round(b1 / tmin / 1e9, 2), "threads": threads}
     del Wz, Sz, Wo, So
     # config 2: one attention layer's mixer at contexts attn_ctx
     NQ, NKV, HD, G = c["NQ"], c["NKV"], c["HD"], c["GROUP"]
@@ -240,7 +258,7 @@ def cpu_configs(q27o, attn_ctx, reps=5):
         b2 = ((qr + 2 * kvr) * H * i8 + nr * H * 4 + nr * (qr + 2 * kvr) * 2 + 2.0 * ctx * kvr * (1 + 4.0 / G) +
               H * att * i8 + nr * H * 6)
         out[f"config2_attention_ctx{L0}"] = {"ms": round(tmin * 1e3, 3), "ms_median": round(tmed * 1e3, 3),
-                                             "bytes": b2, "GB_s": round(b2 / tmin / 1e9, 2)}
+                                             "bytes": b2, "GB_s": round(b2 / tmin / 1e9, 2), "threads": threads}
     out["host"] = host_info()
     return out
 
@@ -505,7 +523,7 @@ def main():
     if not args.no_cpu:
         q27o = _load("q27o", os.path.join(ROOT, "oracle", "q27o.py"))
         log("cpu baseline (oracle) ...")
-        cpu = cpu_baseline(cfg.as_dict(), q27o, K)
+        cpu = cpu_baseline(cfg.as_dict(), q27o, K, args.prompt)
         log(f"cpu: {cpu}")
         cpu_cfg = cpu_configs(q27o, attn_ctx)
         log(f"configs 0-2 (CPU): {cpu_cfg}")

@@ -562,6 +562,7 @@ void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z,
         for (int p = 0; p < npend; ++p) { h[0] = h[1]; h[1] = h[2]; h[2] = P.raw[(size_t)p * nqkv + c]; }
         conv_hist[3 * c] = h[0]; conv_hist[3 * c + 1] = h[1]; conv_hist[3 * c + 2] = h[2];
     }
+#pragma omp parallel for schedule(static)
     for (int hh = 0; hh < vh; ++hh) {
         const int kk = hh / ratio;
         float* Sh = S + (size_t)hh * hs;
@@ -579,7 +580,6 @@ void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z,
     uint16_t* hw = (uint16_t*)malloc((size_t)nqkv * 3 * sizeof(uint16_t));
     memcpy(hw, conv_hist, (size_t)nqkv * 3 * sizeof(uint16_t));
     float* cv = (float*)malloc((size_t)nqkv * sizeof(float));
-    float qn[128], kn[128], qh_[128], kh_[128], mixed[128], A[128], B[128];
     for (int n = 0; n < nr; ++n) {
         const uint16_t* xr = qkv_raw + (size_t)n * qkv_stride;
         for (int c = 0; c < nqkv; ++c) {
@@ -593,7 +593,11 @@ void q27o_gdn_verify(const uint16_t* qkv_raw, int qkv_stride, const uint16_t* z,
             cv[c] = q27o_bf2f(q27o_f2bf(q27o_silu(acc)));
             P.raw[(size_t)n * nqkv + c] = x;
         }
+        /* value heads are independent within a row (each writes only its own state, pending
+         * slots and outputs; the key-head k^ slot by its first value head only): threads over them */
+#pragma omp parallel for schedule(static)
         for (int hh = 0; hh < vh; ++hh) {
+            float qn[128], kn[128], qh_[128], kh_[128], mixed[128], A[128], B[128];
             const int kk = hh / ratio;
             const float* qv = cv + (size_t)kk * d;
             const float* kv = cv + (size_t)kh * d + (size_t)kk * d;
@@ -750,70 +754,73 @@ void q27o_attn_rows(const uint16_t* qh, const uint16_t* qkv_gate, int qkv_stride
     const int kvrows = nkv * hd;
     const int qw = gate ? 2 * hd : hd;
     const float sl2e = (float)((1.0 / sqrt((double)hd)) * 1.4426950408889634);
-    float q[256], kd[256], o[256], os[256];
-    float* yv = (float*)malloc((size_t)nq * hd * sizeof(float));
-    for (int r = 0; r < nr; ++r) {
+    float* yv = (float*)malloc((size_t)nr * nq * hd * sizeof(float));
+    /* every (row, query head) is independent and keeps its own fixed order: threads over them */
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int rh = 0; rh < nr * nq; ++rh) {
+        const int r = rh / nq, hq = rh % nq;
         const int L = pos0 + r + 1;
         const int ns = (L + Q27O_SPLIT - 1) / Q27O_SPLIT;
-        for (int hq = 0; hq < nq; ++hq) {
-            const int kvh = hq / G;
-            for (int i = 0; i < hd; ++i) q[i] = q27o_bf2f(qh[(size_t)r * nq * hd + (size_t)hq * hd + i]);
-            float M = -INFINITY, den = 0.0f;
-            float* ms = (float*)malloc((size_t)ns * sizeof(float));
-            float* ls = (float*)malloc((size_t)ns * sizeof(float));
-            float* ob = (float*)malloc((size_t)ns * hd * sizeof(float));
-            for (int s = 0; s < ns; ++s) {
-                const int k0 = s * Q27O_SPLIT;
-                const int k1 = (k0 + Q27O_SPLIT < L) ? k0 + Q27O_SPLIT : L;
-                float xsc[Q27O_SPLIT];
-                float m = -INFINITY;
-                for (int k = k0; k < k1; ++k) {
-                    const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
-                    for (int i = 0; i < hd; ++i) kd[i] = (float)kc[off + i] * ks[(off + i) / kv_group];
-                    const float x = score_4chain(q, kd, hd) * sl2e;
-                    xsc[k - k0] = x;
-                    m = fmaxf(m, x);
-                }
-                /* l: the 64 keys' p (0 past the valid ones) summed by the shfl_down tree */
-                float pl[Q27O_SPLIT];
-                for (int i = 0; i < Q27O_SPLIT; ++i) pl[i] = 0.0f;
-                float oc[4][256];
-                for (int j = 0; j < 4; ++j)
-                    for (int i = 0; i < hd; ++i) oc[j][i] = 0.0f;
-                for (int k = k0; k < k1; ++k) {
-                    const float p = q27o_exp2(xsc[k - k0] - m);
-                    pl[k - k0] = p;
-                    const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
-                    float* oj = oc[(k - k0) / (Q27O_SPLIT / 4)];
-                    for (int i = 0; i < hd; ++i) oj[i] = fmaf(p, (float)vc[off + i] * vs[(off + i) / kv_group], oj[i]);
-                }
-                for (int i = 0; i < hd; ++i) os[i] = ((oc[0][i] + oc[1][i]) + oc[2][i]) + oc[3][i];
-                const float l = tree64(pl);
-                ms[s] = m; ls[s] = l;
-                memcpy(ob + (size_t)s * hd, os, (size_t)hd * sizeof(float));
-                M = fmaxf(M, m);
+        const int kvh = hq / G;
+        float q[256], kd[256], o[256], os[256];
+        for (int i = 0; i < hd; ++i) q[i] = q27o_bf2f(qh[(size_t)r * nq * hd + (size_t)hq * hd + i]);
+        float M = -INFINITY, den = 0.0f;
+        float* ms = (float*)malloc((size_t)ns * sizeof(float));
+        float* ls = (float*)malloc((size_t)ns * sizeof(float));
+        float* ob = (float*)malloc((size_t)ns * hd * sizeof(float));
+        for (int s = 0; s < ns; ++s) {
+            const int k0 = s * Q27O_SPLIT;
+            const int k1 = (k0 + Q27O_SPLIT < L) ? k0 + Q27O_SPLIT : L;
+            float xsc[Q27O_SPLIT];
+            float m = -INFINITY;
+            for (int k = k0; k < k1; ++k) {
+                const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
+                for (int i = 0; i < hd; ++i) kd[i] = (float)kc[off + i] * ks[(off + i) / kv_group];
+                const float x = score_4chain(q, kd, hd) * sl2e;
+                xsc[k - k0] = x;
+                m = fmaxf(m, x);
             }
-            for (int i = 0; i < hd; ++i) o[i] = 0.0f;
-            for (int s = 0; s < ns; ++s) {
-                const float w = q27o_exp2(ms[s] - M);
-                den = fmaf(ls[s], w, den);
-                for (int i = 0; i < hd; ++i) o[i] = fmaf(ob[(size_t)s * hd + i], w, o[i]);
+            /* l: the 64 keys' p (0 past the valid ones) summed by the shfl_down tree */
+            float pl[Q27O_SPLIT];
+            for (int i = 0; i < Q27O_SPLIT; ++i) pl[i] = 0.0f;
+            float oc[4][256];
+            for (int j = 0; j < 4; ++j)
+                for (int i = 0; i < hd; ++i) oc[j][i] = 0.0f;
+            for (int k = k0; k < k1; ++k) {
+                const float p = q27o_exp2(xsc[k - k0] - m);
+                pl[k - k0] = p;
+                const size_t off = (size_t)k * kvrows + (size_t)kvh * hd;
+                float* oj = oc[(k - k0) / (Q27O_SPLIT / 4)];
+                for (int i = 0; i < hd; ++i) oj[i] = fmaf(p, (float)vc[off + i] * vs[(off + i) / kv_group], oj[i]);
             }
-            const float inv = 1.0f / den;
-            for (int i = 0; i < hd; ++i) {
-                float v = o[i] * inv;
-                if (gate) {
-                    const float gt = q27o_bf2f(qkv_gate[(size_t)r * qkv_stride + (size_t)hq * qw + hd + i]);
-                    v = v * q27o_sigmoid(gt);
-                }
-                const uint16_t bv = q27o_f2bf(v);
-                out[(size_t)r * nq * hd + (size_t)hq * hd + i] = bv;
-                yv[(size_t)hq * hd + i] = q27o_bf2f(bv);
-            }
-            free(ms); free(ls); free(ob);
+            for (int i = 0; i < hd; ++i) os[i] = ((oc[0][i] + oc[1][i]) + oc[2][i]) + oc[3][i];
+            const float l = tree64(pl);
+            ms[s] = m; ls[s] = l;
+            memcpy(ob + (size_t)s * hd, os, (size_t)hd * sizeof(float));
+            M = fmaxf(M, m);
         }
-        if (xq) q27o_quant_f32(yv, nq * hd, 16, xq + (size_t)r * nq * hd, xs + (size_t)r * (nq * hd / 16));
+        for (int i = 0; i < hd; ++i) o[i] = 0.0f;
+        for (int s = 0; s < ns; ++s) {
+            const float w = q27o_exp2(ms[s] - M);
+            den = fmaf(ls[s], w, den);
+            for (int i = 0; i < hd; ++i) o[i] = fmaf(ob[(size_t)s * hd + i], w, o[i]);
+        }
+        const float inv = 1.0f / den;
+        for (int i = 0; i < hd; ++i) {
+            float v = o[i] * inv;
+            if (gate) {
+                const float gt = q27o_bf2f(qkv_gate[(size_t)r * qkv_stride + (size_t)hq * qw + hd + i]);
+                v = v * q27o_sigmoid(gt);
+            }
+            const uint16_t bv = q27o_f2bf(v);
+            out[(size_t)r * nq * hd + (size_t)hq * hd + i] = bv;
+            yv[(size_t)r * nq * hd + (size_t)hq * hd + i] = q27o_bf2f(bv);
+        }
+        free(ms); free(ls); free(ob);
     }
+    if (xq)
+        for (int r = 0; r < nr; ++r)
+            q27o_quant_f32(yv + (size_t)r * nq * hd, nq * hd, 16, xq + (size_t)r * nq * hd, xs + (size_t)r * (nq * hd / 16));
     free(yv);
 }
 

@@ -157,6 +157,7 @@ int  q27o_model_prefill(q27o_model* m, const int32_t* ids, int n);          /* r
 int  q27o_model_decode_step(q27o_model* m);                                 /* returns token */
 int  q27o_model_spec_round(q27o_model* m, int32_t* out, const int32_t* forced); /* ncommit */
 int  q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* nx);
+int  q27o_model_set_pos(q27o_model* m, int pos);   /* benchmark set-up: next verify at pos */
 int  q27o_model_verify_logits(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance);
 /* The same pass recording, per layer, r1 and r2 (fp32 [n_layers][nr][H]) and the post norm's codes
  * and per-16 scales ([n_layers][nr][H], [n_layers][nr][H/16]); any of them may be NULL. */

@@ -67,6 +67,7 @@ _SIGS = {
     "q27o_rmsnorm_f32_rows": ([VP, I, I, VP, F, F, I, VP, VP, I, VP, I, I, I], None),
     "q27o_model_decode_step": ([VP], I), "q27o_model_spec_round": ([VP, VP, VP], I),
     "q27o_model_verify_rows": ([VP, I, VP, VP], I),
+    "q27o_model_set_pos": ([VP, I], I),
     "q27o_model_verify_logits": ([VP, I, VP, VP, VP, I], I),
     "q27o_model_verify_trace": ([VP, I, VP, VP, VP, I, VP, VP, VP, VP], I),
     "q27o_model_mtp_pass": ([VP, I, VP, VP, I, I, VP, VP], I),

@@ -686,6 +686,15 @@ int q27o_model_verify_rows(q27o_model* m, int nr, const int32_t* toks, int32_t* 
     return 0;
 }
 
+/* Benchmark set-up: the next verify runs at position pos (rows pos.., attending to whatever the
+ * caches hold below it), the next draft pass at pos - 1; every committed row of the GDN layers is
+ * taken as applied. */
+int q27o_model_set_pos(q27o_model* m, int pos) {
+    if (pos < 1 || pos + 8 > m->c.ctx) return -1;
+    m->pos = pos; m->gdn_npend = 0; m->ncatch = 0; m->have_h = 1;
+    return 0;
+}
+
 /* One verify pass at the current position with its logits [nr][vocab] (for the float64 pin of the
  * trunk composition). advance != 0 commits the rows as a prompt chunk does: pos += nr. */
 int q27o_model_verify_logits(q27o_model* m, int nr, const int32_t* toks, int32_t* nx, float* logits, int advance) {

@@ -375,37 +375,72 @@ def test_round_phase_times_are_reported(tiny_pair):
     assert sum(parts) < st.decode_ms * 1.05, (parts, st.decode_ms)
 
 
-def test_full_width_rounds_match_oracle(gpu, O):
-    """BASELINE widths (hidden 5120, inter 17408, vocab 62080, GDN 16/48 heads, attention 32q/8kv,
-    kv_group 32, MTP layer on) at 4 layers (3 GDN + 1 attention), against the oracle: prefill of
-    64 tokens, natural rounds and forced rounds with planted wrong drafts (partial acceptance),
-    each round's tokens, drafts, hand-off, MTP state and GDN state bit for bit. These are the
-    engine's full-width kernel instantiations (norm prologues at K = 5120, split SwiGLU units, the
-    32q/8kv attention, the 62080-row lm_head with argmax partials)."""
-    X = gpu
-    cfg = X.default_config(spec_k=2, n_layers=4, ctx=256)
+def full_width_rounds(X, O, cfg, prompt, natural, forced_rounds, seed, prefill="decode", tag=""):
+    """Natural rounds, then forced rounds with planted wrong drafts (partial acceptance), on the
+    engine and the oracle side by side: every round's tokens and the whole round state
+    (check_round_state) bit for bit."""
+    K = cfg.spec_k
     eng, om = X.Engine(cfg, SEED), O.Model(cfg, SEED)
-    p = prompt_of(cfg, 64, seed=31)
-    first = om.prefill(p)
-    assert eng.prefill(p) == first
+    ing_e = eng.prefill if prefill == "decode" else eng.prefill_gemm
+    ing_o = om.prefill if prefill == "decode" else (lambda ids: om.prefill_gemm(ids, 0))
+    first = ing_o(prompt)
+    print(f"{tag}: oracle ingested {len(prompt)} tokens", flush=True)
+    assert ing_e(prompt) == first
     assert np.array_equal(eng.read("hprev", -1, np.uint16, cfg.hidden), om.tensor("hprev", -1, np.uint16))
-    for r in range(3):
+    for r in range(natural):
         a, b = eng.spec_round(), om.spec_round()
-        assert a == b, (r, a, b)
-        check_round_state(eng, om, cfg, f"full width round {r}")
-    # partial acceptance at full width
-    om.prefill(p)
-    plain = [first] + [om.decode_step() for _ in range(16)]
-    forced = corrupted_stream(plain, cfg.vocab, seed=33, density=0.35)
-    assert eng.prefill(p) == om.prefill(p)
+        assert a == b, (tag, r, a, b)
+        check_round_state(eng, om, cfg, f"{tag} natural round {r}")
+    print(f"{tag}: {natural} natural rounds match", flush=True)
+    # plain greedy continuation (the oracle's), then drafts from it with wrong tokens planted
+    ing_o(prompt)
+    plain = [first] + [om.decode_step() for _ in range(forced_rounds * (K + 1) + 2)]
+    forced = corrupted_stream(plain, cfg.vocab, seed=seed, density=0.12 if K >= 5 else 0.35)
+    assert ing_e(prompt) == ing_o(prompt) == first
     eng.set_forced(forced)
-    n = len(p)
-    for r in range(4):
+    n, seen, out = len(prompt), set(), [first]
+    for r in range(forced_rounds):
         b0 = int(om.tensor("pos", -1, np.int32)[0]) - n
-        d = list(forced[b0 + 1:b0 + 3])
+        d = list(forced[b0 + 1:b0 + 1 + K])
         got_o = om.spec_round(forced=np.array(d + [0] * 8, np.int32))
         got_g = eng.spec_round()
-        assert got_g == got_o, (r, got_g, got_o)
-        check_round_state(eng, om, cfg, f"full width forced round {r}")
+        assert got_g == got_o, (tag, r, got_g, got_o)
+        check_round_state(eng, om, cfg, f"{tag} forced round {r}")
+        seen.add(len(got_o) - 1)
+        out.extend(got_o)
+    assert out == plain[:len(out)]
+    print(f"{tag}: {forced_rounds} forced rounds match, acceptance lengths {sorted(seen)}", flush=True)
+    eng.set_forced([])
     eng.close()
     om.close()
+    return seen
+
+
+@pytest.mark.parametrize("k", [2, 5, 7])
+def test_full_width_rounds_match_oracle(gpu, O, k):
+    """BASELINE widths (hidden 5120, inter 17408, vocab 62080, GDN 16/48 heads, attention 32q/8kv,
+    kv_group 32, MTP layer on) at 4 layers (3 GDN + 1 attention), against the oracle at K = 2, 5
+    and 7 (3, 6 and 8 verify rows): prefill of 64 tokens, 3 natural rounds and 4 forced rounds with
+    planted wrong drafts (partial acceptance), each round's tokens, drafts, hand-off, MTP state and
+    GDN state bit for bit. These are the engine's full-width kernel instantiations at every row
+    count the BASELINE configs use: the norm prologues at K = 5120 (two rows per 256-thread group
+    past 4 rows), the split SwiGLU units, the conv epilogue and a/b rows, the 32q/8kv attention,
+    the one-pass 8-row down and the 62080-row lm_head with argmax partials."""
+    X = gpu
+    cfg = X.default_config(spec_k=k, n_layers=4, ctx=256)
+    p = prompt_of(cfg, 64, seed=31)
+    seen = full_width_rounds(X, O, cfg, p, natural=3, forced_rounds=4, seed=33 + k, tag=f"full width K={k}")
+    assert any(s < k for s in seen), (k, sorted(seen))
+
+
+def test_full_width_long_context_rounds_match_oracle(gpu, O):
+    """Past 2048 positions at 8 kv heads each attention block takes several 64-key splits in turn
+    (the grid holds 32 blocks per kv head), and the step's new positions fall in a later split of a
+    block. Full-width attention geometry (hidden 5120, 32q/8kv, GDN 16/48 heads, vocab 62080) with
+    one GDN and one attention layer and a narrow MLP (inter 1024) so that the oracle ingests a
+    2100-token prompt (GEMM prefill) in seconds; then K = 7 rounds, natural and forced, against the
+    oracle round by round."""
+    X = gpu
+    cfg = X.default_config(spec_k=7, n_layers=2, attn_period=2, inter=1024, ctx=2304)
+    p = prompt_of(cfg, 2100, seed=35)
+    full_width_rounds(X, O, cfg, p, natural=3, forced_rounds=4, seed=37, prefill="gemm", tag="ctx 2.1K K=7")
