@@ -48,13 +48,13 @@ def test_catalog_census_and_host_pointers(X, ckdir, synth):
 
 def test_census_fails_closed(X, ckdir):
     d, n, b = ckdir
-    for kw, msg in (((n + 1, b), "tensors"), ((n, b - 1), "payload bytes")):
+    for kw, msg in (((n + 1, b), "tensors"), ((n, b - 1), "bytes of tensor data")):
         with pytest.raises(X.Q27XError) as e:
             open_ck(X, d, *kw)
         assert "census" in str(e.value) and msg in str(e.value)
     with pytest.raises(X.Q27XError) as e:
         open_ck(X, d, nshards=4)                                    # shard 3 of 4 does not exist
-    assert "open(" in str(e.value)
+    assert "cannot open" in str(e.value)
 
 
 def test_shards_numbered_from_one(X, tmp_path, synth):
@@ -83,7 +83,7 @@ def corrupt(tmp_path, header_edit=None, raw=None):
 
 @pytest.mark.parametrize("case,want", [
     ("offsets_outside", "outside"), ("shape_bytes", "shape needs"), ("dtype", "unknown dtype"),
-    ("no_offsets", "required"), ("header_len", "header length"), ("not_json", "not a JSON object"),
+    ("no_offsets", "required"), ("header_len", "header length field"), ("not_json", "not a JSON object"),
     ("duplicate", "duplicate")])
 def test_header_checks_fail_closed(X, tmp_path, case, want):
     edits = {
