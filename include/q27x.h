@@ -275,6 +275,11 @@ typedef struct q27x_config {
     int spec;            /* Q27_SPEC: 1 = speculative decode */
     int spec_k;          /* Q27_SPEC_K: drafts per round, [1, 7] */
     int ctx;             /* context capacity in positions */
+    int pf_gs;           /* Q27_Q8_GS: K-group size of the prefill GEMM's per-(row, group) weight
+                            and per-(token, group) activation scales: 0 = the whole K (the
+                            reference default, src/q27_load.cpp:1622-1623, src/q27_main.cpp:4020),
+                            or 1024. The MTP prompt pass always uses the whole K
+                            (src/q27_main.cpp:2625-2628, 2665-2668). */
 } q27x_config;
 
 /* Statistics of a decode run (the reference's Q27_SPEC / Q27_SPEC_T lines,

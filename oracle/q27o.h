@@ -147,6 +147,7 @@ typedef struct q27o_cfg {
     float rms_eps;
     int head_double_residual, mtp_swap, mtp_plus_one;
     int spec_k, ctx;
+    int pf_gs;           /* prefill GEMM K-group: 0 = the whole K, or 1024 (the reference's Q27_Q8_GS) */
 } q27o_cfg;
 
 typedef struct q27o_model q27o_model;

@@ -21,7 +21,7 @@ class Cfg(ctypes.Structure):
         ("n_q", I), ("n_kv", I), ("head_dim", I), ("attn_gate", I), ("rot_dims", I),
         ("rope_theta", D), ("kv_group", I), ("rms_eps", F),
         ("head_double_residual", I), ("mtp_swap", I), ("mtp_plus_one", I),
-        ("spec_k", I), ("ctx", I),
+        ("spec_k", I), ("ctx", I), ("pf_gs", I),
     ]
 
 
@@ -109,6 +109,7 @@ def bf2f(b):
 def cfg_from(c):
     """A q27o config from a q27x Config (or a dict with the same fields)."""
     d = c.as_dict() if hasattr(c, "as_dict") else dict(c)
+    d.setdefault("pf_gs", 0)           # (configs recorded before the prefill group setting)
     o = Cfg()
     for f, _ in Cfg._fields_:
         setattr(o, f, d[f])

@@ -475,15 +475,16 @@ int q27o_model_prefill(q27o_model* m, const int32_t* ids, int n) {
 static int g_pf_plant = 0;
 void q27o_debug_plant(int code) { g_pf_plant = code; }
 
-/* Group size of the prefill GEMM over K (the reference's q8gs: 1024, or the whole K). */
-static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
+/* Group size of the trunk's prefill GEMMs over K (the reference's Q27_Q8_GS, src/q27_load.cpp:1623,
+ * src/q27_main.cpp:4020): the whole K (0, the default) or pf_gs columns when they divide K. */
+static int pf_gs(const q27o_cfg* c, int K) { return (c->pf_gs > 0 && K % c->pf_gs == 0) ? c->pf_gs : K; }
 /* y[M][rows] = GEMM(W, act) * 1 (+ rs * res), W's per-64 mirror requantized per (row, group)
  * (src/q27_epi.hip:14-35) and act quantized per (token, group) from fp32 values v [M][K]
  * (src/q27_epi.hip:64-75); the GEMM and its fp32 fold follow src/q27_rb.cpp:43-55 and
  * src/q27_epi.hip:189-243. rows0/nrows select a row range of W. */
 static void pf_proj(const i8m* W, int row0, int nrows, const float* v, int M, float* y, int ldy,
-                    const float* res, int ldr, float rs, float alpha, float in_scale) {
-    const int K = W->K, gs = pf_gs(K), ng = K / gs;
+                    const float* res, int ldr, float rs, float alpha, float in_scale, int gs) {
+    const int K = W->K, ng = K / gs;
     int8_t* wg = (int8_t*)malloc((size_t)nrows * K);
     float* sg = (float*)malloc((size_t)nrows * ng * 4);
     q27o_i8g64_to_grp(W->w + (size_t)row0 * K, W->s + (size_t)row0 * (K / 64), nrows, K, gs, wg, sg);
@@ -529,7 +530,7 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
             float* o = (float*)malloc((size_t)C * wq * 4);
             const int rq[4] = { 0, qr, qr + kvr, wq };
             for (int i = 0; i < 3; ++i)
-                pf_proj(&Y->qkv, rq[i], rq[i + 1] - rq[i], v, C, o + rq[i], wq, NULL, 0, 0.0f, Y->al_qkv[i], Y->is_in);
+                pf_proj(&Y->qkv, rq[i], rq[i + 1] - rq[i], v, C, o + rq[i], wq, NULL, 0, 0.0f, Y->al_qkv[i], Y->is_in, pf_gs(c, Y->qkv.K));
             f_to_bf(o, pb, (size_t)C * wq);
             free(o);
             for (int r0 = 0; r0 < C; r0 += 8) {
@@ -541,11 +542,11 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
                                c->n_kv, c->head_dim, c->attn_gate, p0 + r0, cn, mix + (size_t)r0 * att, NULL, NULL);
             }
             bf_to_f(mix, v, (size_t)C * att);
-            pf_proj(&Y->o, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out);
+            pf_proj(&Y->o, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out, pf_gs(c, Y->o.K));
         } else {
             float* o = (float*)malloc((size_t)C * wz * 4);
-            pf_proj(&Y->qkvz, 0, nqkv, v, C, o, wz, NULL, 0, 0.0f, Y->al_qkv[0], Y->is_in);
-            pf_proj(&Y->qkvz, nqkv, nz, v, C, o + nqkv, wz, NULL, 0, 0.0f, Y->al_qkv[1], Y->is_in);
+            pf_proj(&Y->qkvz, 0, nqkv, v, C, o, wz, NULL, 0, 0.0f, Y->al_qkv[0], Y->is_in, pf_gs(c, Y->qkvz.K));
+            pf_proj(&Y->qkvz, nqkv, nz, v, C, o + nqkv, wz, NULL, 0, 0.0f, Y->al_qkv[1], Y->is_in, pf_gs(c, Y->qkvz.K));
             f_to_bf(o, pb, (size_t)C * wz);
             free(o);
             /* a / b: the decode path's bf16 GEMV on the bf16 normed rows, bf16 outputs */
@@ -568,19 +569,19 @@ static void pf_chunk(q27o_model* m, const int32_t* ids, int p0, int C, uint16_t*
             q27o_gdn_verify(NULL, 0, NULL, 0, NULL, NULL, 0, Y->A_log, Y->dt_bias, Y->gdn_norm, Y->conv_w, Y->S,
                             Y->conv_hist, Y->pend, npend, c->gdn_kh, VH, D, c->rms_eps, NULL, 0, NULL, NULL, 0);
             bf_to_f(mix, v, (size_t)C * nz);
-            pf_proj(&Y->out_proj, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out);
+            pf_proj(&Y->out_proj, 0, H, v, C, x, H, hf, H, 1.0f, Y->al_o, Y->is_out, pf_gs(c, Y->out_proj.K));
         }
         q27o_rmsnorm_f32_rows(x, 0, H, Y->post_norm, 1.0f, c->rms_eps, H, h, NULL, H, v, H, 0, C);
         bf_to_f(h, hf, (size_t)C * H);
-        pf_proj(&Y->gate, 0, I, v, C, g, I, NULL, 0, 0.0f, Y->al_gate, Y->is_post);
-        pf_proj(&Y->up, 0, I, v, C, u, I, NULL, 0, 0.0f, Y->al_up, Y->is_post);
+        pf_proj(&Y->gate, 0, I, v, C, g, I, NULL, 0, 0.0f, Y->al_gate, Y->is_post, pf_gs(c, Y->gate.K));
+        pf_proj(&Y->up, 0, I, v, C, u, I, NULL, 0, 0.0f, Y->al_up, Y->is_post, pf_gs(c, Y->up.K));
         const float gsc = 1.0f / Y->is_down;
         for (size_t i = 0; i < (size_t)C * I; ++i) {   /* q27o_swiglu_quant_rows' value */
             const float a = g[i];
             const float sw = a / (1.0f + q27o_exp(-a));
             v[i] = sw * u[i] * gsc;
         }
-        pf_proj(&Y->down, 0, H, v, C, x, H, hf, H, g_pf_plant == 1 ? 0.0f : 1.0f, Y->al_down, 1.0f);
+        pf_proj(&Y->down, 0, H, v, C, x, H, hf, H, g_pf_plant == 1 ? 0.0f : 1.0f, Y->al_down, 1.0f, pf_gs(c, Y->down.K));
     }
     m->gdn_npend = 0;
     for (int r = 0; r < C; ++r)
@@ -616,10 +617,10 @@ static void pf_mtp(q27o_model* m, const int32_t* ids, int p0, int C, const uint1
     const int sw = c->mtp_swap ^ (g_pf_plant == 2);
     const i8m* fe = sw ? &m->fc0 : &m->fc1;   /* the half that multiplies the embedding */
     const i8m* fh = sw ? &m->fc1 : &m->fc0;
-    pf_proj(fe, 0, H, ve, C, res, H, NULL, 0, 0.0f, 1.0f, 1.0f);
-    pf_proj(fh, 0, H, vh, C, res, H, res, H, 1.0f, 1.0f, 1.0f);
+    pf_proj(fe, 0, H, ve, C, res, H, NULL, 0, 0.0f, 1.0f, 1.0f, fe->K);
+    pf_proj(fh, 0, H, vh, C, res, H, res, H, 1.0f, 1.0f, 1.0f, fh->K);
     q27o_rmsnorm_f32_rows(res, 0, H, Y->in_norm, po, c->rms_eps, H, NULL, NULL, H, ve, H, 0, C);
-    pf_proj(&Y->qkv, qr, 2 * kvr, ve, C, kv, 2 * kvr, NULL, 0, 0.0f, 1.0f, 1.0f);
+    pf_proj(&Y->qkv, qr, 2 * kvr, ve, C, kv, 2 * kvr, NULL, 0, 0.0f, 1.0f, 1.0f, Y->qkv.K);
     for (int r = 0; r < C; ++r)
         for (int k = 0; k < 2 * kvr; ++k) pb[(size_t)r * wq + qr + k] = q27o_f2bf(kv[(size_t)r * 2 * kvr + k]);
     for (int r0 = 0; r0 < C; r0 += 8) {

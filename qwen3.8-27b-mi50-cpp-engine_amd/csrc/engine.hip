@@ -41,9 +41,9 @@ struct Mat {
     // per-output scale of the stacked source tensors (alpha = input_scale x weight_scale; 1 for
     // weights made from their values, as the synthetic ones)
     float alpha = 1.0f; AlphaSel asel{};
-    // the prefill GEMM's representation of the same matrix (per-(row, group) codes and scales),
-    // made on the first GEMM prefill after a load
-    int8_t* pw = nullptr; float* ps = nullptr;
+    // the prefill GEMM's representation of the same matrix (per-(row, group) codes and scales,
+    // groups of pgs columns), made on the first GEMM prefill after a load
+    int8_t* pw = nullptr; float* ps = nullptr; int pgs = 0;
 };
 
 struct LayerDev {
@@ -637,7 +637,7 @@ int q27x_config_default(q27x_config* c) {
     c->gdn_kh = 16; c->gdn_vh = 48; c->gdn_d = 128;
     c->n_q = 32; c->n_kv = 8; c->head_dim = 128; c->attn_gate = 1; c->rot_dims = 32; c->rope_theta = 1e7;
     c->kv_group = 32; c->rms_eps = 1e-6f; c->head_double_residual = 1; c->mtp_swap = 1; c->mtp_plus_one = 1;
-    c->spec = 1; c->spec_k = 2; c->ctx = 2048;
+    c->spec = 1; c->spec_k = 2; c->ctx = 2048; c->pf_gs = 0;
     return Q27X_OK;
 }
 int q27x_config_tiny(q27x_config* c) {
@@ -676,6 +676,14 @@ int q27x_spec_config_from_env(q27x_config* c) {
     c->spec_k = k;
     c->mtp_swap = env_flag("Q27_MTP_SWAP", c->mtp_swap);
     c->mtp_plus_one = env_int("Q27_MTP_PO", c->mtp_plus_one);
+    // src/q27_load.cpp:1623, src/q27_main.cpp:4020: Q27_Q8_GS, default 0 (the whole K); the only
+    // other group the reference's prefill runs is 1024
+    const int gs = env_int("Q27_Q8_GS", 0);
+    if (gs != 0 && gs != 1024) {
+        fprintf(stderr, "FATAL Q27_Q8_GS=%d: the prefill groups are 0 (the whole K) or 1024.\n", gs);
+        abort();
+    }
+    c->pf_gs = gs;
     return Q27X_OK;
 }
 
@@ -1332,7 +1340,9 @@ static int pf_streams() {   // chunks in flight: Q27X_PF_STREAMS (1 .. 3), defau
     const int v = env_int("Q27X_PF_STREAMS", 2);
     return v < 1 ? 1 : (v > 3 ? 3 : v);
 }
-static int pf_gs(int K) { return (K % 1024 == 0) ? 1024 : K; }
+// K-group of the trunk's prefill GEMMs: the whole K (pf_gs 0, the reference default) or pf_gs
+// columns when they divide K
+static int pf_gs(const q27x_config& c, int K) { return (c.pf_gs > 0 && K % c.pf_gs == 0) ? c.pf_gs : K; }
 
 static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
     if (*slot && (*slot)->cap >= cap) return Q27X_OK;
@@ -1379,8 +1389,8 @@ static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
 // or fp32 with row stride ldy
 static int pf_gemm(q27x_ctx* x, const Mat& W, int r0, int nrows, const int8_t* xq, const float* xs, int M, void* y,
                    int ldy, int out_bf16, const void* res, int res_bf16 = 1) {
-    const int K = W.K, gs = pf_gs(K);
-    if (!W.pw) { set_error("prefill: no GEMM representation of a %d x %d matrix", W.rows, K); return Q27X_E_STATE; }
+    const int K = W.K, gs = W.pgs;
+    if (!W.pw || gs < 1) { set_error("prefill: no GEMM representation of a %d x %d matrix", W.rows, K); return Q27X_E_STATE; }
     // the stacked tensors' scales, for rows counted from r0
     AlphaSel as = W.asel;
     float a0 = W.alpha;
@@ -1401,9 +1411,14 @@ static int pf_weights(q27x_ctx* x) {
     for (LayerDev& Y : x->L) {
         for (Mat* m : { &Y.qkvz, &Y.out_proj, &Y.qkv, &Y.o, &Y.gu, &Y.down }) if (m->w) ms.push_back(m);
     }
+    const size_t n_trunk = ms.size();
     for (Mat* m : { &x->fc0, &x->fc1, &x->mtp.qkv }) if (m->w) ms.push_back(m);
-    for (Mat* m : ms) {
-        const int K = m->K, gs = pf_gs(K);
+    for (size_t i = 0; i < ms.size(); ++i) {
+        Mat* m = ms[i];
+        // the MTP layer's matrices always in whole-K groups (src/q27_main.cpp:2625-2628, 2665-2668)
+        const int K = m->K, gs = i < n_trunk ? pf_gs(x->c, K) : K;
+        if (m->pw && m->pgs != gs) { set_error("prefill: GEMM representation group changed"); return Q27X_E_STATE; }
+        m->pgs = gs;
         if (!m->pw) {
             hipError_t e = hipMalloc((void**)&m->pw, (size_t)m->rows * K);
             if (e != hipSuccess) return hip_fail(e, "hipMalloc (prefill weights)");
@@ -1418,13 +1433,13 @@ static int pf_weights(q27x_ctx* x) {
     x->pf_wready = 1;
     return Q27X_OK;
 }
-// norm of C rows (values to B.yf) and their per-(token, group) codes
-static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs, float in_scale = 1.0f) {
+// norm of C rows (values to B.yf) and their per-(token, group) codes in groups of gs columns
+static int pf_norm_quant(q27x_ctx* x, NormArgs n, int C, int8_t* xq, float* xs, int gs, float in_scale = 1.0f) {
     PfBuf& B = *x->pfc;
     n.yf = B.yf; n.yfstride = x->H;
     int rc = launch_norm(n, C, x->pfs);
     if (rc) return rc;
-    return launch_quant_tok_grp(B.yf, x->H, C, x->H, pf_gs(x->H), in_scale, xq, xs, x->pfs);
+    return launch_quant_tok_grp(B.yf, x->H, C, x->H, gs, in_scale, xq, xs, x->pfs);
 }
 
 static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
@@ -1442,7 +1457,8 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
     } else {
         nin = norm_of(x, B.x, 0, Y.in_norm, 1.0f, 0, B.h, Y.is_attn ? nullptr : B.y);
     }
-    if ((rc = pf_norm_quant(x, nin, C, B.xq, B.xs, Y.in_s_in))) return rc;
+    const int gH = pf_gs(c, H);
+    if ((rc = pf_norm_quant(x, nin, C, B.xq, B.xs, gH, Y.in_s_in))) return rc;
     if (Y.is_attn) {
         const int wq = Y.qkv.rows;
         if ((rc = pf_gemm(x, Y.qkv, 0, wq, B.xq, B.xs, C, B.pb, wq, 1, nullptr))) return rc;
@@ -1461,7 +1477,7 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
             t.zrows = 8; t.ztotal = cq; t.out = B.mix + (size_t)q0 * x->att;
             if ((rc = launch_attn(t, 8, s, false))) return rc;
         }
-        if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(x->att), Y.in_s_out, B.xq, B.xs, s))) return rc;
+        if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(c, x->att), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.o, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     } else {
         const int wz = Y.qkvz.rows;
@@ -1476,13 +1492,14 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         // scratch: yf (free after the in_qkv|in_z GEMM's quantizer) for q^|k^, the third rowsc
         // slab for k^.q^, the gate|up output (free until the MLP) for the mixed rows
         if ((rc = launch_gdn_scan(g, C, B.yf, B.rowsc + (size_t)2 * B.cap * c.gdn_vh, B.gu, s))) return rc;
-        if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(x->nz), Y.in_s_out, B.xq, B.xs, s))) return rc;
+        if ((rc = launch_pf_quant_bf16(B.mix, x->nz, C, x->nz, pf_gs(c, x->nz), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.out_proj, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;
     }
-    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, Y.post_norm, 1.0f, 0, B.h, nullptr), C, B.xq, B.xs, Y.in_s_post)))
+    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, Y.post_norm, 1.0f, 0, B.h, nullptr), C, B.xq, B.xs, gH,
+                            Y.in_s_post)))
         return rc;
     if ((rc = pf_gemm(x, Y.gu, 0, 2 * I, B.xq, B.xs, C, B.gu, 2 * I, 0, nullptr))) return rc;
-    if ((rc = launch_pf_swiglu_quant(B.gu, I, pf_gs(I), 1.0f / Y.in_s_down, C, B.xq, B.xs, s))) return rc;
+    if ((rc = launch_pf_swiglu_quant(B.gu, I, pf_gs(c, I), 1.0f / Y.in_s_down, C, B.xq, B.xs, s))) return rc;
     return pf_gemm(x, Y.down, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h);
 }
 
@@ -1497,15 +1514,16 @@ static int pf_mtp(q27x_ctx* x, int p0, int C) {
     int rc;
     NormArgs ne = norm_of(x, nullptr, 1, x->pre_emb, po, 0, nullptr, nullptr);
     ne.emb = x->emb; ne.tok = x->prompt_dev + p0 + 1;
-    if ((rc = pf_norm_quant(x, ne, C, B.xq, B.xs))) return rc;
+    // (every quantizer of the MTP prompt pass in whole-K groups, as its GEMM weights)
+    if ((rc = pf_norm_quant(x, ne, C, B.xq, B.xs, H))) return rc;
     if ((rc = pf_norm_quant(x, norm_of(x, x->hall + (size_t)p0 * H, 1, x->pre_hid, po, 0, nullptr, nullptr), C,
-                            B.xq2, B.xs2))) return rc;
+                            B.xq2, B.xs2, H))) return rc;
     const Mat& fe = c.mtp_swap ? x->fc0 : x->fc1;    // the half that multiplies the embedding
     const Mat& fh = c.mtp_swap ? x->fc1 : x->fc0;
     if ((rc = pf_gemm(x, fe, 0, H, B.xq, B.xs, C, B.x, H, 0, nullptr))) return rc;
     // (fp32 residual: the first half's output, read and written in place)
     if ((rc = pf_gemm(x, fh, 0, H, B.xq2, B.xs2, C, B.x, H, 0, B.x, 0))) return rc;
-    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, M.in_norm, po, 0, nullptr, nullptr), C, B.xq, B.xs))) return rc;
+    if ((rc = pf_norm_quant(x, norm_of(x, B.x, 0, M.in_norm, po, 0, nullptr, nullptr), C, B.xq, B.xs, H))) return rc;
     const int wq = M.qkv.rows;
     if ((rc = pf_gemm(x, M.qkv, x->qr, 2 * x->kvr, B.xq, B.xs, C, B.pb + x->qr, wq, 1, nullptr))) return rc;
     AttnArgs a{};

@@ -208,6 +208,26 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
     const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = I / gs;
     __shared__ float red[4];
     const float* row = gu + (size_t)tok * 2 * I;
+    auto value = [&](int i) __attribute__((always_inline)) {
+        const int gr = (i >> 4) * 32 + (i & 15);
+        const float gv = row[gr], uv = row[gr + 16];
+        const float swv = gv / (1.0f + qexp(-gv));
+        return swv * uv * gscale;
+    };
+    if (gs > 256 * 8) {
+        // a group wider than the values a thread holds (the whole I): the group max first, then
+        // every value computed again by the same expression and quantized
+        float mx = 0.0f;
+        for (int j = t; j < gs; j += 256) mx = fmaxf(mx, fabsf(value(g * gs + j)));
+        mx = max_xor(mx, 64);
+        if ((t & 63) == 0) red[t >> 6] = mx;
+        __syncthreads();
+        const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+        if (t == 0) xs[(size_t)tok * ng + g] = sc;
+        for (int j = t; j < gs; j += 256) xq[(size_t)tok * I + g * gs + j] = qcode(value(g * gs + j), qi);
+        return;
+    }
     constexpr int VPT = 8;                         // values per thread held for the two passes
     float v[VPT];
     float mx = 0.0f;
@@ -216,10 +236,7 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
         const int i = g * gs + t + 256 * u;
         v[u] = 0.0f;
         if (t + 256 * u < gs) {
-            const int gr = (i >> 4) * 32 + (i & 15);
-            const float gv = row[gr], uv = row[gr + 16];
-            const float swv = gv / (1.0f + qexp(-gv));
-            v[u] = swv * uv * gscale;
+            v[u] = value(i);
             mx = fmaxf(mx, fabsf(v[u]));
         }
     }
@@ -235,7 +252,7 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
 }
 int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
                            hipStream_t s) {
-    if (!gu || !xq || !xs || C < 1 || (I & 31) || gs < 16 || gs > 2048 || (I % gs)) {
+    if (!gu || !xq || !xs || C < 1 || (I & 31) || gs < 16 || (gs & 15) || (I % gs)) {
         set_error("prefill swiglu: bad arguments (I %d, gs %d)", I, gs);
         return Q27X_E_ARG;
     }

@@ -62,21 +62,25 @@ def run_case(X, O, cfg, n, rounds, chunk=None, seed=3):
         om.close()
 
 
-@pytest.mark.parametrize("n,chunk", [(1, None), (9, None), (300, None), (150, 64), (70, 8)])
-def test_tiny_prefill_gemm_matches_oracle(gpu, O, n, chunk):
-    run_case(gpu, O, gpu.tiny_config(spec_k=2), n, 3, chunk)
+@pytest.mark.parametrize("n,chunk,gs", [(1, None, 0), (9, None, 0), (300, None, 0), (150, 64, 0), (70, 8, 0),
+                                        (300, None, 1024), (70, 8, 1024)])
+def test_tiny_prefill_gemm_matches_oracle(gpu, O, n, chunk, gs):
+    """gs: the K-group of the trunk's GEMMs (Q27_Q8_GS): 0 = the whole K (the reference default),
+    1024 (at the tiny widths only the K = 2048 down has two groups)."""
+    run_case(gpu, O, gpu.tiny_config(spec_k=2, pf_gs=gs), n, 3, chunk)
 
 
 def test_tiny_k7_prefill_gemm_matches_oracle(gpu, O):
     run_case(gpu, O, gpu.tiny_config(spec_k=7), 45, 2, 16)
 
 
-@pytest.mark.parametrize("n,chunk", [(64, None), (96, 32)])
-def test_full_width_prefill_gemm_matches_oracle(gpu, O, n, chunk):
+@pytest.mark.parametrize("n,chunk,gs", [(64, None, 0), (96, 32, 0), (64, None, 1024)])
+def test_full_width_prefill_gemm_matches_oracle(gpu, O, n, chunk, gs):
     """BASELINE widths at 4 layers (3 GDN + 1 attention): the 16384-row in_qkv|in_z, 34816-row
-    gate|up and K = 17408 down GEMMs, 32q/8kv attention, the 62080-row head. (96 tokens in 32-row
+    gate|up and K = 17408 down GEMMs, 32q/8kv attention, the 62080-row head, with whole-K groups
+    (the reference default) and with 1024-column groups (5, 6 and 17 of them). (96 tokens in 32-row
     chunks: three chunks on alternating streams, each layer behind the previous chunk's.)"""
-    run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=512), n, 2, chunk)
+    run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=512, pf_gs=gs), n, 2, chunk)
 
 
 def test_full_model_spec_equals_plain_after_prefill_gemm(gpu):

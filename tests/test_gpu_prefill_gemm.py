@@ -58,6 +58,9 @@ def oracle_gemm(O, w, sw, x, sx, gs, alpha, res=None, rs=0.0):
     (1024, 384, 17408, 1024, False),   # 256-token tiles (register-staged), 17 groups
     (520, 128, 1152, 1152, True),      # 256-token tiles, K % 256 != 0: the LDS-DMA ring
     (777, 256, 3200, 640, False),      # 256-token tiles, K % 256 != 0, 5 groups of 640
+    (600, 256, 5120, 5120, True),      # 256-token tiles, one group over the whole K (the default arm)
+    (130, 256, 17408, 17408, False),   # down's K as one group
+    (1024, 384, 17408, 17408, True),   # 256-token tiles, down's K as one group
 ])
 def test_gemm_i8g(gpu, O, M, N, K, gs, with_res):
     rng = np.random.default_rng(0x51E70400 + M + N + K)
@@ -71,12 +74,14 @@ def test_gemm_i8g(gpu, O, M, N, K, gs, with_res):
     same(f"gemm {M}x{N}x{K}/{gs}", y, oracle_gemm(O, w, sw, x, sx, gs, 0.8125, res, 1.0))
 
 
-def test_gemm_i8g_full_shape_sampled(gpu, O):
-    # the prefill shape of gate (M = 4096 tokens, N = 17408, K = 5120): the whole product on the GPU,
-    # eight token rows (first, last, and across the token tiles) recomputed by the oracle
+@pytest.mark.parametrize("gs", [5120, 1024])
+def test_gemm_i8g_full_shape_sampled(gpu, O, gs):
+    # the prefill shape of gate (M = 4096 tokens, N = 17408, K = 5120) with whole-K groups (the
+    # default) and 1024-column groups: the whole product on the GPU, eight token rows (first, last,
+    # and across the token tiles) recomputed by the oracle
     X = gpu
     rng = np.random.default_rng(0x51E70404)
-    M, N, K, gs = 4096, 17408, 5120, 1024
+    M, N, K = 4096, 17408, 5120
     w, x = codes(rng, (N, K)), codes(rng, (M, K))
     sw = rng.uniform(1e-4, 2e-3, (N, K // gs)).astype(np.float32)
     sx = rng.uniform(1e-3, 5e-2, (M, K // gs)).astype(np.float32)
@@ -96,7 +101,7 @@ def test_gemm_i8g_rejects_shapes(gpu):
     a.free()
 
 
-@pytest.mark.parametrize("K,gs", [(5120, 1024), (5120, 5120), (17408, 1024)])
+@pytest.mark.parametrize("K,gs", [(5120, 1024), (5120, 5120), (17408, 1024), (17408, 17408)])
 def test_quant_tok_groups(gpu, O, K, gs):
     X = gpu
     rng = np.random.default_rng(0x51E70410 + K + gs)
