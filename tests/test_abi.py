@@ -82,7 +82,7 @@ def _env_config(env):
     code = ("import sys, ctypes; sys.path.insert(0, %r); import importlib.util as u;"
             "s = u.spec_from_file_location('q27x', %r); m = u.module_from_spec(s); s.loader.exec_module(m);"
             "c = m.default_config(); m.call('q27x_spec_config_from_env', ctypes.byref(c));"
-            "print(c.spec, c.spec_k)") % (ROOT, os.path.join(ROOT, "qwen3.8-27b-mi50-cpp-engine_amd", "q27x.py"))
+            "print(c.spec, c.spec_k, c.pf_gs)") % (ROOT, os.path.join(ROOT, "qwen3.8-27b-mi50-cpp-engine_amd", "q27x.py"))
     e = {k: v for k, v in os.environ.items() if not k.startswith("Q27_")}
     e.update(env)
     return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=e, timeout=120)
@@ -101,10 +101,20 @@ def _env_config(env):
 def test_spec_env_semantics(env, expect):
     r = _env_config(env)
     assert r.returncode == 0, r.stderr
-    assert tuple(int(v) for v in r.stdout.split()) == expect
+    assert tuple(int(v) for v in r.stdout.split())[:2] == expect
 
 
-@pytest.mark.parametrize("env", [{"Q27_SPEC": "maybe"}, {"Q27_SPEC_K": "2x"}, {"Q27_SPEC_K": "two"}])
+@pytest.mark.parametrize("env,expect", [({}, 0), ({"Q27_Q8_GS": "0"}, 0), ({"Q27_Q8_GS": "1024"}, 1024),
+                                        ({"Q27_Q8_GS": ""}, 0)])
+def test_prefill_group_env(env, expect):
+    """Q27_Q8_GS (src/q27_load.cpp:1623, src/q27_main.cpp:4020): 0 = the whole K, the default; 1024."""
+    r = _env_config(env)
+    assert r.returncode == 0, r.stderr
+    assert int(r.stdout.split()[2]) == expect
+
+
+@pytest.mark.parametrize("env", [{"Q27_SPEC": "maybe"}, {"Q27_SPEC_K": "2x"}, {"Q27_SPEC_K": "two"},
+                                 {"Q27_Q8_GS": "512"}, {"Q27_Q8_GS": "full"}])
 def test_spec_env_fails_closed(env):
     """An unparseable value prints FATAL and aborts (include/q27.h:189-206), never guesses."""
     r = _env_config(env)
