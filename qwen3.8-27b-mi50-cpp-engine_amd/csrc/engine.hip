@@ -691,9 +691,13 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     if (!cfg || !out) { set_error("q27x_ctx_create: null argument"); return Q27X_E_ARG; }
     *out = nullptr;
     const q27x_config& c = *cfg;
-    if ((c.hidden != 1024 && c.hidden != 5120) || c.inter % 1024 || c.gdn_d != 128 || c.head_dim != 128 ||
+    const bool rot_ok = c.rot_dims >= 2 && (c.rot_dims & (c.rot_dims - 1)) == 0 &&
+                        (c.rot_dims <= 64 || (c.rot_dims == 128 && c.head_dim == 128));
+    if ((c.hidden != 1024 && c.hidden != 5120) || c.inter % 1024 || c.gdn_d != 128 ||
+        (c.head_dim != 128 && c.head_dim != 256) || !rot_ok ||
         c.n_layers < 1 || c.attn_period < 1 || c.spec_k < 1 || c.spec_k > 7 || c.ctx < 16 || c.vocab < 16 ||
-        c.gdn_vh % c.gdn_kh || c.n_q % c.n_kv || (c.n_q / c.n_kv) * 8 > 64 || c.kv_group < 16) {
+        c.gdn_vh % c.gdn_kh || c.n_q % c.n_kv || (c.n_q / c.n_kv) * 8 > 64 || c.kv_group < 16 ||
+        (c.pf_gs != 0 && c.pf_gs != 1024)) {
         set_error("q27x_ctx_create: unsupported geometry");
         return Q27X_E_SHAPE;
     }
@@ -717,7 +721,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     int n_attn = 0;
     for (int l = 0; l < c.n_layers; ++l) {
         wb += 2 * H * 2 + 512 + i8b(2 * I, H) + i8b(H, I);
-        if (is_attn_layer(c, l)) { wb += i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 2 * 128 * 2 + 512; ++n_attn; }
+        if (is_attn_layer(c, l)) { wb += i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 2 * (size_t)c.head_dim * 2 + 1024; ++n_attn; }
         else wb += i8b(x->nqkv + x->nz, H) + 2 * (size_t)c.gdn_vh * H * 2 + (size_t)x->nqkv * 4 * 2 + i8b(H, x->nz) + 4096;
     }
     wb += 2 * H * 2 + i8b(2 * I, H) + 4 * i8b(H, I / 4) + i8b(x->qr + 2 * x->kvr, H) + i8b(H, x->att) + 4096;   // MTP
@@ -739,7 +743,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     sb += sizeof(Dctl) + R * H * 2 * 4 + R * H * 4 + xqn + xqn / 16 * 4 + R * (size_t)x->nz * 2 + 256;
     sb += (size_t)kSwMaxSplit * 16 * R * 4 + kSwMaxSplit * 4 + 512 + 2 * R * (size_t)c.gdn_vh * 4 + 256;
     sb += pbn * 2 + 2 * R * (size_t)x->att * 2 + R * 2 * H * 2 + R * H * 2 * 3 + H * 2;
-    sb += attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4 + R * (size_t)x->pstride * 8;
+    sb += attn_work_floats(c.n_q, c.head_dim, x->max_splits, kMaxRows) * 4 + R * (size_t)x->pstride * 8;
     x->ring_cap = c.ctx + 64; x->forced_cap = c.ctx + 64; x->prompt_cap = c.ctx + 64;
     sb += (size_t)(x->ring_cap + x->forced_cap + x->prompt_cap) * 4 + (size_t)c.ctx * H * 2;
     sb += (size_t)c.ctx * (c.rot_dims / 2) * 4 * 2 + 64 * 256;
@@ -780,7 +784,7 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
     x->mtp_res = (uint16_t*)salloc(x, R * H * 2);
     x->hcatch = (uint16_t*)salloc(x, R * H * 2);
     x->hprev = (uint16_t*)salloc(x, H * 2);
-    x->attn_work = (float*)salloc(x, attn_work_floats(c.n_q, 128, x->max_splits, kMaxRows) * 4);
+    x->attn_work = (float*)salloc(x, attn_work_floats(c.n_q, c.head_dim, x->max_splits, kMaxRows) * 4);
     x->sw_part = (float*)salloc(x, (size_t)kSwMaxSplit * 16 * R * 4);
     x->sw_cnt = (unsigned*)salloc(x, kSwMaxSplit * 4);
     x->gab = (float*)salloc(x, (size_t)2 * kMaxRows * c.gdn_vh * 4);
@@ -917,8 +921,8 @@ int q27x_load_synthetic(q27x_ctx* x, uint64_t seed) {
                                 tensor_key(seed, tid(code, T_K)), 0, 0, s))) return r2;
         if ((r2 = launch_gen_i8(Y.qkv.w + (size_t)(x->qr + x->kvr) * H, Y.qkv.s + (size_t)(x->qr + x->kvr) * (H / 64),
                                 x->kvr, H, tensor_key(seed, tid(code, T_V)), 0, 0, s))) return r2;
-        VEC(Y.q_norm, tid(code, T_Q_NORM), 128, 0.02f, 0.0f, 0);
-        VEC(Y.k_norm, tid(code, T_K_NORM), 128, 0.02f, 0.0f, 0);
+        VEC(Y.q_norm, tid(code, T_Q_NORM), c.head_dim, 0.02f, 0.0f, 0);
+        VEC(Y.k_norm, tid(code, T_K_NORM), c.head_dim, 0.02f, 0.0f, 0);
         if ((r2 = gen_i8m(x, Y.o, H, x->att))) return r2;
         if ((r2 = launch_gen_i8(Y.o.w, Y.o.s, H, x->att, tensor_key(seed, tid(code, T_O)), 0, 0, s))) return r2;
         return Q27X_OK;
@@ -1375,7 +1379,7 @@ static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
         (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
         (rc = A((void**)&B->gu, C * std::max(2 * I, x->nz) * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
         (rc = A((void**)&B->rowsc, 3 * C * c.gdn_vh * 4)) ||
-        (rc = A((void**)&B->work, attn_work_floats(c.n_q, 128, (int)ms, kPfAttnRows) * 4)) ||
+        (rc = A((void**)&B->work, attn_work_floats(c.n_q, c.head_dim, (int)ms, kPfAttnRows) * 4)) ||
         (rc = A((void**)&B->cv, C * x->nqkv * 2))) {
         for (void* p : B->allocs) (void)hipFree(p);
         delete B;

@@ -70,7 +70,62 @@ __device__ __forceinline__ void store_kv(const AttnArgs& a, float y0, float y1, 
     }
 }
 
+// The same prep for a head of HD = 64 NC dims (128 or 256): lane l holds dims l + 64 i, i < NC.
+// The head's sum of squares adds the 64-dim chunks' trees in order (((w0 + w1) + w2) + w3); RoPE on
+// the first rot <= 64 dims (all in chunk 0, partner lane l ^ rot/2), or on all 128 dims of a
+// 128-wide head (partners l and l + 64).
+template <int HD>
+__device__ __forceinline__ void norm_rope_n(const AttnArgs& a, const uint16_t* src, const uint16_t* wgt, int pos, int l,
+                                            float (&y)[HD / 64]) {
+    constexpr int NC = HD / 64;
+    float x[NC], wg[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) { x[i] = bf2f(src[l + 64 * i]); wg[i] = bf2f(wgt[l + 64 * i]); }
+    const int half = a.rot >> 1;
+    const int f = (a.rot <= 64) ? (l & (half - 1)) : l;
+    const float c = a.rope_cos[(size_t)pos * half + f], s = a.rope_sin[(size_t)pos * half + f];
+    float ss = bcast0(tree64(x[0] * x[0]));
+#pragma unroll
+    for (int i = 1; i < NC; ++i) ss = ss + bcast0(tree64(x[i] * x[i]));
+    const float inv = rsqrt_cr(ss * (1.0f / (float)HD) + a.eps);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) y[i] = x[i] * inv * (1.0f + wg[i]);
+    if (a.rot <= 64) {
+        const float pv = __shfl_xor(y[0], half, 64);
+        if (l < a.rot) {
+            const float rv = (l < half) ? -pv : pv;
+            y[0] = y[0] * c + rv * s;
+        }
+    } else if constexpr (HD == 128) {   // rot == 128
+        const float n0 = y[0] * c + (-y[1]) * s;
+        const float n1 = y[1] * c + y[0] * s;
+        y[0] = n0; y[1] = n1;
+    }
+}
+// K (normed, roped) and V (raw) of one kv head row of HD dims -> int8 with one fp32 scale per
+// kv_group (<= 64: a group lies inside one 64-dim chunk) at cache element offset off.
+template <int HD>
+__device__ __forceinline__ void store_kv_n(const AttnArgs& a, const float (&yk)[HD / 64], const float (&yv)[HD / 64],
+                                           size_t off, int l) {
+    const int G = a.kv_group;
+#pragma unroll
+    for (int q = 0; q < 2 * (HD / 64); ++q) {
+        const int i = q % (HD / 64);
+        const float v = (q < HD / 64) ? yk[i] : yv[i];
+        const float mx = max_xor(fabsf(v), G);
+        const float sc = mx * (1.0f / 127.0f);
+        const float qi = (sc > 0.0f) ? (1.0f / sc) : 0.0f;
+        const int dd = l + 64 * i;
+        int8_t* c8 = (q < HD / 64) ? a.kc : a.vc;
+        float* cs8 = (q < HD / 64) ? a.ks : a.vs;
+        c8[off + dd] = qcode(v, qi);
+        if ((dd % G) == 0) cs8[(off + dd) / G] = sc;
+    }
+}
+
+template <int HD>
 __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    constexpr int NC = HD / 64;
     if (stopped(a.stop)) return;
     const int r = blockIdx.y;
     if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
@@ -79,21 +134,23 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
     const int u = blockIdx.x + (a.prep_kv_only ? a.nq : 0);
     const bool isq = u < a.nq;
     const int head = isq ? u : u - a.nq;
-    const int qw = a.gate ? 2 * kHD : kHD;
-    const int qrows = a.nq * qw, kvrows = a.nkv * kHD;
+    const int qw = a.gate ? 2 * HD : HD;
+    const int qrows = a.nq * qw, kvrows = a.nkv * HD;
     const uint16_t* row = a.qkv + (size_t)r * a.qkv_stride;
-    const uint16_t* src = isq ? row + (size_t)head * qw : row + qrows + (size_t)head * kHD;
-    float y0, y1;
-    norm_rope(a, src, isq ? a.q_norm_w : a.k_norm_w, pos, l, y0, y1);
+    const uint16_t* src = isq ? row + (size_t)head * qw : row + qrows + (size_t)head * HD;
+    float y[NC];
+    norm_rope_n<HD>(a, src, isq ? a.q_norm_w : a.k_norm_w, pos, l, y);
     if (isq) {
-        uint16_t* dst = a.qh + (size_t)r * a.nq * kHD + (size_t)head * kHD;
-        dst[l] = f2bf(y0);
-        dst[l + 64] = f2bf(y1);
+        uint16_t* dst = a.qh + (size_t)r * a.nq * HD + (size_t)head * HD;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) dst[l + 64 * i] = f2bf(y[i]);
         return;
     }
-    const uint16_t* vsrc = row + qrows + kvrows + (size_t)head * kHD;
-    float deq[4];
-    store_kv(a, y0, y1, bf2f(vsrc[l]), bf2f(vsrc[l + 64]), (size_t)pos * kvrows + (size_t)head * kHD, l, deq);
+    const uint16_t* vsrc = row + qrows + kvrows + (size_t)head * HD;
+    float v[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) v[i] = bf2f(vsrc[l + 64 * i]);
+    store_kv_n<HD>(a, y, v, (size_t)pos * kvrows + (size_t)head * HD, l);
 }
 
 size_t attn_work_floats(int nq, int hd, int max_splits, int nr) {
@@ -125,16 +182,17 @@ constexpr int kSplitBlocks = 256;
 // dequantized values straight into its tile.
 // Row tiles (a.zrows > 0, prefill): block z of grid.z works on rows z zrows .. of the query rows,
 // at their positions, with its own work region, exactly as a launch of those rows alone would.
+template <int HD = kHD>
 __device__ __forceinline__ void tile_rows(AttnArgs& a, int nr, int& pos0, int& nact) {
     const int z = blockIdx.z;
     const int r0 = z * a.zrows;
     pos0 += r0;
     nact = (a.ztotal - r0 < a.zrows) ? a.ztotal - r0 : a.zrows;
-    a.qh += (size_t)r0 * a.nq * kHD;
+    a.qh += (size_t)r0 * a.nq * HD;
     a.qkv += (size_t)r0 * a.qkv_stride;
-    a.work += (size_t)z * nr * a.nq * a.max_splits * (size_t)(kHD + 2);   // attn_work_floats of the tile
-    a.out += (size_t)r0 * a.nq * kHD;
-    if (a.xq) { a.xq += (size_t)r0 * a.nq * kHD; a.xs += (size_t)r0 * a.nq * kHD / 16; }
+    a.work += (size_t)z * nr * a.nq * a.max_splits * (size_t)(HD + 2);   // attn_work_floats of the tile
+    a.out += (size_t)r0 * a.nq * HD;
+    if (a.xq) { a.xq += (size_t)r0 * a.nq * HD; a.xs += (size_t)r0 * a.nq * HD / 16; }
 }
 template <int NQW, int QPT, bool PREP>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr) {
@@ -411,18 +469,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 // waits count all of them): one round trip for the whole window. Each thread then reads only the
 // column its own wave moved, so only the shared weights need a barrier. Longer contexts take
 // further windows.
-constexpr int kCombWin = 296;                    // splits per LDS window at most (18,944 positions)
+// splits per LDS window at most: 296 for 128-wide heads (18,944 positions), 150 for 256-wide
+__host__ __device__ constexpr int comb_cap(int hd) { return hd == 128 ? 296 : 150; }
 // the window of a launch: its split count, capped (short contexts keep several blocks per CU)
-__host__ __device__ inline int comb_win(int max_splits) { return max_splits < kCombWin ? max_splits : kCombWin; }
-__host__ __device__ inline size_t comb_lds(int max_splits) { return (size_t)comb_win(max_splits) * (kHD + 2) * 4; }
-__global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
+__host__ __device__ inline int comb_win(int max_splits, int hd = kHD) {
+    return max_splits < comb_cap(hd) ? max_splits : comb_cap(hd);
+}
+__host__ __device__ inline size_t comb_lds(int max_splits, int hd = kHD) {
+    return (size_t)comb_win(max_splits, hd) * (hd + 2) * 4;
+}
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a, int nr) {
     if (stopped(a.stop)) return;
     const int hq = blockIdx.x, r = blockIdx.y;
     if (a.nact_ptr && r >= ld_uniform(a.nact_ptr)) return;
     int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
     if (a.zrows) {
         int nact = 0;
-        tile_rows(a, nr, pos0, nact);
+        tile_rows<HD>(a, nr, pos0, nact);
         if (r >= nact) return;
     }
     const int L = pos0 + r + 1;
@@ -430,39 +494,41 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     const int ms = a.max_splits;
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const float* wo = a.work;
-    const float* wm = a.work + (size_t)nr * a.nq * ms * kHD;
+    const float* wm = a.work + (size_t)nr * a.nq * ms * HD;
     const float* wl = wm + (size_t)nr * a.nq * ms;
     const size_t base = ((size_t)r * a.nq + hq) * ms;
-    __shared__ float smax[2];
+    __shared__ float smax[HD / 64];
     extern __shared__ float cwin[];                 // [W][128] outputs | [W] w | [W] l
-    const int W = comb_win(ms);
+    const int W = comb_win(ms, HD);
     float* so = cwin;
-    float* cw = cwin + (size_t)W * kHD;
+    float* cw = cwin + (size_t)W * HD;
     float* cl = cw + W;
     // this wave's 64 dims of splits w0 .. w0 + wn - 1 into LDS (lane l -> dim 64 wv + l)
     auto dma = [&](int w0, int wn) __attribute__((always_inline)) {
         for (int j = 0; j < wn; ++j)
-            __builtin_amdgcn_global_load_lds((const void*)(wo + (base + w0 + j) * kHD + 64 * wv + lane),
-                                             (__attribute__((address_space(3))) void*)&so[j * kHD + 64 * wv], 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(wo + (base + w0 + j) * HD + 64 * wv + lane),
+                                             (__attribute__((address_space(3))) void*)&so[j * HD + 64 * wv], 4, 0, 0);
     };
     // M over all splits: loads 4 splits per thread per batch, all issued before the first use
     // (the first batch and the first window's transfers are issued by every thread: a transfer
     // moves the lanes that execute it)
     float M = -__builtin_huge_valf();
     const int wn0 = ns < W ? ns : W;
-    for (int s0 = t; s0 - t < ns; s0 += 4 * kHD) {
+    for (int s0 = t; s0 - t < ns; s0 += 4 * HD) {
         float mv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) mv[u] = wm[base + ((s0 + u * kHD < ns) ? s0 + u * kHD : ns - 1)];
+        for (int u = 0; u < 4; ++u) mv[u] = wm[base + ((s0 + u * HD < ns) ? s0 + u * HD : ns - 1)];
         if (s0 == t) dma(0, wn0);                   // the first window's transfers, behind the first batch
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            if (s0 + u * kHD < ns) M = fmaxf(M, mv[u]);
+            if (s0 + u * HD < ns) M = fmaxf(M, mv[u]);
     }
     M = max_xor(M, 64);
     if (lane == 0) smax[t >> 6] = M;
     __syncthreads();
-    M = fmaxf(smax[0], smax[1]);
+    M = smax[0];
+#pragma unroll
+    for (int w = 1; w < HD / 64; ++w) M = fmaxf(M, smax[w]);
     float den = 0.0f, o = 0.0f;
     for (int w0 = 0; w0 < ns; w0 += W) {
         const int wn = (ns - w0 < W) ? ns - w0 : W;
@@ -470,21 +536,21 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
             __syncthreads();                        // the previous window is consumed
             dma(w0, wn);
         }
-        for (int j = t; j < wn; j += kHD) { cw[j] = qexp2(wm[base + w0 + j] - M); cl[j] = wl[base + w0 + j]; }
+        for (int j = t; j < wn; j += HD) { cw[j] = qexp2(wm[base + w0 + j] - M); cl[j] = wl[base + w0 + j]; }
         __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's transfers have landed
         __syncthreads();                            // every thread's weights are in LDS
         for (int j = 0; j < wn; ++j) {
             const float w = cw[j];
             den = __builtin_fmaf(cl[j], w, den);
-            o = __builtin_fmaf(so[j * kHD + t], w, o);
+            o = __builtin_fmaf(so[j * HD + t], w, o);
         }
     }
     const float inv = 1.0f / den;
     float v = o * inv;
-    const int qw = a.gate ? 2 * kHD : kHD;
-    if (a.gate) v = v * qsigmoid(bf2f(a.qkv[(size_t)r * a.qkv_stride + (size_t)hq * qw + kHD + t]));
+    const int qw = a.gate ? 2 * HD : HD;
+    if (a.gate) v = v * qsigmoid(bf2f(a.qkv[(size_t)r * a.qkv_stride + (size_t)hq * qw + HD + t]));
     const uint16_t vb = f2bf(v);
-    const size_t k = (size_t)r * a.nq * kHD + (size_t)hq * kHD + t;
+    const size_t k = (size_t)r * a.nq * HD + (size_t)hq * HD + t;
     a.out[k] = vb;
     if (a.xq) {   // the per-16 quantizer with g = 1/in_scale (s = mx g / 127, 1/s -> g / s)
         const float g = (a.in_scale > 0.0f) ? 1.0f / a.in_scale : 1.0f;
@@ -497,13 +563,138 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a, int nr) {
     }
 }
 
+// ---------------------------------------------------------------- general geometry
+// Heads of HD = 256 dims (the reference trunk's 24q / 4kv x 256, include/q27.h:25-35) or GQA groups
+// that are not a power of two. Queries come from qh (the prep runs as its own launch before), K and
+// V from the cache. The splits, and the order of every sum, are those of the kernels above and of
+// the oracle: score = ((c0 + c1) + c2) + c3 with c_j the fmaf chain over dims [j HD/4, (j+1) HD/4),
+// on K values code x scale; the split softmax m = max, p = 2^(x - m), l = the 64-lane shfl_down
+// tree; o = ((o0 + o1) + o2) + o3 with o_j the fmaf chain over the row's visible keys of the split's
+// j-th 16-key block, in key order. Block = (split, kv head), all rows and GQA heads of the kv head:
+// the int8 K/V tile and its scales in LDS (an fp32 tile of 256-wide rows would not leave room for
+// the queries), plain VALU chains, one thread per (query, key) score and per (query, dim) output.
+constexpr int kGThreads = 512;
+constexpr int kSpG = kSplit + 1;                 // score row stride (floats)
+template <int HD>
+__host__ __device__ constexpr int tile_stride_g() { return HD + 16; }   // int8 K/V tile row stride
+template <int HD>
+__global__ __launch_bounds__(kGThreads) void k_attn_split_g(AttnArgs a, int nr) {
+    if (stopped(a.stop)) return;
+    constexpr int KS = tile_stride_g<HD>();
+    constexpr int NSC = HD / 16;                 // scales per key row at most (kv_group >= 16)
+    const int kvh = blockIdx.y;
+    const int G = a.nq / a.nkv;
+    int nact = a.nact_ptr ? ld_uniform(a.nact_ptr) : nr;
+    int pos0 = a.pos0_ptr ? ld_uniform(a.pos0_ptr) : a.pos0_imm;
+    if (a.zrows) tile_rows<HD>(a, nr, pos0, nact);
+    const int Lmax = pos0 + nact;
+    const int nqr = nact * G;
+    const int kvrows = a.nkv * HD;
+    const int ms = a.max_splits;
+    const int KG = a.kv_group, nsc = HD / KG;
+    __shared__ __attribute__((aligned(16))) int8_t k8[kSplit * KS];
+    __shared__ __attribute__((aligned(16))) int8_t v8[kSplit * KS];
+    __shared__ float ksc[kSplit * NSC];
+    __shared__ float vsc[kSplit * NSC];
+    extern __shared__ float dyn[];
+    float* qf = dyn;                                // [nr G][HD] queries as fp32
+    float* sp = dyn + (size_t)nr * G * HD;          // [nr G][kSpG] scores, then p
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    float* wo = a.work;
+    float* wm = a.work + (size_t)nr * a.nq * ms * HD;
+    float* wl = wm + (size_t)nr * a.nq * ms;
+    for (int i = t; i < nqr * HD; i += kGThreads) {
+        const int qi = i / HD, d = i - qi * HD;
+        const int r = qi / G, g = qi - r * G;
+        qf[i] = bf2f(a.qh[(size_t)r * a.nq * HD + (size_t)(kvh * G + g) * HD + d]);
+    }
+    for (int s = blockIdx.x; s * kSplit < Lmax; s += gridDim.x) {
+        const int k0 = s * kSplit;
+        const int nk = (Lmax - k0 < kSplit) ? (Lmax - k0) : kSplit;
+        __syncthreads();                            // the previous split's tiles are consumed
+        for (int i = t; i < nk * (HD / 16); i += kGThreads) {
+            const int k = i / (HD / 16), c = i - k * (HD / 16);
+            const size_t off = (size_t)(k0 + k) * kvrows + (size_t)kvh * HD + 16 * c;
+            *(uint4*)&k8[k * KS + 16 * c] = *(const uint4*)(a.kc + off);
+            *(uint4*)&v8[k * KS + 16 * c] = *(const uint4*)(a.vc + off);
+        }
+        for (int i = t; i < nk * nsc; i += kGThreads) {
+            const int k = i / nsc, c = i - k * nsc;
+            const size_t off = ((size_t)(k0 + k) * kvrows + (size_t)kvh * HD) / KG + c;
+            ksc[k * NSC + c] = a.ks[off];
+            vsc[k * NSC + c] = a.vs[off];
+        }
+        __syncthreads();
+        // scores, one (query, key) pair per thread at a time
+        for (int i = t; i < nqr * kSplit; i += kGThreads) {
+            const int qi = i >> 6, key = i & (kSplit - 1);
+            if (key >= nk) continue;
+            const float* q = qf + (size_t)qi * HD;
+            const int8_t* kr = k8 + key * KS;
+            const float* kscr = ksc + key * NSC;
+            float c4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float acc = 0.0f;
+                for (int d = j * (HD / 4); d < (j + 1) * (HD / 4); ++d)
+                    acc = __builtin_fmaf(q[d], (float)kr[d] * kscr[d / KG], acc);
+                c4[j] = acc;
+            }
+            sp[(size_t)qi * kSpG + key] = (((c4[0] + c4[1]) + c4[2]) + c4[3]) * a.sl2e;
+        }
+        __syncthreads();
+        // split softmax, one wave per query, lane = key
+        for (int qi = wv; qi < nqr; qi += kGThreads / 64) {
+            const int r = qi / G, g = qi - r * G;
+            const int L = pos0 + r + 1;
+            const int nv = (L - k0 < nk) ? (L - k0) : nk;       // visible keys of this row in the split
+            const float x = (lane < nv) ? sp[(size_t)qi * kSpG + lane] : -__builtin_huge_valf();
+            const float m = max_xor(x, 64);
+            const float p = (lane < nv) ? qexp2(x - m) : 0.0f;
+            const float l = tree64(p);
+            sp[(size_t)qi * kSpG + lane] = p;
+            if (lane == 0 && nv > 0) {
+                const size_t mi = ((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s;
+                wm[mi] = m;
+                wl[mi] = l;
+            }
+        }
+        __syncthreads();
+        // o = sum_k p_k v_k, one (query, dim) pair per thread at a time
+        for (int i = t; i < nqr * HD; i += kGThreads) {
+            const int qi = i / HD, d = i - qi * HD;
+            const int r = qi / G, g = qi - r * G;
+            const int L = pos0 + r + 1;
+            const int nv = (L - k0 < nk) ? (L - k0) : nk;
+            if (nv <= 0) continue;
+            const float* pr = sp + (size_t)qi * kSpG;
+            float o4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float acc = 0.0f;
+                const int e = (16 * (j + 1) < nv) ? 16 * (j + 1) : nv;
+                for (int key = 16 * j; key < e; ++key)
+                    acc = __builtin_fmaf(pr[key], (float)v8[key * KS + d] * vsc[key * NSC + d / KG], acc);
+                o4[j] = acc;
+            }
+            wo[(((size_t)r * a.nq + (size_t)(kvh * G + g)) * ms + s) * HD + d] = ((o4[0] + o4[1]) + o4[2]) + o4[3];
+        }
+    }
+}
+
+// The 128-wide kernels above need a power-of-two GQA group; the general kernel takes the rest.
+static bool attn_general(const AttnArgs& a) {
+    const int G = a.nq / a.nkv;
+    return a.hd != kHD || (G & (G - 1));
+}
+
 static int attn_check(const AttnArgs& a, int nr) {
-    if (a.hd != kHD || a.nkv < 1 || a.nq % a.nkv || ((a.nq / a.nkv) & (a.nq / a.nkv - 1)) || nr < 1 ||
-        nr > kMaxRows || nr * (a.nq / a.nkv) > kMaxQ ||
-        (a.kv_group != 16 && a.kv_group != 32 && a.kv_group != 64) || a.rot < 2 || a.rot > kHD || (a.rot & (a.rot - 1))) {
-        set_error("attn: unsupported shape (nq=%d nkv=%d: the GQA group must be a power of two; hd=%d nr=%d "
-                  "kv_group=%d rot=%d)", a.nq, a.nkv, a.hd, nr,
-                  a.kv_group, a.rot);
+    const bool rot_ok = a.rot >= 2 && (a.rot & (a.rot - 1)) == 0 && (a.rot <= 64 || (a.rot == kHD && a.hd == kHD));
+    if ((a.hd != 128 && a.hd != 256) || a.nkv < 1 || a.nq % a.nkv || nr < 1 || nr > kMaxRows ||
+        nr * (a.nq / a.nkv) > kMaxQ || (a.kv_group != 16 && a.kv_group != 32 && a.kv_group != 64) || !rot_ok) {
+        set_error("attn: unsupported shape (nq=%d nkv=%d hd=%d nr=%d kv_group=%d rot=%d: hd 128 or 256, at most %d "
+                  "query vectors per kv head, rot a power of two <= 64 or the whole 128-wide head)", a.nq, a.nkv, a.hd,
+                  nr, a.kv_group, a.rot, kMaxQ);
         return Q27X_E_SHAPE;
     }
     return Q27X_OK;
@@ -511,23 +702,39 @@ static int attn_check(const AttnArgs& a, int nr) {
 
 int launch_attn_prep(const AttnArgs& a, int nr, hipStream_t s) {
     if (int rc = attn_check(a, nr)) return rc;
-    if (a.rot == kHD || a.rot <= 64) {
-        hipLaunchKernelGGL(k_attn_prep, dim3(a.nq + a.nkv, nr), dim3(64), 0, s, a);
-        Q27X_HIP(hipGetLastError());
-        return Q27X_OK;
-    }
-    set_error("attn: rot=%d unsupported", a.rot);
-    return Q27X_E_SHAPE;
+    if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep<256>, dim3(a.nq + a.nkv, nr), dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_attn_prep<128>, dim3(a.nq + a.nkv, nr), dim3(64), 0, s, a);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
 }
 
 // prep of any number of rows (prefill): one wave per (head, row); K/V only when a.prep_kv_only
 int launch_attn_prep_rows(const AttnArgs& a, int nrows, hipStream_t s) {
     if (int rc = attn_check(a, 1)) return rc;
-    if (nrows < 1 || !(a.rot == kHD || a.rot <= 64) || a.nact_ptr) {
-        set_error("attn prep: rows=%d rot=%d unsupported", nrows, a.rot);
+    if (nrows < 1 || a.nact_ptr) {
+        set_error("attn prep: rows=%d unsupported", nrows);
         return Q27X_E_SHAPE;
     }
-    hipLaunchKernelGGL(k_attn_prep, dim3(a.prep_kv_only ? a.nkv : a.nq + a.nkv, nrows), dim3(64), 0, s, a);
+    const dim3 grid(a.prep_kv_only ? a.nkv : a.nq + a.nkv, nrows);
+    if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep<256>, grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_attn_prep<128>, grid, dim3(64), 0, s, a);
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
+template <int HD>
+static int launch_split_g(const AttnArgs& a, int nr, hipStream_t s) {
+    const size_t lds = (size_t)nr * (a.nq / a.nkv) * (HD + kSpG) * 4;
+    static std::once_flag attr;
+    static hipError_t attr_e = hipSuccess;
+    std::call_once(attr, [] {
+        attr_e = hipFuncSetAttribute((const void*)k_attn_split_g<HD>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)((size_t)kMaxQ * (HD + kSpG) * 4));
+    });
+    Q27X_HIP(attr_e);
+    const int bx = a.max_splits < kSplitBlocks / a.nkv ? a.max_splits : (kSplitBlocks / a.nkv > 0 ? kSplitBlocks / a.nkv : 1);
+    const dim3 grid(bx, a.nkv, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u);
+    hipLaunchKernelGGL(k_attn_split_g<HD>, grid, dim3(kGThreads), lds, s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }
@@ -564,21 +771,37 @@ static int launch_split(const AttnArgs& a, int nr, hipStream_t s) {
 int launch_attn(const AttnArgs& a, int nr, hipStream_t s, bool prep_fused) {
     if (int rc = attn_check(a, nr)) return rc;
     if (!a.work || a.max_splits < 1) { set_error("attn: no work buffer"); return Q27X_E_ARG; }
-    static bool comb_attr = false;
-    if (!comb_attr) {
-        Q27X_HIP(hipFuncSetAttribute((const void*)k_attn_combine, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)comb_lds(kCombWin)));
-        comb_attr = true;
-    }
-    if (prep_fused && !(a.rot == kHD || a.rot <= 64)) { set_error("attn: rot=%d unsupported", a.rot); return Q27X_E_SHAPE; }
+    static std::once_flag comb_attr;
+    static hipError_t comb_e = hipSuccess;
+    std::call_once(comb_attr, [] {
+        comb_e = hipFuncSetAttribute((const void*)k_attn_combine<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)comb_lds(comb_cap(128), 128));
+        if (comb_e == hipSuccess)
+            comb_e = hipFuncSetAttribute((const void*)k_attn_combine<256>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)comb_lds(comb_cap(256), 256));
+    });
+    Q27X_HIP(comb_e);
     if (a.zrows && (prep_fused || a.zrows != nr || a.ztotal < 1 || a.nact_ptr)) {
         set_error("attn: row tiles need separate prep, zrows == nr and no active-row count");
         return Q27X_E_ARG;
     }
+    const dim3 cgrid(a.nq, nr, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u);
+    if (attn_general(a)) {
+        // the prep (queries to qh, the new K/V to the cache) as a launch of its own, then the splits
+        if (prep_fused) {
+            if (!a.qh) { set_error("attn: the general geometry needs a query buffer"); return Q27X_E_ARG; }
+            if (int rc = launch_attn_prep(a, nr, s)) return rc;
+        }
+        const int rc = a.hd == 256 ? launch_split_g<256>(a, nr, s) : launch_split_g<128>(a, nr, s);
+        if (rc) return rc;
+        if (a.hd == 256) hipLaunchKernelGGL(k_attn_combine<256>, cgrid, dim3(256), comb_lds(a.max_splits, 256), s, a, nr);
+        else hipLaunchKernelGGL(k_attn_combine<128>, cgrid, dim3(128), comb_lds(a.max_splits, 128), s, a, nr);
+        Q27X_HIP(hipGetLastError());
+        return Q27X_OK;
+    }
     const int rc = prep_fused ? launch_split<true>(a, nr, s) : launch_split<false>(a, nr, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, nr, a.zrows ? (unsigned)((a.ztotal + a.zrows - 1) / a.zrows) : 1u),
-                       dim3(kHD), comb_lds(a.max_splits), s, a, nr);
+    hipLaunchKernelGGL(k_attn_combine<128>, cgrid, dim3(kHD), comb_lds(a.max_splits), s, a, nr);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

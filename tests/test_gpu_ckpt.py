@@ -116,3 +116,33 @@ def test_reload_after_rounds_matches_oracle(gpu, O, tmp_path):
     om2.close()
     eng.close()
     ck.close()
+
+
+def test_checkpoint_with_trunk_attention_geometry(gpu, O, tmp_path):
+    """A synthetic checkpoint whose attention has the reference trunk's head shape (256-dim heads,
+    GQA group 6, q_proj emitting q and the gate per head, 64 rotary dims; include/q27.h:25-35) passes
+    the plan check, loads, and matches the oracle through both prefills and rounds."""
+    X = gpu
+    cfg = X.tiny_config(spec_k=2, n_layers=4, n_q=6, n_kv=1, head_dim=256, rot_dims=64)
+    syn = CS.Synth(cfg, seed=21)
+    n, b = CS.write(syn.t, tmp_path)
+    ck = X.Checkpoint(tmp_path, 3, n, b)
+    assert ck.check(cfg) == (0, "")
+    eng = X.Engine(cfg, SEED)
+    eng.load_checkpoint(ck)
+    om = O.Model(cfg, SEED)
+    CS.install_into_oracle(O, om, syn)
+    p = prompt_of(cfg, 37, seed=22)
+    assert eng.prefill(p) == om.prefill(p)
+    for r in range(3):
+        a, b_ = eng.spec_round(), om.spec_round()
+        assert a == b_, (r, a, b_)
+        check_round_state(eng, om, cfg, f"hd256 checkpoint round {r}")
+    assert eng.prefill_gemm(p) == om.prefill_gemm(p, 0)
+    check_prefill_state(eng, om, cfg, "hd256 checkpoint GEMM prefill")
+    for r in range(2):
+        a, b_ = eng.spec_round(), om.spec_round()
+        assert a == b_, (r, a, b_)
+    eng.close()
+    om.close()
+    ck.close()

@@ -294,13 +294,12 @@ def fill_kv(rng, O, L, nkv, hd, group, ctx):
     return kc, ks, vc, vs
 
 
-@pytest.mark.parametrize("L0", [1024, 4096, 16384, 20000])
-def test_attention_config2(gpu, O, L0):
-    """BASELINE config 2: GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows.
-    (20000 positions: 313 splits, past one LDS window of the combine, which then takes two.)"""
-    X = gpu
-    rng = np.random.default_rng(0x51E70002 + L0)
-    nq, nkv, hd, rot, group, nr, gate = 32, 8, 128, 32, 32, 3, 1
+def attention_case(X, O, L0, nq, nkv, hd, rot, group, nr, seed):
+    """Prep (norm, RoPE, K/V to the int8 cache) of nr rows at positions L0.. and their attention over
+    the L0 cached positions before them plus their own, through the kernel tier, against the oracle
+    bit for bit: q, the cache codes and scales, the output, its codes and scales."""
+    rng = np.random.default_rng(seed)
+    gate = 1
     ctx = L0 + nr
     qw = 2 * hd
     qkv_rows = nq * qw + 2 * nkv * hd
@@ -338,6 +337,28 @@ def test_attention_config2(gpu, O, L0):
     same("attention out", dout.download(np.uint16, (nr, nq * hd)), out_o)
     same("attention codes", dxq.download(np.int8, (nr, nq * hd)), xq_o)
     same("attention scales", dxs.download(np.float32, (nr, nq * hd // 16)), xs_o)
+
+
+@pytest.mark.parametrize("L0", [1024, 4096, 16384, 20000])
+def test_attention_config2(gpu, O, L0):
+    """BASELINE config 2: GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows.
+    (20000 positions: 313 splits, past one LDS window of the combine, which then takes two.)"""
+    attention_case(gpu, O, L0, 32, 8, 128, 32, 32, 3, 0x51E70002 + L0)
+
+
+@pytest.mark.parametrize("L0,nr", [(0, 1), (5, 3), (61, 3), (1100, 3), (2100, 8), (9700, 1), (20000, 2)])
+def test_attention_trunk_geometry(gpu, O, L0, nr):
+    """The reference trunk's attention (include/q27.h:25-35): 24 q / 4 kv heads of 256 dims (GQA
+    group 6), q_proj emitting q and the output gate per head, RoPE on the first 64 of 256 dims
+    (src/q27_attn.hip:10-11), int8 KV per 32; rows straddling a 64-key split, one split to several
+    per block (2100 and more positions: 33+ splits on 64 blocks per kv head), and a combine over
+    two LDS windows (20000 positions: 313 splits against a window of 150)."""
+    attention_case(gpu, O, L0, 24, 4, 256, 64, 32, nr, 0x51E70020 + L0)
+
+
+def test_attention_group_6_at_128(gpu, O):
+    """A GQA group that is not a power of two at 128-dim heads (the general kernel at 128)."""
+    attention_case(gpu, O, 700, 24, 4, 128, 32, 32, 3, 0x51E70021)
 
 
 def test_accept(gpu):

@@ -444,3 +444,40 @@ def test_full_width_long_context_rounds_match_oracle(gpu, O):
     cfg = X.default_config(spec_k=7, n_layers=2, attn_period=2, inter=1024, ctx=2304)
     p = prompt_of(cfg, 2100, seed=35)
     full_width_rounds(X, O, cfg, p, natural=3, forced_rounds=4, seed=37, prefill="gemm", tag="ctx 2.1K K=7")
+
+
+# ---------------------------------------------------------------- the reference trunk's attention
+# include/q27.h:25-35, src/q27_attn.hip:10-11: 24 q / 4 kv heads of 256 dims (GQA group 6), q_proj
+# rows [q 256 | gate 256] per head, RoPE on the first 64 of 256 dims
+TRUNK_ATTN = dict(head_dim=256, rot_dims=64)
+
+
+@pytest.mark.parametrize("k", [2, 7])
+def test_trunk_attention_geometry_rounds_match_oracle(gpu, O, k):
+    """Tiny widths with the trunk's attention head shape (6 q / 1 kv heads of 256 dims, group 6,
+    64 rotary dims): decode-path prefill, then rounds with the whole round state against the oracle,
+    and forced rounds with wrong drafts planted (partial acceptance)."""
+    X = gpu
+    cfg = tiny(X, spec_k=k, n_q=6, n_kv=1, **TRUNK_ATTN)
+    p = prompt_of(cfg, 70, seed=80 + k)
+    seen = full_width_rounds(X, O, cfg, p, natural=4, forced_rounds=5, seed=81 + k, tag=f"hd256 tiny K={k}")
+    assert any(s < k for s in seen), sorted(seen)
+
+
+def test_trunk_attention_geometry_gemm_prefill_matches_oracle(gpu, O):
+    """The same geometry through the GEMM-path prefill (several 128-row attention launches of
+    8-row tiles on the general kernel), then rounds."""
+    X = gpu
+    cfg = tiny(X, spec_k=2, n_q=6, n_kv=1, **TRUNK_ATTN)
+    p = prompt_of(cfg, 300, seed=84)
+    full_width_rounds(X, O, cfg, p, natural=3, forced_rounds=3, seed=85, prefill="gemm", tag="hd256 tiny GEMM prefill")
+
+
+def test_full_width_trunk_attention_geometry_rounds_match_oracle(gpu, O):
+    """BASELINE widths with the trunk's attention (hidden 5120, 24 q / 4 kv x 256, group 6, 64 rotary
+    dims; q|k|v 14336 rows, o_proj K = 6144) at 4 layers, K = 2: decode-path prefill and rounds,
+    natural and forced, bit for bit against the oracle."""
+    X = gpu
+    cfg = X.default_config(spec_k=2, n_layers=4, ctx=256, n_q=24, n_kv=4, **TRUNK_ATTN)
+    p = prompt_of(cfg, 64, seed=86)
+    full_width_rounds(X, O, cfg, p, natural=3, forced_rounds=4, seed=87, tag="hd256 full width K=2")
