@@ -10,10 +10,13 @@
 // Layout: S [VH][D=128][D] fp32 key-major. One 512-thread block per value head: thread (g, d)
 // holds key rows 32g..32g+31 of value column d (64 KiB of state per block in VGPRs). Every
 // global load of the block is issued before the first wait, so a call costs one memory round
-// trip plus on-chip work; the rows then run with one barrier each. The rows are VALU-bound on the
-// block's CU (four operations per state element per row), which is why a head stays on one block:
-// splitting its columns over CUs would need a cross-block exchange for the output norm that costs
-// more than it saves at 3 rows.
+// trip plus on-chip work; the rows then run with one barrier each. A head stays on one block: the
+// output norm sums mixed^2 over all 128 value columns, so a head split over two blocks (columns
+// 0..63 | 64..127, the prefill scan's lane layout, no barrier per row) has to exchange the two
+// halves' sums; with agent-scope stores, an arrival counter and the second block finishing the
+// head, that form was bit-exact but measured 12.4 us against this kernel's 8.5 us at 3 rows
+// (10.36 against 10.20 ms per K=7 round), the exchange's dependent round trips costing more than
+// the halved work per SIMD saves.
 // Inputs arrive prepared: the engine convolves the q|k|v channels in the epilogue of the
 // in_qkv|in_z projection and computes each row's (decay, beta) there as well (the a/b dot products
 // and their transcendentals, k_proj), so `rowsc` holds them; the kernel-tier entry passes the a/b
