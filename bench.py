@@ -353,12 +353,13 @@ def kernel_only(q27x, args):
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published
 
 
-def prefill_gemm(q27x, reps=20):
+def prefill_gemm(q27x, reps=20, gs=5120):
     """The prefill ingest GEMM on int8 MFMA (q27x_gemm_i8g) at BASELINE config 4's shape: M = 4096
-    tokens x N = 17408 (gate) x K = 5120, 1024-column groups, seeded codes and scales resident on
-    the device; device events around `reps` back-to-back launches."""
+    tokens x N = 17408 (gate) x K = 5120, groups of gs columns (the whole K by default, the
+    reference's default Q27_Q8_GS arm; 1024 is the other), seeded codes and scales resident on the
+    device; device events around `reps` back-to-back launches."""
     import ctypes
-    M, N, K, gs = 4096, 17408, 5120, 1024
+    M, N, K = 4096, 17408, 5120
     rng = np.random.default_rng(SEED)
     host = [rng.integers(-127, 127, (N, K), dtype=np.int8, endpoint=True),
             rng.uniform(1e-4, 2e-3, (N, K // gs)).astype(np.float32),
@@ -542,6 +543,7 @@ def main():
     log(f"config 4: {cfg4}")
     eng.close()
     pg = prefill_gemm(q27x)
+    pg["gs1024"] = {k_: v_ for k_, v_ in prefill_gemm(q27x, gs=1024).items() if k_ in ("us_per_launch", "achieved", "frac")}
     log(f"prefill GEMM: {pg}")
     cfg4["prefill_gemm_frac_of_int8_peak"] = pg["frac"]
 

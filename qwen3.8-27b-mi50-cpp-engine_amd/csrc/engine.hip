@@ -701,6 +701,12 @@ int q27x_ctx_create(int device, const q27x_config* cfg, q27x_ctx** out) {
         set_error("q27x_ctx_create: unsupported geometry");
         return Q27X_E_SHAPE;
     }
+    // the stored projections' input widths: down (inter), out_proj (value heads x 128), o_proj
+    for (const int K : { c.inter, c.gdn_vh * 128, c.n_q * c.head_dim })
+        if (!proj_k_supported(K)) {
+            set_error("q27x_ctx_create: no projection kernel for an input width of %d", K);
+            return Q27X_E_SHAPE;
+        }
     q27x_ctx* x = new q27x_ctx();
     x->device = device; x->c = c;
     x->H = c.hidden; x->I = c.inter; x->V = c.vocab; x->D = c.gdn_d;

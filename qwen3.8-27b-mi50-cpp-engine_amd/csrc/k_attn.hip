@@ -462,21 +462,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a, int nr)
 
 // Merge the splits of one (row, query head): M = max m_s; w_s = 2^(m_s - M); den and o accumulated
 // over the splits in order (fmaf); x sigmoid(gate) -> bf16 -> per-16 quantize. Thread t owns dim
-// t. The split outputs of up to kCombWin splits go to LDS at once by LDS DMA (each wave moves its
-// 64 dims of every split: up to ~150 KiB per block in flight; staged 32 splits at a time, each
-// chunk waited a full memory round trip), requested right behind the first batch of m_s loads.
-// The waits after that cover every transfer (their count is a run-time loop, so the compiler's
-// waits count all of them): one round trip for the whole window. Each thread then reads only the
-// column its own wave moved, so only the shared weights need a barrier. Longer contexts take
-// further windows.
+// t. The split outputs of a window of splits (contiguous in the work area) go to LDS at once by
+// 16-byte LDS DMA, 1 KiB per wave instruction (up to ~150 KiB per block in flight; staged 32
+// splits at a time, each chunk waited a full memory round trip), requested right behind the first
+// batch of the m_s and l_s loads, whose values then give the first window's weights without a
+// second round trip. The waits after that cover every transfer (their count is a run-time loop,
+// so the compiler's waits count all of them), then a barrier: one round trip for the whole
+// window. Longer contexts take further windows.
 // splits per LDS window at most: 296 for 128-wide heads (18,944 positions), 150 for 256-wide
 __host__ __device__ constexpr int comb_cap(int hd) { return hd == 128 ? 296 : 150; }
 // the window of a launch: its split count, capped (short contexts keep several blocks per CU)
 __host__ __device__ inline int comb_win(int max_splits, int hd = kHD) {
     return max_splits < comb_cap(hd) ? max_splits : comb_cap(hd);
 }
+// the window's split outputs, a 1 KiB pad (the tail of the last 16-byte transfer block), the
+// window's weights and sums
 __host__ __device__ inline size_t comb_lds(int max_splits, int hd = kHD) {
-    return (size_t)comb_win(max_splits, hd) * (hd + 2) * 4;
+    return ((size_t)comb_win(max_splits, hd) * (hd + 2) + 256) * 4;
 }
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a, int nr) {
@@ -497,28 +499,45 @@ __global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a, int nr) {
     const float* wm = a.work + (size_t)nr * a.nq * ms * HD;
     const float* wl = wm + (size_t)nr * a.nq * ms;
     const size_t base = ((size_t)r * a.nq + hq) * ms;
-    __shared__ float smax[HD / 64];
-    extern __shared__ float cwin[];                 // [W][128] outputs | [W] w | [W] l
+    constexpr int NWV = HD / 64;
+    __shared__ float smax[NWV];
+    extern __shared__ __attribute__((aligned(16))) float cwin[];   // [W][HD] outputs | 256 pad | [W] w | [W] l
     const int W = comb_win(ms, HD);
     float* so = cwin;
-    float* cw = cwin + (size_t)W * HD;
+    float* cw = cwin + (size_t)W * HD + 256;
     float* cl = cw + W;
-    // this wave's 64 dims of splits w0 .. w0 + wn - 1 into LDS (lane l -> dim 64 wv + l)
+    // splits w0 .. w0 + wn - 1 (wn HD contiguous floats of the work area) into LDS in 1 KiB blocks,
+    // block b by wave b % NWV, 16 bytes per lane; lanes past the window's end re-read its first
+    // bytes into the pad behind it
+    const uint32_t so_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)so;
     auto dma = [&](int w0, int wn) __attribute__((always_inline)) {
-        for (int j = 0; j < wn; ++j)
-            __builtin_amdgcn_global_load_lds((const void*)(wo + (base + w0 + j) * HD + 64 * wv + lane),
-                                             (__attribute__((address_space(3))) void*)&so[j * HD + 64 * wv], 4, 0, 0);
+        const float* src = wo + (base + w0) * HD;
+        const int nf = wn * HD;
+        for (int b = wv; 256 * b < nf; b += NWV) {
+            const int f = 256 * b + 4 * lane;
+            lds_dma16(src + (f < nf ? f : 0), __builtin_amdgcn_readfirstlane(so_lds + 1024u * b));
+        }
     };
-    // M over all splits: loads 4 splits per thread per batch, all issued before the first use
-    // (the first batch and the first window's transfers are issued by every thread: a transfer
-    // moves the lanes that execute it)
+    // M over all splits: m and l of 4 splits per thread per batch, all issued before the first use;
+    // the first batch's values stay in registers for the first window's weights (4 HD splits cover
+    // any window). The first window's transfers are issued behind the first batch by every thread
+    // (a transfer moves the lanes that execute it).
     float M = -__builtin_huge_valf();
+    float m0v[4], l0v[4];
     const int wn0 = ns < W ? ns : W;
     for (int s0 = t; s0 - t < ns; s0 += 4 * HD) {
-        float mv[4];
+        float mv[4], lv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) mv[u] = wm[base + ((s0 + u * HD < ns) ? s0 + u * HD : ns - 1)];
-        if (s0 == t) dma(0, wn0);                   // the first window's transfers, behind the first batch
+        for (int u = 0; u < 4; ++u) {
+            const size_t i = base + ((s0 + u * HD < ns) ? s0 + u * HD : ns - 1);
+            mv[u] = wm[i];
+            lv[u] = wl[i];
+        }
+        if (s0 == t) {
+            dma(0, wn0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) { m0v[u] = mv[u]; l0v[u] = lv[u]; }
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             if (s0 + u * HD < ns) M = fmaxf(M, mv[u]);
@@ -535,8 +554,14 @@ __global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a, int nr) {
         if (w0 > 0) {
             __syncthreads();                        // the previous window is consumed
             dma(w0, wn);
+            for (int j = t; j < wn; j += HD) { cw[j] = qexp2(wm[base + w0 + j] - M); cl[j] = wl[base + w0 + j]; }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = t + u * HD;
+                if (j < wn) { cw[j] = qexp2(m0v[u] - M); cl[j] = l0v[u]; }
+            }
         }
-        for (int j = t; j < wn; j += HD) { cw[j] = qexp2(wm[base + w0 + j] - M); cl[j] = wl[base + w0 + j]; }
         __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's transfers have landed
         __syncthreads();                            // every thread's weights are in LDS
         for (int j = 0; j < wn; ++j) {

@@ -214,20 +214,6 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
         const float swv = gv / (1.0f + qexp(-gv));
         return swv * uv * gscale;
     };
-    if (gs > 256 * 8) {
-        // a group wider than the values a thread holds (the whole I): the group max first, then
-        // every value computed again by the same expression and quantized
-        float mx = 0.0f;
-        for (int j = t; j < gs; j += 256) mx = fmaxf(mx, fabsf(value(g * gs + j)));
-        mx = max_xor(mx, 64);
-        if ((t & 63) == 0) red[t >> 6] = mx;
-        __syncthreads();
-        const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
-        if (t == 0) xs[(size_t)tok * ng + g] = sc;
-        for (int j = t; j < gs; j += 256) xq[(size_t)tok * I + g * gs + j] = qcode(value(g * gs + j), qi);
-        return;
-    }
     constexpr int VPT = 8;                         // values per thread held for the two passes
     float v[VPT];
     float mx = 0.0f;
@@ -250,14 +236,68 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
     for (int u = 0; u < VPT; ++u)
         if (t + 256 * u < gs) xq[(size_t)tok * I + g * gs + t + 256 * u] = qcode(v[u], qi);
 }
+// The same for groups wider than 2048 outputs (the whole I, the default arm): one 1024-thread
+// block per (group, token) holds the group's values in registers, four consecutive outputs per
+// thread and chunk (one 16-byte gate and one 16-byte up load, one 4-byte code store), so every
+// value is computed once; the max, scale and codes are those of the kernel above.
+constexpr int kSwWideT = 1024, kSwWideQ = 5;       // threads, quads per thread (gs <= 20480)
+__global__ __launch_bounds__(kSwWideT) void k_pf_swiglu_quant_wide(const float* __restrict__ gu, int I, int gs,
+                                                                  float gscale, int8_t* __restrict__ xq,
+                                                                  float* __restrict__ xs) {
+    const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, ng = I / gs;
+    __shared__ float red[kSwWideT / 64];
+    const float* row = gu + (size_t)tok * 2 * I;
+    float v[kSwWideQ][4];
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kSwWideQ; ++u) {
+        const int j = 4 * (t + kSwWideT * u);      // output within the group
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = 0.0f;
+        if (j < gs) {
+            const int i = g * gs + j, gr = (i >> 4) * 32 + (i & 15);
+            const float4 gv4 = *(const float4*)(row + gr), uv4 = *(const float4*)(row + gr + 16);
+            const float gv[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uv[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float swv = gv[e] / (1.0f + qexp(-gv[e]));
+                v[u][e] = swv * uv[e] * gscale;
+                mx = fmaxf(mx, fabsf(v[u][e]));
+            }
+        }
+    }
+    mx = max_xor(mx, 64);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < kSwWideT / 64; ++w) m = fmaxf(m, red[w]);
+    const float sc = m * (1.0f / 127.0f), qi = (sc > 0.0f) ? 1.0f / sc : 0.0f;
+    if (t == 0) xs[(size_t)tok * ng + g] = sc;
+#pragma unroll
+    for (int u = 0; u < kSwWideQ; ++u) {
+        const int j = 4 * (t + kSwWideT * u);
+        if (j < gs) {
+            uint32_t pk = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(v[u][e], qi)) << (8 * e);
+            *(uint32_t*)(xq + (size_t)tok * I + (size_t)g * gs + j) = pk;
+        }
+    }
+}
 int launch_pf_swiglu_quant(const float* gu, int I, int gs, float gscale, int C, int8_t* xq, float* xs,
                            hipStream_t s) {
-    if (!gu || !xq || !xs || C < 1 || (I & 31) || gs < 16 || (gs & 15) || (I % gs)) {
+    if (!gu || !xq || !xs || C < 1 || (I & 31) || gs < 16 || (gs & 15) || (I % gs) || gs > 4 * kSwWideT * kSwWideQ ||
+        ((uintptr_t)gu & 15) || ((uintptr_t)xq & 3) || (I & 3)) {
         set_error("prefill swiglu: bad arguments (I %d, gs %d)", I, gs);
         return Q27X_E_ARG;
     }
-    hipLaunchKernelGGL(k_pf_swiglu_quant, dim3((unsigned)(I / gs), (unsigned)C), dim3(256), 0, s, gu, I, gs, gscale, xq,
-                       xs);
+    if (gs > 256 * 8)
+        hipLaunchKernelGGL(k_pf_swiglu_quant_wide, dim3((unsigned)(I / gs), (unsigned)C), dim3(kSwWideT), 0, s, gu, I, gs,
+                           gscale, xq, xs);
+    else
+        hipLaunchKernelGGL(k_pf_swiglu_quant, dim3((unsigned)(I / gs), (unsigned)C), dim3(256), 0, s, gu, I, gs, gscale,
+                           xq, xs);
     Q27X_HIP(hipGetLastError());
     return Q27X_OK;
 }

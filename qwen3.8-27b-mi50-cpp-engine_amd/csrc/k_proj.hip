@@ -669,6 +669,12 @@ static int route(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     return full ? route_nr<EPI_STORE, true>(a, nr, s) : route_nr<EPI_STORE, false>(a, nr, s);
 }
 
+bool proj_k_supported(int K) {
+    if (K < 64 || (K & 63)) return false;
+    const int ns = (K + 1023) / 1024;
+    return ns == 1 || ns == 2 || ns == 4 || ns == 5 || ns == 6 || (ns == 17 && (K & 1023) == 0);
+}
+
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     if (!a.W || !a.WS || a.rows < 1 || a.K < 64 || (a.K & 63) || nr < 1 || nr > kMaxRows) {
         set_error("proj: bad arguments (rows=%d K=%d nr=%d)", a.rows, a.K, nr);

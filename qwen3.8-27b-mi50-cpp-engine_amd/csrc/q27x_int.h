@@ -83,6 +83,8 @@ struct ProjArgs {
 };
 constexpr int kSwMaxSplit = 256;
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
+// whether the projection kernels have an instance for a plain (stored, no norm prologue) K
+bool proj_k_supported(int K);
 
 // bf16 GEMV: y = W x (fp32 / bf16 out) or, argmax mode, per-block (val, idx) partials
 struct GemvArgs {

@@ -66,6 +66,11 @@ def test_ctx_create_rejects_unsupported_geometry(X):
     assert p.value is None
     c = X.default_config(spec_k=8)
     assert X.lib().q27x_ctx_create(0, ctypes.byref(c), ctypes.byref(p)) == -2
+    # an input width the projection kernels have no instance for (3 x 1024) is refused up front
+    c = X.tiny_config(inter=3072)
+    assert X.lib().q27x_ctx_create(0, ctypes.byref(c), ctypes.byref(p)) == -2
+    assert "input width of 3072" in X.lib().q27x_last_error().decode()
+    assert p.value is None
 
 
 def test_default_config_is_baseline_config3(X):

@@ -70,6 +70,13 @@ def test_tiny_prefill_gemm_matches_oracle(gpu, O, n, chunk, gs):
     run_case(gpu, O, gpu.tiny_config(spec_k=2, pf_gs=gs), n, 3, chunk)
 
 
+def test_tiny_wide_group_swiglu_prefill_matches_oracle(gpu, O):
+    """inter 5120 with whole-K groups: the down projection's input is quantized per (token, 5120)
+    by the wide-group SwiGLU kernel (values held in registers: 1280 quads on 1024 threads, the
+    second chunk partly filled)."""
+    run_case(gpu, O, gpu.tiny_config(spec_k=2, inter=5120, pf_gs=0), 40, 3, None)
+
+
 def test_tiny_k7_prefill_gemm_matches_oracle(gpu, O):
     run_case(gpu, O, gpu.tiny_config(spec_k=7), 45, 2, 16)
 
