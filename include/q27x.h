@@ -280,6 +280,12 @@ typedef struct q27x_config {
                             reference default, src/q27_load.cpp:1622-1623, src/q27_main.cpp:4020),
                             or 1024. The MTP prompt pass always uses the whole K
                             (src/q27_main.cpp:2625-2628, 2665-2668). */
+    int eos_id;          /* stop tokens of q27x_generate (q27_is_eos, src/q27_main.cpp:709-710, */
+    int eos_id2;         /* applied as at 6680-6683): a request ends after the first committed
+                            token equal to either; -1 = none. Defaults 248044 and -1; eos_id2 is
+                            248046 when Q27_EOS_IM_END is set (src/q27_main.cpp:3111). The
+                            single-step entries (q27x_spec_round, q27x_decode_step,
+                            q27x_run_rounds) never stop on them. */
 } q27x_config;
 
 /* Statistics of a decode run (the reference's Q27_SPEC / Q27_SPEC_T lines,

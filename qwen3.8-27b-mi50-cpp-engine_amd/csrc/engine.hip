@@ -76,6 +76,8 @@ struct Dctl {
     int committed, max_new, stop, rounds;
     int forced_on, forced_n, forced_base, ctx;
     int nacc_last, ncommit_last, err, pad0;
+    // q27x_generate's stop tokens (-1: none) and the output length through the first of them (0: none seen)
+    int eos0, eos1, emit_end, pad1;
     long long acc_hist[9];
     long long accepted;
     // per-round phase timing (the reference's Q27_SPEC_T buckets, src/q27_main.cpp:2705-2707,
@@ -277,8 +279,11 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
         // state by ncommit positions; a later call continues after them)
         const int ncommit = nacc + 1;
         int c = d->committed;
-        for (int j = 0; j < ncommit; ++j, ++c)
+        for (int j = 0; j < ncommit; ++j, ++c) {
             if (c < ring_cap) ring[c] = d->nx[j];
+            // q27x_generate's stop tokens: the request's output ends after the first one
+            if (d->emit_end == 0 && (d->nx[j] == d->eos0 || d->nx[j] == d->eos1)) d->emit_end = c + 1;
+        }
         for (int j = 0; j < nacc; ++j) d->catch_tok[j] = d->nx[j];
         d->ncatch = nacc;
         d->tok = d->nx[nacc];
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
         for (int j = 0; j <= nacc && j < 9; ++j) d->acc_hist[j] += 1;
         d->nacc_last = nacc;
         d->ncommit_last = ncommit;
-        if (c >= d->max_new) d->stop = 1;
+        if (c >= d->max_new || d->emit_end > 0) d->stop = 1;
         if (mb) {
             for (int j = 0; j < 8; ++j) mb->tok[j] = j < ncommit ? d->nx[j] : -1;
             mb->ncommit = ncommit;
@@ -318,13 +323,14 @@ __global__ __launch_bounds__(256) void k_plain_post(Dctl* d, const uint16_t* hfi
     if (threadIdx.x == 0) {
         const int c = d->committed;
         if (c < ring_cap) ring[c] = d->nx[0];
+        if (d->emit_end == 0 && (d->nx[0] == d->eos0 || d->nx[0] == d->eos1)) d->emit_end = c + 1;
         d->committed = c + 1;
         d->tok = d->nx[0];
         d->pos += 1;
         d->gdn_npend = 1;
         d->ncatch = 0;
         d->rounds += 1;
-        if (d->committed >= d->max_new) d->stop = 1;
+        if (d->committed >= d->max_new || d->emit_end > 0) d->stop = 1;
         if (mb) {
             mb->tok[0] = d->nx[0];
             mb->ncommit = 1;
@@ -638,6 +644,7 @@ int q27x_config_default(q27x_config* c) {
     c->n_q = 32; c->n_kv = 8; c->head_dim = 128; c->attn_gate = 1; c->rot_dims = 32; c->rope_theta = 1e7;
     c->kv_group = 32; c->rms_eps = 1e-6f; c->head_double_residual = 1; c->mtp_swap = 1; c->mtp_plus_one = 1;
     c->spec = 1; c->spec_k = 2; c->ctx = 2048; c->pf_gs = 0;
+    c->eos_id = 248044; c->eos_id2 = -1;
     return Q27X_OK;
 }
 int q27x_config_tiny(q27x_config* c) {
@@ -684,6 +691,9 @@ int q27x_spec_config_from_env(q27x_config* c) {
         abort();
     }
     c->pf_gs = gs;
+    // src/q27_main.cpp:709-710, 3111: <|im_end|> stops a request when Q27_EOS_IM_END is set (the
+    // reference defaults it to its serve mode, which this library does not have)
+    c->eos_id2 = env_flag("Q27_EOS_IM_END", 0) ? 248046 : -1;
     return Q27X_OK;
 }
 
@@ -1274,6 +1284,7 @@ int q27x_reset(q27x_ctx* x) {
     Dctl h{};
     h.ctx = c.ctx;
     h.max_new = 0x7fffffff;
+    h.eos0 = h.eos1 = -1;
     Q27X_HIP(hipMemcpyAsync(x->dctl, &h, sizeof h, hipMemcpyHostToDevice, s));
     Q27X_HIP(hipStreamSynchronize(s));
     memset((void*)x->mbox, 0, sizeof(Mailbox));
@@ -1669,16 +1680,35 @@ static int run_step(q27x_ctx* x, int spec) {
 // for a call that may commit up to max_new tokens in total. A call that reached its budget left
 // stop = 1; the next call clears it, so decode continues from the current state. A device error
 // stays set and is reported (a new prompt resets it).
-static int arm(q27x_ctx* x, int max_new, Dctl* h) {
+// Arms the next launches: max_new, the stop flag, and the stop tokens (eos: q27x_generate; the
+// single-step entries pass none). With stop tokens, the tokens already committed since the prompt
+// (its first token, earlier calls) are searched first: a request that already holds one is over.
+static int arm(q27x_ctx* x, int max_new, Dctl* h, bool eos = false) {
     Q27X_HIP(hipStreamSynchronize(x->stream));
     Q27X_HIP(hipMemcpy(h, x->dctl, sizeof *h, hipMemcpyDeviceToHost));
     if (h->err) return check_device_err(x);
-    const int stop = h->committed >= max_new ? 1 : 0;
+    int e0 = -1, e1 = -1, emit = 0;
+    if (eos) {
+        e0 = x->c.eos_id;
+        e1 = x->c.eos_id2;
+        const int n = h->committed < x->ring_cap ? h->committed : x->ring_cap;
+        if (n > 0 && (e0 >= 0 || e1 >= 0)) {
+            std::vector<int32_t> toks((size_t)n);
+            Q27X_HIP(hipMemcpy(toks.data(), x->out_ring, (size_t)n * 4, hipMemcpyDeviceToHost));
+            for (int i = 0; i < n && !emit; ++i)
+                if (toks[i] == e0 || toks[i] == e1) emit = i + 1;
+        }
+    }
+    const int stop = (h->committed >= max_new || emit > 0) ? 1 : 0;
     int rc = set_ints(x, 2, DOFF(max_new), max_new, DOFF(stop), stop);
+    if (!rc) rc = set_ints(x, 3, DOFF(eos0), e0, DOFF(eos1), e1, DOFF(emit_end), emit);
     if (rc) return rc;
     Q27X_HIP(hipStreamSynchronize(x->stream));
     h->max_new = max_new;
     h->stop = stop;
+    h->eos0 = e0;
+    h->eos1 = e1;
+    h->emit_end = emit;
     memset((void*)x->mbox, 0, sizeof(Mailbox));   // no kernel is in flight
     return Q27X_OK;
 }
@@ -1785,7 +1815,7 @@ int q27x_generate(q27x_ctx* x, int max_new, int spec, int32_t* out, int* n_out, 
     if (!x || !x->prefilled || max_new < 1 || !out) { set_error("q27x_generate: bad arguments"); return Q27X_E_ARG; }
     if (max_new > x->ring_cap) max_new = x->ring_cap;   // a request never commits more than the context holds
     Dctl h0;
-    int rc = arm(x, max_new, &h0);
+    int rc = arm(x, max_new, &h0, true);
     if (rc) return rc;
     const int K = x->c.spec_k, ctx = x->c.ctx;
     // graphs built outside the timed loop (the plain one is needed at the context edge)
@@ -1825,7 +1855,8 @@ int q27x_generate(q27x_ctx* x, int max_new, int spec, int32_t* out, int* n_out, 
     if ((rc = check_device_err(x))) return rc;
     Dctl h;
     Q27X_HIP(hipMemcpy(&h, x->dctl, sizeof h, hipMemcpyDeviceToHost));
-    const int n = h.committed < max_new ? h.committed : max_new;
+    int n = h.committed < max_new ? h.committed : max_new;
+    if (h.emit_end > 0 && h.emit_end < n) n = h.emit_end;   // through the first stop token
     Q27X_HIP(hipMemcpy(out, x->out_ring, (size_t)n * 4, hipMemcpyDeviceToHost));
     if (n_out) *n_out = n;
     fill_stats(x, st, h0, h, h.committed - h0.committed, std::chrono::duration<double, std::milli>(t1 - t0).count());

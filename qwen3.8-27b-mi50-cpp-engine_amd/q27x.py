@@ -34,7 +34,7 @@ class Config(ctypes.Structure):
         ("kv_group", ctypes.c_int), ("rms_eps", ctypes.c_float),
         ("head_double_residual", ctypes.c_int), ("mtp_swap", ctypes.c_int),
         ("mtp_plus_one", ctypes.c_int), ("spec", ctypes.c_int), ("spec_k", ctypes.c_int),
-        ("ctx", ctypes.c_int), ("pf_gs", ctypes.c_int),
+        ("ctx", ctypes.c_int), ("pf_gs", ctypes.c_int), ("eos_id", ctypes.c_int), ("eos_id2", ctypes.c_int),
     ]
 
     def as_dict(self):

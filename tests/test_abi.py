@@ -87,7 +87,7 @@ def _env_config(env):
     code = ("import sys, ctypes; sys.path.insert(0, %r); import importlib.util as u;"
             "s = u.spec_from_file_location('q27x', %r); m = u.module_from_spec(s); s.loader.exec_module(m);"
             "c = m.default_config(); m.call('q27x_spec_config_from_env', ctypes.byref(c));"
-            "print(c.spec, c.spec_k, c.pf_gs)") % (ROOT, os.path.join(ROOT, "qwen3.8-27b-mi50-cpp-engine_amd", "q27x.py"))
+            "print(c.spec, c.spec_k, c.pf_gs, c.eos_id, c.eos_id2)") % (ROOT, os.path.join(ROOT, "qwen3.8-27b-mi50-cpp-engine_amd", "q27x.py"))
     e = {k: v for k, v in os.environ.items() if not k.startswith("Q27_")}
     e.update(env)
     return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=e, timeout=120)
@@ -118,8 +118,17 @@ def test_prefill_group_env(env, expect):
     assert int(r.stdout.split()[2]) == expect
 
 
+@pytest.mark.parametrize("env,expect", [({}, (248044, -1)), ({"Q27_EOS_IM_END": "1"}, (248044, 248046)),
+                                        ({"Q27_EOS_IM_END": "0"}, (248044, -1))])
+def test_stop_token_env(env, expect):
+    """q27_is_eos (src/q27_main.cpp:709-710): 248044 always, <|im_end|> 248046 with Q27_EOS_IM_END."""
+    r = _env_config(env)
+    assert r.returncode == 0, r.stderr
+    assert tuple(int(v) for v in r.stdout.split()[3:5]) == expect
+
+
 @pytest.mark.parametrize("env", [{"Q27_SPEC": "maybe"}, {"Q27_SPEC_K": "2x"}, {"Q27_SPEC_K": "two"},
-                                 {"Q27_Q8_GS": "512"}, {"Q27_Q8_GS": "full"}])
+                                 {"Q27_Q8_GS": "512"}, {"Q27_Q8_GS": "full"}, {"Q27_EOS_IM_END": "sometimes"}])
 def test_spec_env_fails_closed(env):
     """An unparseable value prints FATAL and aborts (include/q27.h:189-206), never guesses."""
     r = _env_config(env)

@@ -339,6 +339,59 @@ def test_generate_continues_after_its_budget(tiny_pair):
     assert len(stream) == c and stream == plain[:c], (stream, plain[:c])
 
 
+def _first_occurrence_at(stream, lo, residue, mod):
+    """An index j >= lo with j % mod == residue whose token does not occur before it."""
+    for j in range(lo, len(stream)):
+        if j % mod == residue and stream[j] not in stream[:j]:
+            return j
+    raise AssertionError("no token with a first occurrence at the wanted index")
+
+
+def test_generate_stops_after_the_stop_token(gpu, O):
+    """q27x_generate ends a request after the first committed stop token (src/q27_main.cpp:6680-6683):
+    the output is the oracle's greedy stream through that token, also when it is the middle token
+    of a forced round (the round still commits all of its tokens to the state); a later generate
+    returns the same output, the single-step entries continue the stream, and a prompt whose first
+    token is the stop token yields only that token."""
+    X = gpu
+    base = tiny(X, spec_k=2)
+    om = O.Model(base, SEED)
+    p = prompt_of(base, 17, seed=31)
+    first = om.prefill(p)
+    plain = [first] + [om.decode_step() for _ in range(48)]
+    om.close()
+    for spec, forced, field in ((True, False, "eos_id"), (False, False, "eos_id"), (True, True, "eos_id2")):
+        # forced rounds commit indices 1 + 3r .. 3 + 3r: index 3r + 2 is a round's middle token
+        j = _first_occurrence_at(plain, 6, 2, 3) if forced else _first_occurrence_at(plain, 6, 0, 1)
+        cfg = tiny(X, spec_k=2, eos_id=-1, eos_id2=-1)
+        setattr(cfg, field, plain[j])
+        eng = X.Engine(cfg, SEED)
+        assert eng.prefill(p) == first
+        if forced:
+            eng.set_forced(np.array(plain + [0] * 16, np.int32))
+        out, st = eng.generate(40, spec=spec)
+        assert out == plain[:j + 1], (spec, forced, j, out)
+        committed = int(eng.read("pos", -1, np.int32, 1)[0]) - len(p) + 1
+        if forced:
+            assert committed == j + 2, committed          # the whole round
+        elif not spec:
+            assert committed == j + 1, committed
+        else:
+            assert j + 1 <= committed <= j + 3, committed  # natural rounds commit 1 + nacc
+        again, _ = eng.generate(40, spec=spec)
+        assert again == plain[:j + 1]
+        eng.set_forced([])
+        assert eng.decode_step() == plain[committed]
+        eng.close()
+    # the prompt's own first token is the stop token: the request is over at once
+    cfg = tiny(X, spec_k=2, eos_id=first, eos_id2=-1)
+    eng = X.Engine(cfg, SEED)
+    assert eng.prefill(p) == first
+    out, st = eng.generate(40, spec=True)
+    assert out == [first] and st.rounds == 0
+    eng.close()
+
+
 def test_generate_runs_to_the_end_of_the_context(gpu, O):
     """max_new past the context: speculative rounds while pos + K < ctx, then plain steps, and the
     request ends with the context full (src/q27_main.cpp:6384, 6391) -- no error, and the tokens are
