@@ -163,9 +163,15 @@ def attend(O, A, qh, group, nq, nkv, hd, gate, L0, nr):
     return out
 
 
-def test_attn_prep_against_float64(O):
-    nq, nkv, hd, rot, group, nr, L0 = 4, 2, 128, 32, 32, 3, 100
-    rng = np.random.default_rng(50)
+# (nq, nkv, hd, rot): the BASELINE attention's shape, and the reference trunk's (24q/4kv x 256 with 64
+# rotary dims, include/q27.h:25-35, src/q27_attn.hip:10-11) at one kv head with its GQA group of 6
+GEOMS = [(4, 2, 128, 32), (6, 1, 256, 64), (12, 2, 256, 64)]
+
+
+@pytest.mark.parametrize("nq,nkv,hd,rot", GEOMS)
+def test_attn_prep_against_float64(O, nq, nkv, hd, rot):
+    group, nr, L0 = 32, 3, 100
+    rng = np.random.default_rng(50 + hd + nq)
     A = attn_setup(O, rng, L0, nq, nkv, hd, rot, group, nr)
     qh = prep(O, A, rot, group, nq, nkv, hd, 1, L0, nr)
     raw = ref64.bf2f(A["qkv"]).astype(np.float64)
@@ -206,10 +212,11 @@ def test_rope_relative_position(O):
     np.testing.assert_allclose(np.arctan2(sn[1:50, 0], cs[1:50, 0]), np.angle(np.exp(1j * np.arange(1, 50))), atol=1e-6)
 
 
-@pytest.mark.parametrize("L0", [5, 63, 64, 200])
-def test_attention_against_float64(O, L0):
-    nq, nkv, hd, rot, group, nr = 8, 2, 128, 32, 32, 3
-    rng = np.random.default_rng(60 + L0)
+@pytest.mark.parametrize("L0,nq,nkv,hd,rot", [(5, 8, 2, 128, 32), (63, 8, 2, 128, 32), (64, 8, 2, 128, 32),
+                                               (200, 8, 2, 128, 32), (63, 6, 1, 256, 64), (200, 12, 2, 256, 64)])
+def test_attention_against_float64(O, L0, nq, nkv, hd, rot):
+    group, nr = 32, 3
+    rng = np.random.default_rng(60 + L0 + hd)
     A = attn_setup(O, rng, L0, nq, nkv, hd, rot, group, nr)
     qh = prep(O, A, rot, group, nq, nkv, hd, 1, L0, nr)
     out = attend(O, A, qh, group, nq, nkv, hd, 1, L0, nr)
