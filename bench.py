@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """Benchmark of the chained-MTP K=2 speculative decode of the random-init int8 27B model on one
-MI355X: committed tok/s and verify-step HBM GB/s.
+MI355X (benchmark config 3): committed tok/s and verify-step HBM GB/s.
 
 A step is one chained-MTP round (K=2 drafts through the MTP layer, a 3-row verify through all 64
 layers, greedy acceptance, rollback and hand-off, all on the device, one HIP graph launch). The
@@ -141,13 +141,13 @@ def cpu_baseline(cfg_dict, q27o, k, pos):
                       f"random codes; weight generation {gen_s:.1f} s not timed"}
 
 
-# ---------------------------------------------------------------- BASELINE configs 0-2
+# ---------------------------------------------------------------- benchmark configs 0-2
 CFG_SHAPES = dict(H=5120, I=17408, KH=16, VH=48, D=128, NQ=32, NKV=8, HD=128, GROUP=32, NR=3)
 
 
 def cpu_configs(q27o, attn_ctx, reps=5):
-    """BASELINE configs 0-2 on the host through the oracle's kernel-tier functions (OpenMP over
-    output rows), on seeded synthetic inputs of the BASELINE shapes; best and median of reps."""
+    """Benchmark configs 0-2 on the host through the oracle's kernel-tier functions (OpenMP over
+    output rows), on seeded synthetic inputs of the benchmark shapes; best and median of reps."""
     L = q27o.lib()
     c = CFG_SHAPES
     H, I, nr, D, VH, KH = c["H"], c["I"], c["NR"], c["D"], c["VH"], c["KH"]
@@ -264,7 +264,7 @@ def cpu_configs(q27o, attn_ctx, reps=5):
 
 
 def gpu_config0(q27x, iters=50, copies=6):
-    """BASELINE config 0 on the GPU through the kernel tier (q27x_proj_rows, fp32 out): 3 rows x
+    """Benchmark config 0 on the GPU through the kernel tier (q27x_proj_rows, fp32 out): 3 rows x
     [17408 x 5120]; launches cycle through `copies` weight copies (570 MB) so none hits the
     Infinity Cache; device events around iters launches."""
     import ctypes
@@ -308,11 +308,11 @@ def gpu_config0(q27x, iters=50, copies=6):
 
 
 COPY_BYTES = 1 << 28       # calibration copy: 256 MiB read + 256 MiB written per launch
-CFG4_PROMPT = 16320        # ctx 16384; the prompt leaves room for one 8-row verify
+CFG4_PROMPT = 16320        # benchmark config 4: ctx 16384; the prompt leaves room for one 8-row verify
 
 
 def config4(eng, cfg, prefill):
-    """BASELINE config 4 (K = 7, ctx 16384) on the bench's own context: a CFG4_PROMPT-token prompt
+    """Benchmark config 4 (K = 7, ctx 16384) on the bench's own context: a CFG4_PROMPT-token prompt
     ingested on the GEMM path (wall clock), then the 8-row verify (K = 7: NR = 8) over all 64 layers
     at that context, timed with device events over 10 launches; its algorithmic bytes (weights once,
     the KV of CFG4_PROMPT positions per attention layer, the GDN state read and written) give GB/s.
@@ -354,7 +354,7 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published
 
 
 def prefill_gemm(q27x, reps=20, gs=5120):
-    """The prefill ingest GEMM on int8 MFMA (q27x_gemm_i8g) at BASELINE config 4's shape: M = 4096
+    """The prefill ingest GEMM on int8 MFMA (q27x_gemm_i8g) at benchmark config 4's shape: M = 4096
     tokens x N = 17408 (gate) x K = 5120, groups of gs columns (the whole K by default, the
     reference's default Q27_Q8_GS arm; 1024 is the other), seeded codes and scales resident on the
     device; device events around `reps` back-to-back launches."""
@@ -468,7 +468,7 @@ def main():
 
     # ---- natural acceptance
     # prompt ingest: the verify kernels over the prompt (q27x_prefill) and the layer-major int8-MFMA
-    # GEMM path (q27x_prefill_gemm, BASELINE config 4's prefill ingest), wall clock per call
+    # GEMM path (q27x_prefill_gemm, benchmark config 4's prefill ingest), wall clock per call
     t = time.time()
     eng.prefill(prompt)
     prefill_s = time.time() - t
@@ -527,7 +527,7 @@ def main():
         kernels[name] = {"us": round(ms_ * 1e3, 2), "GB_s": round(b_ / (ms_ / 1e3) / 1e9, 1)}
     log(f"kernels: {kernels}")
 
-    # ---- BASELINE configs 0-2 on the GPU (3 rows; config 0 through the kernel tier, 1 and 2 on the
+    # ---- benchmark configs 0-2 on the GPU (3 rows; config 0 through the kernel tier, 1 and 2 on the
     # engine's own kernels; these overwrite the context's state, so they run last)
     gpu_cfg = {"config0_projection": gpu_config0(q27x)}
     ms_, b_ = eng.bench_mixer(False, args.prompt, 3, 48)

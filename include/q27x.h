@@ -305,7 +305,7 @@ typedef struct q27x_stats {
 
 typedef struct q27x_ctx q27x_ctx;
 
-/* The BASELINE config-3 geometry (64 layers: 48 GDN + 16 attention). */
+/* The benchmark config-3 geometry (64 layers: 48 GDN + 16 attention). */
 int q27x_config_default(q27x_config* c);
 /* A tiny geometry with the same structure for CPU-checkable parity runs. */
 int q27x_config_tiny(q27x_config* c);
@@ -423,7 +423,7 @@ int q27x_bench_verify(q27x_ctx* ctx, int nr, int iters, float* ms_per_verify);
  * Infinity Cache; reports ms per launch and its algorithmic bytes (weights + scales + input rows +
  * outputs). Overwrites the context's activation scratch and clears the stop flag. */
 int q27x_bench_kernel(q27x_ctx* ctx, int layer, int which, int nr, int iters, float* ms, double* bytes);
-/* BASELINE configs 1 and 2 on the engine's own kernels: the mixer half of one layer (attn = 0:
+/* Benchmark configs 1 and 2 on the engine's own kernels: the mixer half of one layer (attn = 0:
  * GDN -- in_qkv|in_z with the input-norm prologue, the GDN kernel, out_proj + residual; attn = 1:
  * q|k|v with the prologue, attention over positions 0..pos+nr-1, o_proj + residual) for nr rows at
  * position pos, averaged over iters launches that cycle through the layers of that kind; reports

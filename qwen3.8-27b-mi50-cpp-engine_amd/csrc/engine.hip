@@ -547,7 +547,15 @@ static int mtp_pass(q27x_ctx* x, int nr, int head, int kv_only) {
     // down as four K = I/4 column slices, each added into the bf16 residual with its own bf16
     // rounding (src/q27_main.cpp:2605-2612: one fp32 slice projection, then q27_add_inplace)
     const int I4 = I / 4;
-    for (int j = 0; j < 4; ++j) {
+    const bool one = down4_supported(I4, nr);          // one launch (same bits as the four below)
+    if (one) {
+        Down4Args d4{};
+        for (int j = 0; j < 4; ++j) { d4.W[j] = Y.down4[j].w; d4.WS[j] = Y.down4[j].s; d4.alpha[j] = 1.0f; }
+        d4.rows = H; d4.K4 = I4; d4.xq = xact; d4.xst = I; d4.xs = sact;
+        d4.y = x->mtp_res; d4.ystride = H; d4.stop = &d->stop;
+        if ((rc = launch_down4(d4, nr, s))) return rc;
+    }
+    for (int j = 0; j < 4 && !one; ++j) {
         ProjArgs dn{};
         dn.W = Y.down4[j].w; dn.WS = Y.down4[j].s; dn.rows = H; dn.K = I4; dn.alpha = 1.0f;
         dn.xq = xact + (size_t)j * I4; dn.xst = I; dn.xs = sact + (size_t)j * (I4 / 16);
@@ -2001,7 +2009,7 @@ int q27x_bench_kernel(q27x_ctx* x, int layer, int which, int nr, int iters, floa
     return rc;
 }
 
-// The mixer half of one verify layer (GDN -- in_qkv|in_z with its input-norm
+// The mixer half of one verify layer (benchmark config 1: GDN -- in_qkv|in_z with its input-norm
 // prologue, the GDN kernel, out_proj + residual; config 2: attention -- q|k|v with its prologue,
 // the attention over positions 0 .. pos+nr-1, o_proj + residual), timed with device events over
 // iters launches that cycle through the layers of that kind (layer 0 excluded: its prologue reads

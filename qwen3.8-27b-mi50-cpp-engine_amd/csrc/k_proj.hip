@@ -709,6 +709,138 @@ int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s) {
     return rc;
 }
 
+// ---------------------------------------------------------------- the MTP layer's down, one launch
+// The reference projects the MTP layer's down in four column slices of K/4 and adds each slice's
+// fp32 result into the bf16 residual with its own bf16 rounding, slice after slice
+// (src/q27_main.cpp:2605-2612). Four slice launches of the projection above do exactly that; this
+// kernel gives the same bits in one launch for up to 4 rows. A wave takes the units (row r,
+// slice j) of its rows in order: the unit's dot products in the lane-slab order (slab s on lane
+// s % 64 at step s / 64, acc = fmaf((float)d, ws64 * xs16, acc)), the slice's own shfl_down tree,
+// and after the fourth slice the four additions in slice order, each rounded to bf16. Units
+// alternate between two weight register sets: a unit's set is refilled with the unit two ahead
+// once its products have issued, so the next unit's bytes are in flight while one computes. The
+// rows' codes and scales for the whole K are staged in LDS once per block.
+constexpr int kD4Waves = 8;
+template <int NR, int NS>
+__global__ __launch_bounds__(kD4Waves * 64) void k_down4(Down4Args a) {
+    constexpr int SLS = NS * 64;                       // staged slabs per slice and row
+    constexpr int NT = kD4Waves * 64;
+    constexpr int P = Pow2<NR>::value, LPV = 64 / P;
+    __shared__ uint4 sx[NR * 4 * SLS];
+    __shared__ float ssc[NR * 4 * SLS];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K4 = a.K4, nsl = K4 >> 4, ng = K4 >> 6;
+    const int nw = gridDim.x * kD4Waves;
+    uint4 W[2][NS];
+    float S[2][NS];
+    // unit (row, slice j) into set b: loads issued on every path (a unit past the wave's last reads
+    // the last row, not used). A lane past the slice's slabs reads the row's first slab and scale:
+    // its staged activation slab and scale are zero, so its product is dot 0 times scale 0 and
+    // fmaf(0, 0, acc) leaves acc's bits as they are (acc starts at +0 and +0 + -0 is +0). No select
+    // on the loaded values, which would wait for the loads where the select stands.
+    auto ld = [&](int b, int row, int j) __attribute__((always_inline)) {
+        row = row < a.rows ? row : a.rows - 1;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int sl = t * 64 + lane;
+            const int sc = sl < nsl ? sl : 0;
+            W[b][t] = ld_nt16(a.W[j] + (size_t)row * K4 + 16 * sc);
+            S[b][t] = a.WS[j][(size_t)row * ng + (sc >> 2)];
+        }
+    };
+    // one unit from set b: its products, the set refilled with unit (rq, jq), the slice's tree
+    auto unit = [&](int b, int j, int rq, int jq) __attribute__((always_inline)) -> float {
+        // an opaque copy of the lane's slab index: the unit's LDS reads stay in the unit (they
+        // do not depend on the row, and hoisted out of the row loop they would hold every slice's
+        // activations in registers)
+        int sl0 = lane;
+        asm volatile("" : "+v"(sl0));
+        float acc[P];
+#pragma unroll
+        for (int v = 0; v < P; ++v) acc[v] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+#pragma unroll
+            for (int n = 0; n < NR; ++n) {
+                const int si = (n * 4 + j) * SLS + t * 64 + sl0;
+                const int d = dot16(W[b][t], sx[si]);
+                acc[n] = __builtin_fmaf((float)d, S[b][t] * ssc[si], acc[n]);
+            }
+        }
+        ld(b, rq, jq);
+        return tree_t<P>(acc, lane) * a.alpha[j];
+    };
+    // stage: slice j's slab s of row n at (n * 4 + j) * SLS + s; slabs past the slice are zero
+    for (int i = threadIdx.x; i < NR * 4 * SLS; i += NT) {
+        const int nj = i / SLS, sb = i - nj * SLS, n = nj >> 2, j = nj & 3;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        float sc = 0.0f;
+        if (sb < nsl) {
+            v = *(const uint4*)(a.xq + (size_t)n * a.xst + (size_t)j * K4 + 16 * sb);
+            sc = a.xs[(size_t)n * (a.xst >> 4) + (size_t)j * nsl + sb];
+        }
+        sx[i] = v;
+        ssc[i] = sc;
+    }
+    int r = blockIdx.x * kD4Waves + wave;              // this wave's rows: r, r + nw, ...
+    // set 0's loads all issue before set 1's, as in the loop (the wait counts at the loop's top
+    // hold for both ways in)
+    ld(0, r, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    ld(1, r, 1);
+    if (stopped(a.stop)) return;
+    __syncthreads();
+    // lane n LPV holds row n's four slice results after the trees
+    const bool holder = (lane % LPV) == 0 && lane / LPV < NR;
+    for (; r < a.rows; r += nw) {
+        // the residual is read before the units' loads are issued (loads retire in order, and a
+        // read issued after them would wait for all of them), by every lane (lanes that hold no
+        // value read row 0's), so that no select or branch waits for it here
+        uint16_t* yp = a.y + (size_t)(holder ? lane / LPV : 0) * a.ystride + r;
+        uint16_t y = *yp;
+        const float d0 = unit(0, 0, r, 2);
+        const float d1 = unit(1, 1, r, 3);
+        const float d2 = unit(0, 2, r + nw, 0);
+        const float d3 = unit(1, 3, r + nw, 1);
+        // add them into the residual in slice order
+        if (holder) {
+            y = f2bf(d0 + 1.0f * bf2f(y));
+            y = f2bf(d1 + 1.0f * bf2f(y));
+            y = f2bf(d2 + 1.0f * bf2f(y));
+            y = f2bf(d3 + 1.0f * bf2f(y));
+            *yp = y;
+        }
+    }
+}
+// instances: K/4 up to 2048 (the small test geometries) and 4097 .. 5120 (the model's 4352)
+bool down4_supported(int K4, int nr) {
+    const int ns = (K4 + 1023) / 1024;
+    return nr >= 1 && nr <= 4 && K4 >= 64 && (K4 & 63) == 0 && (ns == 1 || ns == 2 || ns == 5);
+}
+int launch_down4(const Down4Args& a, int nr, hipStream_t s) {
+    if (!down4_supported(a.K4, nr) || a.rows < 1 || !a.xq || !a.xs || !a.y ||
+        (a.xst & 15) || a.xst < 4 * a.K4 || !a.W[0] || !a.W[1] || !a.W[2] || !a.W[3] || !a.WS[0] || !a.WS[1] ||
+        !a.WS[2] || !a.WS[3]) {
+        set_error("down4: no kernel for rows=%d K/4=%d nr=%d", a.rows, a.K4, nr);
+        return Q27X_E_SHAPE;
+    }
+    const int grid = num_cus(), ns = (a.K4 + 1023) / 1024;
+    auto go = [&](auto nsc) {
+        constexpr int NS = decltype(nsc)::value;
+        switch (nr) {
+            case 1: hipLaunchKernelGGL((k_down4<1, NS>), dim3(grid), dim3(kD4Waves * 64), 0, s, a); break;
+            case 2: hipLaunchKernelGGL((k_down4<2, NS>), dim3(grid), dim3(kD4Waves * 64), 0, s, a); break;
+            case 3: hipLaunchKernelGGL((k_down4<3, NS>), dim3(grid), dim3(kD4Waves * 64), 0, s, a); break;
+            default: hipLaunchKernelGGL((k_down4<4, NS>), dim3(grid), dim3(kD4Waves * 64), 0, s, a); break;
+        }
+    };
+    if (ns == 1) go(std::integral_constant<int, 1>{});
+    else if (ns == 2) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 5>{});
+    Q27X_HIP(hipGetLastError());
+    return Q27X_OK;
+}
+
 // ---------------------------------------------------------------- int32 slab partials
 __global__ __launch_bounds__(256) void k_proj_partials(const int8_t* __restrict__ W, int rows, int K,
                                                        const int8_t* __restrict__ xq, int xst,

@@ -83,6 +83,18 @@ struct ProjArgs {
 };
 constexpr int kSwMaxSplit = 256;
 int launch_proj(const ProjArgs& a, int epi, int nr, hipStream_t s);
+// The MTP layer's down as four column slices of K4 = K/4 (W[j], WS[j]: [rows][K4] codes and
+// per-64 scales), each slice's projection times alpha[j] added into the bf16 rows y in slice order
+// with its own bf16 rounding; xq/xs: the rows' codes and per-16 scales for the whole K (stride xst).
+struct Down4Args {
+    const int8_t* W[4]; const float* WS[4]; float alpha[4];
+    int rows; int K4;
+    const int8_t* xq; int xst; const float* xs;
+    uint16_t* y; int ystride;
+    const int* stop;
+};
+bool down4_supported(int K4, int nr);
+int launch_down4(const Down4Args& a, int nr, hipStream_t s);
 // whether the projection kernels have an instance for a plain (stored, no norm prologue) K
 bool proj_k_supported(int K);
 

@@ -1,6 +1,6 @@
 """Kernel-tier parity: every gfx950 kernel against the CPU oracle on the same seeded inputs,
 through the C ABI. Integer results and fp32/bf16 outputs are compared bit for bit (the kernels
-and the oracle share one fixed reduction order); shapes are BASELINE configs 0-2."""
+and the oracle share one fixed reduction order); shapes are benchmark configs 0-2."""
 import ctypes
 
 import numpy as np
@@ -65,7 +65,7 @@ def test_quant_rows(gpu, O, nr):
 
 @pytest.mark.parametrize("nr", [3])
 def test_proj_config0(gpu, O, nr):
-    """3 rows x [17408 x 5120] int8 W8A8, per-64 / per-16 scales."""
+    """Benchmark config 0: 3 rows x [17408 x 5120] int8 W8A8, per-64 / per-16 scales."""
     X = gpu
     rng = np.random.default_rng(0x51E70000)
     rows, K = 17408, 5120
@@ -234,7 +234,7 @@ def gdn_inputs(rng, O, nr, kh=16, vh=48, d=128):
 
 @pytest.mark.parametrize("rollback", [0, 1, 2])
 def test_gdn_verify_config1(gpu, O, rollback):
-    """BASELINE config 1 GDN core: 3 verify rows, state ~N(0, 0.1), a/b ~U(-4, 0), then a second
+    """Benchmark config 1 GDN core: 3 verify rows, state ~N(0, 0.1), a/b ~U(-4, 0), then a second
     call that commits an accepted prefix of rollback + 1 rows (the rest rolled back), then the
     commit-only entry for that call's accepted prefix followed by a call with nothing pending --
     all compared bit for bit with the oracle."""
@@ -341,7 +341,7 @@ def attention_case(X, O, L0, nq, nkv, hd, rot, group, nr, seed):
 
 @pytest.mark.parametrize("L0", [1024, 4096, 16384, 20000])
 def test_attention_config2(gpu, O, L0):
-    """GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows.
+    """Benchmark config 2: GQA 32q/8kv x 128, RoPE theta 1e7, int8 KV per 32, 3 causal verify rows.
     (20000 positions: 313 splits, past one LDS window of the combine, which then takes two.)"""
     attention_case(gpu, O, L0, 32, 8, 128, 32, 32, 3, 0x51E70002 + L0)
 

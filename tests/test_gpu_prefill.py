@@ -3,7 +3,7 @@ restatement (q27o_model_prefill_gemm): after the prompt, the first token and the
 state bit for bit (h_prev, every GDN layer's state and conv history, every attention layer's and
 the MTP layer's KV cache), then speculative rounds continuing from it, round by round with their
 drafts and hand-off. Prompts span several chunks (Q27X_PF_CHUNK) and several attention launches
-(128 query rows each); the BASELINE widths run at 4 layers; the full 64-layer model checks that
+(128 query rows each); the the model's widths run at 4 layers; the full 64-layer model checks that
 spec == plain greedy after a GEMM prefill."""
 import os
 
@@ -83,7 +83,7 @@ def test_tiny_k7_prefill_gemm_matches_oracle(gpu, O):
 
 @pytest.mark.parametrize("n,chunk,gs", [(64, None, 0), (96, 32, 0), (64, None, 1024)])
 def test_full_width_prefill_gemm_matches_oracle(gpu, O, n, chunk, gs):
-    """BASELINE widths at 4 layers (3 GDN + 1 attention): the 16384-row in_qkv|in_z, 34816-row
+    """The model's widths at 4 layers (3 GDN + 1 attention): the 16384-row in_qkv|in_z, 34816-row
     gate|up and K = 17408 down GEMMs, 32q/8kv attention, the 62080-row head, with whole-K groups
     (the reference default) and with 1024-column groups (5, 6 and 17 of them). (96 tokens in 32-row
     chunks: three chunks on alternating streams, each layer behind the previous chunk's.)"""

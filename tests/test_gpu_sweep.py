@@ -1,5 +1,5 @@
 """Seeded random cases of the whole round against the oracle: K in 1..7, tiny geometries with the
-BASELINE-shaped and the trunk-shaped attention (GQA groups 4, 6 and 8, 128- and 256-dim heads),
+benchmark-shaped and the trunk-shaped attention (GQA groups 4, 6 and 8, 128- and 256-dim heads),
 more SwiGLU units than blocks, two-layer attention periods, prompts of 1..259 tokens through
 either prefill and either prefill group setting; each case runs natural rounds, then forced rounds
 with planted wrong drafts, and compares every round's tokens and whole state bit for bit."""

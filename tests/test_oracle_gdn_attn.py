@@ -163,7 +163,7 @@ def attend(O, A, qh, group, nq, nkv, hd, gate, L0, nr):
     return out
 
 
-# (nq, nkv, hd, rot): the BASELINE attention's shape, and the reference trunk's (24q/4kv x 256 with 64
+# (nq, nkv, hd, rot): the benchmark attention's shape, and the reference trunk's (24q/4kv x 256 with 64
 # rotary dims, include/q27.h:25-35, src/q27_attn.hip:10-11) at one kv head with its GQA group of 6
 GEOMS = [(4, 2, 128, 32), (6, 1, 256, 64), (12, 2, 256, 64)]
 
