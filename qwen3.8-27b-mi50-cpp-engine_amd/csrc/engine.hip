@@ -258,16 +258,30 @@ __global__ __launch_bounds__(256) void k_draft_post(Dctl* d, uint16_t* mtp_hin, 
     }
 }
 // [3] greedy acceptance, [4] rollback (= how many rows the next GDN call commits) and hand-off
-// (src/q27_main.cpp:2811-2812, 2929-2950); one-round-lagged mailbox to the host
+// (src/q27_main.cpp:2811-2812, 2929-2950); one-round-lagged mailbox to the host. The round's
+// tokens and counters are read into registers up front, all loads in one round trip: stores to
+// the ring and the mailbox may alias the control block as far as the compiler knows, so reading
+// the block between them would wait for a load after each store.
 __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal, uint16_t* hcatch, uint16_t* hprev,
                                                 int32_t* ring, int ring_cap, Mailbox* mb, int H, int K) {
     if (d->stop) return;
     __shared__ int s_nacc;
     __shared__ unsigned long long s_t0;
+    int nx[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nx[j] = d->nx[j];
     if (threadIdx.x == 0) {
         s_t0 = __builtin_amdgcn_s_memrealtime();
+        int dt[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dt[j] = d->dt[j];
         int nacc = 0;
-        while (nacc < K && d->nx[nacc] == d->dt[nacc]) ++nacc;
+        bool run = true;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            run = run && j < K && nx[j] == dt[j];
+            nacc += run ? 1 : 0;
+        }
         s_nacc = nacc;
     }
     __syncthreads();
@@ -275,38 +289,56 @@ __global__ __launch_bounds__(256) void k_accept(Dctl* d, const uint16_t* hfinal,
     for (int j = 0; j < nacc; ++j) copy_row(hcatch + (size_t)j * H, hfinal + (size_t)j * H, H);
     copy_row(hprev, hfinal + (size_t)nacc * H, H);
     if (threadIdx.x == 0) {
+        const int eos0 = d->eos0, eos1 = d->eos1, max_new = d->max_new;
+        const int c0 = d->committed, rounds = d->rounds + 1;
+        int emit_end = d->emit_end, stop = d->stop;
+        const long long accepted = d->accepted;
+        const unsigned long long t_begin = d->t_begin, t_draft = d->t_draft, t_verify = d->t_verify;
+        const int pos = d->pos;
         // every committed token goes to the ring (a round that passes max_new still advanced the
         // state by ncommit positions; a later call continues after them)
         const int ncommit = nacc + 1;
-        int c = d->committed;
-        for (int j = 0; j < ncommit; ++j, ++c) {
-            if (c < ring_cap) ring[c] = d->nx[j];
-            // q27x_generate's stop tokens: the request's output ends after the first one
-            if (d->emit_end == 0 && (d->nx[j] == d->eos0 || d->nx[j] == d->eos1)) d->emit_end = c + 1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < ncommit) {
+                const int c = c0 + j;
+                if (c < ring_cap) ring[c] = nx[j];
+                // q27x_generate's stop tokens: the request's output ends after the first one
+                if (emit_end == 0 && (nx[j] == eos0 || nx[j] == eos1)) emit_end = c + 1;
+            }
         }
-        for (int j = 0; j < nacc; ++j) d->catch_tok[j] = d->nx[j];
+        const int c = c0 + ncommit;
+        int tok = nx[0];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < nacc) d->catch_tok[j] = nx[j];
+            if (j == nacc) tok = nx[j];
+        }
         d->ncatch = nacc;
-        d->tok = d->nx[nacc];
-        d->pos += ncommit;
+        d->tok = tok;
+        d->pos = pos + ncommit;
         d->gdn_npend = ncommit;
         d->committed = c;
-        d->rounds += 1;
-        d->accepted += nacc;
+        d->rounds = rounds;
+        d->accepted = accepted + nacc;
         for (int j = 0; j <= nacc && j < 9; ++j) d->acc_hist[j] += 1;
         d->nacc_last = nacc;
         d->ncommit_last = ncommit;
-        if (c >= d->max_new || d->emit_end > 0) d->stop = 1;
+        d->emit_end = emit_end;
+        if (c >= max_new || emit_end > 0) stop = 1;
+        d->stop = stop;
         if (mb) {
-            for (int j = 0; j < 8; ++j) mb->tok[j] = j < ncommit ? d->nx[j] : -1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) mb->tok[j] = j < ncommit ? nx[j] : -1;
             mb->ncommit = ncommit;
             mb->committed = c;
-            mb->stop = d->stop;
+            mb->stop = stop;
             __threadfence_system();
-            mb->round = d->rounds;
+            mb->round = rounds;
         }
-        d->sp_t[0] += d->t_draft - d->t_begin;
-        d->sp_t[1] += d->t_verify - d->t_draft;
-        d->sp_t[2] += s_t0 - d->t_verify;
+        d->sp_t[0] += t_draft - t_begin;
+        d->sp_t[1] += t_verify - t_draft;
+        d->sp_t[2] += s_t0 - t_verify;
         d->sp_t[3] += __builtin_amdgcn_s_memrealtime() - s_t0;
     }
 }
