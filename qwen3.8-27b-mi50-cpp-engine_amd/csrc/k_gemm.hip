@@ -25,6 +25,9 @@
 // for its own loads). At the end of each group the int32 tiles are folded into fp32
 // accumulators with the group's scales (staged in LDS for the whole K at the start) and
 // restarted from zero.
+#include <stdlib.h>
+#include <type_traits>
+
 #include "q27x_dev.h"
 #include "q27x_int.h"
 
@@ -359,6 +362,160 @@ _Pragma("unroll")                                                               
         }
 }
 
+// One group over the whole K (the reference's default arm) on 256-token x 256-row tiles: 4 waves,
+// one per SIMD, each owning a 128 x 128 quarter as 4 x 4 v_mfma_i32_32x32x32_i8 tiles (256
+// accumulator registers; no fp32 group accumulators are needed, the scales apply once at the end),
+// so each MFMA reads half a KiB of LDS operands instead of the 64 x 64 quarter's full KiB. K
+// advances 128 bytes per stage (each stage row is one whole 128-byte line of a row, which halves
+// the load requests of 64-byte stages) through two 64 KiB LDS stages filled by LDS DMA. The
+// operand reads are pipelined one 32-byte slice ahead of the MFMAs, across the stage barrier too:
+// the barrier that certifies stage s + 1 sits before the last slice of stage s, whose operands
+// are already in registers, and the next stage's first slice is read while that slice multiplies.
+// Rows are 128 bytes, chunk c of row R in slot c ^ ((R >> 1) & 7) (the 16 rows of one operand read
+// fill a 256-byte bank window). Same tile order as k_gemm_i8g; the int32 sums are exact, so the
+// outputs are the other kernels' bits.
+constexpr int kW4B = 256, kW4K = 128, kW4S = 2;
+constexpr int kW4Stage = 2 * kW4B * kW4K;              // 64 KiB: A rows, then B rows
+constexpr int kW4NI = kW4Stage / (1024 * 4);           // 1 KiB transfers per wave per stage (16)
+// RES: no residual (0), fp32 (1) or bf16 (2) residual rows; OBF: bf16 output. Instances per
+// epilogue form: with per-element branches on them the unrolled epilogue of 256 values per lane
+// cost ~20 us per tile.
+template <int RES, bool OBF>
+__global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
+    __shared__ __align__(16) int8_t sR[kW4S * kW4Stage];
+    __shared__ float sSx[kW4B], sSw[kW4B];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nt = a.N / kW4B, mt = (a.M + kW4B - 1) / kW4B, T = nt * mt;
+    const int b = blockIdx.x;
+    const int tile = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int grp = tile / (4 * nt), fm = grp * 4, gsz = (mt - fm < 4) ? mt - fm : 4;
+    const int within = tile - grp * 4 * nt;
+    const int m0 = (fm + within % gsz) * kW4B, n0 = (within / gsz) * kW4B;
+    const int K = a.K, nsteps = K / kW4K;
+    // DMA: transfer i (< 16) of wave w fills stage rows 8 (16 w + i) .. +8; lane l writes row
+    // 8 (16 w + i) + l / 8, slot l % 8, so it loads that row's chunk (l % 8) ^ ((row >> 1) & 7)
+    // (waves 0 and 1 fill the A rows, waves 2 and 3 the B rows: one base per wave, byte offsets
+    // below 2^31 for the row counts and K this kernel takes)
+    const int8_t* gb = wave < 2 ? a.x : a.w;
+    uint32_t go[kW4NI];
+#pragma unroll
+    for (int i = 0; i < kW4NI; ++i) {
+        const int rs = 8 * (kW4NI * wave + i) + (lane >> 3);
+        const int r = rs < kW4B ? rs : rs - kW4B;
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int row = rs < kW4B ? ((m0 + r < a.M) ? m0 + r : a.M - 1) : n0 + r;   // rows past M repeat row M - 1
+        go[i] = (uint32_t)row * (uint32_t)K + 16 * c;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)sR;
+    auto issue = [&](int step, int slot) __attribute__((always_inline)) {
+        const uint32_t base = lds0 + slot * kW4Stage + 1024 * kW4NI * wave;
+#pragma unroll
+        for (int i = 0; i < kW4NI; ++i)
+            lds_dma16(gb + go[i] + (uint32_t)(step * kW4K), __builtin_amdgcn_readfirstlane(base + 1024 * i));
+    };
+    issue(0, 0);
+    {
+        const int t = (m0 + tid < a.M) ? m0 + tid : a.M - 1;
+        sSx[tid] = a.sx[t];
+        sSw[tid] = a.sw[n0 + tid];
+    }
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    // operand rows of this lane: A (token) wm*128 + 32 i + lane % 32, B (weight row) wn*128 + 32 j +
+    // lane % 32; both take chunk 2 kk + lane / 32 of the stage's 32-byte K slice kk
+    const int arow = wm * 128 + (lane & 31), brow = kW4B + wn * 128 + (lane & 31);
+    const int swa = (arow >> 1) & 7, swb = ((brow - kW4B) >> 1) & 7, kh = lane >> 5;
+    auto rd = [&](v4i (&av)[4], v4i (&bv)[4], int slot, int kk) __attribute__((always_inline)) {
+        const int8_t* st = sR + slot * kW4Stage;
+        const int c = 2 * kk + kh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av[i] = *(const v4i*)(st + (arow + 32 * i) * kW4K + ((c ^ swa) << 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = *(const v4i*)(st + (brow + 32 * j) * kW4K + ((c ^ swb) << 4));
+    };
+    auto mm = [&](const v4i (&av)[4], const v4i (&bv)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
+    };
+    // this wave's transfers of the next stage done and its operand reads of the current one
+    // returned; after the barrier every wave's are (nothing is scheduled across it)
+    auto sync = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    constexpr int SL = kW4K / 32;                      // 32-byte slices per stage
+    v4i oa[2][4], ob[2][4];
+    sync();                                            // stage 0 everywhere (and the scales)
+    issue(1 < nsteps ? 1 : 0, 1);
+    rd(oa[0], ob[0], 0, 0);
+    for (int s = 0; s < nsteps; ++s) {
+#pragma unroll
+        for (int kk = 0; kk < SL; ++kk) {
+            const int cu = kk & 1, nx = cu ^ 1;
+            if (kk + 1 < SL) {
+                rd(oa[nx], ob[nx], s & 1, kk + 1);
+            } else {
+                // stage s + 1 landed everywhere and stage s is read by all: its slot takes stage
+                // s + 2 (past the end: stage 0 again into a slot nobody reads, so every iteration
+                // issues the same transfers); the next stage's first slice is read meanwhile
+                // (past the last stage that is a stale slot, not used)
+                sync();
+                issue(s + 2 < nsteps ? s + 2 : 0, s & 1);
+                rd(oa[nx], ob[nx], (s + 1) & 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            mm(oa[cu], ob[cu]);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        }
+    }
+    // no transfer may still be writing LDS when the block ends
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    // the tile's outputs; rows past M only in the last token tile. Element offsets are 32-bit
+    // (the launcher keeps M x ldy and M x ldr below 2^30), so the stores take the output's base in
+    // scalar registers.
+    const uint32_t nb = (uint32_t)(n0 + wn * 128 + (lane & 31));
+    float swv[4], al[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        swv[j] = sSw[wn * 128 + 32 * j + (lane & 31)];
+        al[j] = alpha_of(a.alpha, a.asel, (int)nb + 32 * j);
+    }
+    auto out = [&](auto full) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), t = m0 + tl;
+                if (decltype(full)::value || t < a.M) {
+                    const float sxv = sSx[tl];
+                    const uint32_t yo = (uint32_t)t * (uint32_t)a.ldy + nb;
+                    const uint32_t ro = (uint32_t)t * (uint32_t)a.ldr + nb;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float o = __builtin_fmaf((float)acc[i][j][r], swv[j] * sxv, 0.0f) * al[j];
+                        if constexpr (RES == 1) o = o + a.rs * a.res[ro + 32 * j];
+                        if constexpr (RES == 2) o = o + a.rs * bf2f(((const uint16_t*)a.res)[ro + 32 * j]);
+                        if constexpr (OBF) ((uint16_t*)a.y)[yo + 32 * j] = f2bf(o);
+                        else a.y[yo + 32 * j] = o;
+                    }
+                }
+            }
+    };
+    if (m0 + kW4B <= a.M) out(std::true_type{});
+    else out(std::false_type{});
+}
+
 // Weights: per-64 mirror -> per-(row, group) codes and scales; one 256-thread block per row.
 // In place when wg == w (each element is read and written by the same thread).
 __global__ __launch_bounds__(256) void k_i8g64_to_grp(const int8_t* w, const float* s64, int K, int gs,
@@ -457,6 +614,16 @@ extern "C" int q27x_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int
 }
 
 namespace q27x {
+static int g_gemm_cus = 0;
+static int gemm_cus() {
+    if (!g_gemm_cus) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        g_gemm_cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
+                      p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
+    }
+    return g_gemm_cus;
+}
 int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, float alpha, const int8_t* x,
                     const float* sx, int M, void* y, int ldy, int out_bf16, const void* res, int ldr, int res_bf16,
                     float rs, hipStream_t s, const AlphaSel* asel) {
@@ -474,6 +641,33 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
     // measured 1-8% slower). Token tiles of 256 (8 waves, one block per CU, a 5-stage ring) from
     // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
     // two blocks per CU, a 4-stage ring, or 3 when 17+ groups' scales take the room).
+    // One group over the whole K: 256 x 256 tiles when their launch takes fewer tile rounds on the
+    // CUs, counting a 256 x 256 tile as 1.6 of the rs kernel's 256 x 128 tiles (their measured
+    // times per round at 4096 x 16384 x 5120: 101 and 63 us); with too few tiles for the CUs the
+    // narrower tiles keep more of them busy. Q27X_GEMM_W4 = 1 / 0 takes / avoids them wherever
+    // the shape allows (tests of the kernel at small shapes, measurements).
+    if (M >= 512 && a.ng == 1 && N % kW4B == 0 && K % kW4K == 0 && K >= 2 * kW4K &&
+        (long)(M > N ? M : N) * K < (1L << 31) && (long)M * ldy < (1L << 30) && (!res || (long)M * ldr < (1L << 30))) {
+        const long mt = (M + 255) / 256, g = gemm_cus();
+        const long rw = ((long)(N / kW4B) * mt + g - 1) / g, ro = ((long)(N / kGN) * mt + g - 1) / g;
+        const char* f = getenv("Q27X_GEMM_W4");
+        const bool force = f && f[0] == '1' && !f[1], avoid = f && f[0] == '0' && !f[1];
+        if (force || (!avoid && rw * 16 < ro * 10)) {
+            const dim3 grid((unsigned)((N / kW4B) * mt));
+            const int rm = !res ? 0 : res_bf16 ? 2 : 1;
+            if (out_bf16) {
+                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, true>), grid, dim3(256), 0, s, a);
+                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, true>), grid, dim3(256), 0, s, a);
+            } else {
+                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, false>), grid, dim3(256), 0, s, a);
+                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, false>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, false>), grid, dim3(256), 0, s, a);
+            }
+            Q27X_HIP(hipGetLastError());
+            return Q27X_OK;
+        }
+    }
     if (M >= 512 && K % 256 == 0 && gs % 128 == 0) {
         const unsigned mt = (unsigned)((M + 255) / 256);
         const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);

@@ -74,6 +74,26 @@ def test_gemm_i8g(gpu, O, M, N, K, gs, with_res):
     same(f"gemm {M}x{N}x{K}/{gs}", y, oracle_gemm(O, w, sw, x, sx, gs, 0.8125, res, 1.0))
 
 
+@pytest.mark.parametrize("M,N,K,with_res", [
+    (512, 256, 256, False),     # one tile, two K stages
+    (600, 512, 5120, True),     # ragged last token tile, two weight tiles, residual
+    (777, 768, 1152, True),     # an odd number of K stages
+    (1024, 256, 17408, False),  # down's K as one group (136 stages)
+])
+def test_gemm_i8g_wide_tiles(gpu, O, monkeypatch, M, N, K, with_res):
+    # the 256 x 256 tiles of the whole-K arm, taken at shapes where the launch would otherwise use
+    # the 256 x 128 ones (Q27X_GEMM_W4 = 1), against the oracle bit for bit
+    monkeypatch.setenv("Q27X_GEMM_W4", "1")
+    rng = np.random.default_rng(0x51E70500 + M + N + K)
+    w, x = codes(rng, (N, K)), codes(rng, (M, K))
+    w[0], x[0] = 127, -127
+    sw = rng.uniform(1e-4, 2e-3, (N, 1)).astype(np.float32)
+    sx = rng.uniform(1e-3, 5e-2, (M, 1)).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32) if with_res else None
+    y = gpu_gemm(gpu, w, sw, x, sx, K, 0.8125, res, 1.0)
+    same(f"wide-tile gemm {M}x{N}x{K}", y, oracle_gemm(O, w, sw, x, sx, K, 0.8125, res, 1.0))
+
+
 @pytest.mark.parametrize("gs", [5120, 1024])
 def test_gemm_i8g_full_shape_sampled(gpu, O, gs):
     # the prefill shape of gate (M = 4096 tokens, N = 17408, K = 5120) with whole-K groups (the
