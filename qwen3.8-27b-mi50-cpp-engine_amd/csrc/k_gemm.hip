@@ -217,6 +217,7 @@ __global__ __launch_bounds__(BM * 2) void k_gemm_i8g(GemmArgs a) {
 // are named at compile time; nsteps (K / 128) must be even. Rows are 128 bytes, chunk c of row R
 // in slot c ^ ((R >> 1) & 7) (the 16 rows one operand read serves fill a 256-byte bank window).
 // Same fold and tile order as k_gemm_i8g.
+template <int RES, bool OBF>   // epilogue form, as k_gemm_i8g_w4's
 __global__ __launch_bounds__(512) void k_gemm_i8g_rs(GemmArgs a) {
     constexpr int BM = 256, BN = kGN, NT = 512, KB = 128, kStage = (BM + BN) * KB;
     __shared__ __align__(16) int8_t sR[2 * kStage];
@@ -343,23 +344,33 @@ _Pragma("unroll")                                                               
 #undef Q27X_LD
 #undef Q27X_ST
 
+    // outputs (32-bit element offsets: the launcher keeps M x ldy and M x ldr below 2^30)
+    const uint32_t nb = (uint32_t)(n0 + wn * 64 + (lane & 31));
+    float al[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) al[j] = alpha_of(a.alpha, a.asel, (int)nb + 32 * j);
+    auto out = [&](auto full) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t < a.M) {
-                    float o = facc[i][j][r] * alpha_of(a.alpha, a.asel, n);
-                    if (a.res) o = o + a.rs * (a.res_bf16 ? bf2f(((const uint16_t*)a.res)[(size_t)t * a.ldr + n])
-                                                          : a.res[(size_t)t * a.ldr + n]);
-                    if (a.out_bf16) ((uint16_t*)a.y)[(size_t)t * a.ldy + n] = f2bf(o);
-                    else a.y[(size_t)t * a.ldy + n] = o;
+                if (decltype(full)::value || t < a.M) {
+                    const uint32_t yo = (uint32_t)t * (uint32_t)a.ldy + nb;
+                    const uint32_t ro = (uint32_t)t * (uint32_t)a.ldr + nb;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        float o = facc[i][j][r] * al[j];
+                        if constexpr (RES == 1) o = o + a.rs * a.res[ro + 32 * j];
+                        if constexpr (RES == 2) o = o + a.rs * bf2f(((const uint16_t*)a.res)[ro + 32 * j]);
+                        if constexpr (OBF) ((uint16_t*)a.y)[yo + 32 * j] = f2bf(o);
+                        else a.y[yo + 32 * j] = o;
+                    }
                 }
             }
-        }
+    };
+    if (m0 + BM <= a.M) out(std::true_type{});
+    else out(std::false_type{});
 }
 
 // One group over the whole K (the reference's default arm) on 256-token x 256-row tiles: 4 waves,
@@ -668,10 +679,21 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
             return Q27X_OK;
         }
     }
-    if (M >= 512 && K % 256 == 0 && gs % 128 == 0) {
+    if (M >= 512 && K % 256 == 0 && gs % 128 == 0 && (long)M * ldy < (1L << 30) &&
+        (!res || (long)M * ldr < (1L << 30))) {
         const unsigned mt = (unsigned)((M + 255) / 256);
         const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);
-        hipLaunchKernelGGL(k_gemm_i8g_rs, dim3((unsigned)(N / kGN) * mt), dim3(512), scl, (hipStream_t)s, a);
+        const dim3 grid((unsigned)(N / kGN) * mt);
+        const int rm = !res ? 0 : res_bf16 ? 2 : 1;
+        if (out_bf16) {
+            if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_rs<0, true>), grid, dim3(512), scl, s, a);
+            else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_rs<1, true>), grid, dim3(512), scl, s, a);
+            else hipLaunchKernelGGL((k_gemm_i8g_rs<2, true>), grid, dim3(512), scl, s, a);
+        } else {
+            if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_rs<0, false>), grid, dim3(512), scl, s, a);
+            else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_rs<1, false>), grid, dim3(512), scl, s, a);
+            else hipLaunchKernelGGL((k_gemm_i8g_rs<2, false>), grid, dim3(512), scl, s, a);
+        }
     } else if (M >= 512) {
         const unsigned mt = (unsigned)((M + 255) / 256);
         const size_t scl = (size_t)(256 + kGN) * a.ng * sizeof(float);
