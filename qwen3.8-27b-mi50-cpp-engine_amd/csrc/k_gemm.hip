@@ -24,7 +24,9 @@
 // to cover the memory latency (one stage ahead measured 16% of the int8 peak: every stage waited
 // for its own loads). At the end of each group the int32 tiles are folded into fp32
 // accumulators with the group's scales (staged in LDS for the whole K at the start) and
-// restarted from zero.
+// restarted from zero. Larger forms: 256-token tiles (k_gemm_i8g_rs, 8 waves), and with one group
+// over the whole K 256 x 256 tiles (k_gemm_i8g_w4, 4 waves of 128 x 128) where the launch needs
+// fewer tile rounds with them.
 #include <stdlib.h>
 #include <type_traits>
 
