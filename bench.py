@@ -385,7 +385,7 @@ def prefill_gemm(q27x, reps=20, gs=5120):
         b.free()
     us = ms.value * 1e3 / reps
     tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    kern = ("k_gemm_i8g_w4 (256 x 256 tiles, 4 waves of 128 x 128, 128-byte LDS-DMA stages, one group over the whole K)"
+    kern = ("k_gemm_i8g_w4 (256 x 256 tiles, 8 waves of 128 x 64, two per SIMD, 128-byte LDS-DMA stages, one group over the whole K)"
             if gs == K else
             "k_gemm_i8g_rs (256-token x 128-row tiles, register-staged 128-byte stages, fp32 group-sum epilogue)")
     return {"kernel": kern,

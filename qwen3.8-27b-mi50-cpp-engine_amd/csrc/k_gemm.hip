@@ -25,7 +25,7 @@
 // for its own loads). At the end of each group the int32 tiles are folded into fp32
 // accumulators with the group's scales (staged in LDS for the whole K at the start) and
 // restarted from zero. Larger forms: 256-token tiles (k_gemm_i8g_rs, 8 waves), and with one group
-// over the whole K 256 x 256 tiles (k_gemm_i8g_w4, 4 waves of 128 x 128) where the launch needs
+// over the whole K 256 x 256 tiles (k_gemm_i8g_w4, 8 waves of 128 x 64) where the launch needs
 // fewer tile rounds with them.
 #include <stdlib.h>
 #include <type_traits>
@@ -375,10 +375,12 @@ _Pragma("unroll")                                                               
     else out(std::false_type{});
 }
 
-// One group over the whole K (the reference's default arm) on 256-token x 256-row tiles: 4 waves,
-// one per SIMD, each owning a 128 x 128 quarter as 4 x 4 v_mfma_i32_32x32x32_i8 tiles (256
+// One group over the whole K (the reference's default arm) on 256-token x 256-row tiles: 8 waves,
+// two per SIMD, each owning 128 tokens x 64 rows as 4 x 2 v_mfma_i32_32x32x32_i8 tiles (128
 // accumulator registers; no fp32 group accumulators are needed, the scales apply once at the end),
-// so each MFMA reads half a KiB of LDS operands instead of the 64 x 64 quarter's full KiB. K
+// so each MFMA reads three quarters of a KiB of LDS operands instead of the 64 x 64 quarter's full
+// KiB, and while one wave of a SIMD waits (a barrier, its operand reads) the other multiplies
+// (with 4 waves of 128 x 128, one per SIMD, the same tile ran 17-20% slower). K
 // advances 128 bytes per stage (each stage row is one whole 128-byte line of a row, which halves
 // the load requests of 64-byte stages) through two 64 KiB LDS stages filled by LDS DMA. The
 // operand reads are pipelined one 32-byte slice ahead of the MFMAs, across the stage barrier too:
@@ -389,16 +391,16 @@ _Pragma("unroll")                                                               
 // outputs are the other kernels' bits.
 constexpr int kW4B = 256, kW4K = 128, kW4S = 2;
 constexpr int kW4Stage = 2 * kW4B * kW4K;              // 64 KiB: A rows, then B rows
-constexpr int kW4NI = kW4Stage / (1024 * 4);           // 1 KiB transfers per wave per stage (16)
+constexpr int kW4NI = kW4Stage / (1024 * 8);           // 1 KiB transfers per wave per stage (8)
 // RES: no residual (0), fp32 (1) or bf16 (2) residual rows; OBF: bf16 output. Instances per
 // epilogue form: with per-element branches on them the unrolled epilogue of 256 values per lane
 // cost ~20 us per tile.
 template <int RES, bool OBF>
-__global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
+__global__ __launch_bounds__(512) void k_gemm_i8g_w4(GemmArgs a) {
     __shared__ __align__(16) int8_t sR[kW4S * kW4Stage];
     __shared__ float sSx[kW4B], sSw[kW4B];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;
     const int nt = a.N / kW4B, mt = (a.M + kW4B - 1) / kW4B, T = nt * mt;
     const int b = blockIdx.x;
     const int tile = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
@@ -406,11 +408,11 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
     const int within = tile - grp * 4 * nt;
     const int m0 = (fm + within % gsz) * kW4B, n0 = (within / gsz) * kW4B;
     const int K = a.K, nsteps = K / kW4K;
-    // DMA: transfer i (< 16) of wave w fills stage rows 8 (16 w + i) .. +8; lane l writes row
-    // 8 (16 w + i) + l / 8, slot l % 8, so it loads that row's chunk (l % 8) ^ ((row >> 1) & 7)
-    // (waves 0 and 1 fill the A rows, waves 2 and 3 the B rows: one base per wave, byte offsets
-    // below 2^31 for the row counts and K this kernel takes)
-    const int8_t* gb = wave < 2 ? a.x : a.w;
+    // DMA: transfer i (< 8) of wave w fills stage rows 8 (8 w + i) .. +8; lane l writes row
+    // 8 (8 w + i) + l / 8, slot l % 8, so it loads that row's chunk (l % 8) ^ ((row >> 1) & 7)
+    // (waves 0-3 fill the A rows, waves 4-7 the B rows: one base per wave, byte offsets below
+    // 2^31 for the row counts and K this kernel takes)
+    const int8_t* gb = wave < 4 ? a.x : a.w;
     uint32_t go[kW4NI];
 #pragma unroll
     for (int i = 0; i < kW4NI; ++i) {
@@ -428,35 +430,35 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
             lds_dma16(gb + go[i] + (uint32_t)(step * kW4K), __builtin_amdgcn_readfirstlane(base + 1024 * i));
     };
     issue(0, 0);
-    {
+    if (tid < kW4B) {
         const int t = (m0 + tid < a.M) ? m0 + tid : a.M - 1;
         sSx[tid] = a.sx[t];
         sSw[tid] = a.sw[n0 + tid];
     }
-    v16i acc[4][4];
+    v16i acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-    // operand rows of this lane: A (token) wm*128 + 32 i + lane % 32, B (weight row) wn*128 + 32 j +
+    // operand rows of this lane: A (token) wm*128 + 32 i + lane % 32, B (weight row) wn*64 + 32 j +
     // lane % 32; both take chunk 2 kk + lane / 32 of the stage's 32-byte K slice kk
-    const int arow = wm * 128 + (lane & 31), brow = kW4B + wn * 128 + (lane & 31);
+    const int arow = wm * 128 + (lane & 31), brow = kW4B + wn * 64 + (lane & 31);
     const int swa = (arow >> 1) & 7, swb = ((brow - kW4B) >> 1) & 7, kh = lane >> 5;
-    auto rd = [&](v4i (&av)[4], v4i (&bv)[4], int slot, int kk) __attribute__((always_inline)) {
+    auto rd = [&](v4i (&av)[4], v4i (&bv)[2], int slot, int kk) __attribute__((always_inline)) {
         const int8_t* st = sR + slot * kW4Stage;
         const int c = 2 * kk + kh;
 #pragma unroll
         for (int i = 0; i < 4; ++i) av[i] = *(const v4i*)(st + (arow + 32 * i) * kW4K + ((c ^ swa) << 4));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bv[j] = *(const v4i*)(st + (brow + 32 * j) * kW4K + ((c ^ swb) << 4));
+        for (int j = 0; j < 2; ++j) bv[j] = *(const v4i*)(st + (brow + 32 * j) * kW4K + ((c ^ swb) << 4));
     };
-    auto mm = [&](const v4i (&av)[4], const v4i (&bv)[4]) __attribute__((always_inline)) {
+    auto mm = [&](const v4i (&av)[4], const v4i (&bv)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
     };
     // this wave's transfers of the next stage done and its operand reads of the current one
     // returned; after the barrier every wave's are (nothing is scheduled across it)
@@ -468,7 +470,7 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     };
     constexpr int SL = kW4K / 32;                      // 32-byte slices per stage
-    v4i oa[2][4], ob[2][4];
+    v4i oa[2][4], ob[2][2];
     sync();                                            // stage 0 everywhere (and the scales)
     issue(1 < nsteps ? 1 : 0, 1);
     rd(oa[0], ob[0], 0, 0);
@@ -487,9 +489,9 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
                 issue(s + 2 < nsteps ? s + 2 : 0, s & 1);
                 rd(oa[nx], ob[nx], (s + 1) & 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
             mm(oa[cu], ob[cu]);
-            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         }
     }
     // no transfer may still be writing LDS when the block ends
@@ -497,11 +499,11 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
     // the tile's outputs; rows past M only in the last token tile. Element offsets are 32-bit
     // (the launcher keeps M x ldy and M x ldr below 2^30), so the stores take the output's base in
     // scalar registers.
-    const uint32_t nb = (uint32_t)(n0 + wn * 128 + (lane & 31));
-    float swv[4], al[4];
+    const uint32_t nb = (uint32_t)(n0 + wn * 64 + (lane & 31));
+    float swv[2], al[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        swv[j] = sSw[wn * 128 + 32 * j + (lane & 31)];
+    for (int j = 0; j < 2; ++j) {
+        swv[j] = sSw[wn * 64 + 32 * j + (lane & 31)];
         al[j] = alpha_of(a.alpha, a.asel, (int)nb + 32 * j);
     }
     auto out = [&](auto full) __attribute__((always_inline)) {
@@ -515,7 +517,7 @@ __global__ __launch_bounds__(256) void k_gemm_i8g_w4(GemmArgs a) {
                     const uint32_t yo = (uint32_t)t * (uint32_t)a.ldy + nb;
                     const uint32_t ro = (uint32_t)t * (uint32_t)a.ldr + nb;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < 2; ++j) {
                         float o = __builtin_fmaf((float)acc[i][j][r], swv[j] * sxv, 0.0f) * al[j];
                         if constexpr (RES == 1) o = o + a.rs * a.res[ro + 32 * j];
                         if constexpr (RES == 2) o = o + a.rs * bf2f(((const uint16_t*)a.res)[ro + 32 * j]);
@@ -655,9 +657,9 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
     // 512 tokens on: a third fewer bytes per MAC through the CU's load path; else 128 (4 waves,
     // two blocks per CU, a 4-stage ring, or 3 when 17+ groups' scales take the room).
     // One group over the whole K: 256 x 256 tiles when their launch takes fewer tile rounds on the
-    // CUs, counting a 256 x 256 tile as 1.6 of the rs kernel's 256 x 128 tiles (their measured
-    // times per round at 4096 x 16384 x 5120: 101 and 63 us); with too few tiles for the CUs the
-    // narrower tiles keep more of them busy. Q27X_GEMM_W4 = 1 / 0 takes / avoids them wherever
+    // CUs, counting a round of 256 x 256 tiles as 1.4 rounds of the rs kernel's 256 x 128 tiles
+    // (measured per round at 4096 x 16384 x 5120: 90 and 63 us); with too few tiles for the CUs
+    // the narrower tiles keep more of them busy. Q27X_GEMM_W4 = 1 / 0 takes / avoids them wherever
     // the shape allows (tests of the kernel at small shapes, measurements).
     if (M >= 512 && a.ng == 1 && N % kW4B == 0 && K % kW4K == 0 && K >= 2 * kW4K &&
         (long)(M > N ? M : N) * K < (1L << 31) && (long)M * ldy < (1L << 30) && (!res || (long)M * ldr < (1L << 30))) {
@@ -665,17 +667,17 @@ int launch_gemm_i8g(const int8_t* w, const float* sw, int N, int K, int gs, floa
         const long rw = ((long)(N / kW4B) * mt + g - 1) / g, ro = ((long)(N / kGN) * mt + g - 1) / g;
         const char* f = getenv("Q27X_GEMM_W4");
         const bool force = f && f[0] == '1' && !f[1], avoid = f && f[0] == '0' && !f[1];
-        if (force || (!avoid && rw * 16 < ro * 10)) {
+        if (force || (!avoid && rw * 14 < ro * 10)) {
             const dim3 grid((unsigned)((N / kW4B) * mt));
             const int rm = !res ? 0 : res_bf16 ? 2 : 1;
             if (out_bf16) {
-                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, true>), grid, dim3(256), 0, s, a);
-                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, true>), grid, dim3(256), 0, s, a);
-                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, true>), grid, dim3(256), 0, s, a);
+                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, true>), grid, dim3(512), 0, s, a);
+                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, true>), grid, dim3(512), 0, s, a);
+                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, true>), grid, dim3(512), 0, s, a);
             } else {
-                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, false>), grid, dim3(256), 0, s, a);
-                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, false>), grid, dim3(256), 0, s, a);
-                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, false>), grid, dim3(256), 0, s, a);
+                if (rm == 0) hipLaunchKernelGGL((k_gemm_i8g_w4<0, false>), grid, dim3(512), 0, s, a);
+                else if (rm == 1) hipLaunchKernelGGL((k_gemm_i8g_w4<1, false>), grid, dim3(512), 0, s, a);
+                else hipLaunchKernelGGL((k_gemm_i8g_w4<2, false>), grid, dim3(512), 0, s, a);
             }
             Q27X_HIP(hipGetLastError());
             return Q27X_OK;
