@@ -192,9 +192,12 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     if constexpr (PRE) {
         // input rows first, then the weights, so waiting for the rows leaves the weights in flight.
         // With two rows per 256-thread group (NR > 4) the held rows and the prefetch do not fit
-        // in 128 registers together; the weights are then requested after the norm.
+        // in 128 registers together; the weights are then requested after the norm. So are the
+        // conv-epilogue kernel's (in_qkv|in_z): with its prefetch in flight during the norm it took
+        // 19.9-20.0 us at 3 rows, with the prefetch after the norm 19.0 (the same change in the
+        // SwiGLU and plain-store kernels measured within the noise).
         PreNorm<NSTEP, NR> pn;
-        constexpr bool EARLY = PreNorm<NSTEP, NR>::RPG == 1;
+        constexpr bool EARLY = PreNorm<NSTEP, NR>::RPG == 1 && !CV;
         pn.load(a.pre);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (EARLY) prefetch();
