@@ -90,6 +90,15 @@ def test_full_width_prefill_gemm_matches_oracle(gpu, O, n, chunk, gs):
     run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=512, pf_gs=gs), n, 2, chunk)
 
 
+def test_full_width_prefill_wide_gemm_tiles_match_oracle(gpu, O, monkeypatch):
+    """The 256 x 256 GEMM tiles in every epilogue form the prefill uses (fp32 and bf16 outputs, the
+    bf16 residual of down, out_proj and o_proj) at the model's widths: 520 tokens in a 512-row
+    chunk (the tiles need 512 rows) and an 8-row one, with the tiles forced wherever the shape
+    allows them (Q27X_GEMM_W4 = 1); state after the prompt and two rounds bit for bit."""
+    monkeypatch.setenv("Q27X_GEMM_W4", "1")
+    run_case(gpu, O, gpu.default_config(spec_k=2, n_layers=4, ctx=1024), 520, 2)
+
+
 def test_full_model_spec_equals_plain_after_prefill_gemm(gpu):
     X = gpu
     cfg = X.default_config(spec_k=2, ctx=2048)
