@@ -93,6 +93,16 @@ __device__ __forceinline__ float tree_t(float (&x)[P], int lane) {
 // FULL: K == 1024 * NSTEP (no slab bounds checks). PRE: the activation stage is the RMSNorm +
 // quantize of the raw input rows (a.pre), computed by every block (K = NSTEP * 1024, NW = 16).
 constexpr int kSwRows = 288;     // SwiGLU rows one block may hold: 32 F + 8 (quarters per block)
+// The activation stage of NR rows at K = 1024 NSTEP: 16-byte code words and a 4-byte scale per
+// slab in LDS. When all of it does not fit (K = 17408 at 8 rows), the scales of the rows from XL on
+// stay in registers. (512 bytes are left for the kernel's other LDS variables.)
+template <int NR, int NSTEP>
+struct StageFit {
+    static constexpr int kLds = 160 * 1024 - 512;
+    static constexpr int kCodes = NR * NSTEP * 64 * 16;
+    static constexpr int XL = (kCodes + NR * NSTEP * 64 * 4 <= kLds) ? NR : (kLds - kCodes) / (NSTEP * 64 * 4);
+    static constexpr int kBytes = kCodes + XL * NSTEP * 64 * 4;
+};
 template <int NR, int NSTEP, int RPW, int EPI, bool FULL, bool PRE, int NW>
 __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr bool CV = (EPI == EPI_CONV);
@@ -104,12 +114,16 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
     constexpr int V = RPW * NR, P = Pow2<V>::value, LPV = 64 / P;
     static_assert(EPI != EPI_SWIGLU || RPW == 1, "SwiGLU deals single rows");
     static_assert(!PRE || NW == 16, "the norm prologue runs on 16-wave blocks");
-    // XR: the K = 17408 stage of more than 4 rows (NR x 1088 slabs x 20 B) does not fit in 160 KB
-    // with all its scales: rows 0..3 keep their scales in LDS, the rows after them in registers
-    // (each lane holds the scales of its own slabs). With every row's scales in registers the
-    // kernel ran out of them and waited for each LDS code read on its own.
-    constexpr bool XR = (NSTEP >= 17 && NR > 4);
-    constexpr int XL = XR ? 4 : NR;                    // rows whose scales are staged in LDS
+    // XR: the K = 17408 stage of 8 rows (8 x 1088 slabs x 20 B) does not fit in 160 KB with all
+    // its scales: rows 0..4 keep their scales in LDS, rows 5..7 in registers (each lane holds the
+    // scales of its own slabs; with every row's scales in registers the kernel ran out of them).
+    // XB: from 5 rows on each step's LDS reads are requested together ahead of its arithmetic;
+    // left to itself the compiler waits for each read before the next (K = 17408 at 6 rows with
+    // every scale in LDS: 32.6 us unbatched, 20.0 us batched; at 8 rows out_proj 12.9 -> 11.5 us,
+    // o_proj 9.7 -> 9.2, in_qkv|in_z 29.3 -> 28.2, gate|up unchanged).
+    constexpr int XL = StageFit<NR, NSTEP>::XL;        // rows whose scales are staged in LDS
+    constexpr bool XR = XL < NR;
+    constexpr bool XB = (NR > 4);
     static_assert(!XR || (!PRE && FULL && EPI == EPI_STORE), "register scales: plain full-K stage only");
     __shared__ uint4 sx[NR * SL];
     __shared__ float ssc[XL * SL];
@@ -504,11 +518,10 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
 #pragma unroll
         for (int t = 0; t < NSTEP; ++t) {
             const int s = t * 64 + lane;
-            // XR: the step's code reads are requested together ahead of its arithmetic (left to
-            // itself at this register pressure the compiler waits for each read before the next)
-            uint4 xb[XR ? NR : 1];
-            float sb[XR ? XL : 1];
-            if constexpr (XR) {
+            // XB: the step's code and scale reads, requested together ahead of its arithmetic
+            uint4 xb[XB ? NR : 1];
+            float sb[XB ? XL : 1];
+            if constexpr (XB) {
 #pragma unroll
                 for (int n = 0; n < NR; ++n) {
                     xb[n] = sx[n * SL + s];
@@ -518,10 +531,10 @@ __global__ __launch_bounds__(NW * 64) void k_proj(ProjArgs a) {
             }
 #pragma unroll
             for (int n = 0; n < NR; ++n) {
-                const uint4 xa = XR ? xb[XR ? n : 0] : sx[n * SL + s];
+                const uint4 xa = XB ? xb[XB ? n : 0] : sx[n * SL + s];
                 float sa;
                 if (n >= XL) sa = XS[n >= XL ? n - XL : 0][t];
-                else sa = XR ? sb[XR && n < XL ? n : 0] : ssc[n * SL + s];
+                else sa = XB ? sb[XB && n < XL ? n : 0] : ssc[n * SL + s];
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
                     const int d = dot16(W[r][t], xa);
@@ -575,7 +588,11 @@ static int knob_wpc17() { static const int v = env_knob("Q27X_WPC17", 8, 4, 16);
 
 template <int NR, int NSTEP, int EPI, bool FULL, bool PRE, int RPW>
 static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
-    constexpr int NW = (PRE || EPI == EPI_SWIGLU || (FULL && NSTEP < 17)) ? 16 : 4;
+    // K = 17408: 4-wave blocks (two per CU up to 3 rows, one from 4 rows on, where the stage fills
+    // the LDS), and one 8-wave block per CU (two waves per SIMD) at 7 and 8 rows. Measured per row
+    // count (down, 5120 x 17408, 4 -> 8 waves): 23.9 -> 22.9 us at 7 rows and 27.0 -> 25.0 us at
+    // 8, but slower at 4-6 rows (19.1 -> 19.6, 19.7 -> 20.5, 20.0 -> 21.6 us).
+    constexpr int NW = (PRE || EPI == EPI_SWIGLU || (FULL && NSTEP < 17)) ? 16 : (NSTEP >= 17 && NR >= 7) ? 8 : 4;
     int grid;
     if (EPI == EPI_SWIGLU) {
         const int nunits = a.rows >> 5;
@@ -594,7 +611,7 @@ static int run_proj_rpw(const ProjArgs& a, hipStream_t s) {
         const int ngroups = (a.rows + RPW - 1) / RPW;
         int wpc = (NSTEP >= 17) ? knob_wpc17() : knob_wpc5();
         // no more waves per CU than the blocks whose LDS stages fit (160 KB per CU)
-        constexpr int kStage = NR * NSTEP * 64 * 16 + ((NSTEP >= 17 && NR > 4) ? 4 : NR) * NSTEP * 64 * 4;
+        constexpr int kStage = StageFit<NR, NSTEP>::kBytes;
         constexpr int kBpc = (160 * 1024) / kStage > 0 ? (160 * 1024) / kStage : 1;
         if (wpc > kBpc * NW) wpc = kBpc * NW;
         const int wmax = num_cus() * wpc;
