@@ -199,6 +199,16 @@ __device__ __forceinline__ float max_xor(float x, int width) {
 // The same max over the 4 lanes of a quad with DPP quad permutes (a VALU operand route, no LDS
 // crossbar): lane l reads lane l ^ 2 (quad_perm [2,3,0,1]), then l ^ 1 ([1,0,3,2]). The max of the
 // same four values in any order is the same float.
+// lane b's value of each quad of lanes, in all four lanes (b a constant after unrolling)
+__device__ __forceinline__ float quad_bcast(float x, int b) {
+    const int v = __float_as_int(x);
+    switch (b & 3) {
+        case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, false));
+        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, false));
+        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, false));
+        default: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, false));
+    }
+}
 __device__ __forceinline__ float max_quad(float x) {
     x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false)));
     x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false)));

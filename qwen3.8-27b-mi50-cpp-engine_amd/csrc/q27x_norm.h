@@ -218,38 +218,104 @@ struct PreNorm {
             if (r >= NR) break;
             const float ss = ((wsum[j][tg][0] + wsum[j][tg][1]) + wsum[j][tg][2]) + wsum[j][tg][3];
             const float inv = rsqrt_cr(ss * (1.0f / (float)n) + a.eps);
+            // (the two-rows form below, applied at one row per group, made in_qkv|in_z at 3 rows
+            // 18.65 -> 19.0 us; at 8 rows it took gate|up 42.0 -> 41.6 us, in_qkv|in_z 25.4 ->
+            // 25.1 us and the K=7 round 9.67 -> 9.59 ms)
+            if constexpr (RPG == 1) {
+                // one chunk at a time: values, group maximum, the quotient g / s, codes
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int k = i * 1024 + 4 * t;
-                const float wf[4] = {__uint_as_float(wb[i].x << 16), __uint_as_float(wb[i].x & 0xFFFF0000u),
-                                     __uint_as_float(wb[i].y << 16), __uint_as_float(wb[i].y & 0xFFFF0000u)};
-                float q[4], mx = 0.0f;
-                uint16_t yb[4];
+                for (int i = 0; i < NCH; ++i) {
+                    const int k = i * 1024 + 4 * t;
+                    const float wf[4] = {__uint_as_float(wb[i].x << 16), __uint_as_float(wb[i].x & 0xFFFF0000u),
+                                         __uint_as_float(wb[i].y << 16), __uint_as_float(wb[i].y & 0xFFFF0000u)};
+                    float q[4], mx = 0.0f;
+                    uint16_t yb[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float nm = xv[j][i][e] * inv * (a.plus + wf[e]);
-                    if constexpr (WR || QB) yb[e] = f2bf(nm);
-                    q[e] = QB ? bf2f(yb[e]) : nm;
-                    mx = fmaxf(mx, fabsf(q[e]));
+                    for (int e = 0; e < 4; ++e) {
+                        const float nm = xv[j][i][e] * inv * (a.plus + wf[e]);
+                        if constexpr (WR || QB) yb[e] = f2bf(nm);
+                        q[e] = QB ? bf2f(yb[e]) : nm;
+                        mx = fmaxf(mx, fabsf(q[e]));
+                    }
+                    if (WR && writer && a.y)
+                        *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                               (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                    if (WR && ylds)
+                        *(uint2*)(ylds + (size_t)r * n + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                        (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                    mx = max_quad(mx);
+                    const float s = mx * g * (1.0f / 127.0f);
+                    const float qi = (s > 0.0f) ? (g / s) : 0.0f;
+                    uint32_t pk = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(q[e], qi)) << (8 * e);
+                    const int slab = 64 * i + (t >> 2);
+                    sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
+                    if ((t & 3) == 0) ssc[r * SL + slab] = s;
+                    if (WR && writer && a.xq) {
+                        *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
+                        if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
+                    }
                 }
-                if (WR && writer && a.y)
-                    *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
-                                                                           (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
-                if (WR && ylds)
-                    *(uint2*)(ylds + (size_t)r * n + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
-                                                                    (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
-                mx = max_quad(mx);
-                const float s = mx * g * (1.0f / 127.0f);
-                const float qi = (s > 0.0f) ? (g / s) : 0.0f;
-                uint32_t pk = 0;
+            } else {
+                // two rows per group: the row's normalized values and each group's scale first (a
+                // group of 16 is a quad of lanes)
+                float qv[NCH][4], sv[NCH];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) pk |= ((uint32_t)(uint8_t)qcode(q[e], qi)) << (8 * e);
-                const int slab = 64 * i + (t >> 2);
-                sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
-                if ((t & 3) == 0) ssc[r * SL + slab] = s;
-                if (WR && writer && a.xq) {
-                    *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
-                    if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
+                for (int i = 0; i < NCH; ++i) {
+                    const int k = i * 1024 + 4 * t;
+                    const float wf[4] = {__uint_as_float(wb[i].x << 16), __uint_as_float(wb[i].x & 0xFFFF0000u),
+                                         __uint_as_float(wb[i].y << 16), __uint_as_float(wb[i].y & 0xFFFF0000u)};
+                    float mx = 0.0f;
+                    uint16_t yb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float nm = xv[j][i][e] * inv * (a.plus + wf[e]);
+                        if constexpr (WR || QB) yb[e] = f2bf(nm);
+                        qv[i][e] = QB ? bf2f(yb[e]) : nm;
+                        mx = fmaxf(mx, fabsf(qv[i][e]));
+                    }
+                    if (WR && writer && a.y)
+                        *(uint2*)(a.y + (size_t)r * a.ystride + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                               (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                    if (WR && ylds)
+                        *(uint2*)(ylds + (size_t)r * n + k) = make_uint2((uint32_t)yb[0] | ((uint32_t)yb[1] << 16),
+                                                                        (uint32_t)yb[2] | ((uint32_t)yb[3] << 16));
+                    sv[i] = max_quad(mx) * g * (1.0f / 127.0f);
+                }
+                // the groups' quotients g / s: lane m of a quad divides for the chunks m, m + 4, ...
+                // (every lane of the quad holds the same s), then each chunk's quotient is broadcast
+                // from its lane; the same correctly rounded division as in every lane, a quarter of
+                // the instructions
+                constexpr int ND = (NCH + 3) / 4;
+                const int m = t & 3;
+                float qd[ND];
+#pragma unroll
+                for (int d = 0; d < ND; ++d) {
+                    float den = sv[4 * d];
+#pragma unroll
+                    for (int u = 1; u < 4; ++u)
+                        if (4 * d + u < NCH) den = (m == u) ? sv[(4 * d + u < NCH) ? 4 * d + u : 0] : den;
+                    qd[d] = (den > 0.0f) ? (g / den) : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    const int k = i * 1024 + 4 * t;
+                    const float s = sv[i];
+                    const float qi = quad_bcast(qd[i >> 2], i);
+                    int c[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) c[e] = qcode(qv[i][e], qi);
+                    // the four codes' low bytes, in order
+                    const uint32_t pk = __builtin_amdgcn_perm((uint32_t)c[1], (uint32_t)c[0], 0x0c0c0400u) |
+                                        __builtin_amdgcn_perm((uint32_t)c[3], (uint32_t)c[2], 0x04000c0cu);
+                    const int slab = 64 * i + (t >> 2);
+                    sxw[((size_t)r * SL + slab) * 4 + (t & 3)] = pk;
+                    if ((t & 3) == 0) ssc[r * SL + slab] = s;
+                    if (WR && writer && a.xq) {
+                        *(uint32_t*)(a.xq + (size_t)r * n + k) = pk;
+                        if ((t & 3) == 0) a.xs[(size_t)r * (n >> 4) + (k >> 4)] = s;
+                    }
                 }
             }
         }
