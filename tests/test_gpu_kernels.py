@@ -114,7 +114,8 @@ def test_proj_config0(gpu, O, nr):
 
 @pytest.mark.parametrize("rows,K,nr", [(5120, 6144, 3), (5120, 17408, 3), (5120, 17408, 8), (5120, 17408, 5),
                                        (1000, 17408, 7), (5120, 17408, 4), (5120, 17408, 6), (10240, 5120, 8),
-                                       (5120, 4096, 2), (1000, 1024, 5)])
+                                       (5120, 6144, 8), (5120, 4096, 7), (5120, 4096, 2), (1000, 1024, 5),
+                                       (1000, 3136, 6)])
 def test_proj_shapes(gpu, O, rows, K, nr):
     X = gpu
     rng = np.random.default_rng(rows * 7 + K + nr)
