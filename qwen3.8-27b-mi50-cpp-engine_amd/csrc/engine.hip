@@ -108,7 +108,7 @@ struct PfBuf {
     float* gu = nullptr;         // [cap][max(2I, nz)] gate|up GEMM output (GDN scan's mixed rows before)
     uint16_t* mix = nullptr;     // [cap][max(nz, att)] mixer output
     float* rowsc = nullptr;      // [3][cap][vh] GDN decay, beta; the scan's k^.q^ ([cap][kh])
-    float* work = nullptr;       // attention split partials of kPfAttnRows rows
+    float* work = nullptr;       // attention split partials of one launch (pf_attn_work_rows rows)
     uint16_t* cv = nullptr;      // [cap][nqkv] convolved q|k|v rows
     std::vector<void*> allocs;
 };
@@ -1385,7 +1385,14 @@ int q27x_prefill(q27x_ctx* x, const int32_t* ids, int n, int32_t* first_token) {
 // brought to that representation from its per-64 mirror right before its GEMM; the norms, GDN
 // conv / row scalars / scan, attention, SwiGLU and residual adds keep the decode path's
 // arithmetic. The MTP prompt pass fills only the draft KV cache (src/q27_main.cpp:2647-2688).
-constexpr int kPfAttnRows = 128;    // query rows per attention launch (tiles of 8)
+constexpr int kPfAttnRows = 128;    // query rows per attention launch
+// rows per attention row tile: up to 16, at most 64 query vectors per kv head (one block holds
+// them); a launch's tiles take the work area of ceil(kPfAttnRows / tile) whole tiles
+static int pf_attn_tile(const q27x_config& c) { return std::max(1, std::min(16, 64 / (c.n_q / c.n_kv))); }
+static int pf_attn_work_rows(const q27x_config& c) {
+    const int zr = pf_attn_tile(c);
+    return (kPfAttnRows + zr - 1) / zr * zr;
+}
 static int env_int(const char* name, int def);
 // Rows per pass over the layers for an n-token prompt: 1024 from 2048 tokens on, else 512 (with the two
 // streams below, smaller chunks overlap more: at 4096 tokens 1024-row chunks measured 15.1K tok/s
@@ -1436,7 +1443,7 @@ static int pf_alloc(q27x_ctx* x, int cap, PfBuf** slot) {
         (rc = A((void**)&B->pb, C * wmax * 2)) || (rc = A((void**)&B->qh, C * std::max(x->att, 1) * 2)) ||
         (rc = A((void**)&B->gu, C * std::max(2 * I, x->nz) * 4)) || (rc = A((void**)&B->mix, C * std::max(x->nz, x->att) * 2)) ||
         (rc = A((void**)&B->rowsc, 3 * C * c.gdn_vh * 4)) ||
-        (rc = A((void**)&B->work, attn_work_floats(c.n_q, c.head_dim, (int)ms, kPfAttnRows) * 4)) ||
+        (rc = A((void**)&B->work, attn_work_floats(c.n_q, c.head_dim, (int)ms, pf_attn_work_rows(c)) * 4)) ||
         (rc = A((void**)&B->cv, C * x->nqkv * 2))) {
         for (void* p : B->allocs) (void)hipFree(p);
         delete B;
@@ -1530,13 +1537,14 @@ static int pf_layer(q27x_ctx* x, int l, int p0, int C) {
         a.nq = c.n_q; a.nkv = c.n_kv; a.hd = c.head_dim; a.gate = c.attn_gate; a.eps = c.rms_eps;
         a.pos0_imm = p0; a.sl2e = x->sl2e; a.stop = &d->stop;
         if ((rc = launch_attn_prep_rows(a, C, s))) return rc;
+        const int zr = pf_attn_tile(c);
         for (int q0 = 0; q0 < C; q0 += kPfAttnRows) {
             const int cq = std::min(kPfAttnRows, C - q0);
             AttnArgs t = a;
             t.qh = B.qh + (size_t)q0 * x->att; t.qkv = B.pb + (size_t)q0 * wq; t.pos0_imm = p0 + q0;
             t.work = B.work; t.max_splits = (p0 + q0 + cq + kSplit - 1) / kSplit;
-            t.zrows = 8; t.ztotal = cq; t.out = B.mix + (size_t)q0 * x->att;
-            if ((rc = launch_attn(t, 8, s, false))) return rc;
+            t.zrows = zr; t.ztotal = cq; t.out = B.mix + (size_t)q0 * x->att;
+            if ((rc = launch_attn(t, zr, s, false))) return rc;
         }
         if ((rc = launch_pf_quant_bf16(B.mix, x->att, C, x->att, pf_gs(c, x->att), Y.in_s_out, B.xq, B.xs, s))) return rc;
         if ((rc = pf_gemm(x, Y.o, 0, H, B.xq, B.xs, C, B.x, H, 0, B.h))) return rc;

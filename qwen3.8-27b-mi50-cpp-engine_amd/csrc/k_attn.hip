@@ -715,7 +715,8 @@ static bool attn_general(const AttnArgs& a) {
 
 static int attn_check(const AttnArgs& a, int nr) {
     const bool rot_ok = a.rot >= 2 && (a.rot & (a.rot - 1)) == 0 && (a.rot <= 64 || (a.rot == kHD && a.hd == kHD));
-    if ((a.hd != 128 && a.hd != 256) || a.nkv < 1 || a.nq % a.nkv || nr < 1 || nr > kMaxRows ||
+    // (row tiles of a prefill may hold more rows than a verify step, as many as kMaxQ query vectors)
+    if ((a.hd != 128 && a.hd != 256) || a.nkv < 1 || a.nq % a.nkv || nr < 1 || nr > (a.zrows ? kMaxQ : kMaxRows) ||
         nr * (a.nq / a.nkv) > kMaxQ || (a.kv_group != 16 && a.kv_group != 32 && a.kv_group != 64) || !rot_ok) {
         set_error("attn: unsupported shape (nq=%d nkv=%d hd=%d nr=%d kv_group=%d rot=%d: hd 128 or 256, at most %d "
                   "query vectors per kv head, rot a power of two <= 64 or the whole 128-wide head)", a.nq, a.nkv, a.hd,
