@@ -327,6 +327,7 @@ __global__ __launch_bounds__(64 * WPB) void k_gdn_scan(GdnArgs a, const float* _
     constexpr int R = 8 * WPB;                           // rows staged per batch
     constexpr int CPT = 2 * kD / NT;                     // q|k channels loaded per thread
     constexpr int BPH = kD / NC;                         // blocks per head
+    static_assert(CPT >= 1 && CPT * NT == 2 * kD && BPH * NC == kD, "1, 2 or 4 waves per block");
     const int h = blockIdx.x / BPH, part = blockIdx.x % BPH;
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = lane >> 4, cw = 16 * wv + (lane & 15);      // column within the block's NC
